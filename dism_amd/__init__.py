@@ -1,0 +1,15 @@
+"""dism_amd: MI355X-native (gfx950) flash_dism hard suffix-matching core.
+
+Public API mirrors the reference flash_dism hard path (dism_v3/python/flash_dism/
+{hard_forward,hard_backward,summary}.py) on hand-written HIP kernels behind the C ABI of
+include/dism_hard.h (libdism_hip.so, loaded with ctypes).
+"""
+from .hard_backward import backward_hard, backward_hard_recompute
+from .hard_forward import forward_hard, hard_dlog_weights, hard_log_weights, hard_readout
+from .labels import sign_labels
+from .summary import hard_boundary, hard_chunk_scan, summarize_hard
+from .core import HardCore, dism_core_hard
+
+__all__ = ["forward_hard", "hard_readout", "hard_log_weights", "hard_dlog_weights",
+           "backward_hard", "backward_hard_recompute", "summarize_hard", "hard_chunk_scan",
+           "hard_boundary", "sign_labels", "HardCore", "dism_core_hard"]

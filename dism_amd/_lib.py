@@ -1,0 +1,66 @@
+"""ctypes binding of libdism_hip.so (C ABI declared in include/dism_hard.h).
+
+The library is loaded from this package directory.  If it is missing the import of the
+compute entry points raises: there is no CPU fallback for the hard core.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libdism_hip.so")
+
+# name -> argtypes (all return int32 status)
+_P, _I32, _I64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+SIGNATURES = {
+    "dism_sign_labels": [_P, _I32, _I64, _I64, _I64, _I32, _P, _P],
+    "dism_hard_log_weights": [_P, _I32, _I64, _P, _P],
+    "dism_hard_dlog_weights": [_P, _I32, _I64, _P, _P],
+    "dism_hard_summary": [_P, _P, _P, _I64, _I64, _I64, _P, _P],
+    "dism_hard_chunk": [_P, _P, _I64, _I64, _P],
+    "dism_hard_boundary": [_P, _P, _P, _I64, _I64, _I64, _I32, _I32, _P, _P],
+    "dism_hard_readout": [_P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _I64, _I64, _I64, _I64,
+                          _I32, _I32, _P, _I32, _P, _P, _P, _P],
+    "dism_hard_backward": [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _P, _I64, _P, _I64,
+                           _I64, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P],
+    "dism_hard_backward_queries": [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _P, _I64,
+                                   _P, _I64, _I64, _I64, _I32, _I32, _P, _P, _P],
+    "dism_hard_backward_keys": [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _I64, _P, _I64,
+                                _I64, _I64, _I32, _I32, _P, _P, _P],
+    "dism_hard_tau_reduce": [_P, _I64, _I64, _I64, _P, _P],
+}
+
+_lib = None
+
+
+class DismNativeMissing(RuntimeError):
+    pass
+
+
+def load():
+    """Load (once) and return the ctypes handle; raise if the HIP library is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise DismNativeMissing(
+                f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`"
+                " (the hard core has no CPU fallback)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int32
+        lib.dism_last_error.restype = ctypes.c_char_p
+        lib.dism_last_error.argtypes = []
+        lib.dism_abi_version.restype = ctypes.c_int32
+        lib.dism_abi_version.argtypes = []
+        _lib = lib
+    return _lib
+
+
+def call(name, *args):
+    """Invoke a C-ABI entry point; translate a non-zero status into RuntimeError."""
+    lib = load()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        msg = lib.dism_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name}: {msg}")

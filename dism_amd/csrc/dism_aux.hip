@@ -1,0 +1,203 @@
+// dism_aux.hip -- small kernels around the hard-core sweeps:
+//   sign binarizer (labels), log2 weight table and its tau derivative, strip summaries,
+//   summary composition (chunk pass), composed boundaries, deterministic tau reduction.
+// All are HBM- or latency-bound elementwise/scan kernels; none of them is on the MFMA path.
+#include "dism_device.h"
+#include "dism_launch.h"
+
+namespace dism {
+
+// ---- labels: x [B,N,H,d] -> labels [B,H,N], bit k set iff x[...,k] > 0 (NaN, +-0 -> 0).
+// Thread per (b,h,n) with n fastest so the int32 label stores are coalesced.
+template <typename T>
+__global__ __launch_bounds__(256) void sign_labels_kernel(const T* __restrict__ x, long B,
+                                                          long N, long H, int d,
+                                                          int32_t* __restrict__ out) {
+    long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    long total = B * H * N;
+    if (t >= total) return;
+    long n = t % N, bh = t / N, h = bh % H, b = bh / H;
+    const T* row = x + ((b * N + n) * H + h) * d;
+    int32_t lab = 0;
+    for (int k = 0; k < d; ++k) {
+        float v;
+        if constexpr (sizeof(T) == 2) {
+            v = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(row)[k] << 16);
+        } else {
+            v = reinterpret_cast<const float*>(row)[k];
+        }
+        if (v > 0.0f) lab |= (1 << k);
+    }
+    out[t] = lab;
+}
+
+// ---- weight tables: thread per (length, head)
+__global__ __launch_bounds__(256) void log_weights_kernel(const float* __restrict__ tau,
+                                                          long stride, float* __restrict__ out) {
+    long l = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (l >= stride) return;
+    out[(long)blockIdx.y * stride + l] = log_weight(tau[blockIdx.y], l);
+}
+
+__global__ __launch_bounds__(256) void dlog_weights_kernel(const float* __restrict__ tau,
+                                                           long stride, float* __restrict__ out) {
+    long l = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (l >= stride) return;
+    out[(long)blockIdx.y * stride + l] = dlog_weight(tau[blockIdx.y], l);
+}
+
+// ---- strip summaries / composed boundaries.
+// Entry (c, j) of a (b,h) row refers to the last row r = cS+S-1 of strip c.  One thread
+// owns one signed diagonal d = r - j of one (b,h) and walks its strips in order, carrying
+// the diagonal's running match length from strip to strip (the max-composition of the
+// reference's chunk pass collapses to "add the previous strip's length when the whole strip
+// segment matched").  Threads with d < 0 own only non-causal cells, which are -1.
+//   composed = 1: j - L[r, j]               (hard_chunk_scan output)
+//   composed = 0: last mismatching key coordinate inside the strip, -1 if none
+//                 (summarize_hard output)
+// fill_all = 0 skips the non-causal / soft-row -1 stores (the readout never reads them).
+__global__ __launch_bounds__(256) void boundary_kernel(const int32_t* __restrict__ iq,
+                                                       const int32_t* __restrict__ ik,
+                                                       const uint8_t* __restrict__ hard,
+                                                       int n, int strip, int composed,
+                                                       int fill_all, int32_t* __restrict__ out) {
+    int bh = blockIdx.y;
+    int d = (int)((long)blockIdx.x * blockDim.x + threadIdx.x) - (n - 1);
+    if (d > n - 1) return;
+    long C = (n - 1) / strip;
+    int32_t* o = out + (long)bh * C * n;
+    const int32_t* q = iq + (long)bh * n;
+    const int32_t* k = ik + (long)bh * n;
+    bool on = hard[bh] != 0 && d >= 0;
+    int carried = 0;
+    for (long c = 0; c < C; ++c) {
+        int r = (int)(c * strip + strip - 1);
+        int j = r - d;
+        if (j < 0 || j >= n) continue;
+        if (!on) {
+            if (fill_all) o[c * n + j] = -1;
+            continue;
+        }
+        int cnt = 0;
+        while (cnt < strip && j - cnt >= 0 && q[r - cnt] == k[j - cnt]) ++cnt;
+        int value;
+        if (composed) {
+            int L = cnt == strip ? strip + carried : cnt;
+            carried = L;
+            value = j - L;
+        } else {
+            int seg = strip < j + 1 ? strip : j + 1;
+            value = cnt == seg ? -1 : j - cnt;
+        }
+        o[c * n + j] = value;
+    }
+}
+
+// ---- chunk pass over arbitrary strip-32 summaries (compose_cpu semantics):
+//   out[c, j] = max(s[c, j], out[c-1, j-32]) for j >= 32, s[c, j] otherwise, then -1 for
+//   non-causal j >= 32c+32.  Cells (c, j) -> (c+1, j+32) form independent chains; one thread
+//   per chain.  Each chain reads an element before writing the same element, so in-place
+//   use is safe.
+__global__ __launch_bounds__(256) void chunk_kernel(const int32_t* __restrict__ summary,
+                                                    int32_t* __restrict__ out, long C, int n) {
+    long bh = blockIdx.y;
+    long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    long chains = n + (C > 1 ? (C - 1) * 32 : 0);
+    if (t >= chains) return;
+    long c0, j0;
+    if (t < n) { c0 = 0; j0 = t; } else { c0 = 1 + (t - n) / 32; j0 = (t - n) % 32; }
+    const int32_t* s = summary + bh * C * n;
+    int32_t* o = out + bh * C * n;
+    int32_t prev = -1;
+    for (long c = c0, j = j0; c < C && j < n; ++c, j += 32) {
+        int32_t v = s[c * n + j];
+        if (c > c0 && prev > v) v = prev;
+        if (j >= c * 32 + 32) v = -1;
+        o[c * n + j] = v;
+        prev = v;
+    }
+}
+
+// ---- tau reduction: dtau[h] = sum over (b, i) of rowtau[b,h,i], in the fixed order
+// "blocks of TAU_BLOCK consecutive (b, i) rows summed sequentially in double, then block
+// sums added sequentially in double", one workgroup per head.
+constexpr int TAU_BLOCK = 256;
+__global__ __launch_bounds__(256) void tau_reduce_kernel(const float* __restrict__ rowtau,
+                                                         int B, int H, long n,
+                                                         float* __restrict__ dtau) {
+    __shared__ double part[256];
+    int h = blockIdx.x;
+    long total = (long)B * n;
+    long blocks = (total + TAU_BLOCK - 1) / TAU_BLOCK;
+    double outer = 0.0;
+    for (long base = 0; base < blocks; base += 256) {
+        long blk = base + threadIdx.x;
+        double inner = 0.0;
+        if (blk < blocks) {
+            for (long x = blk * TAU_BLOCK; x < blk * TAU_BLOCK + TAU_BLOCK && x < total; ++x) {
+                long b = x / n, i = x % n;
+                inner += (double)rowtau[((long)b * H + h) * n + i];
+            }
+        }
+        part[threadIdx.x] = inner;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            long cnt = blocks - base < 256 ? blocks - base : 256;
+            for (long u = 0; u < cnt; ++u) outer += part[u];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) dtau[h] = (float)outer;
+}
+
+// ---------------------------------------------------------------------------------------
+hipError_t launch_sign_labels(const void* x, int dtype, long B, long N, long H, int d,
+                              int32_t* out, hipStream_t s) {
+    long total = B * H * N;
+    dim3 grid((unsigned)((total + 255) / 256));
+    if (dtype == DTYPE_BF16)
+        hipLaunchKernelGGL(sign_labels_kernel<bf16_t>, grid, dim3(256), 0, s,
+                           (const bf16_t*)x, B, N, H, d, out);
+    else
+        hipLaunchKernelGGL(sign_labels_kernel<float>, grid, dim3(256), 0, s, (const float*)x,
+                           B, N, H, d, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_log_weights(const float* tau, int H, long stride, float* out, hipStream_t s) {
+    dim3 grid((unsigned)((stride + 255) / 256), (unsigned)H);
+    hipLaunchKernelGGL(log_weights_kernel, grid, dim3(256), 0, s, tau, stride, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_dlog_weights(const float* tau, int H, long stride, float* out, hipStream_t s) {
+    dim3 grid((unsigned)((stride + 255) / 256), (unsigned)H);
+    hipLaunchKernelGGL(dlog_weights_kernel, grid, dim3(256), 0, s, tau, stride, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_boundary(const int32_t* iq, const int32_t* ik, const uint8_t* hard, long BH,
+                           int n, int strip, int composed, int fill_all, int32_t* out,
+                           hipStream_t s) {
+    dim3 grid((unsigned)((2L * n - 1 + 255) / 256), (unsigned)BH);
+    hipLaunchKernelGGL(boundary_kernel, grid, dim3(256), 0, s, iq, ik, hard, n, strip,
+                       composed, fill_all, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_chunk(const int32_t* summary, int32_t* out, long BH, long C, int n,
+                        hipStream_t s) {
+    long chains = n + (C > 1 ? (C - 1) * 32 : 0);
+    dim3 grid((unsigned)((chains + 255) / 256), (unsigned)BH);
+    hipLaunchKernelGGL(chunk_kernel, grid, dim3(256), 0, s, summary, out, C, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_tau_reduce(const float* rowtau, int B, int H, long n, float* dtau,
+                             hipStream_t s) {
+    hipLaunchKernelGGL(tau_reduce_kernel, dim3((unsigned)H), dim3(256), 0, s, rowtau, B, H, n,
+                       dtau);
+    return hipGetLastError();
+}
+
+}  // namespace dism

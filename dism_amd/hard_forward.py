@@ -1,0 +1,149 @@
+"""Hard-only forward on the MI355X library.
+
+Mirrors dism_v3/python/flash_dism/hard_forward.py:9-47 (hard_log_weights, hard_readout,
+forward_hard): same names, argument meaning, defaults and RuntimeError texts.
+
+Differences by design (the reference's chain is summary -> chunk -> LUT -> readout with an
+O(B*H*N^2/32) int32 boundary in between):
+  * forward_hard computes the LUT and runs the readout directly; match lengths are
+    recomputed from the labels inside the readout, optionally helped by a composed boundary
+    of strip height ``carry_strip`` (default 256: B*H*N^2/256 int32, an 8x smaller buffer
+    that bounds the per-match walk on long repeats).  With save_state=True the reference's
+    strip-32 summary/boundary are produced too, so callers that inspect them still work;
+  * fp32 vectors are accepted besides bf16 (all vectors share one dtype);
+  * ``return_matches=True`` additionally returns, per query, the longest match length and
+    its key index (ties -> most recent key, -1 if none).
+"""
+import os
+
+import torch
+
+from . import _lib
+from ._checks import (DTYPE_CODE, check_ctas, check_graph_choice, check_hard, check_labels,
+                      check_layout, check_tensor, check_vectors, require)
+from .summary import hard_boundary, hard_chunk_scan, summarize_hard
+
+DEFAULT_CARRY_STRIP = int(os.environ.get("DISM_HARD_CARRY_STRIP", "256"))
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+@torch.no_grad()
+def hard_log_weights(tau, max_length, *, _graph_choice=None):
+    """Fresh FP32 log2 geometric-sum table [H, max_length+1]; entry 0 is -1e6."""
+    require(isinstance(tau, torch.Tensor) and tau.is_cuda and tau.dtype == torch.float32 and
+            tau.dim() == 1 and tau.is_contiguous() and 0 < tau.numel() <= 65535,
+            "tau must be contiguous CUDA FP32 [H]")
+    require(isinstance(max_length, int) and max_length > 0 and max_length % 256 == 0,
+            "LUT maximum length must be positive and 256-aligned")
+    check_graph_choice(_graph_choice)
+    out = torch.empty((tau.numel(), max_length + 1), dtype=torch.float32, device=tau.device)
+    with torch.cuda.device(tau.device):
+        _lib.call("dism_hard_log_weights", tau.data_ptr(), tau.numel(), max_length,
+                  out.data_ptr(), _stream(tau))
+    return out
+
+
+@torch.no_grad()
+def hard_dlog_weights(tau, stride):
+    """FP32 [H, stride] natural-tau derivative of ln W_L (entry 0 is 0)."""
+    require(isinstance(tau, torch.Tensor) and tau.is_cuda and tau.dtype == torch.float32 and
+            tau.dim() == 1 and tau.is_contiguous() and 0 < tau.numel() <= 65535,
+            "tau must be contiguous CUDA FP32 [H]")
+    out = torch.empty((tau.numel(), stride), dtype=torch.float32, device=tau.device)
+    with torch.cuda.device(tau.device):
+        _lib.call("dism_hard_dlog_weights", tau.data_ptr(), tau.numel(), stride,
+                  out.data_ptr(), _stream(tau))
+    return out
+
+
+def _readout(sq, sk, v, idx_q, idx_k, hard, boundary, strip, log_weights, out_dtype,
+             matches):
+    b, n, h, r, dv, dt = check_vectors(sq, sk, v)
+    check_labels(idx_q, idx_k, b, h, n, sq.device)
+    check_hard(hard, b, h, sq.device)
+    require(isinstance(log_weights, torch.Tensor) and log_weights.device == sq.device and
+            log_weights.dtype == torch.float32 and log_weights.dim() == 2 and
+            log_weights.shape[0] == h and log_weights.is_contiguous(),
+            "invalid hard log-weight table")
+    require(log_weights.shape[1] > n, "hard log-weight table is too short")
+    if boundary is not None:
+        check_tensor(boundary, torch.int32, (b, h, (n - 1) // strip, n), "hard boundary",
+                     sq.device)
+    out = torch.empty((b, n, h, dv), dtype=out_dtype, device=sq.device)
+    lse2 = torch.empty((b, h, n), dtype=torch.float32, device=sq.device)
+    lmax = jarg = None
+    if matches:
+        lmax = torch.empty((b, h, n), dtype=torch.int32, device=sq.device)
+        jarg = torch.empty((b, h, n), dtype=torch.int32, device=sq.device)
+    ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
+    with torch.cuda.device(sq.device):
+        _lib.call("dism_hard_readout", sq.data_ptr(), sk.data_ptr(), v.data_ptr(),
+                  DTYPE_CODE[dt], idx_q.data_ptr(), idx_k.data_ptr(), hard.data_ptr(),
+                  ptr(boundary), strip if boundary is not None else 0, log_weights.data_ptr(),
+                  log_weights.shape[1], b, n, h, r, dv, out.data_ptr(),
+                  DTYPE_CODE[out_dtype], lse2.data_ptr(), ptr(lmax), ptr(jarg), _stream(sq))
+    return out, lse2, lmax, jarg
+
+
+@torch.no_grad()
+def hard_readout(sq, sk, v, idx_q, idx_k, hard, boundary, log_weights, *, layout=None, ctas=0,
+                 _graph_choice=None):
+    """Fused hard matching/normalization/readout with integer incoming boundaries.
+
+    SQ/SK/V: contiguous BF16 (or FP32) BNHD; labels: int32 BHN; hard: sequence bool [B,H];
+    boundary: the strip-32 composed boundary [B,H,(N-1)//32,N] of these labels (or None:
+    lengths are then recomputed from the labels alone).  Returns output BNHD in the vectors'
+    dtype and the FP32 log2 normalizer BHN.  Soft sequences give zero output/statistics.
+    """
+    check_ctas(ctas)
+    check_layout(layout)
+    check_graph_choice(_graph_choice)
+    out, lse2, _, _ = _readout(sq, sk, v, idx_q, idx_k, hard, boundary, 32, log_weights,
+                               sq.dtype, False)
+    return out, lse2
+
+
+def _forward_core(sq, sk, v, idx_q, idx_k, hard, tau, carry_strip, out_dtype, matches):
+    """LUT + (optional carry boundary) + readout; returns (out, lse2, lut, carry, strip,
+    lmax, jarg)."""
+    b, n, h, _, _, dt = check_vectors(sq, sk, v)
+    check_labels(idx_q, idx_k, b, h, n, sq.device)
+    check_hard(hard, b, h, sq.device)
+    require(isinstance(tau, torch.Tensor) and tau.is_cuda and tau.dtype == torch.float32 and
+            tau.shape == (h,) and tau.is_contiguous(), "tau must be contiguous CUDA FP32 [H]")
+    strip = DEFAULT_CARRY_STRIP if carry_strip is None else int(carry_strip)
+    lut = hard_log_weights(tau, n)
+    carry = None
+    if strip > 0 and (n - 1) // strip > 0:
+        carry = hard_boundary(idx_q, idx_k, hard, strip=strip, fill_all=False)
+    out, lse2, lmax, jarg = _readout(sq, sk, v, idx_q, idx_k, hard, carry, strip, lut,
+                                     out_dtype or dt, matches)
+    return out, lse2, lut, carry, strip, lmax, jarg
+
+
+@torch.no_grad()
+def forward_hard(sq, sk, v, idx_q, idx_k, hard, tau, *, layout=None, ctas=0, save_state=False,
+                 _graph_choice=None, carry_strip=None, return_matches=False, out_dtype=None):
+    """Complete standalone hard contribution: LUT and fused readout.
+
+    Returns (O, lse2) or, with save_state, (O, lse2, dict(summary, boundary, log_weights,
+    tau, strip, carry, carry_strip)); with return_matches a further dict(length, index).
+    O has the vectors' dtype unless out_dtype is given.
+    """
+    check_ctas(ctas)
+    check_layout(layout)
+    check_graph_choice(_graph_choice)
+    out, lse2, lut, carry, strip, lmax, jarg = _forward_core(
+        sq, sk, v, idx_q, idx_k, hard, tau, carry_strip, out_dtype, return_matches)
+    result = [out, lse2]
+    if save_state:
+        summary = summarize_hard(idx_q, idx_k, hard)
+        boundary = hard_chunk_scan(summary)
+        result.append(dict(summary=summary, boundary=boundary, log_weights=lut, tau=tau,
+                           strip=32, carry=carry, carry_strip=strip))
+    if return_matches:
+        result.append(dict(length=lmax, index=jarg))
+    return tuple(result)

@@ -1,0 +1,123 @@
+/*
+ * dism_hard.h -- C ABI of the MI355X flash_dism hard (integer-label) core.
+ *
+ * Library: dism_amd/libdism_hip.so (gfx950).  Every entry point takes raw device pointers,
+ * sizes and a HIP stream (passed as void*, a hipStream_t; NULL = default stream), enqueues
+ * its kernels on that stream and returns without synchronising.  The caller allocates all
+ * outputs; the library owns no device memory and keeps no mutable global state, so calls
+ * on different streams or threads are independent.  Return value: 0 on success, otherwise
+ * a DISM_ERR_* code with a thread-local message from dism_last_error().
+ *
+ * Layouts follow the reference: vectors BNHD ([B,N,H,R] / [B,N,H,DV], contiguous), labels
+ * BHN int32, sequence hard flags [B,H] bool (uint8).  Vector dtype code: 0 = bf16, 1 = f32.
+ * Supported readout dims R in {2,4,8,16,32}, DV in {32,64,128}.
+ *
+ * Each function names the reference interface it replaces (paths under cicuvc/dism).
+ */
+#ifndef DISM_HARD_H
+#define DISM_HARD_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    DISM_OK = 0,
+    DISM_ERR_INVALID = 1,     /* bad shape / size / pointer: reference raises RuntimeError */
+    DISM_ERR_UNSUPPORTED = 2, /* (R, DV, dtype) combination not compiled */
+    DISM_ERR_HIP = 3          /* HIP launch error */
+};
+enum { DISM_BF16 = 0, DISM_F32 = 1 };
+
+/* Thread-local message of the last failing call on this thread ("" if none). */
+const char* dism_last_error(void);
+/* ABI version of this library. */
+int32_t dism_abi_version(void);
+
+/* Sign binarizer, the label producer of this build: labels[b,h,n] = sum_k [x[b,n,h,k] > 0] 2^k
+ * for k < d (d <= 30).  Replaces the vocabulary argmax label producer
+ * dism_v3/python/flash_dism/emb_kernel.py:83-108 for hypercube codebooks (first-index tie
+ * rule: x == 0 gives bit 0). */
+int32_t dism_sign_labels(const void* x, int32_t dtype, int64_t B, int64_t N, int64_t H,
+                         int32_t d, int32_t* labels, void* stream);
+
+/* log2 geometric weight table lut[h, l] = log2 sum_{s=1..l} e^{s tau_h}, lut[h,0] = -1e6,
+ * l in [0, max_length].  Replaces cu.hard_log_weights (dism_v3/src/host/hard_forward.cpp:11-23,
+ * kernel dism_v3/src/hard_forward.cu:10-25). */
+int32_t dism_hard_log_weights(const float* tau, int32_t H, int64_t max_length, float* lut,
+                              void* stream);
+
+/* Natural-tau derivative g[h, l] = d ln W_l / d tau_h, g[h,0] = 0, l < stride.
+ * Replaces hard_dlog_weights_kernel (dism_v3/src/hard_backward.cu:8-23). */
+int32_t dism_hard_dlog_weights(const float* tau, int32_t H, int64_t stride, float* dlut,
+                               void* stream);
+
+/* Strip-32 summaries int32 [B,H,(N-1)/32,N]: last mismatching key coordinate on the strip's
+ * diagonal segment ending at (32c+31, j), -1 if none / non-causal / soft.
+ * Replaces cu.hard_summary (dism_v3/src/host/hard_summary.cpp:11-72). */
+int32_t dism_hard_summary(const int32_t* iq, const int32_t* ik, const uint8_t* hard, int64_t B,
+                          int64_t H, int64_t N, int32_t* summary, void* stream);
+
+/* Composition out[c,j] = max(s[c,j], out[c-1,j-32]) with non-causal -1, summaries of shape
+ * [BH,(N-1)/32,N]; out may alias summary (in place).
+ * Replaces cu.hard_chunk (dism_v3/src/host/hard_chunk.cpp:10-69). */
+int32_t dism_hard_chunk(const int32_t* summary, int32_t* boundary, int64_t BH, int64_t N,
+                        void* stream);
+
+/* Composed boundaries in one pass for any strip height S: boundary[b,h,c,j] = j - L[cS+S-1, j]
+ * on causal hard cells; non-causal/soft cells are -1 when fill_all != 0 and left untouched
+ * otherwise.  S = 32 equals dism_hard_chunk(dism_hard_summary(.)) -- the fused replacement of
+ * summarize_hard + hard_chunk_scan (dism_v3/python/flash_dism/summary.py:5-29). */
+int32_t dism_hard_boundary(const int32_t* iq, const int32_t* ik, const uint8_t* hard, int64_t B,
+                           int64_t H, int64_t N, int32_t strip, int32_t fill_all,
+                           int32_t* boundary, void* stream);
+
+/* Hard readout: O [B,N,H,DV] (out_dtype bf16|f32) and lse2 [B,H,N] fp32; optional lmax/jarg
+ * [B,H,N] int32 = longest match length per query and its key (ties -> most recent key,
+ * -1 if none).  boundary may be NULL (lengths recomputed from labels alone) or a composed
+ * boundary of strip height `strip`.  lut_stride >= N+1.  Soft rows give zeros.
+ * Replaces cu.hard_readout (dism_v3/src/host/hard_forward.cpp:25-113). */
+int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t dtype,
+                          const int32_t* iq, const int32_t* ik, const uint8_t* hard,
+                          const int32_t* boundary, int32_t strip, const float* lut,
+                          int64_t lut_stride, int64_t B, int64_t N, int64_t H, int32_t R,
+                          int32_t DV, void* out, int32_t out_dtype, float* lse2, int32_t* lmax,
+                          int32_t* jarg, void* stream);
+
+/* Hard backward: dsq, dsk [B,N,H,R], dv [B,N,H,DV], rowtau [B,H,N] (scratch, caller-owned)
+ * and dtau [H], all fp32, deterministic (no atomics).  lse2 is the forward's log2
+ * normalizer; lut/dlut share lut_stride >= N+1.
+ * Replaces cu.hard_backward (dism_v3/src/host/hard_backward.cpp:13-140). */
+int32_t dism_hard_backward(const void* sq, const void* sk, const void* v, const void* dout,
+                           int32_t dtype, const int32_t* iq, const int32_t* ik,
+                           const uint8_t* hard, const int32_t* boundary, int32_t strip,
+                           const float* lut, const float* dlut, int64_t lut_stride,
+                           const float* lse2, int64_t B, int64_t N, int64_t H, int32_t R,
+                           int32_t DV, float* dsq, float* dsk, float* dv, float* rowtau,
+                           float* dtau, void* stream);
+
+/* The three stages of dism_hard_backward, callable separately (same arguments):
+ * query sweep -> dsq, rowtau; key sweep -> dsk, dv; fixed-order reduction rowtau -> dtau.
+ * Together they replace the single hard_backward_kernel + hard_tau_reduce_kernel launch pair
+ * of dism_v3/src/host/hard_backward.cpp:242-252. */
+int32_t dism_hard_backward_queries(const void* sq, const void* sk, const void* v,
+                                   const void* dout, int32_t dtype, const int32_t* iq,
+                                   const int32_t* ik, const uint8_t* hard,
+                                   const int32_t* boundary, int32_t strip, const float* lut,
+                                   const float* dlut, int64_t lut_stride, const float* lse2,
+                                   int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
+                                   float* dsq, float* rowtau, void* stream);
+int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, const void* dout,
+                                int32_t dtype, const int32_t* iq, const int32_t* ik,
+                                const uint8_t* hard, const int32_t* boundary, int32_t strip,
+                                const float* lut, int64_t lut_stride, const float* lse2,
+                                int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
+                                float* dsk, float* dv, void* stream);
+int32_t dism_hard_tau_reduce(const float* rowtau, int64_t B, int64_t H, int64_t N, float* dtau,
+                             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DISM_HARD_H */

@@ -1,0 +1,183 @@
+"""CPU oracle for the flash_dism hard core -- TEST INFRASTRUCTURE ONLY.
+
+Two independent layers:
+  * ``oracle.dense``: FP64 numpy restatement of the reference's dense torch oracle
+    (dism_v3/python/flash_dism/reference/dism_v3_ref.py), feasible for N <= ~2048;
+  * ``liboracle.so`` (built from ``dism_cpu_model.c``): the CPU model with the exact fp32
+    operation order of the HIP kernels, used for bit-exact checks and as the timed CPU
+    baseline (``cpu_baseline.kind = "port"``).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this package.
+The product path (dism_amd) must never import it.
+
+Parity pinning status of every function is asserted in tests/test_oracle.py.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+SOURCE = os.path.join(HERE, "dism_cpu_model.c")
+CFLAGS = ["-O3", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off", "-mfma", "-mavx2",
+          "-fno-fast-math", "-Wall"]
+
+_lib = None
+
+
+def build(force=False):
+    """Compile dism_cpu_model.c -> liboracle.so with gcc (recipe also in oracle/Makefile)."""
+    if force or not os.path.exists(LIB_PATH) or \
+            os.path.getmtime(LIB_PATH) < os.path.getmtime(SOURCE):
+        subprocess.check_call(["gcc", *CFLAGS, "-o", LIB_PATH, SOURCE, "-lm"])
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        i32, i64 = ctypes.c_int, ctypes.c_long
+        L.orc_exp2f.restype = ctypes.c_float
+        L.orc_exp2f.argtypes = [ctypes.c_float]
+        L.orc_log2f.restype = ctypes.c_float
+        L.orc_log2f.argtypes = [ctypes.c_float]
+        L.orc_logd.restype = ctypes.c_double
+        L.orc_logd.argtypes = [ctypes.c_double]
+        L.orc_expd.restype = ctypes.c_double
+        L.orc_expd.argtypes = [ctypes.c_double]
+        L.orc_log_weight.restype = ctypes.c_float
+        L.orc_log_weight.argtypes = [ctypes.c_float, i64]
+        L.orc_dlog_weight.restype = ctypes.c_float
+        L.orc_dlog_weight.argtypes = [ctypes.c_float, i64]
+        L.orc_lut.argtypes = [P, i32, i64, P]
+        L.orc_dlut.argtypes = [P, i32, i64, P]
+        L.orc_sign_labels.argtypes = [P, i64, i32, P]
+        L.orc_boundary.argtypes = [P, P, P, i32, i32, i64, i32, i32, P]
+        L.orc_chunk.argtypes = [P, i64, i64, i64, P]
+        L.orc_suffix_walk.restype = i64
+        L.orc_suffix_walk.argtypes = [P, P, i64, i64]
+        L.orc_forward.argtypes = [P, P, P, P, P, P, P, i64, i32, i64, i32, i32, i32, P, P, P,
+                                  P, i32]
+        L.orc_backward.argtypes = [P, P, P, P, P, P, P, P, P, i64, P, i32, i64, i32, i32, i32,
+                                   P, P, P, P, i32]
+        L.orc_tau_reduce.argtypes = [P, i32, i32, i64, i64, P]
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(x):
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+
+
+def _i32(x):
+    return np.ascontiguousarray(np.asarray(x, dtype=np.int32))
+
+
+def _flags(hard):
+    return np.ascontiguousarray(np.asarray(hard, dtype=np.uint8).reshape(-1))
+
+
+def bf16_round(x):
+    """Round float32 -> bfloat16 (round to nearest even), returned as float32 values."""
+    x = _f32(x)
+    b = x.view(np.uint32).astype(np.uint64)
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16) << 16
+    out = r.astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(x), x, out)
+
+
+def exp2f(x):
+    return lib().orc_exp2f(float(x))
+
+
+def log2f(x):
+    return lib().orc_log2f(float(x))
+
+
+def sign_labels(x):
+    """x [B,N,H,d] -> int32 labels [B,H,N], bit d set iff x[...,d] > 0."""
+    x = _f32(x)
+    B, N, H, d = x.shape
+    out = np.empty((B, N, H), dtype=np.int32)
+    lib().orc_sign_labels(_p(x), B * N * H, d, _p(out))
+    return np.ascontiguousarray(out.transpose(0, 2, 1))
+
+
+def log_weights(tau, max_length):
+    tau = _f32(tau)
+    out = np.empty((tau.shape[0], max_length + 1), dtype=np.float32)
+    lib().orc_lut(_p(tau), tau.shape[0], max_length + 1, _p(out))
+    return out
+
+
+def dlog_weights(tau, max_length):
+    tau = _f32(tau)
+    out = np.empty((tau.shape[0], max_length + 1), dtype=np.float32)
+    lib().orc_dlut(_p(tau), tau.shape[0], max_length + 1, _p(out))
+    return out
+
+
+def boundary(iq, ik, hard, strip=32, composed=True):
+    """Strip summaries (composed=False) or composed boundaries, int32 [B,H,(N-1)//S,N]."""
+    iq, ik = _i32(iq), _i32(ik)
+    B, H, N = iq.shape
+    out = np.empty((B, H, (N - 1) // strip, N), dtype=np.int32)
+    lib().orc_boundary(_p(iq), _p(ik), _p(_flags(hard)), B, H, N, strip, int(composed), _p(out))
+    return out
+
+
+def chunk(summary):
+    s = _i32(summary)
+    B, H, C, N = s.shape
+    out = np.empty_like(s)
+    lib().orc_chunk(_p(s), B * H, C, N, _p(out))
+    return out
+
+
+def suffix_walk(q, k, i, j):
+    q, k = _i32(q), _i32(k)
+    return lib().orc_suffix_walk(_p(q), _p(k), i, j)
+
+
+def forward(sq, sk, v, iq, ik, hard, lut, threads=0):
+    """CPU model forward.  Returns (O fp32 [B,N,H,DV], lse2 [B,H,N], Lmax, argmax)."""
+    sq, sk, v, lut = _f32(sq), _f32(sk), _f32(v), _f32(lut)
+    iq, ik = _i32(iq), _i32(ik)
+    B, N, H, R = sq.shape
+    DV = v.shape[-1]
+    out = np.empty((B, N, H, DV), dtype=np.float32)
+    lse2 = np.empty((B, H, N), dtype=np.float32)
+    lmax = np.empty((B, H, N), dtype=np.int32)
+    jarg = np.empty((B, H, N), dtype=np.int32)
+    lib().orc_forward(_p(sq), _p(sk), _p(v), _p(iq), _p(ik), _p(_flags(hard)), _p(lut),
+                      lut.shape[1], B, N, H, R, DV, _p(out), _p(lse2), _p(lmax), _p(jarg),
+                      threads)
+    return out, lse2, lmax, jarg
+
+
+def backward(sq, sk, v, dout, iq, ik, hard, lut, dlut, lse2, threads=0, block=256):
+    """CPU model backward.  Returns (dSQ, dSK, dV fp32, dtau [H], rowtau [B,H,N])."""
+    sq, sk, v, dout, lut, dlut, lse2 = map(_f32, (sq, sk, v, dout, lut, dlut, lse2))
+    iq, ik = _i32(iq), _i32(ik)
+    B, N, H, R = sq.shape
+    DV = v.shape[-1]
+    dsq = np.empty_like(sq)
+    dsk = np.empty_like(sk)
+    dv = np.empty_like(v)
+    rowtau = np.empty((B, H, N), dtype=np.float32)
+    lib().orc_backward(_p(sq), _p(sk), _p(v), _p(dout), _p(iq), _p(ik), _p(_flags(hard)),
+                       _p(lut), _p(dlut), lut.shape[1], _p(lse2), B, N, H, R, DV, _p(dsq),
+                       _p(dsk), _p(dv), _p(rowtau), threads)
+    dtau = np.empty(H, dtype=np.float32)
+    lib().orc_tau_reduce(_p(rowtau), B, H, N, block, _p(dtau))
+    return dsq, dsk, dv, dtau, rowtau

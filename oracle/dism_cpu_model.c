@@ -1,0 +1,436 @@
+/*
+ * dism_cpu_model.c -- CPU restatement of the flash_dism hard (integer-label) core.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity checker and the timed CPU
+ * baseline.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * may load it.  The product path (dism_amd/) never calls into it.
+ *
+ * What it restates (reference paths relative to /root/reference):
+ *   - match length recurrence L[i,j] = (iq[i]==ik[j]) ? L[i-1,j-1]+1 : 0, computed here
+ *     with the textbook two-row dynamic programme (dism_v3/tests/test_hard_chunk.py:24-36,
+ *     dense_boundary), NOT with the GPU's walk-back + boundary method;
+ *   - strip summaries R (dism_v3/tests/test_hard_summary.py:37-49) and their max
+ *     composition (dism_v3/tests/test_hard_chunk.py:14-21, compose_cpu);
+ *   - log2 geometric-weight table (dism_v3/src/hard_forward.cu:10-25) and its natural-tau
+ *     derivative (dism_v3/src/hard_backward.cu:8-23);
+ *   - normalised signed readout with online max starting at 0 and unit fallback
+ *     (dism_v3/include/forward/readout.cuh:16-61, store_output :63-100);
+ *   - explicit backward dSQ/dSK/dV and the centred four-moment dtau
+ *     (dism_v3/python/flash_dism/reference/dism_v3_ref.py:108-127,
+ *      dism_v3/src/hard_backward.cu:71-120,156-197).
+ *
+ * Floating point: the fp32 operation sequence per query row / per key is the one the
+ * HIP kernels document (ascending key order per row, ascending query order per key,
+ * explicit fmaf, software exp2/log2 from the same published method), so outputs can be
+ * compared bit for bit.  Build with -ffp-contract=off.  The LUT/dLUT are evaluated in
+ * double with series/Horner schemes using only IEEE basic operations.
+ *
+ * Parity pinning of each function is listed in tests/test_oracle.py.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define LOG_ZERO (-1.0e6f)
+
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline double u2d(uint64_t u) { double d; memcpy(&d, &u, 8); return d; }
+static inline uint64_t d2u(double d) { uint64_t u; memcpy(&u, &d, 8); return u; }
+
+/* ---------------- fp32 exp2 / log2 (Cody-Waite reduction + polynomial) -------------
+ * exp2: x = n + f, n = rint(x), |f| <= 1/2, 2^f by a degree-6 least-squares minimax
+ * polynomial (coefficients fitted for this project, max rel err 1.3 ulp incl. rounding),
+ * scaled by 2^n through the exponent field. */
+static const float E2C[7] = {0x1.000000p+0f, 0x1.62e430p-1f, 0x1.ebfbdap-3f, 0x1.c6aed4p-5f,
+                             0x1.3b2dbap-7f, 0x1.5f456cp-10f, 0x1.41d3e2p-13f};
+
+float orc_exp2f(float x) {
+    if (x != x) return x;
+    if (!(x >= -149.0f)) return 0.0f;
+    if (x >= 128.0f) return INFINITY;
+    float n = rintf(x);
+    float f = x - n;
+    float p = E2C[6];
+    for (int k = 5; k >= 0; --k) p = fmaf(p, f, E2C[k]);
+    int ni = (int)n;
+    if (ni > 127) { p = p * 2.0f; ni -= 1; }
+    if (ni < -126) { p = p * 0x1p-64f; ni += 64; }
+    return p * u2f((uint32_t)(ni + 127) << 23);
+}
+
+/* log2 of a positive normal float: x = m 2^e, m in [sqrt(1/2), sqrt(2)), s=(m-1)/(m+1),
+ * log2 m = s * sum_k 2/((2k+1) ln 2) s^(2k), six terms. */
+static const float L2C[6] = {0x1.715476p+1f, 0x1.ec709ep-1f, 0x1.2776c6p-1f,
+                             0x1.a61762p-2f, 0x1.484b14p-2f, 0x1.0c9a84p-2f};
+
+float orc_log2f(float x) {
+    uint32_t b = f2u(x);
+    int e = (int)((b >> 23) & 255u) - 127;
+    float m = u2f((b & 0x7FFFFFu) | 0x3F800000u);
+    if (m > 0x1.6a09e6p+0f) { m = m * 0.5f; e += 1; }
+    float s = (m - 1.0f) / (m + 1.0f);
+    float t = s * s;
+    float p = L2C[5];
+    for (int k = 4; k >= 0; --k) p = fmaf(p, t, L2C[k]);
+    return (float)e + s * p;
+}
+
+/* ---------------- double helpers for the weight tables ---------------- */
+static const double LN2 = 0x1.62e42fefa39efp-1;
+static const double LN2_HI = 0x1.62e42fee00000p-1;
+static const double LN2_LO = 0x1.a39ef35793c76p-33;
+static const double INV_LN2 = 0x1.71547652b82fep+0;
+
+/* natural log, x > 0 normal: atanh series in s=(m-1)/(m+1), 14 terms */
+double orc_logd(double x) {
+    uint64_t b = d2u(x);
+    int e = (int)((b >> 52) & 0x7ffu) - 1023;
+    double m = u2d((b & 0xFFFFFFFFFFFFFull) | 0x3FF0000000000000ull);
+    if (m > 0x1.6a09e667f3bcdp+0) { m = m * 0.5; e += 1; }
+    double s = (m - 1.0) / (m + 1.0);
+    double t = s * s;
+    double p = 1.0 / 27.0;
+    for (int k = 12; k >= 0; --k) p = fma(p, t, 1.0 / (double)(2 * k + 1));
+    return fma((double)e, LN2, (2.0 * s) * p);
+}
+
+static const double INV_FACT[19] = {
+    1.0, 1.0, 1.0 / 2.0, 1.0 / 6.0, 1.0 / 24.0, 1.0 / 120.0, 1.0 / 720.0, 1.0 / 5040.0,
+    1.0 / 40320.0, 1.0 / 362880.0, 1.0 / 3628800.0, 1.0 / 39916800.0, 1.0 / 479001600.0,
+    1.0 / 6227020800.0, 1.0 / 87178291200.0, 1.0 / 1307674368000.0, 1.0 / 20922789888000.0,
+    1.0 / 355687428096000.0, 1.0 / 6402373705728000.0};
+
+/* e^x for x <= 709: n = rint(x/ln2), r = x - n ln2 (two-part), Taylor degree 16 */
+double orc_expd(double x) {
+    if (x < -745.0) return 0.0;
+    if (x > 709.0) return INFINITY;
+    double n = rint(x * INV_LN2);
+    double r = fma(-n, LN2_HI, x);
+    r = fma(-n, LN2_LO, r);
+    double p = INV_FACT[16];
+    for (int k = 15; k >= 0; --k) p = fma(p, r, INV_FACT[k]);
+    int ni = (int)n;
+    if (ni < -1022) { p = p * 0x1p-60; ni += 60; }
+    return p * u2d((uint64_t)(ni + 1023) << 52);
+}
+
+/* (1 - e^-x)/x for x >= 0 (equals 1 at 0) */
+double orc_one_minus_exp_neg_over(double x) {
+    if (x < 1.0) {
+        double p = INV_FACT[18];
+        for (int k = 17; k >= 1; --k) p = fma(p, -x, INV_FACT[k]);
+        return p;
+    }
+    return (1.0 - orc_expd(-x)) / x;
+}
+
+/* e^x - 1 for x >= 0 */
+double orc_expm1d(double x) {
+    if (x < 1.0) {
+        double p = INV_FACT[18];
+        for (int k = 17; k >= 1; --k) p = fma(p, x, INV_FACT[k]);
+        return x * p;
+    }
+    return orc_expd(x) - 1.0;
+}
+
+/* log2 W_L, W_L = sum_{s=1..L} e^{s tau}; W_0 -> LOG_ZERO.
+ * log W = (tau>0 ? L tau : tau) + ln L + ln q(L|tau|) - ln q(|tau|), q(x)=(1-e^-x)/x.
+ * Reference branches: dism_v3/src/hard_forward.cu:15-22. */
+float orc_log_weight(float tau, long L) {
+    if (L <= 0) return LOG_ZERO;
+    double t = (double)tau, a = fabs(t), l = (double)L;
+    double lead = t > 0.0 ? l * t : t;
+    double r = lead + orc_logd(l);
+    r = r + orc_logd(orc_one_minus_exp_neg_over(l * a));
+    r = r - orc_logd(orc_one_minus_exp_neg_over(a));
+    return (float)(r * INV_LN2);
+}
+
+/* g_L = d ln W_L / d tau (natural units).  Series for |L tau| < 0.1 from
+ * g = (L+1)/2 + (L coth(L tau/2) - coth(tau/2))/2, closed form elsewhere.
+ * Reference: dism_v3/src/hard_backward.cu:8-23. */
+float orc_dlog_weight(float tau, long L) {
+    if (L <= 0) return 0.0f;
+    double t = (double)tau, l = (double)L, x = l * t;
+    if (fabs(x) < 0.1) {
+        static const double C[6] = {1.0 / 12.0, -1.0 / 720.0, 1.0 / 30240.0, -1.0 / 1209600.0,
+                                    1.0 / 47900160.0, -691.0 / 1307674368000.0};
+        double l2 = l * l, t2 = t * t;
+        double lp = l2, acc;
+        double terms[6];
+        for (int n = 0; n < 6; ++n) { terms[n] = C[n] * (lp - 1.0); lp = lp * l2; }
+        acc = terms[5];
+        for (int n = 4; n >= 0; --n) acc = fma(acc, t2, terms[n]);
+        return (float)(fma(t, acc, (l + 1.0) * 0.5));
+    }
+    double a = fabs(t);
+    double big = l / orc_expm1d(l * a);
+    double small = 1.0 / orc_expm1d(a);
+    double g = t > 0.0 ? (l + big) - small : (1.0 - big) + small;
+    return (float)g;
+}
+
+void orc_lut(const float* tau, int heads, long stride, float* out) {
+    for (int h = 0; h < heads; ++h)
+        for (long l = 0; l < stride; ++l) out[(long)h * stride + l] = orc_log_weight(tau[h], l);
+}
+
+void orc_dlut(const float* tau, int heads, long stride, float* out) {
+    for (int h = 0; h < heads; ++h)
+        for (long l = 0; l < stride; ++l) out[(long)h * stride + l] = orc_dlog_weight(tau[h], l);
+}
+
+/* ---------------- integer core ---------------- */
+
+/* Sign binarizer: label = sum_d [x_d > 0] 2^d (x [rows, d], labels [rows]) */
+void orc_sign_labels(const float* x, long rows, int d, int32_t* out) {
+    for (long r = 0; r < rows; ++r) {
+        int32_t lab = 0;
+        for (int k = 0; k < d; ++k)
+            if (x[r * d + k] > 0.0f) lab |= (1 << k);
+        out[r] = lab;
+    }
+}
+
+/* Strip summaries (composed=0) or composed boundaries (composed=1), strip height S.
+ * out [B,H,(N-1)/S,N]; entry (c,j): row r=cS+S-1; causal j<=r on hard rows; else -1.
+ * composed: j - L[r,j] with L the full-history match length (dense_boundary).
+ * summary : last mismatching key coordinate inside strip c, -1 if none (oracle :37-49). */
+void orc_boundary(const int32_t* iq, const int32_t* ik, const uint8_t* hard, int B, int H,
+                  long N, int S, int composed, int32_t* out) {
+    long C = (N - 1) / S;
+    int32_t* len = (int32_t*)malloc(sizeof(int32_t) * (size_t)N);
+    int32_t* prv = (int32_t*)malloc(sizeof(int32_t) * (size_t)N);
+    for (int bh = 0; bh < B * H; ++bh) {
+        const int32_t* q = iq + (long)bh * N;
+        const int32_t* k = ik + (long)bh * N;
+        int32_t* o = out + (long)bh * C * N;
+        for (long x = 0; x < C * N; ++x) o[x] = -1;
+        if (!hard[bh]) continue;
+        if (composed) {
+            for (long j = 0; j < N; ++j) len[j] = 0;
+            for (long row = 0; row < C * S; ++row) {
+                for (long j = N - 1; j >= 0; --j) {
+                    int32_t in = j ? len[j - 1] : 0;
+                    len[j] = (q[row] == k[j]) ? in + 1 : 0;
+                }
+                if (row % S == S - 1) {
+                    long c = row / S;
+                    for (long j = 0; j <= row && j < N; ++j) o[c * N + j] = (int32_t)(j - len[j]);
+                }
+            }
+        } else {
+            for (long c = 0; c < C; ++c) {
+                for (long j = 0; j < N; ++j) prv[j] = -1;
+                for (long row = c * S; row < c * S + S; ++row) {
+                    for (long j = N - 1; j >= 0; --j) {
+                        int32_t in = j ? prv[j - 1] : -1;
+                        int32_t here = (q[row] == k[j]) ? -1 : (int32_t)j;
+                        prv[j] = in > here ? in : here;
+                    }
+                }
+                for (long j = 0; j <= c * S + S - 1 && j < N; ++j) o[c * N + j] = prv[j];
+            }
+        }
+    }
+    free(len);
+    free(prv);
+}
+
+/* compose_cpu (test_hard_chunk.py:14-21): summaries [BH,C,N], strip 32 */
+void orc_chunk(const int32_t* summary, long BH, long C, long N, int32_t* out) {
+    memcpy(out, summary, sizeof(int32_t) * (size_t)(BH * C * N));
+    for (long bh = 0; bh < BH; ++bh) {
+        int32_t* r = out + bh * C * N;
+        for (long c = 0; c < C; ++c) {
+            if (c)
+                for (long j = 32; j < N; ++j) {
+                    int32_t a = r[c * N + j], b = r[(c - 1) * N + j - 32];
+                    r[c * N + j] = a > b ? a : b;
+                }
+            for (long j = c * 32 + 32; j < N; ++j) r[c * N + j] = -1;
+        }
+    }
+}
+
+/* Brute-force match length at (i,j) by direct suffix walk (tiny-input pin). */
+long orc_suffix_walk(const int32_t* q, const int32_t* k, long i, long j) {
+    long c = 0;
+    while (i - c >= 0 && j - c >= 0 && q[i - c] == k[j - c]) ++c;
+    return c;
+}
+
+/* ---------------- forward ----------------
+ * Vectors fp32 BNHD (bf16 inputs widened exactly by the caller), labels BHN, hard [B*H].
+ * Per row i (ascending j over matches):
+ *   lut = LUT[L]; if lut > m: alpha=exp2(m-lut); den*=alpha; acc*=alpha; m=lut
+ *   p = exp2(lut-m); den += p; s = fma-chain(sq_i . sk_j); ps = p*s; acc = fma(ps, v_j, acc)
+ * out = acc/den, lse2 = m + log2(den); match argmax: longest L, ties -> largest j. */
+void orc_forward(const float* sq, const float* sk, const float* v, const int32_t* iq,
+                 const int32_t* ik, const uint8_t* hard, const float* lut, long lut_stride,
+                 int B, long N, int H, int R, int DV, float* out, float* lse2, int32_t* lmax,
+                 int32_t* jarg, int threads) {
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 1)
+#endif
+    for (int bh = 0; bh < B * H; ++bh) {
+        int b = bh / H, h = bh % H;
+        const int32_t* q = iq + (long)bh * N;
+        const int32_t* k = ik + (long)bh * N;
+        const float* tab = lut + (long)h * lut_stride;
+        int32_t* la = (int32_t*)calloc((size_t)N + 1, sizeof(int32_t));
+        int32_t* lb = (int32_t*)calloc((size_t)N + 1, sizeof(int32_t));
+        float* acc = (float*)malloc(sizeof(float) * (size_t)DV);
+        for (long i = 0; i < N; ++i) {
+            long row = ((long)b * N + i) * H + h;
+            float* o = out + row * DV;
+            if (!hard[bh]) {
+                for (int d = 0; d < DV; ++d) o[d] = 0.0f;
+                lse2[(long)bh * N + i] = 0.0f;
+                if (lmax) lmax[(long)bh * N + i] = 0;
+                if (jarg) jarg[(long)bh * N + i] = -1;
+                continue;
+            }
+            /* lb[j+1] = L[i,j]; la[j] = L[i-1,j-1] */
+            float m = 0.0f, den = 1.0f;
+            int32_t best = 0, bj = -1;
+            for (int d = 0; d < DV; ++d) acc[d] = 0.0f;
+            const float* sqi = sq + row * R;
+            for (long j = 0; j <= i; ++j) {
+                if (q[i] != k[j]) { lb[j + 1] = 0; continue; }
+                int32_t L = la[j] + 1;
+                lb[j + 1] = L;
+                if (L >= best) { best = L; bj = (int32_t)j; }
+                float lw = tab[L];
+                if (lw > m) {
+                    float alpha = orc_exp2f(m - lw);
+                    den = den * alpha;
+                    for (int d = 0; d < DV; ++d) acc[d] = acc[d] * alpha;
+                    m = lw;
+                }
+                float p = orc_exp2f(lw - m);
+                den = den + p;
+                long krow = ((long)b * N + j) * H + h;
+                const float* skj = sk + krow * R;
+                float s = 0.0f;
+                for (int r = 0; r < R; ++r) s = fmaf(sqi[r], skj[r], s);
+                float ps = p * s;
+                const float* vj = v + krow * DV;
+                for (int d = 0; d < DV; ++d) acc[d] = fmaf(ps, vj[d], acc[d]);
+            }
+            for (int d = 0; d < DV; ++d) o[d] = acc[d] / den;
+            lse2[(long)bh * N + i] = m + orc_log2f(den);
+            if (lmax) lmax[(long)bh * N + i] = best;
+            if (jarg) jarg[(long)bh * N + i] = bj;
+            int32_t* t = la; la = lb; lb = t;
+        }
+        free(la);
+        free(lb);
+        free(acc);
+    }
+}
+
+/* ---------------- backward ----------------
+ * Row-major traversal (i ascending, j ascending) gives every per-key accumulator its
+ * ascending-i order and every per-row accumulator its ascending-j order:
+ *   p = exp2(LUT[L]-lse2_i); s = sq_i.sk_j; e = dO_i.v_j (fma chains)
+ *   ps=p*s; pe=p*e; pse=ps*e; g = G[L]-G[i+1]
+ *   dsq_i += pe*sk_j; dsk_j += pe*sq_i; dv_j += ps*dO_i
+ *   u += pse; vv = fma(p,g,vv); w = fma(pse,g,w); z += p
+ *   rowtau_i = (w - u*((vv - f c)/(z+f)))/(z+f),  f = exp2(-lse2_i), c = G[i+1]
+ * dtau_h = sum over (b,i) of rowtau in the fixed blocked order of orc_tau_reduce. */
+void orc_backward(const float* sq, const float* sk, const float* v, const float* dout,
+                  const int32_t* iq, const int32_t* ik, const uint8_t* hard, const float* lut,
+                  const float* dlut, long lut_stride, const float* lse2in, int B, long N, int H,
+                  int R, int DV, float* dsq, float* dsk, float* dv, float* rowtau, int threads) {
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 1)
+#endif
+    for (int bh = 0; bh < B * H; ++bh) {
+        int b = bh / H, h = bh % H;
+        const int32_t* q = iq + (long)bh * N;
+        const int32_t* k = ik + (long)bh * N;
+        const float* tab = lut + (long)h * lut_stride;
+        const float* gt = dlut + (long)h * lut_stride;
+        int32_t* la = (int32_t*)calloc((size_t)N + 1, sizeof(int32_t));
+        int32_t* lb = (int32_t*)calloc((size_t)N + 1, sizeof(int32_t));
+        float* dq = (float*)malloc(sizeof(float) * (size_t)R);
+        for (long x = 0; x < N; ++x) {
+            long row = ((long)b * N + x) * H + h;
+            for (int r = 0; r < R; ++r) { dsq[row * R + r] = 0.0f; dsk[row * R + r] = 0.0f; }
+            for (int d = 0; d < DV; ++d) dv[row * DV + d] = 0.0f;
+            rowtau[(long)bh * N + x] = 0.0f;
+        }
+        if (hard[bh]) {
+            for (long i = 0; i < N; ++i) {
+                long row = ((long)b * N + i) * H + h;
+                const float* sqi = sq + row * R;
+                const float* doi = dout + row * DV;
+                float l2 = lse2in[(long)bh * N + i];
+                float c = gt[i + 1];
+                float u = 0.0f, vv = 0.0f, w = 0.0f, z = 0.0f;
+                for (int r = 0; r < R; ++r) dq[r] = 0.0f;
+                for (long j = 0; j <= i; ++j) {
+                    if (q[i] != k[j]) { lb[j + 1] = 0; continue; }
+                    int32_t L = la[j] + 1;
+                    lb[j + 1] = L;
+                    float p = orc_exp2f(tab[L] - l2);
+                    long krow = ((long)b * N + j) * H + h;
+                    const float* skj = sk + krow * R;
+                    const float* vj = v + krow * DV;
+                    float s = 0.0f;
+                    for (int r = 0; r < R; ++r) s = fmaf(sqi[r], skj[r], s);
+                    float e = 0.0f;
+                    for (int d = 0; d < DV; ++d) e = fmaf(doi[d], vj[d], e);
+                    float ps = p * s, pe = p * e, pse = ps * e;
+                    float g = gt[L] - c;
+                    for (int r = 0; r < R; ++r) dq[r] = fmaf(pe, skj[r], dq[r]);
+                    float* dkj = dsk + krow * R;
+                    for (int r = 0; r < R; ++r) dkj[r] = fmaf(pe, sqi[r], dkj[r]);
+                    float* dvj = dv + krow * DV;
+                    for (int d = 0; d < DV; ++d) dvj[d] = fmaf(ps, doi[d], dvj[d]);
+                    u = u + pse;
+                    vv = fmaf(p, g, vv);
+                    w = fmaf(pse, g, w);
+                    z = z + p;
+                }
+                    for (int r = 0; r < R; ++r) dsq[row * R + r] = dq[r];
+                float f = orc_exp2f(-l2);
+                float mass = z + f;
+                float mean = fmaf(-f, c, vv) / mass;
+                rowtau[(long)bh * N + i] = fmaf(-u, mean, w) / mass;
+                int32_t* t = la; la = lb; lb = t;
+            }
+        }
+        free(la);
+        free(lb);
+        free(dq);
+    }
+}
+
+/* dtau_h: for each head, the B*N row terms in (b, i) order are cut into blocks of
+ * `block` rows; each block is summed sequentially in double; block sums are then summed
+ * sequentially in double; the result is rounded to float. */
+void orc_tau_reduce(const float* rowtau, int B, int H, long N, long block, float* dtau) {
+    for (int h = 0; h < H; ++h) {
+        long total = (long)B * N;
+        double outer = 0.0;
+        for (long s = 0; s < total; s += block) {
+            double inner = 0.0;
+            for (long x = s; x < s + block && x < total; ++x) {
+                long b = x / N, i = x % N;
+                inner += (double)rowtau[((long)b * H + h) * N + i];
+            }
+            outer += inner;
+        }
+        dtau[h] = (float)outer;
+    }
+}
