@@ -62,7 +62,6 @@ def main():
     import torch
     import dism_amd
     from dism_amd import _lib
-    from dism_amd.hard_forward import _readout
     from dism_amd._checks import DTYPE_CODE
 
     dev = torch.device("cuda:0")
@@ -82,7 +81,14 @@ def main():
     dvv = torch.empty((B, T, H, DV), dtype=torch.float32, device=dev)
     rowtau = torch.empty((B, H, T), dtype=torch.float32, device=dev)
     dtau = torch.empty((H,), dtype=torch.float32, device=dev)
-    names = ["labels", "lut", "carry", "forward", "dlut", "bwd_queries", "bwd_keys", "tau_reduce"]
+    names = ["labels", "lut", "carry", "prepare", "forward", "dlut", "bwd_prepare",
+             "bwd_queries", "bwd_keys", "tau_reduce"]
+    out = torch.empty((B, T, H, DV), dtype=torch.bfloat16, device=dev)
+    lse2 = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+    code = DTYPE_CODE[torch.bfloat16]
+    nbytes = _lib.workspace_bytes(B, T, H, D, DV, code)
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+    W = ws.data_ptr()
 
     def step(events=None):
         def mark(i):
@@ -96,32 +102,41 @@ def main():
         mark(2)
         carry = dism_amd.hard_boundary(iq, ik, hard, strip=strip, fill_all=False) \
             if strip > 0 else None
-        mark(3)
-        out, lse2, _, _ = _readout(tq, tk, tv, iq, ik, hard, carry, strip, lut, torch.bfloat16,
-                                   False)
-        mark(4)
-        dlut = dism_amd.hard_dlog_weights(tau, n + 1)
-        mark(5)
         cp = 0 if carry is None else carry.data_ptr()
-        _lib.call("dism_hard_backward_queries", tq.data_ptr(), tk.data_ptr(), tv.data_ptr(),
-                  tdo.data_ptr(), DTYPE_CODE[torch.bfloat16], iq.data_ptr(), ik.data_ptr(),
-                  hard.data_ptr(), cp, strip, lut.data_ptr(), dlut.data_ptr(), n + 1,
-                  lse2.data_ptr(), B, T, H, D, DV, dsq.data_ptr(), rowtau.data_ptr(), S)
+        mark(3)
+        _lib.call("dism_hard_prepare", tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), code,
+                  iq.data_ptr(), ik.data_ptr(), B, T, H, D, DV, W, nbytes, S)
+        mark(4)
+        _lib.call("dism_hard_readout", tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), code,
+                  iq.data_ptr(), ik.data_ptr(), hard.data_ptr(), cp, strip, lut.data_ptr(),
+                  n + 1, B, T, H, D, DV, W, nbytes, out.data_ptr(), code, lse2.data_ptr(), 0, 0,
+                  S)
+        mark(5)
+        dlut = dism_amd.hard_dlog_weights(tau, n + 1)
         mark(6)
-        _lib.call("dism_hard_backward_keys", tq.data_ptr(), tk.data_ptr(), tv.data_ptr(),
-                  tdo.data_ptr(), DTYPE_CODE[torch.bfloat16], iq.data_ptr(), ik.data_ptr(),
-                  hard.data_ptr(), cp, strip, lut.data_ptr(), n + 1, lse2.data_ptr(), B, T, H,
-                  D, DV, dsk.data_ptr(), dvv.data_ptr(), S)
+        _lib.call("dism_hard_backward_prepare", tq.data_ptr(), tk.data_ptr(), tv.data_ptr(),
+                  tdo.data_ptr(), code, iq.data_ptr(), ik.data_ptr(), lse2.data_ptr(), B, T, H,
+                  D, DV, W, nbytes, S)
         mark(7)
-        _lib.call("dism_hard_tau_reduce", rowtau.data_ptr(), B, H, T, dtau.data_ptr(), S)
+        _lib.call("dism_hard_backward_queries", tq.data_ptr(), tk.data_ptr(), tv.data_ptr(),
+                  tdo.data_ptr(), code, iq.data_ptr(), ik.data_ptr(), hard.data_ptr(), cp, strip,
+                  lut.data_ptr(), dlut.data_ptr(), n + 1, lse2.data_ptr(), B, T, H, D, DV, W,
+                  nbytes, dsq.data_ptr(), rowtau.data_ptr(), S)
         mark(8)
+        _lib.call("dism_hard_backward_keys", tq.data_ptr(), tk.data_ptr(), tv.data_ptr(),
+                  tdo.data_ptr(), code, iq.data_ptr(), ik.data_ptr(), hard.data_ptr(), cp, strip,
+                  lut.data_ptr(), n + 1, lse2.data_ptr(), B, T, H, D, DV, W, nbytes,
+                  dsk.data_ptr(), dvv.data_ptr(), S)
+        mark(9)
+        _lib.call("dism_hard_tau_reduce", rowtau.data_ptr(), B, H, T, dtau.data_ptr(), S)
+        mark(10)
         return out
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    per = [[torch.cuda.Event(enable_timing=True) for _ in range(9)] for _ in range(args.steps)]
+    per = [[torch.cuda.Event(enable_timing=True) for _ in range(11)] for _ in range(args.steps)]
     t0 = time.perf_counter()
     start.record(stream)
     for s in range(args.steps):

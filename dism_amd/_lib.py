@@ -18,14 +18,17 @@ SIGNATURES = {
     "dism_hard_summary": [_P, _P, _P, _I64, _I64, _I64, _P, _P],
     "dism_hard_chunk": [_P, _P, _I64, _I64, _P],
     "dism_hard_boundary": [_P, _P, _P, _I64, _I64, _I64, _I32, _I32, _P, _P],
+    "dism_hard_prepare": [_P, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _I32, _I32, _P, _I64, _P],
     "dism_hard_readout": [_P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _I64, _I64, _I64, _I64,
-                          _I32, _I32, _P, _I32, _P, _P, _P, _P],
+                          _I32, _I32, _P, _I64, _P, _I32, _P, _P, _P, _P],
     "dism_hard_backward": [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _P, _I64, _P, _I64,
-                           _I64, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P],
+                           _I64, _I64, _I32, _I32, _P, _I64, _P, _P, _P, _P, _P, _P],
+    "dism_hard_backward_prepare": [_P, _P, _P, _P, _I32, _P, _P, _P, _I64, _I64, _I64, _I32,
+                                   _I32, _P, _I64, _P],
     "dism_hard_backward_queries": [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _P, _I64,
-                                   _P, _I64, _I64, _I64, _I32, _I32, _P, _P, _P],
+                                   _P, _I64, _I64, _I64, _I32, _I32, _P, _I64, _P, _P, _P],
     "dism_hard_backward_keys": [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _I64, _P, _I64,
-                                _I64, _I64, _I32, _I32, _P, _P, _P],
+                                _I64, _I64, _I32, _I32, _P, _I64, _P, _P, _P],
     "dism_hard_tau_reduce": [_P, _I64, _I64, _I64, _P, _P],
 }
 
@@ -53,6 +56,8 @@ def load():
         lib.dism_last_error.argtypes = []
         lib.dism_abi_version.restype = ctypes.c_int32
         lib.dism_abi_version.argtypes = []
+        lib.dism_hard_workspace_bytes.restype = ctypes.c_int64
+        lib.dism_hard_workspace_bytes.argtypes = [_I64, _I64, _I64, _I32, _I32, _I32]
         _lib = lib
     return _lib
 
@@ -64,3 +69,11 @@ def call(name, *args):
     if status != 0:
         msg = lib.dism_last_error().decode(errors="replace")
         raise RuntimeError(f"{name}: {msg}")
+
+
+def workspace_bytes(B, N, H, R, DV, dtype_code):
+    """Bytes of the caller-owned sweep workspace (raises for unsupported dimensions)."""
+    nbytes = load().dism_hard_workspace_bytes(B, N, H, R, DV, dtype_code)
+    if nbytes < 0:
+        raise RuntimeError(f"unsupported hard-core dimensions B={B} N={N} H={H} R={R} DV={DV}")
+    return nbytes

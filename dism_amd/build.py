@@ -18,7 +18,8 @@ LIB = os.path.join(HERE, "libdism_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("DISM_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["dism_aux.hip", "dism_forward.hip", "dism_backward.hip", "dism_capi.cpp"]
+SOURCES = ["dism_aux.hip", "dism_bucket.hip", "dism_forward.hip", "dism_backward.hip",
+           "dism_capi.cpp"]
 
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",

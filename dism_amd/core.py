@@ -21,9 +21,9 @@ class HardCore(torch.autograd.Function):
         ik = idx_k.to(torch.int32).contiguous()
         sq_c, sk_c, v_c = sq.contiguous(), sk.contiguous(), v.contiguous()
         hard_c, tau_c = hard.contiguous(), tau.detach().float().contiguous()
-        out, lse2, lut, carry, strip, _, _ = _forward_core(
+        out, lse2, lut, carry, strip, _, _, ws = _forward_core(
             sq_c, sk_c, v_c, iq, ik, hard_c, tau_c, None, None, False)
-        ctx.save_for_backward(sq_c, sk_c, v_c, iq, ik, hard_c, tau_c, lse2, lut,
+        ctx.save_for_backward(sq_c, sk_c, v_c, iq, ik, hard_c, tau_c, lse2, lut, ws,
                               *(() if carry is None else (carry,)))
         ctx.strip = strip
         ctx.has_carry = carry is not None
@@ -33,10 +33,10 @@ class HardCore(torch.autograd.Function):
     @torch.autograd.function.once_differentiable
     def backward(ctx, dout):
         saved = ctx.saved_tensors
-        sq, sk, v, iq, ik, hard, tau, lse2, lut = saved[:9]
-        carry = saved[9] if ctx.has_carry else None
+        sq, sk, v, iq, ik, hard, tau, lse2, lut, ws = saved[:10]
+        carry = saved[10] if ctx.has_carry else None
         dout = dout.to(sq.dtype).contiguous()
-        state = dict(log_weights=lut, tau=tau, carry=carry, carry_strip=ctx.strip)
+        state = dict(log_weights=lut, tau=tau, carry=carry, carry_strip=ctx.strip, workspace=ws)
         dsq, dsk, dv, dtau = backward_hard(sq, sk, v, dout, iq, ik, hard, lse2, state)
         return dsq, dsk, dv, None, None, None, dtau
 

@@ -193,6 +193,18 @@ hipError_t launch_chunk(const int32_t* summary, int32_t* out, long BH, long C, i
     return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* p, long count, int32_t value) {
+    long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < count) p[e] = value;
+}
+
+hipError_t launch_fill_i32(int32_t* p, long count, int32_t value, hipStream_t s) {
+    if (count <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, p,
+                       count, value);
+    return hipGetLastError();
+}
+
 hipError_t launch_tau_reduce(const float* rowtau, int B, int H, long n, float* dtau,
                              hipStream_t s) {
     hipLaunchKernelGGL(tau_reduce_kernel, dim3((unsigned)H), dim3(256), 0, s, rowtau, B, H, n,

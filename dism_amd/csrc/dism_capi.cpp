@@ -1,5 +1,6 @@
-// dism_capi.cpp -- extern "C" boundary of libdism_hip.so: argument validation, launch
-// dispatch, thread-local error text.  Declarations and reference mapping: include/dism_hard.h.
+// dism_capi.cpp -- extern "C" boundary of libdism_hip.so: argument validation, workspace
+// layout, launch dispatch, thread-local error text.  Declarations and reference mapping:
+// include/dism_hard.h.
 #include <hip/hip_runtime.h>
 #include <climits>
 #include <cstdarg>
@@ -35,28 +36,118 @@ int32_t hip_status(hipError_t e, const char* what) {
 }
 
 bool dims_ok(int64_t B, int64_t N, int64_t H) {
-    return B > 0 && H > 0 && N > 0 && N <= INT_MAX - 1024 && B * H <= INT_MAX &&
-           ((N + 255) / 256) * B * H <= INT_MAX;
+    return B > 0 && H > 0 && N > 0 && N <= INT_MAX / 64 && B * H <= 65535 &&
+           B * H * ((N + 63) / 64 + dism::BUCKETS) * 2 <= INT_MAX;
 }
 bool rdv_ok(int32_t R, int32_t DV) {
-    return (R == 2 || R == 4 || R == 8 || R == 16 || R == 32) && (DV == 32 || DV == 64 || DV == 128);
+    return (R == 2 || R == 4 || R == 8 || R == 16 || R == 32) &&
+           (DV == 32 || DV == 64 || DV == 128);
 }
+bool dtype_ok(int32_t d) { return d == DISM_BF16 || d == DISM_F32; }
 hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+int words_of(int32_t dtype, int64_t n) { return dtype == DISM_BF16 ? (int)((n + 1) / 2) : (int)n; }
+
+// Workspace layout (each section 256-byte aligned).
+struct Layout {
+    int64_t qpos, kpos, qoff, koff, qcs, kcs, bad, krec, qrec, total;
+    int stride;
+};
+
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV, int32_t dtype) {
+    Layout L;
+    const int64_t BH = B * H;
+    const int raw = 4 + words_of(dtype, R) + words_of(dtype, DV);
+    L.stride = (raw + 15) / 16 * 16;
+    int64_t o = 0;
+    auto take = [&](int64_t bytes) {
+        int64_t at = o;
+        o += align256(bytes);
+        return at;
+    };
+    L.qpos = take(BH * N * 4);
+    L.kpos = take(BH * N * 4);
+    L.qoff = take(BH * (dism::BUCKETS + 1) * 4);
+    L.koff = take(BH * (dism::BUCKETS + 1) * 4);
+    L.qcs = take(BH * (dism::BUCKETS + 1) * 4);
+    L.kcs = take(BH * (dism::BUCKETS + 1) * 4);
+    L.bad = take(BH * 4);
+    L.krec = take(BH * N * L.stride * 4);
+    L.qrec = take(BH * N * L.stride * 4);
+    L.total = o;
+    return L;
+}
+
+template <typename P>
+P* at(void* ws, int64_t off) {
+    return reinterpret_cast<P*>(reinterpret_cast<char*>(ws) + off);
+}
+
+dism::SweepCommon common(const Layout& L, void* ws, int64_t B, int64_t N, int64_t H,
+                         const int32_t* iq, const int32_t* ik, const uint8_t* hard,
+                         const int32_t* boundary, int32_t strip, const float* lut,
+                         int64_t lut_stride, bool key_records) {
+    dism::SweepCommon c;
+    c.B = (int)B;
+    c.H = (int)H;
+    c.n = (int)N;
+    c.iq = iq;
+    c.ik = ik;
+    c.hard = hard;
+    c.bound = boundary;
+    c.strip = boundary ? strip : 0;
+    c.lut = lut;
+    c.lut_stride = lut_stride;
+    c.qpos = at<int32_t>(ws, L.qpos);
+    c.kpos = at<int32_t>(ws, L.kpos);
+    c.qoff = at<int32_t>(ws, L.qoff);
+    c.koff = at<int32_t>(ws, L.koff);
+    c.qcs = at<int32_t>(ws, L.qcs);
+    c.kcs = at<int32_t>(ws, L.kcs);
+    c.bad = at<int32_t>(ws, L.bad);
+    c.slots = (int)((N + 63) / 64 + dism::BUCKETS);
+    c.prec = at<uint32_t>(ws, key_records ? L.krec : L.qrec);
+    c.pstride = L.stride;
+    return c;
+}
+
+int32_t check_common(const void* sq, const void* sk, const void* v, int32_t dtype,
+                     const int32_t* iq, const int32_t* ik, int64_t B, int64_t N, int64_t H,
+                     int32_t R, int32_t DV, const void* ws, int64_t ws_bytes, const char* what) {
+    if (!sq || !sk || !v || !iq || !ik || !ws)
+        return fail(DISM_ERR_INVALID, "%s: null pointer", what);
+    if (!dims_ok(B, N, H)) return fail(DISM_ERR_INVALID, "%s: positive dimensions required", what);
+    if (!rdv_ok(R, DV))
+        return fail(DISM_ERR_UNSUPPORTED, "%s: unsupported R=%d DV=%d", what, R, DV);
+    if (!dtype_ok(dtype))
+        return fail(DISM_ERR_UNSUPPORTED, "%s: vector dtype must be bf16 or f32", what);
+    if (ws_bytes < layout(B, N, H, R, DV, dtype).total)
+        return fail(DISM_ERR_INVALID, "%s: workspace too small", what);
+    return DISM_OK;
+}
+
+int32_t flag_nonfinite(const void* x, int32_t dtype, int64_t B, int64_t N, int64_t H, int D,
+                       int32_t* bad, hipStream_t s) {
+    return hip_status(dism::launch_nonfinite(x, dtype, B, N, H, D, bad, s), "non-finite scan");
+}
 }  // namespace
 
 extern "C" {
 
 const char* dism_last_error(void) { return g_error.c_str(); }
-int32_t dism_abi_version(void) { return 1; }
+int32_t dism_abi_version(void) { return 2; }
 
 int32_t dism_sign_labels(const void* x, int32_t dtype, int64_t B, int64_t N, int64_t H, int32_t d,
                          int32_t* labels, void* stream) {
     if (!x || !labels) return fail(DISM_ERR_INVALID, "sign labels: null pointer");
-    if (!dims_ok(B, N, H)) return fail(DISM_ERR_INVALID, "sign labels: positive dimensions required");
+    if (B <= 0 || N <= 0 || H <= 0 || B * N * H > ((int64_t)1 << 40))
+        return fail(DISM_ERR_INVALID, "sign labels: positive dimensions required");
     if (d < 1 || d > 30) return fail(DISM_ERR_INVALID, "sign labels: symbol width must be in [1,30]");
-    if (dtype != DISM_BF16 && dtype != DISM_F32)
-        return fail(DISM_ERR_UNSUPPORTED, "sign labels: dtype must be bf16 or f32");
-    return hip_status(dism::launch_sign_labels(x, dtype, B, N, H, d, labels, S(stream)), "sign labels");
+    if (!dtype_ok(dtype)) return fail(DISM_ERR_UNSUPPORTED, "sign labels: dtype must be bf16 or f32");
+    return hip_status(dism::launch_sign_labels(x, dtype, B, N, H, d, labels, S(stream)),
+                      "sign labels");
 }
 
 int32_t dism_hard_log_weights(const float* tau, int32_t H, int64_t max_length, float* lut,
@@ -81,7 +172,8 @@ int32_t dism_hard_dlog_weights(const float* tau, int32_t H, int64_t stride, floa
 int32_t dism_hard_summary(const int32_t* iq, const int32_t* ik, const uint8_t* hard, int64_t B,
                           int64_t H, int64_t N, int32_t* summary, void* stream) {
     if (!iq || !ik || !hard || !summary) return fail(DISM_ERR_INVALID, "hard summary: null pointer");
-    if (!dims_ok(B, N, H)) return fail(DISM_ERR_INVALID, "positive dimensions required");
+    if (B <= 0 || H <= 0 || N <= 0 || N > INT_MAX / 2 || B * H > 65535)
+        return fail(DISM_ERR_INVALID, "positive dimensions required");
     if ((N - 1) / 32 == 0) return ok();
     return hip_status(dism::launch_boundary(iq, ik, hard, B * H, (int)N, 32, 0, 1, summary,
                                             S(stream)), "hard summary");
@@ -90,7 +182,7 @@ int32_t dism_hard_summary(const int32_t* iq, const int32_t* ik, const uint8_t* h
 int32_t dism_hard_chunk(const int32_t* summary, int32_t* boundary, int64_t BH, int64_t N,
                         void* stream) {
     if (!summary || !boundary) return fail(DISM_ERR_INVALID, "hard chunk: null pointer");
-    if (BH <= 0 || BH > 65535 || N <= 0 || N > INT_MAX - 1024)
+    if (BH <= 0 || BH > 65535 || N <= 0 || N > INT_MAX / 2)
         return fail(DISM_ERR_INVALID, "invalid fixed batch/head count");
     int64_t C = (N - 1) / 32;
     if (C == 0) return ok();
@@ -100,58 +192,121 @@ int32_t dism_hard_chunk(const int32_t* summary, int32_t* boundary, int64_t BH, i
 int32_t dism_hard_boundary(const int32_t* iq, const int32_t* ik, const uint8_t* hard, int64_t B,
                            int64_t H, int64_t N, int32_t strip, int32_t fill_all,
                            int32_t* boundary, void* stream) {
-    if (!iq || !ik || !hard || !boundary) return fail(DISM_ERR_INVALID, "hard boundary: null pointer");
-    if (!dims_ok(B, N, H)) return fail(DISM_ERR_INVALID, "positive dimensions required");
+    if (!iq || !ik || !hard || !boundary)
+        return fail(DISM_ERR_INVALID, "hard boundary: null pointer");
+    if (B <= 0 || H <= 0 || N <= 0 || N > INT_MAX / 2 || B * H > 65535)
+        return fail(DISM_ERR_INVALID, "positive dimensions required");
     if (strip < 1) return fail(DISM_ERR_INVALID, "boundary strip height must be positive");
     if ((N - 1) / strip == 0) return ok();
-    if (B * H > 65535) return fail(DISM_ERR_INVALID, "hard boundary: too many batch-head rows");
     return hip_status(dism::launch_boundary(iq, ik, hard, B * H, (int)N, strip, 1, fill_all,
                                             boundary, S(stream)), "hard boundary");
+}
+
+int64_t dism_hard_workspace_bytes(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
+                                  int32_t dtype) {
+    if (!dims_ok(B, N, H) || !rdv_ok(R, DV) || !dtype_ok(dtype)) return -1;
+    return layout(B, N, H, R, DV, dtype).total;
+}
+
+int32_t dism_hard_prepare(const void* sq, const void* sk, const void* v, int32_t dtype,
+                          const int32_t* iq, const int32_t* ik, int64_t B, int64_t N, int64_t H,
+                          int32_t R, int32_t DV, void* workspace, int64_t workspace_bytes,
+                          void* stream) {
+    int32_t st = check_common(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
+                              workspace_bytes, "hard prepare");
+    if (st) return st;
+    const Layout L = layout(B, N, H, R, DV, dtype);
+    hipStream_t s = S(stream);
+    dism::BucketArgs ba{iq, ik, B * H, (int)N, at<int32_t>(workspace, L.qpos),
+                        at<int32_t>(workspace, L.kpos), at<int32_t>(workspace, L.qoff),
+                        at<int32_t>(workspace, L.koff), at<int32_t>(workspace, L.qcs),
+                        at<int32_t>(workspace, L.kcs)};
+    if ((st = hip_status(dism::launch_buckets(ba, s), "hard buckets"))) return st;
+    int32_t* bad = at<int32_t>(workspace, L.bad);
+    if ((st = hip_status(dism::launch_fill_i32(bad, B * H, 0, s), "hard flags"))) return st;
+    if ((st = flag_nonfinite(sq, dtype, B, N, H, R, bad, s))) return st;
+    if ((st = flag_nonfinite(sk, dtype, B, N, H, R, bad, s))) return st;
+    if ((st = flag_nonfinite(v, dtype, B, N, H, DV, bad, s))) return st;
+    dism::RecordArgs ra{(int)B, (int)H, (int)N, at<int32_t>(workspace, L.kpos), ik, sk, v,
+                        nullptr, words_of(dtype, R), words_of(dtype, DV), L.stride,
+                        at<uint32_t>(workspace, L.krec)};
+    return hip_status(dism::launch_records(ra, s), "hard key records");
 }
 
 int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t dtype,
                           const int32_t* iq, const int32_t* ik, const uint8_t* hard,
                           const int32_t* boundary, int32_t strip, const float* lut,
                           int64_t lut_stride, int64_t B, int64_t N, int64_t H, int32_t R,
-                          int32_t DV, void* out, int32_t out_dtype, float* lse2, int32_t* lmax,
-                          int32_t* jarg, void* stream) {
-    if (!sq || !sk || !v || !iq || !ik || !hard || !lut || !out || !lse2)
-        return fail(DISM_ERR_INVALID, "hard readout: null pointer");
-    if (!dims_ok(B, N, H)) return fail(DISM_ERR_INVALID, "positive dimensions required");
-    if (!rdv_ok(R, DV))
-        return fail(DISM_ERR_UNSUPPORTED, "hard readout: unsupported R=%d DV=%d", R, DV);
-    if (dtype != DISM_BF16 && dtype != DISM_F32)
-        return fail(DISM_ERR_UNSUPPORTED, "hard readout: vector dtype must be bf16 or f32");
-    if (out_dtype != DISM_BF16 && out_dtype != DISM_F32)
+                          int32_t DV, void* workspace, int64_t workspace_bytes, void* out,
+                          int32_t out_dtype, float* lse2, int32_t* lmax, int32_t* jarg,
+                          void* stream) {
+    int32_t st = check_common(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
+                              workspace_bytes, "hard readout");
+    if (st) return st;
+    if (!hard || !lut || !out || !lse2) return fail(DISM_ERR_INVALID, "hard readout: null pointer");
+    if (!dtype_ok(out_dtype))
         return fail(DISM_ERR_UNSUPPORTED, "hard readout: output dtype must be bf16 or f32");
     if (lut_stride < N + 1) return fail(DISM_ERR_INVALID, "hard log-weight table is too short");
     if (boundary && strip < 1) return fail(DISM_ERR_INVALID, "invalid hard boundary strip");
-    dism::ForwardArgs a{sq, sk, v, iq, ik, hard, boundary, boundary ? strip : 0, lut, lut_stride,
-                        (int)B, (int)H, (int)N, out, out_dtype, lse2, lmax, jarg};
+    const Layout L = layout(B, N, H, R, DV, dtype);
+    dism::ForwardArgs a;
+    a.c = common(L, workspace, B, N, H, iq, ik, hard, boundary, strip, lut, lut_stride, true);
+    a.sq = sq;
+    a.sk = sk;
+    a.v = v;
+    a.out = out;
+    a.out_dtype = out_dtype;
+    a.lse2 = lse2;
+    a.lmax = lmax;
+    a.jarg = jarg;
     return hip_status(dism::launch_forward(a, R, DV, dtype, S(stream)), "hard readout");
 }
 
-static int32_t backward_args(const void* sq, const void* sk, const void* v, const void* dout,
-                             int32_t dtype, const int32_t* iq, const int32_t* ik,
-                             const uint8_t* hard, const int32_t* boundary, int32_t strip,
-                             const float* lut, const float* dlut, int64_t lut_stride,
-                             const float* lse2, int64_t B, int64_t N, int64_t H, int32_t R,
-                             int32_t DV, float* dsq, float* dsk, float* dv, float* rowtau,
-                             bool need_rows, bool need_keys, dism::BackwardArgs* a) {
-    if (!sq || !sk || !v || !dout || !iq || !ik || !hard || !lut || !lse2)
-        return fail(DISM_ERR_INVALID, "hard backward: null pointer");
-    if ((need_rows && (!dlut || !dsq || !rowtau)) || (need_keys && (!dsk || !dv)))
-        return fail(DISM_ERR_INVALID, "hard backward: null pointer");
-    if (!dims_ok(B, N, H)) return fail(DISM_ERR_INVALID, "positive dimensions required");
-    if (!rdv_ok(R, DV))
-        return fail(DISM_ERR_UNSUPPORTED, "hard backward: unsupported R=%d DV=%d", R, DV);
-    if (dtype != DISM_BF16 && dtype != DISM_F32)
-        return fail(DISM_ERR_UNSUPPORTED, "hard backward: vector dtype must be bf16 or f32");
+}  // extern "C"
+
+static int32_t backward_common(const void* sq, const void* sk, const void* v, const void* dout,
+                               int32_t dtype, const int32_t* iq, const int32_t* ik,
+                               const uint8_t* hard, const int32_t* boundary, int32_t strip,
+                               const float* lut, int64_t lut_stride, const float* lse2,
+                               int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
+                               void* workspace, int64_t workspace_bytes, bool key_records,
+                               dism::BackwardArgs* a, const char* what) {
+    int32_t st = check_common(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
+                              workspace_bytes, what);
+    if (st) return st;
+    if (!dout || !hard || !lut || !lse2) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
     if (lut_stride < N + 1) return fail(DISM_ERR_INVALID, "hard log-weight table is too short");
     if (boundary && strip < 1) return fail(DISM_ERR_INVALID, "invalid hard boundary strip");
-    *a = dism::BackwardArgs{sq, sk, v, dout, iq, ik, hard, boundary, boundary ? strip : 0, lut,
-                            dlut, lut_stride, lse2, (int)B, (int)H, (int)N, dsq, dsk, dv, rowtau};
+    const Layout L = layout(B, N, H, R, DV, dtype);
+    a->c = common(L, workspace, B, N, H, iq, ik, hard, boundary, strip, lut, lut_stride,
+                  key_records);
+    a->sq = sq;
+    a->sk = sk;
+    a->v = v;
+    a->dout = dout;
+    a->lse2 = lse2;
     return DISM_OK;
+}
+
+extern "C" {
+
+int32_t dism_hard_backward_prepare(const void* sq, const void* sk, const void* v,
+                                   const void* dout, int32_t dtype, const int32_t* iq,
+                                   const int32_t* ik, const float* lse2, int64_t B, int64_t N,
+                                   int64_t H, int32_t R, int32_t DV, void* workspace,
+                                   int64_t workspace_bytes, void* stream) {
+    int32_t st = check_common(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
+                              workspace_bytes, "hard backward prepare");
+    if (st) return st;
+    if (!dout || !lse2) return fail(DISM_ERR_INVALID, "hard backward prepare: null pointer");
+    const Layout L = layout(B, N, H, R, DV, dtype);
+    hipStream_t s = S(stream);
+    if ((st = flag_nonfinite(dout, dtype, B, N, H, DV, at<int32_t>(workspace, L.bad), s)))
+        return st;
+    dism::RecordArgs ra{(int)B, (int)H, (int)N, at<int32_t>(workspace, L.qpos), iq, sq, dout,
+                        lse2, words_of(dtype, R), words_of(dtype, DV), L.stride,
+                        at<uint32_t>(workspace, L.qrec)};
+    return hip_status(dism::launch_records(ra, s), "hard query records");
 }
 
 int32_t dism_hard_backward_queries(const void* sq, const void* sk, const void* v,
@@ -160,13 +315,19 @@ int32_t dism_hard_backward_queries(const void* sq, const void* sk, const void* v
                                    const int32_t* boundary, int32_t strip, const float* lut,
                                    const float* dlut, int64_t lut_stride, const float* lse2,
                                    int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
-                                   float* dsq, float* rowtau, void* stream) {
-    dism::BackwardArgs a;
-    int32_t st = backward_args(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut, dlut,
-                               lut_stride, lse2, B, N, H, R, DV, dsq, nullptr, nullptr, rowtau,
-                               true, false, &a);
+                                   void* workspace, int64_t workspace_bytes, float* dsq,
+                                   float* rowtau, void* stream) {
+    dism::BackwardArgs a{};
+    int32_t st = backward_common(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
+                                 lut_stride, lse2, B, N, H, R, DV, workspace, workspace_bytes,
+                                 true, &a, "hard backward queries");
     if (st) return st;
-    return hip_status(dism::launch_backward_rows(a, R, DV, dtype, S(stream)), "hard backward rows");
+    if (!dlut || !dsq || !rowtau) return fail(DISM_ERR_INVALID, "hard backward: null pointer");
+    a.dlut = dlut;
+    a.dsq = dsq;
+    a.rowtau = rowtau;
+    return hip_status(dism::launch_backward_rows(a, R, DV, dtype, S(stream)),
+                      "hard backward rows");
 }
 
 int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, const void* dout,
@@ -174,19 +335,25 @@ int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, c
                                 const uint8_t* hard, const int32_t* boundary, int32_t strip,
                                 const float* lut, int64_t lut_stride, const float* lse2,
                                 int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
-                                float* dsk, float* dv, void* stream) {
-    dism::BackwardArgs a;
-    int32_t st = backward_args(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
-                               nullptr, lut_stride, lse2, B, N, H, R, DV, nullptr, dsk, dv,
-                               nullptr, false, true, &a);
+                                void* workspace, int64_t workspace_bytes, float* dsk, float* dv,
+                                void* stream) {
+    dism::BackwardArgs a{};
+    int32_t st = backward_common(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
+                                 lut_stride, lse2, B, N, H, R, DV, workspace, workspace_bytes,
+                                 false, &a, "hard backward keys");
     if (st) return st;
-    return hip_status(dism::launch_backward_keys(a, R, DV, dtype, S(stream)), "hard backward keys");
+    if (!dsk || !dv) return fail(DISM_ERR_INVALID, "hard backward: null pointer");
+    a.dsk = dsk;
+    a.dv = dv;
+    return hip_status(dism::launch_backward_keys(a, R, DV, dtype, S(stream)),
+                      "hard backward keys");
 }
 
 int32_t dism_hard_tau_reduce(const float* rowtau, int64_t B, int64_t H, int64_t N, float* dtau,
                              void* stream) {
     if (!rowtau || !dtau) return fail(DISM_ERR_INVALID, "tau reduce: null pointer");
-    if (!dims_ok(B, N, H)) return fail(DISM_ERR_INVALID, "positive dimensions required");
+    if (B <= 0 || H <= 0 || N <= 0 || H > 65535)
+        return fail(DISM_ERR_INVALID, "positive dimensions required");
     return hip_status(dism::launch_tau_reduce(rowtau, (int)B, (int)H, N, dtau, S(stream)),
                       "hard tau reduce");
 }
@@ -196,15 +363,19 @@ int32_t dism_hard_backward(const void* sq, const void* sk, const void* v, const 
                            const uint8_t* hard, const int32_t* boundary, int32_t strip,
                            const float* lut, const float* dlut, int64_t lut_stride,
                            const float* lse2, int64_t B, int64_t N, int64_t H, int32_t R,
-                           int32_t DV, float* dsq, float* dsk, float* dv, float* rowtau,
-                           float* dtau, void* stream) {
+                           int32_t DV, void* workspace, int64_t workspace_bytes, float* dsq,
+                           float* dsk, float* dv, float* rowtau, float* dtau, void* stream) {
     if (!dtau) return fail(DISM_ERR_INVALID, "hard backward: null pointer");
-    int32_t st = dism_hard_backward_queries(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip,
-                                            lut, dlut, lut_stride, lse2, B, N, H, R, DV, dsq,
-                                            rowtau, stream);
+    int32_t st = dism_hard_backward_prepare(sq, sk, v, dout, dtype, iq, ik, lse2, B, N, H, R, DV,
+                                            workspace, workspace_bytes, stream);
+    if (st) return st;
+    st = dism_hard_backward_queries(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
+                                    dlut, lut_stride, lse2, B, N, H, R, DV, workspace,
+                                    workspace_bytes, dsq, rowtau, stream);
     if (st) return st;
     st = dism_hard_backward_keys(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
-                                 lut_stride, lse2, B, N, H, R, DV, dsk, dv, stream);
+                                 lut_stride, lse2, B, N, H, R, DV, workspace, workspace_bytes,
+                                 dsk, dv, stream);
     if (st) return st;
     return dism_hard_tau_reduce(rowtau, B, H, N, dtau, stream);
 }

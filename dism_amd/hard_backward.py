@@ -15,7 +15,7 @@ import torch
 from . import _lib
 from ._checks import (DTYPE_CODE, check_ctas, check_graph_choice, check_labels, check_layout,
                       check_tensor, check_vectors, require)
-from .hard_forward import _forward_core, hard_dlog_weights
+from .hard_forward import _forward_core, hard_dlog_weights, prepare_workspace
 
 
 def _stream(t):
@@ -53,6 +53,9 @@ def backward_hard(sq, sk, v, dout, idx_q, idx_k, hard, normalizer, state, *, lay
     if tau is None:  # reference state: recover tau from LUT[:,1] = tau / ln 2
         tau = (lut[:, 1].double() * math.log(2.0)).float().contiguous()
     dlut = hard_dlog_weights(tau, n + 1)
+    ws = state.get("workspace")
+    if ws is None or ws.numel() < _lib.workspace_bytes(b, n, h, r, dv, DTYPE_CODE[dt]):
+        ws = prepare_workspace(sq, sk, v, idx_q, idx_k)
     dsq = torch.empty((b, n, h, r), dtype=torch.float32, device=sq.device)
     dsk = torch.empty((b, n, h, r), dtype=torch.float32, device=sq.device)
     dvv = torch.empty((b, n, h, dv), dtype=torch.float32, device=sq.device)
@@ -63,8 +66,8 @@ def backward_hard(sq, sk, v, dout, idx_q, idx_k, hard, normalizer, state, *, lay
                   dout.data_ptr(), DTYPE_CODE[dt], idx_q.data_ptr(), idx_k.data_ptr(),
                   hard.data_ptr(), 0 if carry is None else carry.data_ptr(), strip,
                   lut.data_ptr(), dlut.data_ptr(), n + 1, normalizer.data_ptr(), b, n, h, r,
-                  dv, dsq.data_ptr(), dsk.data_ptr(), dvv.data_ptr(), rowtau.data_ptr(),
-                  dtau.data_ptr(), _stream(sq))
+                  dv, ws.data_ptr(), ws.numel(), dsq.data_ptr(), dsk.data_ptr(),
+                  dvv.data_ptr(), rowtau.data_ptr(), dtau.data_ptr(), _stream(sq))
     return dsq, dsk, dvv, dtau
 
 
@@ -78,9 +81,10 @@ def backward_hard_recompute(sq, sk, v, dout, iq, ik, hard, tau, *, layout=None, 
     q, k = [x.to(torch.int32).contiguous() for x in (iq, ik)]
     check_ctas(ctas)
     check_graph_choice(_graph_choice)
-    _, norm, lut, carry, strip, _, _ = _forward_core(a, b_, c, q, k, hard.contiguous(),
-                                                     tau.contiguous(), None, None, False)
-    state = dict(log_weights=lut, tau=tau.contiguous(), carry=carry, carry_strip=strip)
+    _, norm, lut, carry, strip, _, _, ws = _forward_core(a, b_, c, q, k, hard.contiguous(),
+                                                         tau.contiguous(), None, None, False)
+    state = dict(log_weights=lut, tau=tau.contiguous(), carry=carry, carry_strip=strip,
+                 workspace=ws)
     result = backward_hard(a, b_, c, do, q, k, hard.contiguous(), norm, state, ctas=ctas,
                            _graph_choice=_graph_choice)
     return dict(zip(("sq_vec", "sk_vec", "v", "rtau"), result))

@@ -59,8 +59,21 @@ def hard_dlog_weights(tau, stride):
     return out
 
 
+def prepare_workspace(sq, sk, v, idx_q, idx_k):
+    """Allocate the sweep workspace and fill it (label buckets, key records, non-finite
+    flags) for these inputs.  Returns the uint8 workspace tensor."""
+    b, n, h, r, dv, dt = check_vectors(sq, sk, v)
+    nbytes = _lib.workspace_bytes(b, n, h, r, dv, DTYPE_CODE[dt])
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=sq.device)
+    with torch.cuda.device(sq.device):
+        _lib.call("dism_hard_prepare", sq.data_ptr(), sk.data_ptr(), v.data_ptr(),
+                  DTYPE_CODE[dt], idx_q.data_ptr(), idx_k.data_ptr(), b, n, h, r, dv,
+                  ws.data_ptr(), nbytes, _stream(sq))
+    return ws
+
+
 def _readout(sq, sk, v, idx_q, idx_k, hard, boundary, strip, log_weights, out_dtype,
-             matches):
+             matches, workspace=None):
     b, n, h, r, dv, dt = check_vectors(sq, sk, v)
     check_labels(idx_q, idx_k, b, h, n, sq.device)
     check_hard(hard, b, h, sq.device)
@@ -72,6 +85,8 @@ def _readout(sq, sk, v, idx_q, idx_k, hard, boundary, strip, log_weights, out_dt
     if boundary is not None:
         check_tensor(boundary, torch.int32, (b, h, (n - 1) // strip, n), "hard boundary",
                      sq.device)
+    if workspace is None:
+        workspace = prepare_workspace(sq, sk, v, idx_q, idx_k)
     out = torch.empty((b, n, h, dv), dtype=out_dtype, device=sq.device)
     lse2 = torch.empty((b, h, n), dtype=torch.float32, device=sq.device)
     lmax = jarg = None
@@ -83,9 +98,10 @@ def _readout(sq, sk, v, idx_q, idx_k, hard, boundary, strip, log_weights, out_dt
         _lib.call("dism_hard_readout", sq.data_ptr(), sk.data_ptr(), v.data_ptr(),
                   DTYPE_CODE[dt], idx_q.data_ptr(), idx_k.data_ptr(), hard.data_ptr(),
                   ptr(boundary), strip if boundary is not None else 0, log_weights.data_ptr(),
-                  log_weights.shape[1], b, n, h, r, dv, out.data_ptr(),
-                  DTYPE_CODE[out_dtype], lse2.data_ptr(), ptr(lmax), ptr(jarg), _stream(sq))
-    return out, lse2, lmax, jarg
+                  log_weights.shape[1], b, n, h, r, dv, workspace.data_ptr(),
+                  workspace.numel(), out.data_ptr(), DTYPE_CODE[out_dtype], lse2.data_ptr(),
+                  ptr(lmax), ptr(jarg), _stream(sq))
+    return out, lse2, lmax, jarg, workspace
 
 
 @torch.no_grad()
@@ -101,14 +117,14 @@ def hard_readout(sq, sk, v, idx_q, idx_k, hard, boundary, log_weights, *, layout
     check_ctas(ctas)
     check_layout(layout)
     check_graph_choice(_graph_choice)
-    out, lse2, _, _ = _readout(sq, sk, v, idx_q, idx_k, hard, boundary, 32, log_weights,
-                               sq.dtype, False)
+    out, lse2, _, _, _ = _readout(sq, sk, v, idx_q, idx_k, hard, boundary, 32, log_weights,
+                                  sq.dtype, False)
     return out, lse2
 
 
 def _forward_core(sq, sk, v, idx_q, idx_k, hard, tau, carry_strip, out_dtype, matches):
     """LUT + (optional carry boundary) + readout; returns (out, lse2, lut, carry, strip,
-    lmax, jarg)."""
+    lmax, jarg, workspace)."""
     b, n, h, _, _, dt = check_vectors(sq, sk, v)
     check_labels(idx_q, idx_k, b, h, n, sq.device)
     check_hard(hard, b, h, sq.device)
@@ -119,9 +135,9 @@ def _forward_core(sq, sk, v, idx_q, idx_k, hard, tau, carry_strip, out_dtype, ma
     carry = None
     if strip > 0 and (n - 1) // strip > 0:
         carry = hard_boundary(idx_q, idx_k, hard, strip=strip, fill_all=False)
-    out, lse2, lmax, jarg = _readout(sq, sk, v, idx_q, idx_k, hard, carry, strip, lut,
-                                     out_dtype or dt, matches)
-    return out, lse2, lut, carry, strip, lmax, jarg
+    out, lse2, lmax, jarg, ws = _readout(sq, sk, v, idx_q, idx_k, hard, carry, strip, lut,
+                                         out_dtype or dt, matches)
+    return out, lse2, lut, carry, strip, lmax, jarg, ws
 
 
 @torch.no_grad()
@@ -130,20 +146,21 @@ def forward_hard(sq, sk, v, idx_q, idx_k, hard, tau, *, layout=None, ctas=0, sav
     """Complete standalone hard contribution: LUT and fused readout.
 
     Returns (O, lse2) or, with save_state, (O, lse2, dict(summary, boundary, log_weights,
-    tau, strip, carry, carry_strip)); with return_matches a further dict(length, index).
+    tau, strip, carry, carry_strip, workspace)); with return_matches a further
+    dict(length, index).
     O has the vectors' dtype unless out_dtype is given.
     """
     check_ctas(ctas)
     check_layout(layout)
     check_graph_choice(_graph_choice)
-    out, lse2, lut, carry, strip, lmax, jarg = _forward_core(
+    out, lse2, lut, carry, strip, lmax, jarg, ws = _forward_core(
         sq, sk, v, idx_q, idx_k, hard, tau, carry_strip, out_dtype, return_matches)
     result = [out, lse2]
     if save_state:
         summary = summarize_hard(idx_q, idx_k, hard)
         boundary = hard_chunk_scan(summary)
         result.append(dict(summary=summary, boundary=boundary, log_weights=lut, tau=tau,
-                           strip=32, carry=carry, carry_strip=strip))
+                           strip=32, carry=carry, carry_strip=strip, workspace=ws))
     if return_matches:
         result.append(dict(length=lmax, index=jarg))
     return tuple(result)

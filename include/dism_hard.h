@@ -73,47 +73,75 @@ int32_t dism_hard_boundary(const int32_t* iq, const int32_t* ik, const uint8_t* 
                            int64_t H, int64_t N, int32_t strip, int32_t fill_all,
                            int32_t* boundary, void* stream);
 
-/* Hard readout: O [B,N,H,DV] (out_dtype bf16|f32) and lse2 [B,H,N] fp32; optional lmax/jarg
- * [B,H,N] int32 = longest match length per query and its key (ties -> most recent key,
- * -1 if none).  boundary may be NULL (lengths recomputed from labels alone) or a composed
- * boundary of strip height `strip`.  lut_stride >= N+1.  Soft rows give zeros.
+/* Size in bytes of the caller-owned workspace used by the bucketed sweeps for these
+ * dimensions (-1 for unsupported dimensions).  Layout: bucket-sorted query/key positions and
+ * bucket tables, non-finite flags, key records and query records (dism_amd/csrc/dism_capi.cpp).
+ * No reference counterpart: the reference keeps an O(B*H*N^2/32) int32 boundary instead. */
+int64_t dism_hard_workspace_bytes(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
+                                  int32_t dtype);
+
+/* Forward preparation into `workspace`: stable counting sort of query and key positions by
+ * label & 255 per (b,h), non-finite flags of sq/sk/v, key records (position, labels, sk row,
+ * v row) in bucket order.  Replaces the summary + chunk passes that precede the reference
+ * readout (dism_v3/python/flash_dism/hard_forward.py:36-40). */
+int32_t dism_hard_prepare(const void* sq, const void* sk, const void* v, int32_t dtype,
+                          const int32_t* iq, const int32_t* ik, int64_t B, int64_t N, int64_t H,
+                          int32_t R, int32_t DV, void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
+/* Hard readout on a prepared workspace: O [B,N,H,DV] (out_dtype bf16|f32) and lse2 [B,H,N]
+ * fp32; optional lmax/jarg [B,H,N] int32 receive the longest match length per query and its
+ * key (ties -> most recent key, -1 if none).  boundary may be NULL (lengths recomputed from
+ * labels alone) or a composed boundary of strip height `strip`.  lut_stride >= N+1.  Soft
+ * rows give zeros.
  * Replaces cu.hard_readout (dism_v3/src/host/hard_forward.cpp:25-113). */
 int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t dtype,
                           const int32_t* iq, const int32_t* ik, const uint8_t* hard,
                           const int32_t* boundary, int32_t strip, const float* lut,
                           int64_t lut_stride, int64_t B, int64_t N, int64_t H, int32_t R,
-                          int32_t DV, void* out, int32_t out_dtype, float* lse2, int32_t* lmax,
-                          int32_t* jarg, void* stream);
+                          int32_t DV, void* workspace, int64_t workspace_bytes, void* out,
+                          int32_t out_dtype, float* lse2, int32_t* lmax, int32_t* jarg,
+                          void* stream);
 
-/* Hard backward: dsq, dsk [B,N,H,R], dv [B,N,H,DV], rowtau [B,H,N] (scratch, caller-owned)
- * and dtau [H], all fp32, deterministic (no atomics).  lse2 is the forward's log2
- * normalizer; lut/dlut share lut_stride >= N+1.
+/* Hard backward on a workspace prepared by dism_hard_prepare for the same inputs: dsq, dsk
+ * [B,N,H,R], dv [B,N,H,DV], rowtau [B,H,N] (caller-owned scratch) and dtau [H], all fp32,
+ * deterministic (no atomics).  lse2 is the forward's log2 normalizer; lut/dlut share
+ * lut_stride >= N+1.  Runs the four stages below in order.
  * Replaces cu.hard_backward (dism_v3/src/host/hard_backward.cpp:13-140). */
 int32_t dism_hard_backward(const void* sq, const void* sk, const void* v, const void* dout,
                            int32_t dtype, const int32_t* iq, const int32_t* ik,
                            const uint8_t* hard, const int32_t* boundary, int32_t strip,
                            const float* lut, const float* dlut, int64_t lut_stride,
                            const float* lse2, int64_t B, int64_t N, int64_t H, int32_t R,
-                           int32_t DV, float* dsq, float* dsk, float* dv, float* rowtau,
-                           float* dtau, void* stream);
+                           int32_t DV, void* workspace, int64_t workspace_bytes, float* dsq,
+                           float* dsk, float* dv, float* rowtau, float* dtau, void* stream);
 
-/* The three stages of dism_hard_backward, callable separately (same arguments):
- * query sweep -> dsq, rowtau; key sweep -> dsk, dv; fixed-order reduction rowtau -> dtau.
- * Together they replace the single hard_backward_kernel + hard_tau_reduce_kernel launch pair
- * of dism_v3/src/host/hard_backward.cpp:242-252. */
+/* Stages of dism_hard_backward, callable separately (same arguments).  Together they replace
+ * the hard_dlog_weights / hard_backward / hard_tau_reduce launch sequence of
+ * dism_v3/src/host/hard_backward.cpp:242-252:
+ *   prepare: non-finite flag of dO, query records (position, labels, lse2, sq row, dO row);
+ *   queries: query sweep -> dsq, rowtau;  keys: key sweep -> dsk, dv;
+ *   tau_reduce: fixed-order reduction rowtau -> dtau. */
+int32_t dism_hard_backward_prepare(const void* sq, const void* sk, const void* v,
+                                   const void* dout, int32_t dtype, const int32_t* iq,
+                                   const int32_t* ik, const float* lse2, int64_t B, int64_t N,
+                                   int64_t H, int32_t R, int32_t DV, void* workspace,
+                                   int64_t workspace_bytes, void* stream);
 int32_t dism_hard_backward_queries(const void* sq, const void* sk, const void* v,
                                    const void* dout, int32_t dtype, const int32_t* iq,
                                    const int32_t* ik, const uint8_t* hard,
                                    const int32_t* boundary, int32_t strip, const float* lut,
                                    const float* dlut, int64_t lut_stride, const float* lse2,
                                    int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
-                                   float* dsq, float* rowtau, void* stream);
+                                   void* workspace, int64_t workspace_bytes, float* dsq,
+                                   float* rowtau, void* stream);
 int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, const void* dout,
                                 int32_t dtype, const int32_t* iq, const int32_t* ik,
                                 const uint8_t* hard, const int32_t* boundary, int32_t strip,
                                 const float* lut, int64_t lut_stride, const float* lse2,
                                 int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
-                                float* dsk, float* dv, void* stream);
+                                void* workspace, int64_t workspace_bytes, float* dsk, float* dv,
+                                void* stream);
 int32_t dism_hard_tau_reduce(const float* rowtau, int64_t B, int64_t H, int64_t N, float* dtau,
                              void* stream);
 

@@ -268,10 +268,15 @@ long orc_suffix_walk(const int32_t* q, const int32_t* k, long i, long j) {
 
 /* ---------------- forward ----------------
  * Vectors fp32 BNHD (bf16 inputs widened exactly by the caller), labels BHN, hard [B*H].
- * Per row i (ascending j over matches):
- *   lut = LUT[L]; if lut > m: alpha=exp2(m-lut); den*=alpha; acc*=alpha; m=lut
- *   p = exp2(lut-m); den += p; s = fma-chain(sq_i . sk_j); ps = p*s; acc = fma(ps, v_j, acc)
- * out = acc/den, lse2 = m + log2(den); match argmax: longest L, ties -> largest j. */
+ * Per row i:
+ *   pass 1 (integer): L for every matching key; m = max(0, max_j LUT[L]); longest match with
+ *                     ties -> largest j;
+ *   pass 2, ascending j over matches:
+ *     den starts at exp2(-m); p = exp2(LUT[L] - m); den += p;
+ *     s = fma-chain(sq_i . sk_j); ps = p*s; acc = fma(ps, v_j, acc)
+ *   out = acc/den, lse2 = m + log2(den).
+ * This is the reference's online-max readout (readout.cuh:16-61) with the final maximum
+ * applied from the start; the unit fallback contributes exp2(0 - m). */
 void orc_forward(const float* sq, const float* sk, const float* v, const int32_t* iq,
                  const int32_t* ik, const uint8_t* hard, const float* lut, long lut_stride,
                  int B, long N, int H, int R, int DV, float* out, float* lse2, int32_t* lmax,
@@ -299,23 +304,22 @@ void orc_forward(const float* sq, const float* sk, const float* v, const int32_t
                 continue;
             }
             /* lb[j+1] = L[i,j]; la[j] = L[i-1,j-1] */
-            float m = 0.0f, den = 1.0f;
+            float m = 0.0f;
             int32_t best = 0, bj = -1;
-            for (int d = 0; d < DV; ++d) acc[d] = 0.0f;
-            const float* sqi = sq + row * R;
             for (long j = 0; j <= i; ++j) {
                 if (q[i] != k[j]) { lb[j + 1] = 0; continue; }
                 int32_t L = la[j] + 1;
                 lb[j + 1] = L;
                 if (L >= best) { best = L; bj = (int32_t)j; }
-                float lw = tab[L];
-                if (lw > m) {
-                    float alpha = orc_exp2f(m - lw);
-                    den = den * alpha;
-                    for (int d = 0; d < DV; ++d) acc[d] = acc[d] * alpha;
-                    m = lw;
-                }
-                float p = orc_exp2f(lw - m);
+                if (tab[L] > m) m = tab[L];
+            }
+            float den = orc_exp2f(-m);
+            for (int d = 0; d < DV; ++d) acc[d] = 0.0f;
+            const float* sqi = sq + row * R;
+            for (long j = 0; j <= i; ++j) {
+                int32_t L = lb[j + 1];
+                if (!L) continue;
+                float p = orc_exp2f(tab[L] - m);
                 den = den + p;
                 long krow = ((long)b * N + j) * H + h;
                 const float* skj = sk + krow * R;
