@@ -99,37 +99,64 @@ __global__ __launch_bounds__(256) void nonfinite_kernel(const T* __restrict__ x,
     }
 }
 
-// one thread per record word; words of a record are contiguous, so stores coalesce
+// One thread per record.  Rows are copied with 16-byte vector accesses when the row length
+// allows it; a record whose readout or value row holds a non-finite value raises bad[bh].
+__device__ __forceinline__ bool word_nonfinite(uint32_t w, bool half) {
+    if (half) return ((w & 0x7F80u) == 0x7F80u) || ((w & 0x7F800000u) == 0x7F800000u);
+    return (w & 0x7F800000u) == 0x7F800000u;
+}
+
 __global__ __launch_bounds__(256) void records_kernel(RecordArgs a) {
-    const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long total = (long)a.B * a.H * a.n * a.stride;
-    if (e >= total) return;
-    const long rec = e / a.stride;
-    const int w = (int)(e - rec * a.stride);
+    const long rec = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long total = (long)a.B * a.H * a.n;
+    if (rec >= total) return;
     const long bh = rec / a.n;
     const int p = a.pos[rec];
     const long b = bh / a.H, h = bh - b * a.H;
-    uint32_t out = 0u;
-    if (w == 0) {
-        out = (uint32_t)p;
-    } else if (w == 1) {
-        out = (uint32_t)a.lab[bh * a.n + p];
-    } else if (w == 2) {
-        out = p >= 1 ? (uint32_t)a.lab[bh * a.n + p - 1] : 0u;
-    } else if (w == 3) {
-        out = a.extra ? __float_as_uint(a.extra[bh * a.n + p]) : 0u;
-    } else if (w < 4 + a.rw) {
-        const long row = (b * a.n + p) * a.H + h;
-        out = reinterpret_cast<const uint32_t*>(a.rrow)[row * a.rw + (w - 4)];
-    } else if (w < 4 + a.rw + a.vw) {
-        const long row = (b * a.n + p) * a.H + h;
-        out = reinterpret_cast<const uint32_t*>(a.vrow)[row * a.vw + (w - 4 - a.rw)];
+    const long row = (b * a.n + p) * a.H + h;
+    const bool half = a.dtype == DTYPE_BF16;
+    uint32_t* out = a.rec + rec * a.stride;
+    const int32_t* lab = a.lab + bh * a.n;
+    reinterpret_cast<uint4*>(out)[0] =
+        make_uint4((uint32_t)p, (uint32_t)lab[p], p >= 1 ? (uint32_t)lab[p - 1] : 0u,
+                   a.extra ? __float_as_uint(a.extra[bh * a.n + p]) : 0u);
+    bool bad = false;
+    const uint32_t* rr = reinterpret_cast<const uint32_t*>(a.rrow) + row * a.rw;
+    const uint32_t* vr = reinterpret_cast<const uint32_t*>(a.vrow) + row * a.vw;
+    if ((a.rw & 3) == 0) {
+        for (int c = 0; c < a.rw; c += 4) {
+            uint4 x = *reinterpret_cast<const uint4*>(rr + c);
+            bad |= word_nonfinite(x.x, half) | word_nonfinite(x.y, half) |
+                   word_nonfinite(x.z, half) | word_nonfinite(x.w, half);
+            *reinterpret_cast<uint4*>(out + 4 + c) = x;
+        }
+    } else {
+        for (int c = 0; c < a.rw; ++c) {
+            uint32_t x = rr[c];
+            bad |= word_nonfinite(x, half);
+            out[4 + c] = x;
+        }
     }
-    a.rec[e] = out;
+    uint32_t* vo = out + 4 + a.rw;
+    if ((a.rw & 3) == 0 && (a.vw & 3) == 0) {
+        for (int c = 0; c < a.vw; c += 4) {
+            uint4 x = *reinterpret_cast<const uint4*>(vr + c);
+            bad |= word_nonfinite(x.x, half) | word_nonfinite(x.y, half) |
+                   word_nonfinite(x.z, half) | word_nonfinite(x.w, half);
+            *reinterpret_cast<uint4*>(vo + c) = x;
+        }
+    } else {
+        for (int c = 0; c < a.vw; ++c) {
+            uint32_t x = vr[c];
+            bad |= word_nonfinite(x, half);
+            vo[c] = x;
+        }
+    }
+    if (bad) atomicOr(&a.bad[bh], 1);
 }
 
 hipError_t launch_records(const RecordArgs& a, hipStream_t s) {
-    const long total = (long)a.B * a.H * a.n * a.stride;
+    const long total = (long)a.B * a.H * a.n;
     hipLaunchKernelGGL(records_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
     return hipGetLastError();
 }

@@ -60,7 +60,7 @@ Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV, int32_t dt
     Layout L;
     const int64_t BH = B * H;
     const int raw = 4 + words_of(dtype, R) + words_of(dtype, DV);
-    L.stride = (raw + 15) / 16 * 16;
+    L.stride = (raw + 3) / 4 * 4;
     int64_t o = 0;
     auto take = [&](int64_t bytes) {
         int64_t at = o;
@@ -128,10 +128,6 @@ int32_t check_common(const void* sq, const void* sk, const void* v, int32_t dtyp
     return DISM_OK;
 }
 
-int32_t flag_nonfinite(const void* x, int32_t dtype, int64_t B, int64_t N, int64_t H, int D,
-                       int32_t* bad, hipStream_t s) {
-    return hip_status(dism::launch_nonfinite(x, dtype, B, N, H, D, bad, s), "non-finite scan");
-}
 }  // namespace
 
 extern "C" {
@@ -224,12 +220,9 @@ int32_t dism_hard_prepare(const void* sq, const void* sk, const void* v, int32_t
     if ((st = hip_status(dism::launch_buckets(ba, s), "hard buckets"))) return st;
     int32_t* bad = at<int32_t>(workspace, L.bad);
     if ((st = hip_status(dism::launch_fill_i32(bad, B * H, 0, s), "hard flags"))) return st;
-    if ((st = flag_nonfinite(sq, dtype, B, N, H, R, bad, s))) return st;
-    if ((st = flag_nonfinite(sk, dtype, B, N, H, R, bad, s))) return st;
-    if ((st = flag_nonfinite(v, dtype, B, N, H, DV, bad, s))) return st;
     dism::RecordArgs ra{(int)B, (int)H, (int)N, at<int32_t>(workspace, L.kpos), ik, sk, v,
-                        nullptr, words_of(dtype, R), words_of(dtype, DV), L.stride,
-                        at<uint32_t>(workspace, L.krec)};
+                        nullptr, words_of(dtype, R), words_of(dtype, DV), L.stride, dtype,
+                        at<uint32_t>(workspace, L.krec), bad};
     return hip_status(dism::launch_records(ra, s), "hard key records");
 }
 
@@ -301,11 +294,9 @@ int32_t dism_hard_backward_prepare(const void* sq, const void* sk, const void* v
     if (!dout || !lse2) return fail(DISM_ERR_INVALID, "hard backward prepare: null pointer");
     const Layout L = layout(B, N, H, R, DV, dtype);
     hipStream_t s = S(stream);
-    if ((st = flag_nonfinite(dout, dtype, B, N, H, DV, at<int32_t>(workspace, L.bad), s)))
-        return st;
     dism::RecordArgs ra{(int)B, (int)H, (int)N, at<int32_t>(workspace, L.qpos), iq, sq, dout,
-                        lse2, words_of(dtype, R), words_of(dtype, DV), L.stride,
-                        at<uint32_t>(workspace, L.qrec)};
+                        lse2, words_of(dtype, R), words_of(dtype, DV), L.stride, dtype,
+                        at<uint32_t>(workspace, L.qrec), at<int32_t>(workspace, L.bad)};
     return hip_status(dism::launch_records(ra, s), "hard query records");
 }
 

@@ -49,7 +49,7 @@ struct SweepCommon {
 // Partner records (dism_bucket.hip): for each (b,h) and bucket-sorted index t of one side,
 //   word 0: position p, 1: label[p], 2: label[p-1] (0 at p = 0), 3: extra (lse2[p] bits for
 //   query records, 0 for key records), then the readout row (R elements of T) and the value
-//   row (DV elements of T) as raw 32-bit words; stride rounded up to 16 words.
+//   row (DV elements of T) as raw 32-bit words; stride rounded up to 4 words.
 struct RecordArgs {
     int B, H, n;
     const int32_t* pos;    // [B*H*N] bucket-sorted positions of the side
@@ -58,7 +58,9 @@ struct RecordArgs {
     const void* vrow;      // [B,N,H,DV] value rows (v for keys, dO for queries)
     const float* extra;    // [B,H,N] or null
     int rw, vw, stride;    // words of readout row, value row, record stride
+    int dtype;             // element type of the rows (non-finite check)
     uint32_t* rec;
+    int32_t* bad;          // [B*H] raised when a copied row holds a non-finite value
 };
 
 struct ForwardArgs {
