@@ -18,7 +18,7 @@ LIB = os.path.join(HERE, "libdism_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("DISM_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["dism_aux.hip", "dism_bucket.hip", "dism_forward.hip", "dism_backward.hip",
+SOURCES = ["dism_aux.hip", "dism_sort.hip", "dism_pairs.hip", "dism_scan.hip",
            "dism_capi.cpp"]
 
 FLAGS = [

@@ -122,30 +122,48 @@ __global__ __launch_bounds__(256) void chunk_kernel(const int32_t* __restrict__ 
 // "blocks of TAU_BLOCK consecutive (b, i) rows summed sequentially in double, then block
 // sums added sequentially in double", one workgroup per head.
 constexpr int TAU_BLOCK = 256;
-__global__ __launch_bounds__(256) void tau_reduce_kernel(const float* __restrict__ rowtau,
-                                                         int B, int H, long n,
-                                                         float* __restrict__ dtau) {
-    __shared__ double part[256];
-    int h = blockIdx.x;
-    long total = (long)B * n;
-    long blocks = (total + TAU_BLOCK - 1) / TAU_BLOCK;
+constexpr int TAU_GROUP = 64;          // blocks staged in LDS per round
+constexpr int TAU_THREADS = 1024;
+__global__ __launch_bounds__(TAU_THREADS) void tau_reduce_kernel(const float* __restrict__ rowtau,
+                                                                 int B, int H, long n,
+                                                                 float* __restrict__ dtau) {
+    // Stage TAU_GROUP blocks with coalesced loads (row pitch TAU_BLOCK + 1 words keeps the
+    // per-block sequential reads below free of bank conflicts), then one lane per block sums
+    // its block in order; lane 0 adds the block sums in order.
+    __shared__ float tile[TAU_GROUP * (TAU_BLOCK + 1)];
+    __shared__ double part[TAU_GROUP];
+    const int h = blockIdx.x;
+    const long total = (long)B * n;
+    const long blocks = (total + TAU_BLOCK - 1) / TAU_BLOCK;
     double outer = 0.0;
-    for (long base = 0; base < blocks; base += 256) {
-        long blk = base + threadIdx.x;
-        double inner = 0.0;
-        if (blk < blocks) {
-            for (long x = blk * TAU_BLOCK; x < blk * TAU_BLOCK + TAU_BLOCK && x < total; ++x) {
-                long b = x / n, i = x % n;
-                inner += (double)rowtau[((long)b * H + h) * n + i];
+    for (long base = 0; base < blocks; base += TAU_GROUP) {
+        const long x0 = base * TAU_BLOCK;
+        for (int e = threadIdx.x; e < TAU_GROUP * TAU_BLOCK; e += TAU_THREADS) {
+            const long x = x0 + e;
+            float v = 0.0f;
+            if (x < total) {
+                const long b = x / n, i = x - b * n;
+                v = rowtau[(b * H + h) * n + i];
             }
+            tile[(e / TAU_BLOCK) * (TAU_BLOCK + 1) + (e % TAU_BLOCK)] = v;
         }
-        part[threadIdx.x] = inner;
+        __syncthreads();
+        if (threadIdx.x < TAU_GROUP) {
+            const long blk = base + threadIdx.x;
+            double inner = 0.0;
+            if (blk < blocks) {
+                const long cnt = total - blk * TAU_BLOCK < TAU_BLOCK ? total - blk * TAU_BLOCK
+                                                                       : TAU_BLOCK;
+                const float* row = tile + threadIdx.x * (TAU_BLOCK + 1);
+                for (long u = 0; u < cnt; ++u) inner += (double)row[u];
+            }
+            part[threadIdx.x] = inner;
+        }
         __syncthreads();
         if (threadIdx.x == 0) {
-            long cnt = blocks - base < 256 ? blocks - base : 256;
+            const long cnt = blocks - base < TAU_GROUP ? blocks - base : TAU_GROUP;
             for (long u = 0; u < cnt; ++u) outer += part[u];
         }
-        __syncthreads();
     }
     if (threadIdx.x == 0) dtau[h] = (float)outer;
 }
@@ -207,7 +225,7 @@ hipError_t launch_fill_i32(int32_t* p, long count, int32_t value, hipStream_t s)
 
 hipError_t launch_tau_reduce(const float* rowtau, int B, int H, long n, float* dtau,
                              hipStream_t s) {
-    hipLaunchKernelGGL(tau_reduce_kernel, dim3((unsigned)H), dim3(256), 0, s, rowtau, B, H, n,
+    hipLaunchKernelGGL(tau_reduce_kernel, dim3((unsigned)H), dim3(TAU_THREADS), 0, s, rowtau, B, H, n,
                        dtau);
     return hipGetLastError();
 }

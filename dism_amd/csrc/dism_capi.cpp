@@ -36,46 +36,52 @@ int32_t hip_status(hipError_t e, const char* what) {
 }
 
 bool dims_ok(int64_t B, int64_t N, int64_t H) {
-    return B > 0 && H > 0 && N > 0 && N <= INT_MAX / 64 && B * H <= 65535 &&
-           B * H * ((N + 63) / 64 + dism::BUCKETS) * 2 <= INT_MAX;
+    return B > 0 && H > 0 && N > 0 && N <= INT_MAX / 64 && B * H <= 65535;
 }
 bool rdv_ok(int32_t R, int32_t DV) {
     return (R == 2 || R == 4 || R == 8 || R == 16 || R == 32) &&
            (DV == 32 || DV == 64 || DV == 128);
 }
 bool dtype_ok(int32_t d) { return d == DISM_BF16 || d == DISM_F32; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-int words_of(int32_t dtype, int64_t n) { return dtype == DISM_BF16 ? (int)((n + 1) / 2) : (int)n; }
-
 // Workspace layout (each section 256-byte aligned).
+//   orders: label order and bigram order of both sides (dism_sort.hip) + sort scratch
+//   pnb/prow: per query row bigram-pair count and record (layout: dism_launch.h)
 struct Layout {
-    int64_t qpos, kpos, qoff, koff, qcs, kcs, bad, krec, qrec, total;
-    int stride;
+    int64_t corder, clab, ctab, bpos[2], blab[2], bplab[2], btab[2], shift, tmp[3];
+    int64_t pnb, prow, total;
+    int prow_stride;
 };
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
-Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV, int32_t dtype) {
+Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     Layout L;
     const int64_t BH = B * H;
-    const int raw = 4 + words_of(dtype, R) + words_of(dtype, DV);
-    L.stride = (raw + 3) / 4 * 4;
+    L.prow_stride = (DV + dism::PREC_Y > R + 4 ? DV + dism::PREC_Y : R + 4);
     int64_t o = 0;
     auto take = [&](int64_t bytes) {
-        int64_t at = o;
+        int64_t a = o;
         o += align256(bytes);
-        return at;
+        return a;
     };
-    L.qpos = take(BH * N * 4);
-    L.kpos = take(BH * N * 4);
-    L.qoff = take(BH * (dism::BUCKETS + 1) * 4);
-    L.koff = take(BH * (dism::BUCKETS + 1) * 4);
-    L.qcs = take(BH * (dism::BUCKETS + 1) * 4);
-    L.kcs = take(BH * (dism::BUCKETS + 1) * 4);
-    L.bad = take(BH * 4);
-    L.krec = take(BH * N * L.stride * 4);
-    L.qrec = take(BH * N * L.stride * 4);
+    L.corder = take(BH * 2 * N * 4);
+    L.clab = take(BH * 2 * N * 4);
+    L.ctab = take(BH * 257 * 4);
+    for (int s = 0; s < 2; ++s) {
+        L.bpos[s] = take(BH * N * 4);
+        L.blab[s] = take(BH * N * 4);
+        L.bplab[s] = take(BH * N * 4);
+        L.btab[s] = take(BH * 257 * 4);
+    }
+    L.shift = take(BH * 4);
+    L.tmp[0] = take(BH * 2 * N * 4);
+    L.tmp[1] = take(BH * N * 4);
+    L.tmp[2] = take(BH * N * 4);
+    L.pnb = take(BH * N * 4);
+    L.prow = take(BH * N * L.prow_stride * 4);
     L.total = o;
     return L;
 }
@@ -85,32 +91,41 @@ P* at(void* ws, int64_t off) {
     return reinterpret_cast<P*>(reinterpret_cast<char*>(ws) + off);
 }
 
-dism::SweepCommon common(const Layout& L, void* ws, int64_t B, int64_t N, int64_t H,
-                         const int32_t* iq, const int32_t* ik, const uint8_t* hard,
-                         const int32_t* boundary, int32_t strip, const float* lut,
-                         int64_t lut_stride, bool key_records) {
-    dism::SweepCommon c;
-    c.B = (int)B;
-    c.H = (int)H;
-    c.n = (int)N;
-    c.iq = iq;
-    c.ik = ik;
-    c.hard = hard;
-    c.bound = boundary;
-    c.strip = boundary ? strip : 0;
-    c.lut = lut;
-    c.lut_stride = lut_stride;
-    c.qpos = at<int32_t>(ws, L.qpos);
-    c.kpos = at<int32_t>(ws, L.kpos);
-    c.qoff = at<int32_t>(ws, L.qoff);
-    c.koff = at<int32_t>(ws, L.koff);
-    c.qcs = at<int32_t>(ws, L.qcs);
-    c.kcs = at<int32_t>(ws, L.kcs);
-    c.bad = at<int32_t>(ws, L.bad);
-    c.slots = (int)((N + 63) / 64 + dism::BUCKETS);
-    c.prec = at<uint32_t>(ws, key_records ? L.krec : L.qrec);
-    c.pstride = L.stride;
-    return c;
+dism::Orders orders(const Layout& L, void* ws) {
+    dism::Orders o;
+    o.corder = at<int32_t>(ws, L.corder);
+    o.clab = at<int32_t>(ws, L.clab);
+    o.ctab = at<int32_t>(ws, L.ctab);
+    for (int s = 0; s < 2; ++s) {
+        o.bpos[s] = at<int32_t>(ws, L.bpos[s]);
+        o.blab[s] = at<int32_t>(ws, L.blab[s]);
+        o.bplab[s] = at<int32_t>(ws, L.bplab[s]);
+        o.btab[s] = at<int32_t>(ws, L.btab[s]);
+    }
+    o.shift = at<int32_t>(ws, L.shift);
+    return o;
+}
+
+dism::PathArgs path(const Layout& L, void* ws, int64_t B, int64_t N, int64_t H,
+                    const int32_t* iq, const int32_t* ik, const uint8_t* hard,
+                    const int32_t* boundary, int32_t strip, const float* lut,
+                    int64_t lut_stride) {
+    dism::PathArgs a{};
+    a.B = (int)B;
+    a.H = (int)H;
+    a.n = (int)N;
+    a.iq = iq;
+    a.ik = ik;
+    a.hard = hard;
+    a.lut = lut;
+    a.lut_stride = lut_stride;
+    a.bound = boundary;
+    a.strip = boundary ? strip : 1;
+    a.o = orders(L, ws);
+    a.pnb = at<int32_t>(ws, L.pnb);
+    a.prow = at<float>(ws, L.prow);
+    a.prow_stride = L.prow_stride;
+    return a;
 }
 
 int32_t check_common(const void* sq, const void* sk, const void* v, int32_t dtype,
@@ -123,7 +138,9 @@ int32_t check_common(const void* sq, const void* sk, const void* v, int32_t dtyp
         return fail(DISM_ERR_UNSUPPORTED, "%s: unsupported R=%d DV=%d", what, R, DV);
     if (!dtype_ok(dtype))
         return fail(DISM_ERR_UNSUPPORTED, "%s: vector dtype must be bf16 or f32", what);
-    if (ws_bytes < layout(B, N, H, R, DV, dtype).total)
+    if (!aligned16(sq) || !aligned16(sk) || !aligned16(v))
+        return fail(DISM_ERR_INVALID, "%s: vector tensors must be 16-byte aligned", what);
+    if (ws_bytes < layout(B, N, H, R, DV).total)
         return fail(DISM_ERR_INVALID, "%s: workspace too small", what);
     return DISM_OK;
 }
@@ -133,7 +150,7 @@ int32_t check_common(const void* sq, const void* sk, const void* v, int32_t dtyp
 extern "C" {
 
 const char* dism_last_error(void) { return g_error.c_str(); }
-int32_t dism_abi_version(void) { return 2; }
+int32_t dism_abi_version(void) { return 3; }
 
 int32_t dism_sign_labels(const void* x, int32_t dtype, int64_t B, int64_t N, int64_t H, int32_t d,
                          int32_t* labels, void* stream) {
@@ -201,7 +218,7 @@ int32_t dism_hard_boundary(const int32_t* iq, const int32_t* ik, const uint8_t* 
 int64_t dism_hard_workspace_bytes(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
                                   int32_t dtype) {
     if (!dims_ok(B, N, H) || !rdv_ok(R, DV) || !dtype_ok(dtype)) return -1;
-    return layout(B, N, H, R, DV, dtype).total;
+    return layout(B, N, H, R, DV).total;
 }
 
 int32_t dism_hard_prepare(const void* sq, const void* sk, const void* v, int32_t dtype,
@@ -211,19 +228,15 @@ int32_t dism_hard_prepare(const void* sq, const void* sk, const void* v, int32_t
     int32_t st = check_common(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
                               workspace_bytes, "hard prepare");
     if (st) return st;
-    const Layout L = layout(B, N, H, R, DV, dtype);
-    hipStream_t s = S(stream);
-    dism::BucketArgs ba{iq, ik, B * H, (int)N, at<int32_t>(workspace, L.qpos),
-                        at<int32_t>(workspace, L.kpos), at<int32_t>(workspace, L.qoff),
-                        at<int32_t>(workspace, L.koff), at<int32_t>(workspace, L.qcs),
-                        at<int32_t>(workspace, L.kcs)};
-    if ((st = hip_status(dism::launch_buckets(ba, s), "hard buckets"))) return st;
-    int32_t* bad = at<int32_t>(workspace, L.bad);
-    if ((st = hip_status(dism::launch_fill_i32(bad, B * H, 0, s), "hard flags"))) return st;
-    dism::RecordArgs ra{(int)B, (int)H, (int)N, at<int32_t>(workspace, L.kpos), ik, sk, v,
-                        nullptr, words_of(dtype, R), words_of(dtype, DV), L.stride, dtype,
-                        at<uint32_t>(workspace, L.krec), bad};
-    return hip_status(dism::launch_records(ra, s), "hard key records");
+    const Layout L = layout(B, N, H, R, DV);
+    dism::SortArgs sa{};
+    sa.lab[0] = iq;
+    sa.lab[1] = ik;
+    sa.BH = B * H;
+    sa.n = (int)N;
+    for (int t = 0; t < 3; ++t) sa.tmp[t] = at<int32_t>(workspace, L.tmp[t]);
+    sa.o = orders(L, workspace);
+    return hip_status(dism::launch_sort(sa, S(stream)), "hard prepare");
 }
 
 int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t dtype,
@@ -241,9 +254,9 @@ int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t
         return fail(DISM_ERR_UNSUPPORTED, "hard readout: output dtype must be bf16 or f32");
     if (lut_stride < N + 1) return fail(DISM_ERR_INVALID, "hard log-weight table is too short");
     if (boundary && strip < 1) return fail(DISM_ERR_INVALID, "invalid hard boundary strip");
-    const Layout L = layout(B, N, H, R, DV, dtype);
-    dism::ForwardArgs a;
-    a.c = common(L, workspace, B, N, H, iq, ik, hard, boundary, strip, lut, lut_stride, true);
+    if (!aligned16(out)) return fail(DISM_ERR_INVALID, "hard readout: output must be 16-byte aligned");
+    const Layout L = layout(B, N, H, R, DV);
+    dism::PathArgs a = path(L, workspace, B, N, H, iq, ik, hard, boundary, strip, lut, lut_stride);
     a.sq = sq;
     a.sk = sk;
     a.v = v;
@@ -252,7 +265,13 @@ int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t
     a.lse2 = lse2;
     a.lmax = lmax;
     a.jarg = jarg;
-    return hip_status(dism::launch_forward(a, R, DV, dtype, S(stream)), "hard readout");
+    int32_t st2 = hip_status(dism::launch_pairs_stats(a, R, DV, dtype, S(stream)),
+                             "hard readout pairs");
+    if (st2) return st2;
+    if ((st2 = hip_status(dism::launch_scan_forward(a, R, DV, dtype, S(stream)), "hard readout")))
+        return st2;
+    return hip_status(dism::launch_pairs_finish(a, R, DV, dtype, S(stream)),
+                      "hard readout pairs");
 }
 
 }  // extern "C"
@@ -262,22 +281,22 @@ static int32_t backward_common(const void* sq, const void* sk, const void* v, co
                                const uint8_t* hard, const int32_t* boundary, int32_t strip,
                                const float* lut, int64_t lut_stride, const float* lse2,
                                int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
-                               void* workspace, int64_t workspace_bytes, bool key_records,
-                               dism::BackwardArgs* a, const char* what) {
+                               void* workspace, int64_t workspace_bytes, dism::PathArgs* a,
+                               const char* what) {
     int32_t st = check_common(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
                               workspace_bytes, what);
     if (st) return st;
     if (!dout || !hard || !lut || !lse2) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
     if (lut_stride < N + 1) return fail(DISM_ERR_INVALID, "hard log-weight table is too short");
     if (boundary && strip < 1) return fail(DISM_ERR_INVALID, "invalid hard boundary strip");
-    const Layout L = layout(B, N, H, R, DV, dtype);
-    a->c = common(L, workspace, B, N, H, iq, ik, hard, boundary, strip, lut, lut_stride,
-                  key_records);
+    if (!aligned16(dout)) return fail(DISM_ERR_INVALID, "%s: dO must be 16-byte aligned", what);
+    const Layout L = layout(B, N, H, R, DV);
+    *a = path(L, workspace, B, N, H, iq, ik, hard, boundary, strip, lut, lut_stride);
     a->sq = sq;
     a->sk = sk;
     a->v = v;
     a->dout = dout;
-    a->lse2 = lse2;
+    a->lse2 = const_cast<float*>(lse2);
     return DISM_OK;
 }
 
@@ -292,12 +311,8 @@ int32_t dism_hard_backward_prepare(const void* sq, const void* sk, const void* v
                               workspace_bytes, "hard backward prepare");
     if (st) return st;
     if (!dout || !lse2) return fail(DISM_ERR_INVALID, "hard backward prepare: null pointer");
-    const Layout L = layout(B, N, H, R, DV, dtype);
-    hipStream_t s = S(stream);
-    dism::RecordArgs ra{(int)B, (int)H, (int)N, at<int32_t>(workspace, L.qpos), iq, sq, dout,
-                        lse2, words_of(dtype, R), words_of(dtype, DV), L.stride, dtype,
-                        at<uint32_t>(workspace, L.qrec), at<int32_t>(workspace, L.bad)};
-    return hip_status(dism::launch_records(ra, s), "hard query records");
+    (void)stream;
+    return ok();
 }
 
 int32_t dism_hard_backward_queries(const void* sq, const void* sk, const void* v,
@@ -308,17 +323,19 @@ int32_t dism_hard_backward_queries(const void* sq, const void* sk, const void* v
                                    int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
                                    void* workspace, int64_t workspace_bytes, float* dsq,
                                    float* rowtau, void* stream) {
-    dism::BackwardArgs a{};
+    dism::PathArgs a{};
     int32_t st = backward_common(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
                                  lut_stride, lse2, B, N, H, R, DV, workspace, workspace_bytes,
-                                 true, &a, "hard backward queries");
+                                 &a, "hard backward queries");
     if (st) return st;
     if (!dlut || !dsq || !rowtau) return fail(DISM_ERR_INVALID, "hard backward: null pointer");
     a.dlut = dlut;
     a.dsq = dsq;
     a.rowtau = rowtau;
-    return hip_status(dism::launch_backward_rows(a, R, DV, dtype, S(stream)),
-                      "hard backward rows");
+    if ((st = hip_status(dism::launch_pairs_rows(a, R, DV, dtype, S(stream)),
+                         "hard backward row pairs")))
+        return st;
+    return hip_status(dism::launch_scan_rows(a, R, DV, dtype, S(stream)), "hard backward rows");
 }
 
 int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, const void* dout,
@@ -328,16 +345,19 @@ int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, c
                                 int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
                                 void* workspace, int64_t workspace_bytes, float* dsk, float* dv,
                                 void* stream) {
-    dism::BackwardArgs a{};
+    dism::PathArgs a{};
     int32_t st = backward_common(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
                                  lut_stride, lse2, B, N, H, R, DV, workspace, workspace_bytes,
-                                 false, &a, "hard backward keys");
+                                 &a, "hard backward keys");
     if (st) return st;
     if (!dsk || !dv) return fail(DISM_ERR_INVALID, "hard backward: null pointer");
     a.dsk = dsk;
     a.dv = dv;
-    return hip_status(dism::launch_backward_keys(a, R, DV, dtype, S(stream)),
-                      "hard backward keys");
+    if ((st = hip_status(dism::launch_scan_keys(a, R, DV, dtype, S(stream)),
+                         "hard backward keys")))
+        return st;
+    return hip_status(dism::launch_pairs_keys(a, R, DV, dtype, S(stream)),
+                      "hard backward key pairs");
 }
 
 int32_t dism_hard_tau_reduce(const float* rowtau, int64_t B, int64_t H, int64_t N, float* dtau,

@@ -7,86 +7,71 @@
 namespace dism {
 
 enum { DTYPE_BF16 = 0, DTYPE_F32 = 1 };
-constexpr int BUCKETS = 256;          // symbol buckets (label & 255)
-constexpr int CHUNK = 64;             // owners per wave
+constexpr int SCAN_ITEM = 64;   // label-order entries that seed one scan work item
 
-// Label buckets of one call (see dism_bucket.hip).  [BH*N] positions, [BH*(BUCKETS+1)] tables.
-struct BucketArgs {
-    const int32_t* iq;
-    const int32_t* ik;
+// Orders of one call (dism_sort.hip), each (b,h) row at offset bh*N (bh*2N for the
+// combined order):
+//   corder/clab/ctab: the 2N entries e = 2p + s (s = 0 key, 1 query at position p) sorted by
+//                     (label, position, s), their labels, and the runs of the last sorted
+//                     digit, (label >> shift) & 255 ([B*H][257]).
+//   bpos/blab/bplab/btab (side 0 queries, 1 keys): positions sorted by
+//                     (label[p-1], label[p], position), label[-1] := 0, with the runs of
+//                     (label[p-1] >> shift) & 255.
+// The digits come from the union of both sides' labels, so all tables share one digit
+// (for labels below 256 a run is one label).
+struct Orders {
+    int32_t* corder;
+    int32_t* clab;
+    int32_t* ctab;
+    int32_t* bpos[2];
+    int32_t* blab[2];
+    int32_t* bplab[2];
+    int32_t* btab[2];
+    int32_t* shift;       // [B*H]
+};
+
+struct SortArgs {
+    const int32_t* lab[2];  // iq, ik  [B*H*N]
     long BH;
     int n;
-    int32_t* qpos;
-    int32_t* kpos;
-    int32_t* qoff;
-    int32_t* koff;
-    int32_t* qcs;
-    int32_t* kcs;
+    int32_t* tmp[3];        // scratch: [B*H*2N] combined, [B*H*N] per bigram side
+    Orders o;
 };
 
-// Everything the sweep kernels share.
-struct SweepCommon {
+// Per query row record (prow, valid when the row's bigram pair count pnb > 0):
+//   forward:  [m, key count, Lmax, argmax, pair range lo, hi, -, -, y[DV]]
+//   backward: [cdq[R], cu, cvv, cw, cz]
+enum { PREC_M = 0, PREC_CNT = 1, PREC_LB = 2, PREC_JB = 3, PREC_LO = 4, PREC_HI = 5,
+       PREC_Y = 8 };
+
+// Everything the pair and scan kernels of the hard core read or write.
+struct PathArgs {
     int B, H, n;
-    const int32_t* iq;     // [B,H,N]
-    const int32_t* ik;     // [B,H,N]
-    const uint8_t* hard;   // [B*H] sequence flags
-    const int32_t* bound;  // composed boundary [B,H,(N-1)/strip,N] or null
-    int strip;
-    const float* lut;      // [H, lut_stride] log2 weights
+    const int32_t* iq;       // [B,H,N]
+    const int32_t* ik;
+    const uint8_t* hard;     // [B*H]
+    const float* lut;        // [H, lut_stride] log2 weights
+    const float* dlut;       // [H, lut_stride] d ln W / d tau (backward)
     long lut_stride;
-    const int32_t* qpos;   // buckets (dism_bucket.hip)
-    const int32_t* kpos;
-    const int32_t* qoff;
-    const int32_t* koff;
-    const int32_t* qcs;
-    const int32_t* kcs;
-    const int32_t* bad;    // [B*H] non-finite input flags (masked accumulation when set)
-    int slots;             // chunk slots per (b,h): ceil(N/64) + BUCKETS
-    const uint32_t* prec;  // partner records in bucket order, [B*H*N][pstride] words
-    int pstride;
-};
-
-// Partner records (dism_bucket.hip): for each (b,h) and bucket-sorted index t of one side,
-//   word 0: position p, 1: label[p], 2: label[p-1] (0 at p = 0), 3: extra (lse2[p] bits for
-//   query records, 0 for key records), then the readout row (R elements of T) and the value
-//   row (DV elements of T) as raw 32-bit words; stride rounded up to 4 words.
-struct RecordArgs {
-    int B, H, n;
-    const int32_t* pos;    // [B*H*N] bucket-sorted positions of the side
-    const int32_t* lab;    // [B,H,N] labels of the side
-    const void* rrow;      // [B,N,H,R] readout rows (sk for keys, sq for queries)
-    const void* vrow;      // [B,N,H,DV] value rows (v for keys, dO for queries)
-    const float* extra;    // [B,H,N] or null
-    int rw, vw, stride;    // words of readout row, value row, record stride
-    int dtype;             // element type of the rows (non-finite check)
-    uint32_t* rec;
-    int32_t* bad;          // [B*H] raised when a copied row holds a non-finite value
-};
-
-struct ForwardArgs {
-    SweepCommon c;
-    const void* sq;        // [B,N,H,R]  bf16|f32
-    const void* sk;        // [B,N,H,R]
-    const void* v;         // [B,N,H,DV]
-    void* out;             // [B,N,H,DV] bf16 (out_dtype 0) or f32 (1)
-    int out_dtype;
-    float* lse2;           // [B,H,N]
-    int32_t* lmax;         // [B,H,N] longest match length (nullable)
-    int32_t* jarg;         // [B,H,N] key of the longest match, ties -> latest (nullable)
-};
-
-struct BackwardArgs {
-    SweepCommon c;
-    const void* sq;
+    const int32_t* bound;    // composed boundary [B,H,(N-1)/strip,N] or null
+    int strip;
+    Orders o;
+    const void* sq;          // [B,N,H,R]  bf16 | f32
     const void* sk;
-    const void* v;
-    const void* dout;      // [B,N,H,DV]
-    const float* dlut;     // [H, lut_stride] natural-tau derivative of ln W_L
-    const float* lse2;     // [B,H,N] saved log2 normalizer
-    float* dsq;            // [B,N,H,R] fp32
-    float* dsk;            // [B,N,H,R] fp32
-    float* dv;             // [B,N,H,DV] fp32
-    float* rowtau;         // [B,H,N] fp32 per-row tau gradient terms
+    const void* v;           // [B,N,H,DV]
+    const void* dout;        // [B,N,H,DV] (backward)
+    void* out;               // [B,N,H,DV] bf16 (out_dtype 0) or f32 (1)
+    int out_dtype;
+    float* lse2;             // [B,H,N] written by the forward, read by the backward
+    int32_t* lmax;           // [B,H,N] nullable
+    int32_t* jarg;           // [B,H,N] nullable
+    int32_t* pnb;            // [B*H*N] bigram pair count per query row
+    float* prow;             // [B*H*N][prow_stride]
+    int prow_stride;
+    float* dsq;              // [B,N,H,R] fp32
+    float* dsk;
+    float* dv;               // [B,N,H,DV] fp32
+    float* rowtau;           // [B,H,N]
 };
 
 hipError_t launch_sign_labels(const void* x, int dtype, long B, long N, long H, int d,
@@ -101,13 +86,14 @@ hipError_t launch_chunk(const int32_t* summary, int32_t* out, long BH, long C, i
 hipError_t launch_tau_reduce(const float* rowtau, int B, int H, long n, float* dtau,
                              hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, long count, int32_t value, hipStream_t s);
-hipError_t launch_buckets(const BucketArgs& a, hipStream_t s);
-hipError_t launch_records(const RecordArgs& a, hipStream_t s);
-hipError_t launch_nonfinite(const void* x, int dtype, long B, long N, long H, int D,
-                            int32_t* flags, hipStream_t s);
-// return hipErrorInvalidValue for an unsupported (R, DV, dtype)
-hipError_t launch_forward(const ForwardArgs& a, int R, int DV, int dtype, hipStream_t s);
-hipError_t launch_backward_rows(const BackwardArgs& a, int R, int DV, int dtype, hipStream_t s);
-hipError_t launch_backward_keys(const BackwardArgs& a, int R, int DV, int dtype, hipStream_t s);
+hipError_t launch_sort(const SortArgs& a, hipStream_t s);
+// The following return hipErrorInvalidValue for an unsupported (R, DV, dtype).
+hipError_t launch_pairs_stats(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
+hipError_t launch_pairs_finish(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
+hipError_t launch_scan_forward(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
+hipError_t launch_pairs_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
+hipError_t launch_scan_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
+hipError_t launch_pairs_keys(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
+hipError_t launch_scan_keys(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 
 }  // namespace dism

@@ -66,6 +66,8 @@ def lib():
                                   P, i32]
         L.orc_backward.argtypes = [P, P, P, P, P, P, P, P, P, i64, P, i32, i64, i32, i32, i32,
                                    P, P, P, P, i32]
+        L.orc_forward_direct.argtypes = L.orc_forward.argtypes
+        L.orc_backward_direct.argtypes = L.orc_backward.argtypes
         L.orc_tau_reduce.argtypes = [P, i32, i32, i64, i64, P]
         _lib = L
     return _lib
@@ -149,8 +151,11 @@ def suffix_walk(q, k, i, j):
     return lib().orc_suffix_walk(_p(q), _p(k), i, j)
 
 
-def forward(sq, sk, v, iq, ik, hard, lut, threads=0):
-    """CPU model forward.  Returns (O fp32 [B,N,H,DV], lse2 [B,H,N], Lmax, argmax)."""
+def forward(sq, sk, v, iq, ik, hard, lut, threads=0, direct=False):
+    """CPU model forward.  Returns (O fp32 [B,N,H,DV], lse2 [B,H,N], Lmax, argmax).
+
+    direct=False: the decomposed fp32 sequence the HIP kernels reproduce bit for bit;
+    direct=True: the pairwise definition (same mathematics, other fp32 association)."""
     sq, sk, v, lut = _f32(sq), _f32(sk), _f32(v), _f32(lut)
     iq, ik = _i32(iq), _i32(ik)
     B, N, H, R = sq.shape
@@ -159,14 +164,17 @@ def forward(sq, sk, v, iq, ik, hard, lut, threads=0):
     lse2 = np.empty((B, H, N), dtype=np.float32)
     lmax = np.empty((B, H, N), dtype=np.int32)
     jarg = np.empty((B, H, N), dtype=np.int32)
-    lib().orc_forward(_p(sq), _p(sk), _p(v), _p(iq), _p(ik), _p(_flags(hard)), _p(lut),
+    fn = lib().orc_forward_direct if direct else lib().orc_forward
+    fn(_p(sq), _p(sk), _p(v), _p(iq), _p(ik), _p(_flags(hard)), _p(lut),
                       lut.shape[1], B, N, H, R, DV, _p(out), _p(lse2), _p(lmax), _p(jarg),
                       threads)
     return out, lse2, lmax, jarg
 
 
-def backward(sq, sk, v, dout, iq, ik, hard, lut, dlut, lse2, threads=0, block=256):
-    """CPU model backward.  Returns (dSQ, dSK, dV fp32, dtau [H], rowtau [B,H,N])."""
+def backward(sq, sk, v, dout, iq, ik, hard, lut, dlut, lse2, threads=0, block=256,
+             direct=False):
+    """CPU model backward.  Returns (dSQ, dSK, dV fp32, dtau [H], rowtau [B,H,N]).
+    `direct` as in forward()."""
     sq, sk, v, dout, lut, dlut, lse2 = map(_f32, (sq, sk, v, dout, lut, dlut, lse2))
     iq, ik = _i32(iq), _i32(ik)
     B, N, H, R = sq.shape
@@ -175,7 +183,8 @@ def backward(sq, sk, v, dout, iq, ik, hard, lut, dlut, lse2, threads=0, block=25
     dsk = np.empty_like(sk)
     dv = np.empty_like(v)
     rowtau = np.empty((B, H, N), dtype=np.float32)
-    lib().orc_backward(_p(sq), _p(sk), _p(v), _p(dout), _p(iq), _p(ik), _p(_flags(hard)),
+    fn = lib().orc_backward_direct if direct else lib().orc_backward
+    fn(_p(sq), _p(sk), _p(v), _p(dout), _p(iq), _p(ik), _p(_flags(hard)),
                        _p(lut), _p(dlut), lut.shape[1], _p(lse2), B, N, H, R, DV, _p(dsq),
                        _p(dsk), _p(dv), _p(rowtau), threads)
     dtau = np.empty(H, dtype=np.float32)

@@ -27,6 +27,7 @@
  *
  * Parity pinning of each function is listed in tests/test_oracle.py.
  */
+#define _GNU_SOURCE
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -277,7 +278,7 @@ long orc_suffix_walk(const int32_t* q, const int32_t* k, long i, long j) {
  *   out = acc/den, lse2 = m + log2(den).
  * This is the reference's online-max readout (readout.cuh:16-61) with the final maximum
  * applied from the start; the unit fallback contributes exp2(0 - m). */
-void orc_forward(const float* sq, const float* sk, const float* v, const int32_t* iq,
+void orc_forward_direct(const float* sq, const float* sk, const float* v, const int32_t* iq,
                  const int32_t* ik, const uint8_t* hard, const float* lut, long lut_stride,
                  int B, long N, int H, int R, int DV, float* out, float* lse2, int32_t* lmax,
                  int32_t* jarg, int threads) {
@@ -350,7 +351,7 @@ void orc_forward(const float* sq, const float* sk, const float* v, const int32_t
  *   u += pse; vv = fma(p,g,vv); w = fma(pse,g,w); z += p
  *   rowtau_i = (w - u*((vv - f c)/(z+f)))/(z+f),  f = exp2(-lse2_i), c = G[i+1]
  * dtau_h = sum over (b,i) of rowtau in the fixed blocked order of orc_tau_reduce. */
-void orc_backward(const float* sq, const float* sk, const float* v, const float* dout,
+void orc_backward_direct(const float* sq, const float* sk, const float* v, const float* dout,
                   const int32_t* iq, const int32_t* ik, const uint8_t* hard, const float* lut,
                   const float* dlut, long lut_stride, const float* lse2in, int B, long N, int H,
                   int R, int DV, float* dsq, float* dsk, float* dv, float* rowtau, int threads) {
@@ -436,5 +437,360 @@ void orc_tau_reduce(const float* rowtau, int B, int H, long N, long block, float
             outer += inner;
         }
         dtau[h] = (float)outer;
+    }
+}
+
+/* ======================================================================================
+ * Decomposed definition (the one the HIP kernels compute bit for bit).
+ *
+ * Split of the valid pairs of a row i (keys j <= i with iq[i] == ik[j]):
+ *   - every valid pair is first counted as a length-1 pair with weight p1 = exp2(LUT[1]-m);
+ *   - a "bigram" pair (i >= 1, j >= 1, iq[i-1] == ik[j-1]) is exactly a pair with L >= 2;
+ *     it adds the correction (p - p1).
+ * The length-1 part factorises through the per-label prefix matrix
+ *   M_i[r][d] = sum over valid keys j of sk_j[r] * v_j[d]   (fma chain, ascending j)
+ * and the key-side suffix matrix
+ *   N_j[r][d] = sum over valid queries i of (p1_i * sq_i[r]) * dO_i[d]   (descending i).
+ * Mathematically this equals the direct sums (orc_forward_direct / orc_backward_direct);
+ * only the fp32 association differs.
+ * ====================================================================================== */
+
+static int cmp_lab_pos(const void* a, const void* b, void* ctx) {
+    const int32_t* lab = (const int32_t*)ctx;
+    int32_t x = *(const int32_t*)a, y = *(const int32_t*)b;
+    uint32_t lx = (uint32_t)lab[x], ly = (uint32_t)lab[y];
+    if (lx != ly) return lx < ly ? -1 : 1;
+    return x < y ? -1 : (x > y);
+}
+
+/* positions 0..N-1 ordered by (unsigned label, position) */
+static void sort_by_label(const int32_t* lab, long N, int32_t* out) {
+    for (long x = 0; x < N; ++x) out[x] = (int32_t)x;
+    qsort_r(out, (size_t)N, sizeof(int32_t), cmp_lab_pos, (void*)lab);
+}
+
+/* Row-group reduction of sum_d a[d]*b[d] over DV columns for readout width R: the columns
+ * are cut into G = 64/R consecutive groups of VPL = DV/G; each group is an fma chain in
+ * ascending d, then the G partials are added as a pairwise tree ((t0 + t1) + (t2 + t3)) + ...
+ * This is the order of the HIP row-group lane layout (lane = r*G + g) with in-row DPP adds. */
+static float rg_reduce(const float* a, const float* b, int DV, int R) {
+    float t[64];
+    const int G = 64 / R, V = DV / G;
+    for (int g = 0; g < G; ++g) {
+        float s = 0.0f;
+        for (int x = 0; x < V; ++x) s = fmaf(a[g * V + x], b[g * V + x], s);
+        t[g] = s;
+    }
+    for (int sz = 1; sz < G; sz *= 2)
+        for (int g = 0; g < G; g += 2 * sz) t[g] = t[g] + t[g + sz];
+    return t[0];
+}
+
+static float dot_chain(const float* a, const float* b, int n) {
+    float s = 0.0f;
+    for (int r = 0; r < n; ++r) s = fmaf(a[r], b[r], s);
+    return s;
+}
+
+/* lower bound of label value x in positions `ord` sorted by label */
+static long label_lb(const int32_t* lab, const int32_t* ord, long N, uint32_t x) {
+    long lo = 0, hi = N;
+    while (lo < hi) {
+        long mid = (lo + hi) / 2;
+        if ((uint32_t)lab[ord[mid]] < x) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+}
+
+/* Forward, per row i of a hard (b,h):
+ *   cnt = #valid keys, last = largest valid key; pairs P = bigram pairs, ascending j, with
+ *   L = suffix walk (>= 2);
+ *   m = 0; if cnt>0 && LUT[1] > m: m = LUT[1]; for j in P: if LUT[L] > m: m = LUT[L]
+ *   Lmax/jarg: P nonempty -> max L, ties to the largest j; else cnt>0 -> (1, last); else (0,-1)
+ *   p1 = exp2(LUT[1]-m)
+ *   for j in P: p = exp2(LUT[L]-m); dp = dp + p; s = chain(sq_i.sk_j); c = (p-p1)*s;
+ *               corr[d] = fma(c, v_j[d], corr[d])
+ *   den = (exp2(-m) + (float)(cnt - |P|) * p1) + dp
+ *   y[d] = chain_r fma(sq_i[r], M_i[r][d])
+ *   out[d] = fma(p1, y[d], corr[d]) * (1/den);  lse2 = m + log2(den). */
+void orc_forward(const float* sq, const float* sk, const float* v, const int32_t* iq,
+                 const int32_t* ik, const uint8_t* hard, const float* lut, long lut_stride,
+                 int B, long N, int H, int R, int DV, float* out, float* lse2, int32_t* lmax,
+                 int32_t* jarg, int threads) {
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 1)
+#endif
+    for (int bh = 0; bh < B * H; ++bh) {
+        const int b = bh / H, h = bh % H;
+        const int32_t* q = iq + (long)bh * N;
+        const int32_t* k = ik + (long)bh * N;
+        const float* tab = lut + (long)h * lut_stride;
+        if (!hard[bh]) {
+            for (long i = 0; i < N; ++i) {
+                long row = ((long)b * N + i) * H + h;
+                for (int d = 0; d < DV; ++d) out[row * DV + d] = 0.0f;
+                lse2[(long)bh * N + i] = 0.0f;
+                if (lmax) lmax[(long)bh * N + i] = 0;
+                if (jarg) jarg[(long)bh * N + i] = -1;
+            }
+            continue;
+        }
+        int32_t* qo = (int32_t*)malloc(sizeof(int32_t) * (size_t)N);
+        int32_t* ko = (int32_t*)malloc(sizeof(int32_t) * (size_t)N);
+        int32_t* pj = (int32_t*)malloc(sizeof(int32_t) * (size_t)N);
+        int32_t* pl = (int32_t*)malloc(sizeof(int32_t) * (size_t)N);
+        float* M = (float*)malloc(sizeof(float) * (size_t)R * DV);
+        float* corr = (float*)malloc(sizeof(float) * (size_t)DV);
+        sort_by_label(q, N, qo);
+        sort_by_label(k, N, ko);
+        const float lut1 = tab[1];
+        long t = 0;
+        while (t < N) {
+            const uint32_t lbl = (uint32_t)q[qo[t]];
+            long te = t;
+            while (te < N && (uint32_t)q[qo[te]] == lbl) ++te;
+            const long kb = label_lb(k, ko, N, lbl);
+            long ke = kb;
+            while (ke < N && (uint32_t)k[ko[ke]] == lbl) ++ke;
+            for (long e = 0; e < (long)R * DV; ++e) M[e] = 0.0f;
+            long kc = kb;
+            int cnt = 0, last = -1;
+            for (; t < te; ++t) {
+                const long i = qo[t];
+                while (kc < ke && ko[kc] <= i) {
+                    const long j = ko[kc];
+                    const long krow = ((long)b * N + j) * H + h;
+                    for (int r = 0; r < R; ++r)
+                        for (int d = 0; d < DV; ++d)
+                            M[r * DV + d] = fmaf(sk[krow * R + r], v[krow * DV + d], M[r * DV + d]);
+                    ++cnt;
+                    last = (int)j;
+                    ++kc;
+                }
+                const long row = ((long)b * N + i) * H + h;
+                const float* sqi = sq + row * R;
+                /* bigram pairs among the valid keys, ascending j */
+                int np = 0;
+                if (i >= 1)
+                    for (long x = kb; x < kc; ++x) {
+                        const long j = ko[x];
+                        if (j >= 1 && k[j - 1] == q[i - 1]) {
+                            pj[np] = (int32_t)j;
+                            pl[np] = (int32_t)orc_suffix_walk(q, k, i, j);
+                            ++np;
+                        }
+                    }
+                float m = 0.0f;
+                if (cnt > 0 && lut1 > m) m = lut1;
+                int32_t best = 0, bj = -1;
+                for (int x = 0; x < np; ++x) {
+                    if (tab[pl[x]] > m) m = tab[pl[x]];
+                    if (pl[x] >= best) { best = pl[x]; bj = pj[x]; }
+                }
+                if (np == 0 && cnt > 0) { best = 1; bj = last; }
+                const float p1 = orc_exp2f(lut1 - m);
+                float dp = 0.0f;
+                for (int d = 0; d < DV; ++d) corr[d] = 0.0f;
+                for (int x = 0; x < np; ++x) {
+                    const long krow = ((long)b * N + pj[x]) * H + h;
+                    const float p = orc_exp2f(tab[pl[x]] - m);
+                    dp = dp + p;
+                    const float s = dot_chain(sqi, sk + krow * R, R);
+                    const float c = (p - p1) * s;
+                    for (int d = 0; d < DV; ++d) corr[d] = fmaf(c, v[krow * DV + d], corr[d]);
+                }
+                const float den = (orc_exp2f(-m) + (float)(cnt - np) * p1) + dp;
+                const float rden = 1.0f / den;
+                float* o = out + row * DV;
+                for (int d = 0; d < DV; ++d) {
+                    float y = 0.0f;
+                    for (int r = 0; r < R; ++r) y = fmaf(sqi[r], M[r * DV + d], y);
+                    o[d] = fmaf(p1, y, corr[d]) * rden;
+                }
+                lse2[(long)bh * N + i] = m + orc_log2f(den);
+                if (lmax) lmax[(long)bh * N + i] = best;
+                if (jarg) jarg[(long)bh * N + i] = bj;
+            }
+        }
+        free(qo); free(ko); free(pj); free(pl); free(M); free(corr);
+    }
+}
+
+/* Backward.  Per row i (l2 = lse2_i, c = G[i+1], G the dlog table):
+ *   P1 = exp2(LUT[1]-l2); g1 = G[1]-c; q1 = P1*g1
+ *   zq[r] = rg_reduce(dO_i, M_i[r]);  se0 = chain_r fma(sq_i[r], zq[r])
+ *   for j in P (ascending): p = exp2(LUT[L]-l2); dp = p-P1; s = chain(sq_i.sk_j);
+ *       e = chain(dO_i.v_j); g = G[L]-c; a = p*g - q1; de = dp*e; ds = dp*s;
+ *       cdq[r] = fma(de, sk_j[r], cdq[r]); cu = fma(ds, e, cu); cvv = cvv + a;
+ *       cw = fma(a, s*e, cw); cz = cz + dp
+ *   dsq[r] = fma(P1, zq[r], cdq[r]); u = fma(P1, se0, cu); vv = fma(cnt, q1, cvv);
+ *   w = fma(q1, se0, cw); z = fma(cnt, P1, cz)
+ *   f = exp2(-l2); mass = z+f; mean = fma(-f, c, vv)/mass; rowtau = fma(-u, mean, w)/mass
+ * Per key j (valid queries i >= j of the same label):
+ *   N_j[r][d] = fma chain over valid queries, DESCENDING i, of (P1_i*sq_i[r]) * dO_i[d]
+ *   dv0[d] = chain_r fma(sk_j[r], N[r][d]);  dsk0[r] = rg_reduce(N[r], v_j)
+ *   for bigram queries i of j (ascending i): p = exp2(LUT[L]-l2_i); dp = p - P1_i;
+ *       s = chain(sq_i.sk_j); e = chain(dO_i.v_j); cdk[r] = fma(dp*e, sq_i[r], cdk[r]);
+ *       cdv[d] = fma(dp*s, dO_i[d], cdv[d])
+ *   dsk[r] = dsk0[r] + cdk[r];  dv[d] = dv0[d] + cdv[d]  (only for keys with bigram pairs). */
+void orc_backward(const float* sq, const float* sk, const float* v, const float* dout,
+                  const int32_t* iq, const int32_t* ik, const uint8_t* hard, const float* lut,
+                  const float* dlut, long lut_stride, const float* lse2in, int B, long N, int H,
+                  int R, int DV, float* dsq, float* dsk, float* dv, float* rowtau, int threads) {
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 1)
+#endif
+    for (int bh = 0; bh < B * H; ++bh) {
+        const int b = bh / H, h = bh % H;
+        const int32_t* q = iq + (long)bh * N;
+        const int32_t* k = ik + (long)bh * N;
+        const float* tab = lut + (long)h * lut_stride;
+        const float* gt = dlut + (long)h * lut_stride;
+        const float* l2v = lse2in + (long)bh * N;
+        for (long x = 0; x < N; ++x) {
+            long row = ((long)b * N + x) * H + h;
+            for (int r = 0; r < R; ++r) { dsq[row * R + r] = 0.0f; dsk[row * R + r] = 0.0f; }
+            for (int d = 0; d < DV; ++d) dv[row * DV + d] = 0.0f;
+            rowtau[(long)bh * N + x] = 0.0f;
+        }
+        if (!hard[bh]) continue;
+        int32_t* qo = (int32_t*)malloc(sizeof(int32_t) * (size_t)N);
+        int32_t* ko = (int32_t*)malloc(sizeof(int32_t) * (size_t)N);
+        float* M = (float*)malloc(sizeof(float) * (size_t)R * DV);
+        float* zq = (float*)malloc(sizeof(float) * (size_t)R);
+        float* cd = (float*)malloc(sizeof(float) * (size_t)(R + DV));
+        float* a = (float*)malloc(sizeof(float) * (size_t)R);
+        sort_by_label(q, N, qo);
+        sort_by_label(k, N, ko);
+        const float lut1 = tab[1];
+        /* ---- rows */
+        long t = 0;
+        while (t < N) {
+            const uint32_t lbl = (uint32_t)q[qo[t]];
+            long te = t;
+            while (te < N && (uint32_t)q[qo[te]] == lbl) ++te;
+            const long kb = label_lb(k, ko, N, lbl);
+            long ke = kb;
+            while (ke < N && (uint32_t)k[ko[ke]] == lbl) ++ke;
+            for (long e = 0; e < (long)R * DV; ++e) M[e] = 0.0f;
+            long kc = kb;
+            int cnt = 0;
+            for (; t < te; ++t) {
+                const long i = qo[t];
+                while (kc < ke && ko[kc] <= i) {
+                    const long krow = ((long)b * N + ko[kc]) * H + h;
+                    for (int r = 0; r < R; ++r)
+                        for (int d = 0; d < DV; ++d)
+                            M[r * DV + d] = fmaf(sk[krow * R + r], v[krow * DV + d], M[r * DV + d]);
+                    ++cnt;
+                    ++kc;
+                }
+                const long row = ((long)b * N + i) * H + h;
+                const float* sqi = sq + row * R;
+                const float* doi = dout + row * DV;
+                const float l2 = l2v[i];
+                const float c = gt[i + 1];
+                const float P1 = orc_exp2f(lut1 - l2);
+                const float g1 = gt[1] - c;
+                const float q1 = P1 * g1;
+                for (int r = 0; r < R; ++r) zq[r] = rg_reduce(doi, M + (long)r * DV, DV, R);
+                const float se0 = dot_chain(sqi, zq, R);
+                float cu = 0.0f, cvv = 0.0f, cw = 0.0f, cz = 0.0f;
+                for (int r = 0; r < R; ++r) cd[r] = 0.0f;
+                if (i >= 1)
+                    for (long x = kb; x < kc; ++x) {
+                        const long j = ko[x];
+                        if (!(j >= 1 && k[j - 1] == q[i - 1])) continue;
+                        const long L = orc_suffix_walk(q, k, i, j);
+                        const long krow = ((long)b * N + j) * H + h;
+                        const float* skj = sk + krow * R;
+                        const float p = orc_exp2f(tab[L] - l2);
+                        const float dp = p - P1;
+                        const float s = dot_chain(sqi, skj, R);
+                        const float e = dot_chain(doi, v + krow * DV, DV);
+                        const float g = gt[L] - c;
+                        const float av = p * g - q1;
+                        const float de = dp * e, ds = dp * s;
+                        for (int r = 0; r < R; ++r) cd[r] = fmaf(de, skj[r], cd[r]);
+                        cu = fmaf(ds, e, cu);
+                        cvv = cvv + av;
+                        cw = fmaf(av, s * e, cw);
+                        cz = cz + dp;
+                    }
+                for (int r = 0; r < R; ++r) dsq[row * R + r] = fmaf(P1, zq[r], cd[r]);
+                const float fc = (float)cnt;
+                const float u = fmaf(P1, se0, cu);
+                const float vv = fmaf(fc, q1, cvv);
+                const float w = fmaf(q1, se0, cw);
+                const float z = fmaf(fc, P1, cz);
+                const float f = orc_exp2f(-l2);
+                const float mass = z + f;
+                const float mean = fmaf(-f, c, vv) / mass;
+                rowtau[(long)bh * N + i] = fmaf(-u, mean, w) / mass;
+            }
+        }
+        /* ---- keys: descending merge per label */
+        long tk = N - 1;
+        while (tk >= 0) {
+            const uint32_t lbl = (uint32_t)k[ko[tk]];
+            long tb = tk;
+            while (tb >= 0 && (uint32_t)k[ko[tb]] == lbl) --tb;
+            /* queries of this label: [qb, qe) in label order */
+            const long qb = label_lb(q, qo, N, lbl);
+            long qe = qb;
+            while (qe < N && (uint32_t)q[qo[qe]] == lbl) ++qe;
+            for (long e = 0; e < (long)R * DV; ++e) M[e] = 0.0f; /* N matrix */
+            long qc = qe - 1;
+            for (; tk > tb; --tk) {
+                const long j = ko[tk];
+                while (qc >= qb && qo[qc] >= j) {
+                    const long i = qo[qc];
+                    const long row = ((long)b * N + i) * H + h;
+                    const float P1 = orc_exp2f(lut1 - l2v[i]);
+                    for (int r = 0; r < R; ++r) a[r] = P1 * sq[row * R + r];
+                    for (int r = 0; r < R; ++r)
+                        for (int d = 0; d < DV; ++d)
+                            M[r * DV + d] = fmaf(a[r], dout[row * DV + d], M[r * DV + d]);
+                    --qc;
+                }
+                const long krow = ((long)b * N + j) * H + h;
+                const float* skj = sk + krow * R;
+                const float* vj = v + krow * DV;
+                for (int r = 0; r < R + DV; ++r) cd[r] = 0.0f;
+                int npair = 0;
+                if (j >= 1)
+                    for (long x = qc + 1; x < qe; ++x) {
+                        const long i = qo[x];
+                        if (!(i >= 1 && q[i - 1] == k[j - 1])) continue;
+                        const long L = orc_suffix_walk(q, k, i, j);
+                        const long row = ((long)b * N + i) * H + h;
+                        const float* sqi = sq + row * R;
+                        const float* doi = dout + row * DV;
+                        const float l2 = l2v[i];
+                        const float P1 = orc_exp2f(lut1 - l2);
+                        const float p = orc_exp2f(tab[L] - l2);
+                        const float dp = p - P1;
+                        const float s = dot_chain(sqi, skj, R);
+                        const float e = dot_chain(doi, vj, DV);
+                        const float de = dp * e, ds = dp * s;
+                        for (int r = 0; r < R; ++r) cd[r] = fmaf(de, sqi[r], cd[r]);
+                        for (int d = 0; d < DV; ++d) cd[R + d] = fmaf(ds, doi[d], cd[R + d]);
+                        ++npair;
+                    }
+                /* corrections are added only to keys that have bigram pairs */
+                for (int r = 0; r < R; ++r) {
+                    const float base = rg_reduce(M + (long)r * DV, vj, DV, R);
+                    dsk[krow * R + r] = npair ? base + cd[r] : base;
+                }
+                for (int d = 0; d < DV; ++d) {
+                    float y = 0.0f;
+                    for (int r = 0; r < R; ++r) y = fmaf(skj[r], M[r * DV + d], y);
+                    dv[krow * DV + d] = npair ? y + cd[R + d] : y;
+                }
+            }
+        }
+        free(qo); free(ko); free(M); free(zq); free(cd); free(a);
     }
 }
