@@ -51,6 +51,7 @@ hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 //   pnb/prow: per query row bigram-pair count and record (layout: dism_launch.h)
 struct Layout {
     int64_t corder, clab, ctab, bpos[2], blab[2], bplab[2], btab[2], shift, tmp[3];
+    int64_t plo[2], pcnt[2], act[2], nact[2];
     int64_t pnb, prow, total;
     int prow_stride;
 };
@@ -77,6 +78,12 @@ Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
         L.btab[s] = take(BH * 257 * 4);
     }
     L.shift = take(BH * 4);
+    for (int s = 0; s < 2; ++s) {
+        L.plo[s] = take(BH * N * 4);
+        L.pcnt[s] = take(BH * N * 4);
+        L.act[s] = take(BH * N * 4);
+        L.nact[s] = take(BH * 4);
+    }
     L.tmp[0] = take(BH * 2 * N * 4);
     L.tmp[1] = take(BH * N * 4);
     L.tmp[2] = take(BH * N * 4);
@@ -103,6 +110,12 @@ dism::Orders orders(const Layout& L, void* ws) {
         o.btab[s] = at<int32_t>(ws, L.btab[s]);
     }
     o.shift = at<int32_t>(ws, L.shift);
+    for (int s = 0; s < 2; ++s) {
+        o.plo[s] = at<int32_t>(ws, L.plo[s]);
+        o.pcnt[s] = at<int32_t>(ws, L.pcnt[s]);
+        o.act[s] = at<int32_t>(ws, L.act[s]);
+        o.nact[s] = at<int32_t>(ws, L.nact[s]);
+    }
     return o;
 }
 
@@ -236,7 +249,9 @@ int32_t dism_hard_prepare(const void* sq, const void* sk, const void* v, int32_t
     sa.n = (int)N;
     for (int t = 0; t < 3; ++t) sa.tmp[t] = at<int32_t>(workspace, L.tmp[t]);
     sa.o = orders(L, workspace);
-    return hip_status(dism::launch_sort(sa, S(stream)), "hard prepare");
+    if ((st = hip_status(dism::launch_sort(sa, S(stream)), "hard prepare"))) return st;
+    dism::PathArgs pa = path(L, workspace, B, N, H, iq, ik, nullptr, nullptr, 0, nullptr, 0);
+    return hip_status(dism::launch_pair_plan(pa, S(stream)), "hard prepare plan");
 }
 
 int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t dtype,

@@ -28,6 +28,13 @@ struct Orders {
     int32_t* bplab[2];
     int32_t* btab[2];
     int32_t* shift;       // [B*H]
+    // bigram-pair plans (dism_pairs.hip), side 0 query rows, 1 keys, by bigram-order index t:
+    //   plo/pcnt: first partner index in the other side's bigram order and partner count;
+    //   act/nact: indices t with pcnt > 0 (in no particular order) and their count per row.
+    int32_t* plo[2];
+    int32_t* pcnt[2];
+    int32_t* act[2];
+    int32_t* nact[2];     // [B*H]
 };
 
 struct SortArgs {
@@ -88,6 +95,7 @@ hipError_t launch_tau_reduce(const float* rowtau, int B, int H, long n, float* d
 hipError_t launch_fill_i32(int32_t* p, long count, int32_t value, hipStream_t s);
 hipError_t launch_sort(const SortArgs& a, hipStream_t s);
 // The following return hipErrorInvalidValue for an unsupported (R, DV, dtype).
+hipError_t launch_pair_plan(const PathArgs& a, hipStream_t s);
 hipError_t launch_pairs_stats(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_pairs_finish(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_scan_forward(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);

@@ -3,383 +3,543 @@
 // A valid pair (j <= i, iq[i] == ik[j]) has L >= 2 exactly when i, j >= 1 and
 // iq[i-1] == ik[j-1], i.e. when the (previous label, label) bigrams of i and j are equal.
 // Bigram orders (dism_sort.hip) make each bigram group one contiguous, position-ascending
-// range, so the owner of a lane (a query row, or a key) finds its partners with two binary
-// searches and visits only them.  Each pair's length comes from the suffix walk (bounded by
-// the composed carry boundary when one is given).  Random labels give ~1/alphabet^2 of the
-// causal pairs here, so these kernels carry little work next to the label scans.
+// range, so an owner (a query row, or a key) finds its partners with binary searches and
+// visits only them.  Each pair's length comes from the suffix walk (bounded by the composed
+// carry boundary when one is given).
 //
-// Mapping: lane = one owner in bigram order (neighbouring lanes usually share a group, so
-// their partner loads coincide); per-lane loops over the owner's partners.
-// fp32 sequences (repeated by the CPU model):
-//   forward, per row: m = max(0, LUT[1], LUT[L] over pairs); p1 = exp2(LUT[1]-m);
-//     ascending j: p = exp2(LUT[L]-m); dp += p; s = chain(sq.sk); c = (p - p1)*s;
-//     corr[d] = fma(c, v_j[d], corr[d])
+// Mapping (MI355X): a wave takes OWNERS = 16 consecutive owners of a bigram order, four
+// lanes per owner ("slot").  The owners' partner lists are consumed in rounds of CK = 8
+// partners per owner:
+//   phase A  lane = (slot, sub): the round's pairs (two per lane) -- walk, exp2, dot
+//            products -- with the per-pair coefficients and partner readout rows put in LDS;
+//   phase B  lane = (slot, column group): each slot folds its round's pairs into its own
+//            running sums in ascending partner order, all 16 owners at once (value-row
+//            segments are loaded straight from HBM, one 4-pair batch at a time).
+// Long partner lists of one owner take ceil(cnt/8) rounds; owners never wait for each other
+// pair by pair.  The longest-match statistics are order-free maxima (LDS atomics).
+// fp32 sequences (repeated by the CPU model), per owner over its pairs in ascending partner
+// position:
+//   forward rows: m = max(0, LUT[1], LUT[L]); p1 = exp2(LUT[1]-m); p = exp2(LUT[L]-m);
+//     dp = dp + p; s = chain(sq.sk); corr[d] = fma((p - p1)*s, v_j[d], corr[d]);
+//     den = (exp2(-m) + (float)(cnt - nb)*p1) + dp; out[d] = fma(p1, y[d], corr[d]) * (1/den)
 //   backward rows (l2 = lse2_i, cc = G[i+1]): P1 = exp2(LUT[1]-l2); q1 = P1*(G[1]-cc);
-//     ascending j: p = exp2(LUT[L]-l2); dp = p-P1; s, e = chains; g = G[L]-cc;
-//     a = p*g - q1; cdq[r] = fma(dp*e, sk[r], cdq[r]); cu = fma(dp*s, e, cu); cvv += a;
+//     p = exp2(LUT[L]-l2); dp = p-P1; s, e = chains; g = G[L]-cc; a = p*g - q1;
+//     cdq[r] = fma(dp*e, sk[r], cdq[r]); cu = fma(dp*s, e, cu); cvv += a;
 //     cw = fma(a, s*e, cw); cz += dp
-//   backward keys, ascending i: p = exp2(LUT[L]-l2_i); dp = p - exp2(LUT[1]-l2_i);
-//     cdk[r] = fma(dp*e, sq_i[r], cdk[r]); cdv[d] = fma(dp*s, dO_i[d], cdv[d])
+//   backward keys: p = exp2(LUT[L]-l2_i); dp = p - exp2(LUT[1]-l2_i);
+//     cdk[r] = fma(dp*e, sq_i[r], cdk[r]); cdv[d] = fma(dp*s, dO_i[d], cdv[d]);
+//     dsk[r] += cdk[r]; dv[d] += cdv[d].
 #include "dism_path.h"
 
 namespace dism {
 
-constexpr int PAIR_ITEM = 64;
+constexpr int OWNERS = 16;  // owners per wave, 4 lanes each
+constexpr int CK = 8;       // partners per owner per round (2 per lane in phase A)
 
-// Owner lane setup shared by the kernels: the owner's position and its partner range in the
-// other side's bigram order (empty when the owner cannot have pairs).
-struct Owner {
-    int bh, b, h, t, p, lo, hi;
-    long so, row0;
+// Partner range of owner t of side SIDE's bigram order (0: query rows with key partners
+// 1 <= j <= i; 1: keys with query partners i >= j): [lo, lo + cnt) of the other side's
+// bigram order.
+template <int SIDE>
+__device__ __forceinline__ void partner_range(const PathArgs& a, int bh, long so, int t, int p,
+                                              int& lo_out, int& cnt_out) {
+    constexpr int OTHER = 1 - SIDE;
+    int lo = 0, hi = 0;
+    if (p >= 1) {
+        bigram_range(a.o.bplab[OTHER] + so, a.o.blab[OTHER] + so,
+                     a.o.btab[OTHER] + (long)bh * 257, a.o.shift[bh],
+                     (uint32_t)a.o.bplab[SIDE][so + t], (uint32_t)a.o.blab[SIDE][so + t], lo,
+                     hi);
+        const int32_t* ob = a.o.bpos[OTHER] + so;
+        if (SIDE == 0) {
+            if (lo < hi && ob[lo] == 0) ++lo;  // key 0 has no predecessor
+            int l = lo, r = hi;                // keys j <= i
+            while (l < r) {
+                const int mid = (l + r) >> 1;
+                if (ob[mid] <= p) l = mid + 1; else r = mid;
+            }
+            hi = l;
+        } else {
+            int l = lo, r = hi;                // queries i >= j
+            while (l < r) {
+                const int mid = (l + r) >> 1;
+                if (ob[mid] < p) l = mid + 1; else r = mid;
+            }
+            lo = l;
+        }
+    }
+    lo_out = lo;
+    cnt_out = hi - lo;
+}
+
+// Plan kernel: one lane per owner (both sides, grid = 2 * B*H * ceil(N/64) items): partner
+// range, pair count per query row (pnb, by position), and the owners with partners appended
+// to act[side] (one atomic per wave).
+__global__ __launch_bounds__(64 * WAVES) void pair_plan_kernel(PathArgs a) {
+    const int n = a.n, lane = lane_id();
+    const int per = (n + 63) / 64;
+    const int item = xcd_work_item();
+    const int side = item & 1;
+    const int bh = (item >> 1) / per;
+    if (bh >= a.B * a.H) return;
+    const long so = (long)bh * n;
+    const int t = ((item >> 1) - bh * per) * 64 + lane;
+    const bool own = t < n;
+    const int tc = own ? t : n - 1;
+    const int p = a.o.bpos[side][so + tc];
+    int lo = 0, cnt = 0;
+    if (own) {
+        if (side == 0) partner_range<0>(a, bh, so, tc, p, lo, cnt);
+        else partner_range<1>(a, bh, so, tc, p, lo, cnt);
+        a.o.plo[side][so + t] = lo;
+        a.o.pcnt[side][so + t] = cnt;
+        if (side == 0) a.pnb[so + p] = cnt;
+    }
+    const unsigned long long m = __ballot(own && cnt > 0);
+    if (m) {
+        int base = 0;
+        if (lane == 0) base = atomicAdd(&a.o.nact[side][bh], __popcll(m));
+        base = __shfl(base, 0);
+        if (own && cnt > 0) {
+            const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
+            a.o.act[side][so + base + __popcll(m & below)] = t;
+        }
+    }
+}
+
+hipError_t launch_pair_plan(const PathArgs& a, hipStream_t s) {
+    const long items = 2L * ((a.n + 63) / 64) * a.B * a.H;
+    hipLaunchKernelGGL(pair_plan_kernel, dim3(grid_for(items)), dim3(64 * WAVES), 0, s, a);
+    return hipGetLastError();
+}
+
+struct Plan {
+    bool own;    // this lane (< OWNERS) holds an owner
+    int p;       // owner position
+    int lo;      // first partner index in the other side's bigram order
+    int cnt;     // partners
+    int maxcnt;  // wave-uniform maximum of cnt
 };
 
-__device__ __forceinline__ bool pair_owner(const PathArgs& a, int side, int item_per_lane,
-                                           Owner& w) {
-    const int n = a.n;
-    const int per = (n + PAIR_ITEM - 1) / PAIR_ITEM;
-    w.bh = item_per_lane / per;
-    if (w.bh >= a.B * a.H) return false;
-    w.t = (item_per_lane - w.bh * per) * PAIR_ITEM + (int)threadIdx.x;
-    if (w.t >= n) return false;
-    w.b = w.bh / a.H;
-    w.h = w.bh - w.b * a.H;
-    w.so = (long)w.bh * n;
-    w.row0 = (long)w.b * n * a.H + w.h;
-    w.p = a.o.bpos[side][w.so + w.t];
-    w.lo = w.hi = 0;
-    if (a.hard[w.bh] && w.p >= 1) {
-        const int other = 1 - side;
-        bigram_range(a.o.bplab[other] + w.so, a.o.blab[other] + w.so,
-                     a.o.btab[other] + (long)w.bh * 257, a.o.shift[w.bh],
-                     (uint32_t)a.o.bplab[side][w.so + w.t], (uint32_t)a.o.blab[side][w.so + w.t],
-                     w.lo, w.hi);
+struct PairItem {
+    int bh, b, h;
+    long so, row0;
+    int k0;      // first entry of the wave in act[side]
+};
+
+// Work item = (b,h) row and a block of OWNERS entries of its active-owner list; items past
+// the list's end return at once.  grid = B*H * ceil(N/OWNERS) items.
+template <int SIDE>
+__device__ __forceinline__ bool pair_item(const PathArgs& a, PairItem& it, Plan& pl) {
+    const int per = (a.n + OWNERS - 1) / OWNERS;
+    const int item = xcd_work_item();
+    it.bh = item / per;
+    if (it.bh >= a.B * a.H || !a.hard[it.bh]) return false;
+    it.k0 = (item - it.bh * per) * OWNERS;
+    const int na = a.o.nact[SIDE][it.bh];
+    if (it.k0 >= na) return false;
+    it.b = it.bh / a.H;
+    it.h = it.bh - it.b * a.H;
+    it.so = (long)it.bh * a.n;
+    it.row0 = (long)it.b * a.n * a.H + it.h;
+    const int lane = lane_id();
+    pl.own = lane < OWNERS && it.k0 + lane < na;
+    const int t = a.o.act[SIDE][it.so + (pl.own ? it.k0 + lane : it.k0)];
+    pl.p = a.o.bpos[SIDE][it.so + t];
+    pl.lo = a.o.plo[SIDE][it.so + t];
+    pl.cnt = pl.own ? a.o.pcnt[SIDE][it.so + t] : 0;
+    int mx = pl.cnt;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const int v = __shfl_xor(mx, o);
+        mx = v > mx ? v : mx;
     }
+    pl.maxcnt = __builtin_amdgcn_readfirstlane(mx);
     return true;
 }
 
 // ---------------------------------------------------------------------------------------
-// forward, pass 1 per query row: pair count, row shift m, longest match (ties -> largest j),
-// partner range.  grid = BH * ceil(N/64)
+// forward, pass 1 per query row: pair count, row shift m, longest match (ties -> largest j).
 template <typename T, int R, int DV>
-__global__ __launch_bounds__(64) void pairs_stats_kernel(PathArgs a) {
-    Owner w;
-    if (!pair_owner(a, 0, xcd_work_item(), w)) return;
-    const int n = a.n, i = w.p;
-    const int32_t* kb = a.o.bpos[1] + w.so;
-    const int32_t* q = a.iq + w.so;
-    const int32_t* k = a.ik + w.so;
-    const int32_t* bnd = bound_of(a, w.bh);
-    const float* lut = a.lut + (long)w.h * a.lut_stride;
+__global__ __launch_bounds__(64 * WAVES) void pairs_stats_kernel(PathArgs a) {
+    __shared__ unsigned s_m_all[WAVES][OWNERS];
+    __shared__ unsigned long long s_key_all[WAVES][OWNERS];
+    auto& s_m = s_m_all[wave_id()];
+    auto& s_key = s_key_all[wave_id()];
+    PairItem it;
+    Plan pl;
+    if (!pair_item<0>(a, it, pl)) return;
+    const int n = a.n, lane = lane_id();
+    const int32_t* kb = a.o.bpos[1] + it.so;
+    const int32_t* q = a.iq + it.so;
+    const int32_t* k = a.ik + it.so;
+    const int32_t* bnd = bound_of(a, it.bh);
+    const float* lut = a.lut + (long)it.h * a.lut_stride;
     const float lut1 = lut[1];
-    float m = lut1 > 0.0f ? lut1 : 0.0f;
-    int nb = 0, best = 0, bj = -1;
-    int lo = w.lo;
-    while (lo < w.hi && kb[lo] == 0) ++lo;
-    for (int x = lo; x < w.hi; ++x) {
-        const int j = kb[x];
-        if (j > i) break;
-        const int L = match_length(q, k, i, j, bnd, a.strip, n);
-        const float lw = lut[L];
-        m = lw > m ? lw : m;
-        if (L >= best) { best = L; bj = j; }
-        ++nb;
+    const float m0 = lut1 > 0.0f ? lut1 : 0.0f;
+    if (lane < OWNERS) {
+        s_m[lane] = __float_as_uint(m0);
+        s_key[lane] = 0ull;
     }
-    a.pnb[w.so + i] = nb;
-    if (nb == 0) return;
-    float* rec = a.prow + (w.so + i) * a.prow_stride;
-    rec[PREC_M] = m;
-    rec[PREC_LB] = __int_as_float(best);
-    rec[PREC_JB] = __int_as_float(bj);
-    rec[PREC_LO] = __int_as_float(lo);
-    rec[PREC_HI] = __int_as_float(lo + nb);
-}
-
-// ---------------------------------------------------------------------------------------
-// forward, pass 2 for rows with pairs (after the label scan wrote y and the key count):
-//   p1 = exp2(LUT[1]-m); ascending j: p = exp2(LUT[L]-m); dp += p; s = chain(sq.sk);
-//   c = (p - p1)*s; corr[d] = fma(c, v_j[d], corr[d])
-//   den = (exp2(-m) + (float)(cnt - nb)*p1) + dp; out[d] = fma(p1, y[d], corr[d]) * (1/den).
-// grid = BH * ceil(N/64) * (DV/DVB)
-template <typename T, int R, int DV, int DVB>
-__global__ __launch_bounds__(64) void pairs_finish_kernel(PathArgs a) {
-    constexpr int NBLK = DV / DVB;
-    const int item = xcd_work_item();
-    const int blk = item % NBLK;
-    const int n = a.n, lane = threadIdx.x;
-    const int per = (n + PAIR_ITEM - 1) / PAIR_ITEM;
-    const int bh = item / NBLK / per;
-    if (bh >= a.B * a.H) return;
-    const int t = (item / NBLK - bh * per) * PAIR_ITEM + lane;
-    if (t >= n) return;
-    const long so = (long)bh * n;
-    const int i = a.o.bpos[0][so + t];
-    const int nb = a.pnb[so + i];
-    if (nb == 0) return;
-    const int b = bh / a.H, h = bh - b * a.H;
-    const long row0 = (long)b * n * a.H + h;
-    const float* rec = a.prow + (so + i) * a.prow_stride;
-    const float m = rec[PREC_M];
-    const int cnt = __float_as_int(rec[PREC_CNT]);
-    const int lo = __float_as_int(rec[PREC_LO]), hi = __float_as_int(rec[PREC_HI]);
-    const int32_t* kb = a.o.bpos[1] + so;
-    const int32_t* q = a.iq + so;
-    const int32_t* k = a.ik + so;
-    const int32_t* bnd = bound_of(a, bh);
-    const float* lut = a.lut + (long)h * a.lut_stride;
-    float sqr[R];
-    load_row<T, R>(reinterpret_cast<const T*>(a.sq) + (row0 + (long)i * a.H) * R, sqr);
-    const float p1 = exp2_fp32(lut[1] - m);
-    float dp = 0.0f, corr[DVB];
+    const int sl = lane >> 2, sub = lane & 3;
+    const int i = __shfl(pl.p, sl), lo = __shfl(pl.lo, sl), cnt = __shfl(pl.cnt, sl);
+    for (int c = 0; c < pl.maxcnt; c += CK) {
 #pragma unroll
-    for (int d = 0; d < DVB; ++d) corr[d] = 0.0f;
-    const T* sk = reinterpret_cast<const T*>(a.sk);
-    const T* v = reinterpret_cast<const T*>(a.v);
-    for (int x = lo; x < hi; ++x) {
-        const int j = kb[x];
-        const int L = match_length(q, k, i, j, bnd, a.strip, n);
-        const float p = exp2_fp32(lut[L] - m);
-        dp = dp + p;
-        float skr[R];
-        const long kr = row0 + (long)j * a.H;
-        load_row<T, R>(sk + kr * R, skr);
-        float s = 0.0f;
-#pragma unroll
-        for (int r = 0; r < R; ++r) s = __builtin_fmaf(sqr[r], skr[r], s);
-        const float c = (p - p1) * s;
-        float vr[DVB];
-        load_row<T, DVB>(v + kr * DV + blk * DVB, vr);
-#pragma unroll
-        for (int d = 0; d < DVB; ++d) corr[d] = __builtin_fmaf(c, vr[d], corr[d]);
-    }
-    const float den = (exp2_fp32(-m) + (float)(cnt - nb) * p1) + dp;
-    const float rden = 1.0f / den;
-    const long orow = row0 + (long)i * a.H;
-    const float* y = rec + PREC_Y + blk * DVB;
-    if (a.out_dtype == DTYPE_F32) {
-        float* o = reinterpret_cast<float*>(a.out) + orow * DV + blk * DVB;
-#pragma unroll
-        for (int d = 0; d < DVB; ++d) o[d] = __builtin_fmaf(p1, y[d], corr[d]) * rden;
-    } else {
-        uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + orow * DV + blk * DVB;
-#pragma unroll
-        for (int d = 0; d < DVB; d += 2) {
-            const uint32_t lo16 = f32_to_bf16_bits(__builtin_fmaf(p1, y[d], corr[d]) * rden);
-            const uint32_t hi16 = f32_to_bf16_bits(__builtin_fmaf(p1, y[d + 1], corr[d + 1]) * rden);
-            reinterpret_cast<uint32_t*>(o)[d / 2] = lo16 | (hi16 << 16);
+        for (int u = 0; u < 2; ++u) {
+            const int kq = c + sub + 4 * u;
+            if (kq < cnt) {
+                const int j = kb[lo + kq];
+                const int L = match_length(q, k, i, j, bnd, a.strip, n);
+                const float lw = lut[L];
+                if (lw > m0) atomicMax(&s_m[sl], __float_as_uint(lw));
+                atomicMax(&s_key[sl], ((unsigned long long)(unsigned)L << 32) | (unsigned)j);
+            }
         }
     }
-    if (blk == 0) {
-        a.lse2[so + i] = m + log2_fp32(den);
-        if (a.lmax) a.lmax[so + i] = __float_as_int(rec[PREC_LB]);
-        if (a.jarg) a.jarg[so + i] = __float_as_int(rec[PREC_JB]);
+    if (pl.own && pl.cnt > 0) {
+        float* rec = a.prow + (it.so + pl.p) * a.prow_stride;
+        const unsigned long long key = s_key[lane];
+        rec[PREC_M] = __uint_as_float(s_m[lane]);
+        rec[PREC_LB] = __int_as_float((int)(key >> 32));
+        rec[PREC_JB] = __int_as_float((int)(key & 0xffffffffu));
     }
 }
 
 // ---------------------------------------------------------------------------------------
-// backward rows: grid = BH * ceil(N/64)
+// forward, pass 2 for rows with pairs (after the label scan wrote y and the key count).
 template <typename T, int R, int DV>
-__global__ __launch_bounds__(64) void pairs_rows_kernel(PathArgs a) {
-    Owner w;
-    if (!pair_owner(a, 0, xcd_work_item(), w)) return;
-    const int n = a.n, i = w.p, h = w.h;
-    const long so = w.so, row0 = w.row0;
-    int lo = w.lo;
-    const int hi = w.hi;
-    const int32_t* kb = a.o.bpos[1] + so;
-    // skip to the first partner; rows without one are done
-    while (lo < hi && kb[lo] == 0) ++lo;
-    if (lo >= hi || kb[lo] > i) {
-        a.pnb[so + i] = 0;
-        return;
+__global__ __launch_bounds__(64 * WAVES) void pairs_finish_kernel(PathArgs a) {
+    constexpr int CPL = DV / 4;  // value columns per lane in phase B
+    __shared__ float s_cf_all[WAVES][OWNERS][CK];
+    __shared__ float s_p_all[WAVES][OWNERS][CK];
+    __shared__ int s_j_all[WAVES][OWNERS][CK];
+    auto& s_cf = s_cf_all[wave_id()];
+    auto& s_p = s_p_all[wave_id()];
+    auto& s_j = s_j_all[wave_id()];
+    PairItem it;
+    Plan pl;
+    if (!pair_item<0>(a, it, pl)) return;
+    const int n = a.n, lane = lane_id();
+    const int32_t* kb = a.o.bpos[1] + it.so;
+    const int32_t* q = a.iq + it.so;
+    const int32_t* k = a.ik + it.so;
+    const int32_t* bnd = bound_of(a, it.bh);
+    const float* lut = a.lut + (long)it.h * a.lut_stride;
+    const T* sq = reinterpret_cast<const T*>(a.sq);
+    const T* sk = reinterpret_cast<const T*>(a.sk);
+    const T* v = reinterpret_cast<const T*>(a.v);
+
+    const int sl = lane >> 2, cg = lane & 3;
+    const int i = __shfl(pl.p, sl), lo = __shfl(pl.lo, sl), cnt = __shfl(pl.cnt, sl);
+    const float* rec = a.prow + (it.so + i) * a.prow_stride;
+    const float m = cnt > 0 ? rec[PREC_M] : 0.0f;
+    const float p1 = exp2_fp32(lut[1] - m);
+    float sqr[R];
+    load_row<T, R>(sq + (it.row0 + (long)i * a.H) * R, sqr);
+    float dp = 0.0f, corr[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) corr[c] = 0.0f;
+
+    for (int c0 = 0; c0 < pl.maxcnt; c0 += CK) {
+        // phase A: pairs (slot, c0 + cg + 4u)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int kq = c0 + cg + 4 * u;
+            if (kq < cnt) {
+                const int j = kb[lo + kq];
+                const int L = match_length(q, k, i, j, bnd, a.strip, n);
+                const float p = exp2_fp32(lut[L] - m);
+                float skr[R];
+                load_row<T, R>(sk + (it.row0 + (long)j * a.H) * R, skr);
+                float s = 0.0f;
+#pragma unroll
+                for (int r = 0; r < R; ++r) s = __builtin_fmaf(sqr[r], skr[r], s);
+                s_cf[sl][cg + 4 * u] = (p - p1) * s;
+                s_p[sl][cg + 4 * u] = p;
+                s_j[sl][cg + 4 * u] = j;
+            }
+        }
+        // phase B: slot sl folds pairs c0 .. c0+7 in order, lane = column group cg
+        const int nv = cnt - c0 < CK ? cnt - c0 : CK;
+#pragma unroll
+        for (int h0 = 0; h0 < CK; h0 += 4) {
+            float vr[4][CPL];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = s_j[sl][h0 + u];
+                if (h0 + u < nv)
+                    load_row<T, CPL>(v + (it.row0 + (long)j * a.H) * DV + cg * CPL, vr[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (h0 + u < nv) {
+                    dp = dp + s_p[sl][h0 + u];
+                    const float cf = s_cf[sl][h0 + u];
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) corr[c] = __builtin_fmaf(cf, vr[u][c], corr[c]);
+                }
+            }
+        }
     }
-    const int32_t* q = a.iq + so;
-    const int32_t* k = a.ik + so;
-    const int32_t* bnd = bound_of(a, w.bh);
-    const float* lut = a.lut + (long)h * a.lut_stride;
-    const float* glut = a.dlut + (long)h * a.lut_stride;
-    const float l2 = a.lse2[so + i];
+    if (cnt > 0) {
+        const int nb = cnt;
+        const int kc = __float_as_int(rec[PREC_CNT]);
+        const float den = (exp2_fp32(-m) + (float)(kc - nb) * p1) + dp;
+        const float rden = 1.0f / den;
+        const long orow = it.row0 + (long)i * a.H;
+        const float* y = rec + PREC_Y + cg * CPL;
+        if (a.out_dtype == DTYPE_F32) {
+            float* o = reinterpret_cast<float*>(a.out) + orow * DV + cg * CPL;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) o[c] = __builtin_fmaf(p1, y[c], corr[c]) * rden;
+        } else {
+            uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + orow * DV + cg * CPL;
+#pragma unroll
+            for (int c = 0; c < CPL; c += 2) {
+                const uint32_t w0 = f32_to_bf16_bits(__builtin_fmaf(p1, y[c], corr[c]) * rden);
+                const uint32_t w1 =
+                    f32_to_bf16_bits(__builtin_fmaf(p1, y[c + 1], corr[c + 1]) * rden);
+                reinterpret_cast<uint32_t*>(o)[c / 2] = w0 | (w1 << 16);
+            }
+        }
+        if (cg == 0) {
+            a.lse2[it.so + i] = m + log2_fp32(den);
+            if (a.lmax) a.lmax[it.so + i] = __float_as_int(rec[PREC_LB]);
+            if (a.jarg) a.jarg[it.so + i] = __float_as_int(rec[PREC_JB]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// backward, query rows: row corrections [cdq[R], cu, cvv, cw, cz] and the pair count.
+template <typename T, int R, int DV>
+__global__ __launch_bounds__(64 * WAVES) void pairs_rows_kernel(PathArgs a) {
+    constexpr int NF = 6;  // de, ds, e, av, se, dp
+    __shared__ float s_f_all[WAVES][OWNERS][CK][NF];
+    __shared__ float s_sk_all[WAVES][OWNERS][CK][R];
+    auto& s_f = s_f_all[wave_id()];
+    auto& s_sk = s_sk_all[wave_id()];
+    PairItem it;
+    Plan pl;
+    if (!pair_item<0>(a, it, pl)) return;
+    const int n = a.n, lane = lane_id();
+    const int32_t* kb = a.o.bpos[1] + it.so;
+    const int32_t* q = a.iq + it.so;
+    const int32_t* k = a.ik + it.so;
+    const int32_t* bnd = bound_of(a, it.bh);
+    const float* lut = a.lut + (long)it.h * a.lut_stride;
+    const float* glut = a.dlut + (long)it.h * a.lut_stride;
+    const T* sq = reinterpret_cast<const T*>(a.sq);
+    const T* sk = reinterpret_cast<const T*>(a.sk);
+    const T* v = reinterpret_cast<const T*>(a.v);
+    const T* dout = reinterpret_cast<const T*>(a.dout);
+
+    const int sl = lane >> 2, cg = lane & 3;
+    const int i = __shfl(pl.p, sl), lo = __shfl(pl.lo, sl), cnt = __shfl(pl.cnt, sl);
+    const float l2 = a.lse2[it.so + i];
     const float cc = glut[i + 1];
     const float P1 = exp2_fp32(lut[1] - l2);
     const float q1 = P1 * (glut[1] - cc);
-    const long qr = row0 + (long)i * a.H;
-    float sqr[R], dor[DV];
-    load_row<T, R>(reinterpret_cast<const T*>(a.sq) + qr * R, sqr);
-    load_row<T, DV>(reinterpret_cast<const T*>(a.dout) + qr * DV, dor);
-    const T* sk = reinterpret_cast<const T*>(a.sk);
-    const T* v = reinterpret_cast<const T*>(a.v);
-    float cdq[R], cu = 0.0f, cvv = 0.0f, cw = 0.0f, cz = 0.0f;
+    const long qr = it.row0 + (long)i * a.H;
+    float sqr[R];
+    load_row<T, R>(sq + qr * R, sqr);
+    constexpr int RL = (R + 3) / 4;  // readout rows handled per lane in phase B
+    float cdq[RL], cu = 0.0f, cvv = 0.0f, cw = 0.0f, cz = 0.0f;
 #pragma unroll
-    for (int r = 0; r < R; ++r) cdq[r] = 0.0f;
-    int nb = 0;
-    for (int x = lo; x < hi; ++x) {
-        const int j = kb[x];
-        if (j > i) break;
-        const int L = match_length(q, k, i, j, bnd, a.strip, n);
-        const long kr = row0 + (long)j * a.H;
-        float skr[R];
-        load_row<T, R>(sk + kr * R, skr);
-        float s = 0.0f;
-#pragma unroll
-        for (int r = 0; r < R; ++r) s = __builtin_fmaf(sqr[r], skr[r], s);
-        float e = 0.0f;
-        constexpr int VC = DV < 32 ? DV : 32;
-#pragma unroll
-        for (int d0 = 0; d0 < DV; d0 += VC) {
-            float vr[VC];
-            load_row<T, VC>(v + kr * DV + d0, vr);
-#pragma unroll
-            for (int d = 0; d < VC; ++d) e = __builtin_fmaf(dor[d0 + d], vr[d], e);
-        }
-        const float p = exp2_fp32(lut[L] - l2);
-        const float dpv = p - P1;
-        const float g = glut[L] - cc;
-        const float av = p * g - q1;
-        const float de = dpv * e, ds = dpv * s;
-#pragma unroll
-        for (int r = 0; r < R; ++r) cdq[r] = __builtin_fmaf(de, skr[r], cdq[r]);
-        cu = __builtin_fmaf(ds, e, cu);
-        cvv = cvv + av;
-        cw = __builtin_fmaf(av, s * e, cw);
-        cz = cz + dpv;
-        ++nb;
-    }
-    a.pnb[so + i] = nb;
-    float* rec = a.prow + (so + i) * a.prow_stride;
-#pragma unroll
-    for (int r = 0; r < R; ++r) rec[r] = cdq[r];
-    rec[R] = cu;
-    rec[R + 1] = cvv;
-    rec[R + 2] = cw;
-    rec[R + 3] = cz;
-}
+    for (int x = 0; x < RL; ++x) cdq[x] = 0.0f;
 
-// ---------------------------------------------------------------------------------------
-// backward keys: adds the bigram-pair corrections to dSK and dV written by the key label scan
-//   ascending i: p = exp2(LUT[L]-l2_i); dp = p - exp2(LUT[1]-l2_i); s, e = chains;
-//   cdk[r] = fma(dp*e, sq_i[r], cdk[r]); cdv[d] = fma(dp*s, dO_i[d], cdv[d]);
-//   dsk[r] += cdk[r]; dv[d] += cdv[d].
-// grid = BH * ceil(N/64) * (DV/DVB)
-template <typename T, int R, int DV, int DVB>
-__global__ __launch_bounds__(64) void pairs_keys_kernel(PathArgs a) {
-    constexpr int NBLK = DV / DVB;
-    const int item = xcd_work_item();
-    const int blk = item % NBLK;
-    Owner w;
-    if (!pair_owner(a, 1, item / NBLK, w)) return;
-    const int n = a.n, j = w.p;
-    const long so = w.so, row0 = w.row0;
-    const int32_t* qb = a.o.bpos[0] + so;
-    int lo = w.lo;
-    const int hi = w.hi;
-    {  // first query at or after j
-        int r = hi;
-        while (lo < r) {
-            const int mid = (lo + r) >> 1;
-            if (qb[mid] < j) lo = mid + 1; else r = mid;
-        }
-    }
-    if (lo >= hi) return;
-    const int32_t* q = a.iq + so;
-    const int32_t* k = a.ik + so;
-    const int32_t* bnd = bound_of(a, w.bh);
-    const float* lut = a.lut + (long)w.h * a.lut_stride;
-    const float lut1 = lut[1];
-    const long kr = row0 + (long)j * a.H;
-    float skr[R], vr[DV];
-    load_row<T, R>(reinterpret_cast<const T*>(a.sk) + kr * R, skr);
-    load_row<T, DV>(reinterpret_cast<const T*>(a.v) + kr * DV, vr);
-    const T* sq = reinterpret_cast<const T*>(a.sq);
-    const T* dout = reinterpret_cast<const T*>(a.dout);
-    float cdk[R], cdv[DVB];
+    for (int c0 = 0; c0 < pl.maxcnt; c0 += CK) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) cdk[r] = 0.0f;
+        for (int u = 0; u < 2; ++u) {
+            const int kq = c0 + cg + 4 * u;
+            if (kq < cnt) {
+                const int j = kb[lo + kq];
+                const int L = match_length(q, k, i, j, bnd, a.strip, n);
+                const long kr = it.row0 + (long)j * a.H;
+                float skr[R];
+                load_row<T, R>(sk + kr * R, skr);
+                float s = 0.0f;
 #pragma unroll
-    for (int d = 0; d < DVB; ++d) cdv[d] = 0.0f;
-    for (int x = lo; x < hi; ++x) {
-        const int i = qb[x];
-        const int L = match_length(q, k, i, j, bnd, a.strip, n);
-        const float l2 = a.lse2[so + i];
-        const float p = exp2_fp32(lut[L] - l2);
-        const float dpv = p - exp2_fp32(lut1 - l2);
-        const long qr = row0 + (long)i * a.H;
-        float sqr[R];
-        load_row<T, R>(sq + qr * R, sqr);
-        float s = 0.0f;
+                for (int r = 0; r < R; ++r) s = __builtin_fmaf(sqr[r], skr[r], s);
+                float e = 0.0f;
+                constexpr int VC = DV < 32 ? DV : 32;
 #pragma unroll
-        for (int r = 0; r < R; ++r) s = __builtin_fmaf(sqr[r], skr[r], s);
-        float e = 0.0f;
-        float dblk[DVB];
-        constexpr int VC = DV < 32 ? DV : 32;
+                for (int d0 = 0; d0 < DV; d0 += VC) {
+                    float dr[VC], vr[VC];
+                    load_row<T, VC>(dout + qr * DV + d0, dr);
+                    load_row<T, VC>(v + kr * DV + d0, vr);
 #pragma unroll
-        for (int d0 = 0; d0 < DV; d0 += VC) {
-            float dr[VC];
-            load_row<T, VC>(dout + qr * DV + d0, dr);
+                    for (int d = 0; d < VC; ++d) e = __builtin_fmaf(dr[d], vr[d], e);
+                }
+                const float p = exp2_fp32(lut[L] - l2);
+                const float dpv = p - P1;
+                const float av = p * (glut[L] - cc) - q1;
+                float* f = s_f[sl][cg + 4 * u];
+                f[0] = dpv * e;
+                f[1] = dpv * s;
+                f[2] = e;
+                f[3] = av;
+                f[4] = s * e;
+                f[5] = dpv;
 #pragma unroll
-            for (int d = 0; d < VC; ++d) {
-                e = __builtin_fmaf(dr[d], vr[d0 + d], e);
-                const int db = d0 + d - blk * DVB;
-                if (db >= 0 && db < DVB) dblk[db] = dr[d];
+                for (int r = 0; r < R; ++r) s_sk[sl][cg + 4 * u][r] = skr[r];
             }
         }
-        const float de = dpv * e, ds = dpv * s;
-        if (blk == 0) {
+        const int nv = cnt - c0 < CK ? cnt - c0 : CK;
+        for (int u = 0; u < nv; ++u) {
+            const float* f = s_f[sl][u];
+            const float de = f[0];
 #pragma unroll
-            for (int r = 0; r < R; ++r) cdk[r] = __builtin_fmaf(de, sqr[r], cdk[r]);
+            for (int x = 0; x < RL; ++x) {
+                const int r = cg + 4 * x;
+                if (r < R) cdq[x] = __builtin_fmaf(de, s_sk[sl][u][r], cdq[x]);
+            }
+            cu = __builtin_fmaf(f[1], f[2], cu);
+            cvv = cvv + f[3];
+            cw = __builtin_fmaf(f[3], f[4], cw);
+            cz = cz + f[5];
         }
-#pragma unroll
-        for (int d = 0; d < DVB; ++d) cdv[d] = __builtin_fmaf(ds, dblk[d], cdv[d]);
     }
-    if (blk == 0) {
-        float* g = a.dsk + kr * R;
+    if (cnt > 0) {
+        float* rec = a.prow + (it.so + i) * a.prow_stride;
 #pragma unroll
-        for (int r = 0; r < R; ++r) g[r] = g[r] + cdk[r];
+        for (int x = 0; x < RL; ++x) {
+            const int r = cg + 4 * x;
+            if (r < R) rec[r] = cdq[x];
+        }
+        if (cg == 0) {
+            rec[R] = cu;
+            rec[R + 1] = cvv;
+            rec[R + 2] = cw;
+            rec[R + 3] = cz;
+        }
     }
-    float* g = a.dv + kr * DV + blk * DVB;
-#pragma unroll
-    for (int d = 0; d < DVB; ++d) g[d] = g[d] + cdv[d];
 }
 
 // ---------------------------------------------------------------------------------------
+// backward keys: adds the bigram-pair corrections to dSK and dV written by the key scan.
 template <typename T, int R, int DV>
-static hipError_t stats_go(const PathArgs& a, hipStream_t s) {
-    long items = (long)((a.n + PAIR_ITEM - 1) / PAIR_ITEM) * a.B * a.H;
-    items = (items + 7) / 8 * 8;
-    hipLaunchKernelGGL((pairs_stats_kernel<T, R, DV>), dim3((unsigned)items), dim3(64), 0, s, a);
-    return hipGetLastError();
-}
-template <typename T, int R, int DV>
-static hipError_t finish_go(const PathArgs& a, hipStream_t s) {
-    constexpr int DVB = DV < 64 ? DV : 64;
-    long items = (long)((a.n + PAIR_ITEM - 1) / PAIR_ITEM) * a.B * a.H * (DV / DVB);
-    items = (items + 7) / 8 * 8;
-    hipLaunchKernelGGL((pairs_finish_kernel<T, R, DV, DVB>), dim3((unsigned)items), dim3(64), 0,
-                       s, a);
-    return hipGetLastError();
-}
-template <typename T, int R, int DV>
-static hipError_t rows_go(const PathArgs& a, hipStream_t s) {
-    long items = (long)((a.n + PAIR_ITEM - 1) / PAIR_ITEM) * a.B * a.H;
-    items = (items + 7) / 8 * 8;
-    hipLaunchKernelGGL((pairs_rows_kernel<T, R, DV>), dim3((unsigned)items), dim3(64), 0, s, a);
-    return hipGetLastError();
-}
-template <typename T, int R, int DV>
-static hipError_t keys_go(const PathArgs& a, hipStream_t s) {
-    constexpr int DVB = DV < 64 ? DV : 64;
-    long items = (long)((a.n + PAIR_ITEM - 1) / PAIR_ITEM) * a.B * a.H * (DV / DVB);
-    items = (items + 7) / 8 * 8;
-    hipLaunchKernelGGL((pairs_keys_kernel<T, R, DV, DVB>), dim3((unsigned)items), dim3(64), 0, s,
-                       a);
-    return hipGetLastError();
+__global__ __launch_bounds__(64 * WAVES) void pairs_keys_kernel(PathArgs a) {
+    constexpr int CPL = DV / 4;
+    __shared__ float s_de_all[WAVES][OWNERS][CK];
+    __shared__ float s_ds_all[WAVES][OWNERS][CK];
+    __shared__ int s_i_all[WAVES][OWNERS][CK];
+    __shared__ float s_sq_all[WAVES][OWNERS][CK][R];
+    auto& s_de = s_de_all[wave_id()];
+    auto& s_ds = s_ds_all[wave_id()];
+    auto& s_i = s_i_all[wave_id()];
+    auto& s_sq = s_sq_all[wave_id()];
+    PairItem it;
+    Plan pl;
+    if (!pair_item<1>(a, it, pl)) return;
+    const int n = a.n, lane = lane_id();
+    const int32_t* qb = a.o.bpos[0] + it.so;
+    const int32_t* q = a.iq + it.so;
+    const int32_t* k = a.ik + it.so;
+    const int32_t* bnd = bound_of(a, it.bh);
+    const float* lut = a.lut + (long)it.h * a.lut_stride;
+    const float lut1 = lut[1];
+    const T* sq = reinterpret_cast<const T*>(a.sq);
+    const T* sk = reinterpret_cast<const T*>(a.sk);
+    const T* v = reinterpret_cast<const T*>(a.v);
+    const T* dout = reinterpret_cast<const T*>(a.dout);
+
+    const int sl = lane >> 2, cg = lane & 3;
+    const int j = __shfl(pl.p, sl), lo = __shfl(pl.lo, sl), cnt = __shfl(pl.cnt, sl);
+    const long kr = it.row0 + (long)j * a.H;
+    float skr[R];
+    load_row<T, R>(sk + kr * R, skr);
+    constexpr int RL = (R + 3) / 4;
+    float cdk[RL], cdv[CPL];
+#pragma unroll
+    for (int x = 0; x < RL; ++x) cdk[x] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) cdv[c] = 0.0f;
+
+    for (int c0 = 0; c0 < pl.maxcnt; c0 += CK) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int kq = c0 + cg + 4 * u;
+            if (kq < cnt) {
+                const int i = qb[lo + kq];
+                const int L = match_length(q, k, i, j, bnd, a.strip, n);
+                const float l2 = a.lse2[it.so + i];
+                const float p = exp2_fp32(lut[L] - l2);
+                const float dpv = p - exp2_fp32(lut1 - l2);
+                const long qr = it.row0 + (long)i * a.H;
+                float sqr[R];
+                load_row<T, R>(sq + qr * R, sqr);
+                float s = 0.0f;
+#pragma unroll
+                for (int r = 0; r < R; ++r) s = __builtin_fmaf(sqr[r], skr[r], s);
+                float e = 0.0f;
+                constexpr int VC = DV < 32 ? DV : 32;
+#pragma unroll
+                for (int d0 = 0; d0 < DV; d0 += VC) {
+                    float dr[VC], vr[VC];
+                    load_row<T, VC>(dout + qr * DV + d0, dr);
+                    load_row<T, VC>(v + kr * DV + d0, vr);
+#pragma unroll
+                    for (int d = 0; d < VC; ++d) e = __builtin_fmaf(dr[d], vr[d], e);
+                }
+                s_de[sl][cg + 4 * u] = dpv * e;
+                s_ds[sl][cg + 4 * u] = dpv * s;
+                s_i[sl][cg + 4 * u] = i;
+#pragma unroll
+                for (int r = 0; r < R; ++r) s_sq[sl][cg + 4 * u][r] = sqr[r];
+            }
+        }
+        const int nv = cnt - c0 < CK ? cnt - c0 : CK;
+#pragma unroll
+        for (int h0 = 0; h0 < CK; h0 += 4) {
+            float dr[4][CPL];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = s_i[sl][h0 + u];
+                if (h0 + u < nv)
+                    load_row<T, CPL>(dout + (it.row0 + (long)i * a.H) * DV + cg * CPL, dr[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (h0 + u < nv) {
+                    const float de = s_de[sl][h0 + u], ds = s_ds[sl][h0 + u];
+#pragma unroll
+                    for (int x = 0; x < RL; ++x) {
+                        const int r = cg + 4 * x;
+                        if (r < R) cdk[x] = __builtin_fmaf(de, s_sq[sl][h0 + u][r], cdk[x]);
+                    }
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) cdv[c] = __builtin_fmaf(ds, dr[u][c], cdv[c]);
+                }
+            }
+        }
+    }
+    if (cnt > 0) {
+#pragma unroll
+        for (int x = 0; x < RL; ++x) {
+            const int r = cg + 4 * x;
+            if (r < R) a.dsk[kr * R + r] = a.dsk[kr * R + r] + cdk[x];
+        }
+        float* g = a.dv + kr * DV + cg * CPL;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) g[c] = g[c] + cdv[c];
+    }
 }
 
-#define DISM_PAIRS_LAUNCHER(NAME, GO)                                                         \
+// ---------------------------------------------------------------------------------------
+#define DISM_PAIRS_LAUNCHER(NAME, KERNEL)                                                     \
+    template <typename T, int R, int DV>                                                      \
+    static hipError_t NAME##_go(const PathArgs& a, hipStream_t s) {                           \
+        const long items = (long)((a.n + OWNERS - 1) / OWNERS) * a.B * a.H;                   \
+        hipLaunchKernelGGL((KERNEL<T, R, DV>), dim3(grid_for(items)), dim3(64 * WAVES), 0, s, \
+                           a);                                                                \
+        return hipGetLastError();                                                             \
+    }                                                                                         \
     template <typename T, int R>                                                              \
     static hipError_t NAME##_dv(const PathArgs& a, int DV, hipStream_t s) {                   \
         switch (DV) {                                                                         \
-            case 32: return GO<T, R, 32>(a, s);                                               \
-            case 64: return GO<T, R, 64>(a, s);                                               \
-            case 128: return GO<T, R, 128>(a, s);                                             \
+            case 32: return NAME##_go<T, R, 32>(a, s);                                        \
+            case 64: return NAME##_go<T, R, 64>(a, s);                                        \
+            case 128: return NAME##_go<T, R, 128>(a, s);                                      \
             default: return hipErrorInvalidValue;                                             \
         }                                                                                     \
     }                                                                                         \
@@ -400,9 +560,9 @@ static hipError_t keys_go(const PathArgs& a, hipStream_t s) {
         return hipErrorInvalidValue;                                                          \
     }
 
-DISM_PAIRS_LAUNCHER(pairs_stats, stats_go)
-DISM_PAIRS_LAUNCHER(pairs_finish, finish_go)
-DISM_PAIRS_LAUNCHER(pairs_rows, rows_go)
-DISM_PAIRS_LAUNCHER(pairs_keys, keys_go)
+DISM_PAIRS_LAUNCHER(pairs_stats, pairs_stats_kernel)
+DISM_PAIRS_LAUNCHER(pairs_finish, pairs_finish_kernel)
+DISM_PAIRS_LAUNCHER(pairs_rows, pairs_rows_kernel)
+DISM_PAIRS_LAUNCHER(pairs_keys, pairs_keys_kernel)
 
 }  // namespace dism

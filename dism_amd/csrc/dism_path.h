@@ -8,12 +8,26 @@
 
 namespace dism {
 
-// Work-item index of this workgroup with an XCD-contiguous mapping: workgroups are dispatched
+// Kernels of the hard core run WAVES independent 64-lane waves per workgroup (fewer,
+// longer-lived workgroups than one-wave launches, so the dispatcher keeps every SIMD fed);
+// each wave owns one work item and its own slice of the workgroup's LDS.
+constexpr int WAVES = 4;
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
+__device__ __forceinline__ int wave_id() { return (int)(threadIdx.x >> 6); }
+
+// Work item of this wave with an XCD-contiguous mapping: workgroups are dispatched
 // round-robin over the 8 XCDs, so consecutive work items (same (b,h) row, whose labels and
 // vectors then stay in one XCD's L2) go to workgroups of one XCD.  grid is a multiple of 8.
 __device__ __forceinline__ int xcd_work_item() {
     const int g = (int)gridDim.x, x = (int)blockIdx.x;
-    return (x & 7) * (g >> 3) + (x >> 3);
+    return ((x & 7) * (g >> 3) + (x >> 3)) * WAVES + wave_id();
+}
+
+// workgroups for `items` work items
+__host__ __forceinline__ unsigned grid_for(long items) {
+    long blocks = (items + WAVES - 1) / WAVES;
+    blocks = (blocks + 7) / 8 * 8;
+    return (unsigned)blocks;
 }
 
 __host__ __device__ constexpr int words_of(int elem_bytes, int n) {
@@ -124,6 +138,116 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 __device__ __forceinline__ const int32_t* bound_of(const PathArgs& a, int bh) {
     return a.bound ? a.bound + (long)bh * ((a.n - 1) / a.strip) * a.n : nullptr;
+}
+
+// ---------------------------------------------------------------------------------------
+// LDS staging shared by the scan and pair kernels.
+constexpr int WBYTES = 4096;  // one value-row window buffer
+
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ void wait_vm0() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): window DMA and staging loads landed
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// pairwise tree over the G consecutive lanes of a row group; the lane with g = 0 holds
+// ((x0 + x1) + (x2 + x3)) + ...
+template <int G>
+__device__ __forceinline__ float group_sum(float x) {
+    if constexpr (G >= 2) x = x + dpp<0xB1>(x);    // quad_perm [1,0,3,2]
+    if constexpr (G >= 4) x = x + dpp<0x4E>(x);    // quad_perm [2,3,0,1]
+    if constexpr (G >= 8) x = x + dpp<0x141>(x);   // row_half_mirror
+    if constexpr (G >= 16) x = x + dpp<0x140>(x);  // row_mirror
+    if constexpr (G >= 32) x = x + __shfl_xor(x, 16);
+    if constexpr (G >= 64) x = x + __shfl_xor(x, 32);
+    return x;
+}
+
+// LDS readers below take generic pointers into __shared__ arrays; after inlining the
+// compiler sees the LDS origin and emits ds_read instructions.
+// NV consecutive elements of T (aligned to NV * sizeof(T) or 16 bytes)
+template <typename T, int NV>
+__device__ __forceinline__ void lds_vals(const unsigned char* p, float (&out)[NV]) {
+    constexpr int BYTES = NV * (int)sizeof(T);
+    uint32_t w[(BYTES + 3) / 4];
+    if constexpr (BYTES % 16 == 0) {
+#pragma unroll
+        for (int c = 0; c < BYTES / 16; ++c) {
+            const uint4 x = reinterpret_cast<const uint4*>(p)[c];
+            w[4 * c] = x.x; w[4 * c + 1] = x.y; w[4 * c + 2] = x.z; w[4 * c + 3] = x.w;
+        }
+    } else if constexpr (BYTES % 8 == 0) {
+#pragma unroll
+        for (int c = 0; c < BYTES / 8; ++c) {
+            const uint2 x = reinterpret_cast<const uint2*>(p)[c];
+            w[2 * c] = x.x; w[2 * c + 1] = x.y;
+        }
+    } else if constexpr (BYTES % 4 == 0) {
+#pragma unroll
+        for (int c = 0; c < BYTES / 4; ++c)
+            w[c] = reinterpret_cast<const uint32_t*>(p)[c];
+    } else {
+        w[0] = *reinterpret_cast<const uint16_t*>(p);
+    }
+#pragma unroll
+    for (int t = 0; t < NV; ++t) out[t] = word_elem<T>(w, t);
+}
+
+template <typename T>
+__device__ __forceinline__ float lds_elem(const unsigned char* row, int d) {
+    if constexpr (sizeof(T) == 2) {
+        const uint16_t u = reinterpret_cast<const uint16_t*>(row)[d];
+        return __uint_as_float((uint32_t)u << 16);
+    } else {
+        return reinterpret_cast<const float*>(row)[d];
+    }
+}
+
+// R fp32 values at p (broadcast read when p is uniform)
+template <int R>
+__device__ __forceinline__ void lds_row_f32(const float* p, float (&out)[R]) {
+    if constexpr (R % 4 == 0) {
+#pragma unroll
+        for (int c = 0; c < R / 4; ++c) {
+            const float4 x = reinterpret_cast<const float4*>(p)[c];
+            out[4 * c] = x.x; out[4 * c + 1] = x.y; out[4 * c + 2] = x.z; out[4 * c + 3] = x.w;
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) out[r] = p[r];
+    }
+}
+
+template <typename T, int DV>
+struct Geo {
+    static constexpr int RB = DV * (int)sizeof(T);
+    static constexpr int WIN = WBYTES / RB < 64 ? WBYTES / RB : 64;
+    static constexpr int NI = WIN * RB / 1024;
+    static_assert((WIN * RB) % 1024 == 0, "window must be whole 1 KiB DMA blocks");
+};
+
+// DMA of `rows` value rows into buf: row s comes from src_of(s) (a byte pointer).
+template <int RB, int NI, typename Src>
+__device__ __forceinline__ void dma_rows(lds_u8* buf, int rows, Src src_of) {
+    const int lane = lane_id();
+    const int need = (rows * RB + 1023) / 1024;
+#pragma unroll
+    for (int t = 0; t < NI; ++t) {
+        if (t < need) {
+            const int byte = t * 1024 + lane * 16;
+            int s = byte / RB;
+            s = s < rows ? s : rows - 1;
+            const unsigned char* src = src_of(s) + byte % RB;
+            __builtin_amdgcn_global_load_lds(src, (lds_void*)(buf + t * 1024), 16, 0, 0);
+        }
+    }
 }
 
 }  // namespace dism

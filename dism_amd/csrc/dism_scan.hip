@@ -30,89 +30,6 @@
 
 namespace dism {
 
-constexpr int WBYTES = 4096;  // one value-row window buffer
-
-typedef __attribute__((address_space(3))) unsigned char lds_u8;
-typedef __attribute__((address_space(3))) void lds_void;
-
-__device__ __forceinline__ void wait_vm0() {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): window DMA and staging loads landed
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
-}
-
-// pairwise tree over the G consecutive lanes of a row group; the lane with g = 0 holds
-// ((x0 + x1) + (x2 + x3)) + ...
-template <int G>
-__device__ __forceinline__ float group_sum(float x) {
-    if constexpr (G >= 2) x = x + dpp<0xB1>(x);    // quad_perm [1,0,3,2]
-    if constexpr (G >= 4) x = x + dpp<0x4E>(x);    // quad_perm [2,3,0,1]
-    if constexpr (G >= 8) x = x + dpp<0x141>(x);   // row_half_mirror
-    if constexpr (G >= 16) x = x + dpp<0x140>(x);  // row_mirror
-    if constexpr (G >= 32) x = x + __shfl_xor(x, 16);
-    if constexpr (G >= 64) x = x + __shfl_xor(x, 32);
-    return x;
-}
-
-// LDS readers below take generic pointers into __shared__ arrays; after inlining the
-// compiler sees the LDS origin and emits ds_read instructions.
-// NV consecutive elements of T (aligned to NV * sizeof(T) or 16 bytes)
-template <typename T, int NV>
-__device__ __forceinline__ void lds_vals(const unsigned char* p, float (&out)[NV]) {
-    constexpr int BYTES = NV * (int)sizeof(T);
-    uint32_t w[(BYTES + 3) / 4];
-    if constexpr (BYTES % 16 == 0) {
-#pragma unroll
-        for (int c = 0; c < BYTES / 16; ++c) {
-            const uint4 x = reinterpret_cast<const uint4*>(p)[c];
-            w[4 * c] = x.x; w[4 * c + 1] = x.y; w[4 * c + 2] = x.z; w[4 * c + 3] = x.w;
-        }
-    } else if constexpr (BYTES % 8 == 0) {
-#pragma unroll
-        for (int c = 0; c < BYTES / 8; ++c) {
-            const uint2 x = reinterpret_cast<const uint2*>(p)[c];
-            w[2 * c] = x.x; w[2 * c + 1] = x.y;
-        }
-    } else if constexpr (BYTES % 4 == 0) {
-#pragma unroll
-        for (int c = 0; c < BYTES / 4; ++c)
-            w[c] = reinterpret_cast<const uint32_t*>(p)[c];
-    } else {
-        w[0] = *reinterpret_cast<const uint16_t*>(p);
-    }
-#pragma unroll
-    for (int t = 0; t < NV; ++t) out[t] = word_elem<T>(w, t);
-}
-
-template <typename T>
-__device__ __forceinline__ float lds_elem(const unsigned char* row, int d) {
-    if constexpr (sizeof(T) == 2) {
-        const uint16_t u = reinterpret_cast<const uint16_t*>(row)[d];
-        return __uint_as_float((uint32_t)u << 16);
-    } else {
-        return reinterpret_cast<const float*>(row)[d];
-    }
-}
-
-// R fp32 values at p (broadcast read when p is uniform)
-template <int R>
-__device__ __forceinline__ void lds_row_f32(const float* p, float (&out)[R]) {
-    if constexpr (R % 4 == 0) {
-#pragma unroll
-        for (int c = 0; c < R / 4; ++c) {
-            const float4 x = reinterpret_cast<const float4*>(p)[c];
-            out[4 * c] = x.x; out[4 * c + 1] = x.y; out[4 * c + 2] = x.z; out[4 * c + 3] = x.w;
-        }
-    } else {
-#pragma unroll
-        for (int r = 0; r < R; ++r) out[r] = p[r];
-    }
-}
-
 // ---------------------------------------------------------------------------------------
 // Window bookkeeping over entries [lo, hi) of the combined order, ascending or descending.
 template <int WIN, bool DESC>
@@ -128,7 +45,7 @@ struct Walk {
         return r < WIN ? r : WIN;
     }
     __device__ __forceinline__ int load(int kk) const {
-        const int lane = threadIdx.x, c = count(kk);
+        const int lane = lane_id(), c = count(kk);
         const int e = lane < c ? lane : c - 1;
         return ord[idx(kk, e < WIN ? e : WIN - 1)];
     }
@@ -182,47 +99,25 @@ __device__ __forceinline__ void for_runs(const int32_t* clab, int c0, int c1, F&
     }
 }
 
-template <typename T, int DV>
-struct Geo {
-    static constexpr int RB = DV * (int)sizeof(T);
-    static constexpr int WIN = WBYTES / RB < 64 ? WBYTES / RB : 64;
-    static constexpr int NI = WIN * RB / 1024;
-    static_assert((WIN * RB) % 1024 == 0, "window must be whole 1 KiB DMA blocks");
-};
-
-// DMA of `rows` value rows into buf: row s comes from src_of(s) (a byte pointer).
-template <int RB, int NI, typename Src>
-__device__ __forceinline__ void dma_rows(lds_u8* buf, int rows, Src src_of) {
-    const int lane = threadIdx.x;
-    const int need = (rows * RB + 1023) / 1024;
-#pragma unroll
-    for (int t = 0; t < NI; ++t) {
-        if (t < need) {
-            const int byte = t * 1024 + lane * 16;
-            int s = byte / RB;
-            s = s < rows ? s : rows - 1;
-            const unsigned char* src = src_of(s) + byte % RB;
-            __builtin_amdgcn_global_load_lds(src, (lds_void*)(buf + t * 1024), 16, 0, 0);
-        }
-    }
-}
-
 // ---------------------------------------------------------------------------------------
 // forward.  Rows without bigram pairs are finished here:
 //   out[d] = fma(p1, y[d], 0) * (1/den),  den = exp2(-m) + cnt*p1,  m = max(0, LUT[1]) if
 //   cnt > 0 else 0;  rows with pairs get y and cnt in their record for the pair kernel.
 template <typename T, int R, int DV>
-__global__ __launch_bounds__(64) void scan_forward_kernel(PathArgs a) {
+__global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
     using G_ = Geo<T, DV>;
     constexpr int WIN = G_::WIN, RB = G_::RB, NI = G_::NI;
     constexpr int COLS = (DV + 63) / 64;
     constexpr int W = words_of(sizeof(T), R);
-    __shared__ __attribute__((aligned(16))) unsigned char s_v[2][WBYTES];
-    __shared__ __attribute__((aligned(16))) float s_r[WIN][R];
-    __shared__ int s_slot[WIN];
+    __shared__ __attribute__((aligned(16))) unsigned char s_v_all[WAVES][2][WBYTES];
+    auto& s_v = s_v_all[wave_id()];
+    __shared__ __attribute__((aligned(16))) float s_r_all[WAVES][WIN][R];
+    auto& s_r = s_r_all[wave_id()];
+    __shared__ int s_slot_all[WAVES][WIN];
+    auto& s_slot = s_slot_all[wave_id()];
     Item it;
     if (!scan_item(a, it)) return;
-    const int lane = threadIdx.x;
+    const int lane = lane_id();
     const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
     const int32_t* corder = a.o.corder + 2 * it.so;
     const int32_t* clab = a.o.clab + 2 * it.so;
@@ -387,17 +282,20 @@ __global__ __launch_bounds__(64) void scan_forward_kernel(PathArgs a) {
 // backward, query rows: dSQ and the per-row tau term (row corrections from the pair kernel).
 // Row-group layout: lane = r*G + g holds M[r][g*VPL .. g*VPL+VPL).
 template <typename T, int R, int DV>
-__global__ __launch_bounds__(64) void scan_rows_kernel(PathArgs a) {
+__global__ __launch_bounds__(64 * WAVES) void scan_rows_kernel(PathArgs a) {
     using G_ = Geo<T, DV>;
     constexpr int WIN = G_::WIN, RB = G_::RB, NI = G_::NI;
     constexpr int W = words_of(sizeof(T), R);
     constexpr int G = 64 / R, VPL = DV / G;
-    __shared__ __attribute__((aligned(16))) unsigned char s_v[2][WBYTES];
-    __shared__ __attribute__((aligned(16))) float s_r[WIN][R];
-    __shared__ __attribute__((aligned(16))) float s_c[WIN][R];
+    __shared__ __attribute__((aligned(16))) unsigned char s_v_all[WAVES][2][WBYTES];
+    auto& s_v = s_v_all[wave_id()];
+    __shared__ __attribute__((aligned(16))) float s_r_all[WAVES][WIN][R];
+    auto& s_r = s_r_all[wave_id()];
+    __shared__ __attribute__((aligned(16))) float s_c_all[WAVES][WIN][R];
+    auto& s_c = s_c_all[wave_id()];
     Item it;
     if (!scan_item(a, it)) return;
-    const int lane = threadIdx.x, rl = lane / G, gl = lane % G;
+    const int lane = lane_id(), rl = lane / G, gl = lane % G;
     const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
     const int32_t* corder = a.o.corder + 2 * it.so;
     const int32_t* clab = a.o.clab + 2 * it.so;
@@ -546,17 +444,19 @@ __global__ __launch_bounds__(64) void scan_rows_kernel(PathArgs a) {
 // key pair kernel).  Merge in DESCENDING position order: a query at the key's own position
 // comes before the key.  N is kept in both layouts: column (for dV) and row-group (for dSK).
 template <typename T, int R, int DV>
-__global__ __launch_bounds__(64) void scan_keys_kernel(PathArgs a) {
+__global__ __launch_bounds__(64 * WAVES) void scan_keys_kernel(PathArgs a) {
     using G_ = Geo<T, DV>;
     constexpr int WIN = G_::WIN, RB = G_::RB, NI = G_::NI;
     constexpr int COLS = (DV + 63) / 64;
     constexpr int W = words_of(sizeof(T), R);
     constexpr int G = 64 / R, VPL = DV / G;
-    __shared__ __attribute__((aligned(16))) unsigned char s_v[2][WBYTES];
-    __shared__ __attribute__((aligned(16))) float s_r[WIN][R];
+    __shared__ __attribute__((aligned(16))) unsigned char s_v_all[WAVES][2][WBYTES];
+    auto& s_v = s_v_all[wave_id()];
+    __shared__ __attribute__((aligned(16))) float s_r_all[WAVES][WIN][R];
+    auto& s_r = s_r_all[wave_id()];
     Item it;
     if (!scan_item(a, it)) return;
-    const int lane = threadIdx.x, rl = lane / G, gl = lane % G;
+    const int lane = lane_id(), rl = lane / G, gl = lane % G;
     const int32_t* corder = a.o.corder + 2 * it.so;
     const int32_t* clab = a.o.clab + 2 * it.so;
     const int32_t* ctab = a.o.ctab + (long)it.bh * 257;
@@ -681,9 +581,9 @@ __global__ __launch_bounds__(64) void scan_keys_kernel(PathArgs a) {
 #define DISM_SCAN_LAUNCHER(NAME, KERNEL)                                                      \
     template <typename T, int R, int DV>                                                      \
     static hipError_t NAME##_go(const PathArgs& a, hipStream_t s) {                           \
-        long items = 256L * a.B * a.H;                                                        \
-        items = (items + 7) / 8 * 8;                                                          \
-        hipLaunchKernelGGL((KERNEL<T, R, DV>), dim3((unsigned)items), dim3(64), 0, s, a);     \
+        const long items = 256L * a.B * a.H;                                                  \
+        hipLaunchKernelGGL((KERNEL<T, R, DV>), dim3(grid_for(items)), dim3(64 * WAVES), 0, s, \
+                           a);                                                                \
         return hipGetLastError();                                                             \
     }                                                                                         \
     template <typename T, int R>                                                              \
