@@ -3,9 +3,12 @@
 A step is one training pass of the hard DISM op over one synthetic batch of the headline
 configuration (B=4, H=16, T=16384, d_qk=8, d_v=64, bf16, periodic
 component on 25% of the heads):
-    labels (sign binarizer, q and k) -> log2 weight table -> carry boundary -> readout
-    -> dlog table -> query sweep (dSQ, tau terms) -> key sweep (dV, dSK) -> tau reduction.
-Inputs are resident in HBM before timing.  Prints ONE JSON line.
+    labels (sign binarizer, q and k) -> log2 weight table -> [carry boundary, off by default]
+    -> prepare (position orders, bigram-pair plans) -> readout -> dlog table
+    -> row pairs -> query-row scan (dSQ, tau terms) -> key scan (dV, dSK) -> key pairs
+    -> tau reduction.
+Inputs are resident in HBM before timing.  Prints ONE JSON line; `kernel_ms` times each stage
+with events on the launch stream, `roofline` covers the dominant single-kernel stage.
 """
 import argparse
 import json
@@ -18,7 +21,6 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-P_INT = 256 * 2.4e9 * 64      # int32 lane-ops/s (256 CUs x 2.4 GHz x 64 lanes)
 HBM_PEAK = 8.0e12             # bytes/s
 
 
@@ -50,9 +52,12 @@ def main():
     ap.add_argument("--dqk", type=int, default=8)
     ap.add_argument("--dv", type=int, default=64)
     ap.add_argument("--tau", type=float, default=0.5)
-    ap.add_argument("--carry-strip", type=int, default=256)
+    ap.add_argument("--carry-strip", type=int, default=0,
+                    help="composed carry boundary strip height (0 = off)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-heads", type=int, default=16)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="only run 5 device-to-device copies of BYTES bytes (the reference "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (single-GPU boxes); "
@@ -60,6 +65,14 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.calibrate_copy:
+        src = torch.empty(args.calibrate_copy, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": args.calibrate_copy}), flush=True)
+        return
     import dism_amd
     from dism_amd import _lib
     from dism_amd._checks import DTYPE_CODE
@@ -81,14 +94,15 @@ def main():
     dvv = torch.empty((B, T, H, DV), dtype=torch.float32, device=dev)
     rowtau = torch.empty((B, H, T), dtype=torch.float32, device=dev)
     dtau = torch.empty((H,), dtype=torch.float32, device=dev)
-    names = ["labels", "lut", "carry", "prepare", "forward", "dlut", "bwd_prepare",
-             "bwd_queries", "bwd_keys", "tau_reduce"]
+    names = ["labels", "lut", "carry", "prepare", "readout", "dlut", "row_pairs", "queries",
+             "keys", "key_pairs", "tau_reduce"]
     out = torch.empty((B, T, H, DV), dtype=torch.bfloat16, device=dev)
     lse2 = torch.empty((B, H, T), dtype=torch.float32, device=dev)
     code = DTYPE_CODE[torch.bfloat16]
     nbytes = _lib.workspace_bytes(B, T, H, D, DV, code)
     ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
     W = ws.data_ptr()
+    hp = hard.data_ptr()
 
     def step(events=None):
         def mark(i):
@@ -97,6 +111,7 @@ def main():
         mark(0)
         iq = dism_amd.sign_labels(tq)
         ik = dism_amd.sign_labels(tk)
+        qp, kp = iq.data_ptr(), ik.data_ptr()
         mark(1)
         lut = dism_amd.hard_log_weights(tau, n)
         mark(2)
@@ -104,39 +119,38 @@ def main():
             if strip > 0 else None
         cp = 0 if carry is None else carry.data_ptr()
         mark(3)
-        _lib.call("dism_hard_prepare", tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), code,
-                  iq.data_ptr(), ik.data_ptr(), B, T, H, D, DV, W, nbytes, S)
+        vec = (tq.data_ptr(), tk.data_ptr(), tv.data_ptr())
+        _lib.call("dism_hard_prepare", *vec, code, qp, kp, B, T, H, D, DV, W, nbytes, S)
         mark(4)
-        _lib.call("dism_hard_readout", tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), code,
-                  iq.data_ptr(), ik.data_ptr(), hard.data_ptr(), cp, strip, lut.data_ptr(),
+        _lib.call("dism_hard_readout", *vec, code, qp, kp, hp, cp, strip, lut.data_ptr(),
                   n + 1, B, T, H, D, DV, W, nbytes, out.data_ptr(), code, lse2.data_ptr(), 0, 0,
                   S)
         mark(5)
         dlut = dism_amd.hard_dlog_weights(tau, n + 1)
         mark(6)
-        _lib.call("dism_hard_backward_prepare", tq.data_ptr(), tk.data_ptr(), tv.data_ptr(),
-                  tdo.data_ptr(), code, iq.data_ptr(), ik.data_ptr(), lse2.data_ptr(), B, T, H,
-                  D, DV, W, nbytes, S)
+        bw = (*vec, tdo.data_ptr(), code, qp, kp, hp, cp, strip, lut.data_ptr())
+        _lib.call("dism_hard_backward_row_pairs", *bw, dlut.data_ptr(), n + 1, lse2.data_ptr(),
+                  B, T, H, D, DV, W, nbytes, S)
         mark(7)
-        _lib.call("dism_hard_backward_queries", tq.data_ptr(), tk.data_ptr(), tv.data_ptr(),
-                  tdo.data_ptr(), code, iq.data_ptr(), ik.data_ptr(), hard.data_ptr(), cp, strip,
-                  lut.data_ptr(), dlut.data_ptr(), n + 1, lse2.data_ptr(), B, T, H, D, DV, W,
-                  nbytes, dsq.data_ptr(), rowtau.data_ptr(), S)
+        _lib.call("dism_hard_backward_queries", *bw, dlut.data_ptr(), n + 1, lse2.data_ptr(),
+                  B, T, H, D, DV, W, nbytes, dsq.data_ptr(), rowtau.data_ptr(), S)
         mark(8)
-        _lib.call("dism_hard_backward_keys", tq.data_ptr(), tk.data_ptr(), tv.data_ptr(),
-                  tdo.data_ptr(), code, iq.data_ptr(), ik.data_ptr(), hard.data_ptr(), cp, strip,
-                  lut.data_ptr(), n + 1, lse2.data_ptr(), B, T, H, D, DV, W, nbytes,
-                  dsk.data_ptr(), dvv.data_ptr(), S)
+        _lib.call("dism_hard_backward_keys", *bw, n + 1, lse2.data_ptr(), B, T, H, D, DV, W,
+                  nbytes, dsk.data_ptr(), dvv.data_ptr(), S)
         mark(9)
-        _lib.call("dism_hard_tau_reduce", rowtau.data_ptr(), B, H, T, dtau.data_ptr(), S)
+        _lib.call("dism_hard_backward_key_pairs", *bw, n + 1, lse2.data_ptr(), B, T, H, D, DV,
+                  W, nbytes, dsk.data_ptr(), dvv.data_ptr(), S)
         mark(10)
+        _lib.call("dism_hard_tau_reduce", rowtau.data_ptr(), B, H, T, dtau.data_ptr(), S)
+        mark(11)
         return out
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    per = [[torch.cuda.Event(enable_timing=True) for _ in range(11)] for _ in range(args.steps)]
+    per = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+           for _ in range(args.steps)]
     t0 = time.perf_counter()
     start.record(stream)
     for s in range(args.steps):
@@ -151,18 +165,19 @@ def main():
     units = B * H * T
     value = units / (ms_step / 1e3)
 
-    # int-VALU roofline of BASELINE.md: 2 int ops per causal pair per pass, 2 passes
-    pairs = T * (T + 1) / 2 * B * H
-    t_int = 4 * pairs / P_INT
-    # dominant kernel: algorithmic HBM bytes per launch (no O(N^2) state)
-    dom = max(("forward", "bwd_queries", "bwd_keys"), key=lambda x: kern_ms[x])
-    per_unit = {  # bytes per (b,h,t) unit the kernel must move at minimum
-        "forward": 2 * D * 2 + 2 * DV + 2 * DV + 4 + 4 * 2,        # sq,sk,v in; O,lse2 out; labels
-        "bwd_queries": 2 * D * 2 + 2 * DV * 2 + 4 + 4 * D + 4 + 4 * 2,
-        "bwd_keys": 2 * D * 2 + 2 * DV * 2 + 4 + 4 * D + 4 * DV + 4 * 2,
-    }[dom]
-    alg_bytes = per_unit * units
+    # Roofline of the dominant single-kernel stage.  Algorithmic bytes per (b,h,t) unit: the
+    # rows the kernel must read once and write once (bf16 vectors, fp32 outputs), plus the
+    # combined-order entry and label of the unit's key and query (4 x 4 B).
+    order = 16
+    per_unit = {
+        "queries": 2 * D * 2 + 2 * DV * 2 + 3 * 4 + 4 * D + 4 + order,     # sq,sk,v,dO,lse2,G,nb -> dsq,rowtau
+        "keys": 2 * D * 2 + 2 * DV * 2 + 4 + 4 * D + 4 * DV + order,       # sq,sk,v,dO,lse2 -> dsk,dv
+    }
+    dom = max(per_unit, key=lambda x: kern_ms[x])
+    kernel_of = {"queries": "scan_rows_kernel", "keys": "scan_keys_kernel"}
+    alg_bytes = per_unit[dom] * units
     achieved = alg_bytes / (kern_ms[dom] / 1e3)
+    traffic = measured_traffic(kernel_of[dom])
     result = {
         "metric": "DISM fwd+bwd tokens/sec (B*H*T/s) at T=16k, 1 GPU",
         "value": value,
@@ -175,52 +190,67 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int32+fp32 (bf16 vectors)",
-        "data": "synthetic (BASELINE config 3 generator, seed 20261203)",
+        "dtype": "fp32 (int32 labels, bf16 vectors)",
+        "data": "synthetic (BASELINE configs[2] generator, seed 20261203)",
         "config": {"workload": "BASELINE configs[2]: hard DISM fwd+bwd, periodic heads",
                    "B": B, "H": H, "T": T, "d_qk": D, "d_v": DV, "tau": args.tau,
                    "carry_strip": strip, "global_batch": B, "seq_len": T,
                    "parallelism": "single-gpu"},
         "kernel_ms": kern_ms,
-        "int_valu_roofline": {"t_roof_ms": t_int * 1e3, "frac": t_int / (ms_step / 1e3),
-                              "peak_int_ops": P_INT,
-                              "note": "BASELINE.md accounting (2 int ops/pair/pass); the "
-                                      "bitmask sweep does far fewer ops, so frac may exceed 1"},
-        "roofline": {"kernel": dom, "bound": "hbm", "achieved": achieved / 1e9,
+        "roofline": {"kernel": kernel_of[dom], "bound": "hbm", "achieved": achieved / 1e9,
                      "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": achieved / HBM_PEAK,
-                     "traffic": None, "alg_bytes_per_unit": per_unit},
+                     "traffic": traffic, "alg_bytes_per_unit": per_unit[dom],
+                     "launch_ms": kern_ms[dom]},
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(q, k, v, do, args)
     print(json.dumps(result), flush=True)
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` on this workload from the committed rocprofv3 PMC
+    summary (profiles/traffic.json: FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), or
+    None when no measurement is committed."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        return t["kernels"][kernel]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(q, k, v, do, args):
-    """CPU model (oracle/dism_cpu_model.c) fwd+bwd on a bounded sample: batch 0, the first
-    `cpu_heads` heads (head 0 carries the periodic component), full T, all host threads."""
+    """CPU model (oracle/dism_cpu_model.c, the decomposed fp32 sequence the GPU reproduces)
+    fwd+bwd on the whole workload, OpenMP over (b,h) rows, repeated until >= 10 s of wall
+    time; threads = the host cores available to this process (at most 16)."""
     import oracle
     oracle.build()
     from oracle import bf16_round
-    hs = slice(0, args.cpu_heads)
-    sq = bf16_round(q[:1, :, hs])
-    sk = bf16_round(k[:1, :, hs])
-    vv = bf16_round(v[:1, :, hs])
-    dd = bf16_round(do[:1, :, hs])
-    Hs = sq.shape[2]
+    sq, sk, vv, dd = bf16_round(q), bf16_round(k), bf16_round(v), bf16_round(do)
+    Bs, _, Hs, _ = sq.shape
     iq, ik = oracle.sign_labels(sq), oracle.sign_labels(sk)
     tau = np.full(Hs, args.tau, np.float32)
-    hard = np.ones((1, Hs), bool)
-    threads = os.cpu_count() or 1
-    t0 = time.perf_counter()
-    lut = oracle.log_weights(tau, args.T)
-    dl = oracle.dlog_weights(tau, args.T)
-    _, l2, _, _ = oracle.forward(sq, sk, vv, iq, ik, hard, lut, threads=threads)
-    oracle.backward(sq, sk, vv, dd, iq, ik, hard, lut, dl, l2, threads=threads)
-    dt = time.perf_counter() - t0
-    units = Hs * args.T
-    return {"value": units / dt, "unit": "B*H*T/s", "cores": min(threads, Hs), "kind": "port",
-            "sample": f"B=1 H={Hs} T={args.T} fwd+bwd, OpenMP over (b,h) rows, {dt:.1f}s",
-            "host_threads": threads}
+    hard = np.ones((Bs, Hs), bool)
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    threads = max(1, min(16, avail))
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        lut = oracle.log_weights(tau, args.T)
+        dl = oracle.dlog_weights(tau, args.T)
+        _, l2, _, _ = oracle.forward(sq, sk, vv, iq, ik, hard, lut, threads=threads)
+        oracle.backward(sq, sk, vv, dd, iq, ik, hard, lut, dl, l2, threads=threads)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= 10.0:
+            break
+    units = reps * Bs * Hs * args.T
+    return {"value": units / dt, "unit": "B*H*T/s", "cores": threads, "kind": "port",
+            "sample": f"full workload B={Bs} H={Hs} T={args.T} fwd+bwd x{reps} "
+                      f"({dt:.1f} s wall, {threads} threads)"}
 
 
 if __name__ == "__main__":

@@ -23,12 +23,14 @@ SIGNATURES = {
                           _I32, _I32, _P, _I64, _P, _I32, _P, _P, _P, _P],
     "dism_hard_backward": [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _P, _I64, _P, _I64,
                            _I64, _I64, _I32, _I32, _P, _I64, _P, _P, _P, _P, _P, _P],
-    "dism_hard_backward_prepare": [_P, _P, _P, _P, _I32, _P, _P, _P, _I64, _I64, _I64, _I32,
-                                   _I32, _P, _I64, _P],
+    "dism_hard_backward_row_pairs": [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _P, _I64,
+                                     _P, _I64, _I64, _I64, _I32, _I32, _P, _I64, _P],
     "dism_hard_backward_queries": [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _P, _I64,
                                    _P, _I64, _I64, _I64, _I32, _I32, _P, _I64, _P, _P, _P],
     "dism_hard_backward_keys": [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _I64, _P, _I64,
                                 _I64, _I64, _I32, _I32, _P, _I64, _P, _P, _P],
+    "dism_hard_backward_key_pairs": [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _I64, _P,
+                                     _I64, _I64, _I64, _I32, _I32, _P, _I64, _P, _P, _P],
     "dism_hard_tau_reduce": [_P, _I64, _I64, _I64, _P, _P],
 }
 

@@ -19,6 +19,20 @@ __global__ __launch_bounds__(256) void sign_labels_kernel(const T* __restrict__ 
     long n = t % N, bh = t / N, h = bh % H, b = bh / H;
     const T* row = x + ((b * N + n) * H + h) * d;
     int32_t lab = 0;
+    if constexpr (sizeof(T) == 2) {
+        if (d == 8 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {  // one 16-byte row
+            const uint4 w = *reinterpret_cast<const uint4*>(row);
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float v = (k & 1) ? __uint_as_float(ws[k >> 1] & 0xFFFF0000u)
+                                        : __uint_as_float(ws[k >> 1] << 16);
+                if (v > 0.0f) lab |= (1 << k);
+            }
+            out[t] = lab;
+            return;
+        }
+    }
     for (int k = 0; k < d; ++k) {
         float v;
         if constexpr (sizeof(T) == 2) {

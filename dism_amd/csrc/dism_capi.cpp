@@ -317,17 +317,22 @@ static int32_t backward_common(const void* sq, const void* sk, const void* v, co
 
 extern "C" {
 
-int32_t dism_hard_backward_prepare(const void* sq, const void* sk, const void* v,
-                                   const void* dout, int32_t dtype, const int32_t* iq,
-                                   const int32_t* ik, const float* lse2, int64_t B, int64_t N,
-                                   int64_t H, int32_t R, int32_t DV, void* workspace,
-                                   int64_t workspace_bytes, void* stream) {
-    int32_t st = check_common(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
-                              workspace_bytes, "hard backward prepare");
+int32_t dism_hard_backward_row_pairs(const void* sq, const void* sk, const void* v,
+                                     const void* dout, int32_t dtype, const int32_t* iq,
+                                     const int32_t* ik, const uint8_t* hard,
+                                     const int32_t* boundary, int32_t strip, const float* lut,
+                                     const float* dlut, int64_t lut_stride, const float* lse2,
+                                     int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
+                                     void* workspace, int64_t workspace_bytes, void* stream) {
+    dism::PathArgs a{};
+    int32_t st = backward_common(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
+                                 lut_stride, lse2, B, N, H, R, DV, workspace, workspace_bytes,
+                                 &a, "hard backward row pairs");
     if (st) return st;
-    if (!dout || !lse2) return fail(DISM_ERR_INVALID, "hard backward prepare: null pointer");
-    (void)stream;
-    return ok();
+    if (!dlut) return fail(DISM_ERR_INVALID, "hard backward: null pointer");
+    a.dlut = dlut;
+    return hip_status(dism::launch_pairs_rows(a, R, DV, dtype, S(stream)),
+                      "hard backward row pairs");
 }
 
 int32_t dism_hard_backward_queries(const void* sq, const void* sk, const void* v,
@@ -347,9 +352,6 @@ int32_t dism_hard_backward_queries(const void* sq, const void* sk, const void* v
     a.dlut = dlut;
     a.dsq = dsq;
     a.rowtau = rowtau;
-    if ((st = hip_status(dism::launch_pairs_rows(a, R, DV, dtype, S(stream)),
-                         "hard backward row pairs")))
-        return st;
     return hip_status(dism::launch_scan_rows(a, R, DV, dtype, S(stream)), "hard backward rows");
 }
 
@@ -368,9 +370,25 @@ int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, c
     if (!dsk || !dv) return fail(DISM_ERR_INVALID, "hard backward: null pointer");
     a.dsk = dsk;
     a.dv = dv;
-    if ((st = hip_status(dism::launch_scan_keys(a, R, DV, dtype, S(stream)),
-                         "hard backward keys")))
-        return st;
+    return hip_status(dism::launch_scan_keys(a, R, DV, dtype, S(stream)), "hard backward keys");
+}
+
+int32_t dism_hard_backward_key_pairs(const void* sq, const void* sk, const void* v,
+                                     const void* dout, int32_t dtype, const int32_t* iq,
+                                     const int32_t* ik, const uint8_t* hard,
+                                     const int32_t* boundary, int32_t strip, const float* lut,
+                                     int64_t lut_stride, const float* lse2, int64_t B, int64_t N,
+                                     int64_t H, int32_t R, int32_t DV, void* workspace,
+                                     int64_t workspace_bytes, float* dsk, float* dv,
+                                     void* stream) {
+    dism::PathArgs a{};
+    int32_t st = backward_common(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
+                                 lut_stride, lse2, B, N, H, R, DV, workspace, workspace_bytes,
+                                 &a, "hard backward key pairs");
+    if (st) return st;
+    if (!dsk || !dv) return fail(DISM_ERR_INVALID, "hard backward: null pointer");
+    a.dsk = dsk;
+    a.dv = dv;
     return hip_status(dism::launch_pairs_keys(a, R, DV, dtype, S(stream)),
                       "hard backward key pairs");
 }
@@ -392,8 +410,9 @@ int32_t dism_hard_backward(const void* sq, const void* sk, const void* v, const 
                            int32_t DV, void* workspace, int64_t workspace_bytes, float* dsq,
                            float* dsk, float* dv, float* rowtau, float* dtau, void* stream) {
     if (!dtau) return fail(DISM_ERR_INVALID, "hard backward: null pointer");
-    int32_t st = dism_hard_backward_prepare(sq, sk, v, dout, dtype, iq, ik, lse2, B, N, H, R, DV,
-                                            workspace, workspace_bytes, stream);
+    int32_t st = dism_hard_backward_row_pairs(sq, sk, v, dout, dtype, iq, ik, hard, boundary,
+                                              strip, lut, dlut, lut_stride, lse2, B, N, H, R, DV,
+                                              workspace, workspace_bytes, stream);
     if (st) return st;
     st = dism_hard_backward_queries(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
                                     dlut, lut_stride, lse2, B, N, H, R, DV, workspace,
@@ -402,6 +421,10 @@ int32_t dism_hard_backward(const void* sq, const void* sk, const void* v, const 
     st = dism_hard_backward_keys(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
                                  lut_stride, lse2, B, N, H, R, DV, workspace, workspace_bytes,
                                  dsk, dv, stream);
+    if (st) return st;
+    st = dism_hard_backward_key_pairs(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
+                                      lut_stride, lse2, B, N, H, R, DV, workspace,
+                                      workspace_bytes, dsk, dv, stream);
     if (st) return st;
     return dism_hard_tau_reduce(rowtau, B, H, N, dtau, stream);
 }

@@ -165,7 +165,7 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
             const int p = ent >> 1;
             const bool isq = ent & 1;
             load_words<W>((isq ? sq : sk) + (it.row0 + (long)p * a.H) * R, wN);
-            nbN = a.pnb[it.so + p];
+            nbN = isq ? a.pnb[it.so + p] : 0;
             const bool ok = lane < wk.count(kk);
             const unsigned long long km = __ballot(ok && !isq);
             const int nk = __popcll(km);
@@ -333,12 +333,14 @@ __global__ __launch_bounds__(64 * WAVES) void scan_rows_kernel(PathArgs a) {
             const int p = ent >> 1;
             const bool isq = ent & 1;
             load_words<W>((isq ? sq : sk) + (it.row0 + (long)p * a.H) * R, wN);
-            xN[0] = __float_as_uint(a.lse2[it.so + p]);
-            xN[1] = __float_as_uint(glut[p + 1]);
-            xN[2] = (uint32_t)a.pnb[it.so + p];
+            // row statistics only for query entries, corrections only for rows with pairs
+            xN[0] = isq ? __float_as_uint(a.lse2[it.so + p]) : 0u;
+            xN[1] = isq ? __float_as_uint(glut[p + 1]) : 0u;
+            xN[2] = isq ? (uint32_t)a.pnb[it.so + p] : 0u;
             const float* rec = a.prow + (it.so + p) * a.prow_stride;
+            const bool has = isq && xN[2] > 0;
 #pragma unroll
-            for (int x = 0; x < R + 4; ++x) xN[3 + x] = __float_as_uint(rec[x]);
+            for (int x = 0; x < R + 4; ++x) xN[3 + x] = has ? __float_as_uint(rec[x]) : 0u;
             const int n_ok = wk.count(kk);
             dma_rows<RB, NI>((lds_u8*)s_v[kk & 1], n_ok, [&](int s) {
                 const int es = __shfl(ent, s);
@@ -493,7 +495,7 @@ __global__ __launch_bounds__(64 * WAVES) void scan_keys_kernel(PathArgs a) {
             const int p = ent >> 1;
             const bool isq = ent & 1;
             load_words<W>((isq ? sq : sk) + (it.row0 + (long)p * a.H) * R, wN);
-            lN = a.lse2[it.so + p];
+            lN = isq ? a.lse2[it.so + p] : 0.0f;
             dma_rows<RB, NI>((lds_u8*)s_v[kk & 1], wk.count(kk), [&](int s) {
                 const int es = __shfl(ent, s);
                 return ((es & 1) ? db : vb) + (it.row0 + (long)(es >> 1) * a.H) * RB;

@@ -5,11 +5,12 @@ forward_hard): same names, argument meaning, defaults and RuntimeError texts.
 
 Differences by design (the reference's chain is summary -> chunk -> LUT -> readout with an
 O(B*H*N^2/32) int32 boundary in between):
-  * forward_hard computes the LUT and runs the readout directly; match lengths are
-    recomputed from the labels inside the readout, optionally helped by a composed boundary
-    of strip height ``carry_strip`` (default 256: B*H*N^2/256 int32, an 8x smaller buffer
-    that bounds the per-match walk on long repeats).  With save_state=True the reference's
-    strip-32 summary/boundary are produced too, so callers that inspect them still work;
+  * forward_hard computes the LUT and runs the readout directly; match lengths of the
+    (rare) pairs with L >= 2 are recomputed from the labels by a suffix walk inside the
+    readout.  ``carry_strip`` S > 0 (default 0 = off, env DISM_HARD_CARRY_STRIP) adds a
+    composed boundary of strip height S (B*H*N^2/S int32) that bounds each walk by S steps,
+    for inputs with very long repeats.  With save_state=True the reference's strip-32
+    summary/boundary are produced too, so callers that inspect them still work;
   * fp32 vectors are accepted besides bf16 (all vectors share one dtype);
   * ``return_matches=True`` additionally returns, per query, the longest match length and
     its key index (ties -> most recent key, -1 if none).
@@ -23,7 +24,7 @@ from ._checks import (DTYPE_CODE, check_ctas, check_graph_choice, check_hard, ch
                       check_layout, check_tensor, check_vectors, require)
 from .summary import hard_boundary, hard_chunk_scan, summarize_hard
 
-DEFAULT_CARRY_STRIP = int(os.environ.get("DISM_HARD_CARRY_STRIP", "256"))
+DEFAULT_CARRY_STRIP = int(os.environ.get("DISM_HARD_CARRY_STRIP", "0"))
 
 
 def _stream(t):

@@ -73,17 +73,23 @@ int32_t dism_hard_boundary(const int32_t* iq, const int32_t* ik, const uint8_t* 
                            int64_t H, int64_t N, int32_t strip, int32_t fill_all,
                            int32_t* boundary, void* stream);
 
-/* Size in bytes of the caller-owned workspace used by the bucketed sweeps for these
- * dimensions (-1 for unsupported dimensions).  Layout: bucket-sorted query/key positions and
- * bucket tables, non-finite flags, key records and query records (dism_amd/csrc/dism_capi.cpp).
+/* Size in bytes of the caller-owned workspace for these dimensions (-1 for unsupported
+ * dimensions).  It holds the position orders of dism_hard_prepare (combined label order of
+ * queries and keys, bigram orders of each side), the bigram-pair plans, and one record per
+ * query row (pair statistics / partial readout in the forward, row corrections in the
+ * backward); about 4*B*H*N*(DV + 30) bytes.
  * No reference counterpart: the reference keeps an O(B*H*N^2/32) int32 boundary instead. */
 int64_t dism_hard_workspace_bytes(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
                                   int32_t dtype);
 
-/* Forward preparation into `workspace`: stable counting sort of query and key positions by
- * label & 255 per (b,h), non-finite flags of sq/sk/v, key records (position, labels, sk row,
- * v row) in bucket order.  Replaces the summary + chunk passes that precede the reference
- * readout (dism_v3/python/flash_dism/hard_forward.py:36-40). */
+/* Preparation into `workspace` (labels only; the vectors are validated, not read):
+ *   - per (b,h): stable radix sorts giving the combined label order of the 2N query/key
+ *     entries and the bigram order (label[p-1], label[p]) of each side;
+ *   - per query row and per key: the range of its bigram partners (the pairs with match
+ *     length >= 2) and the list of owners that have any.
+ * A workspace prepared once serves dism_hard_readout and the backward entry points for the
+ * same labels.  Replaces the summary + chunk passes that precede the reference readout
+ * (dism_v3/python/flash_dism/hard_forward.py:36-40). */
 int32_t dism_hard_prepare(const void* sq, const void* sk, const void* v, int32_t dtype,
                           const int32_t* iq, const int32_t* ik, int64_t B, int64_t N, int64_t H,
                           int32_t R, int32_t DV, void* workspace, int64_t workspace_bytes,
@@ -93,7 +99,7 @@ int32_t dism_hard_prepare(const void* sq, const void* sk, const void* v, int32_t
  * fp32; optional lmax/jarg [B,H,N] int32 receive the longest match length per query and its
  * key (ties -> most recent key, -1 if none).  boundary may be NULL (lengths recomputed from
  * labels alone) or a composed boundary of strip height `strip`.  lut_stride >= N+1.  Soft
- * rows give zeros.
+ * rows give zeros.  Vector pointers must be 16-byte aligned.
  * Replaces cu.hard_readout (dism_v3/src/host/hard_forward.cpp:25-113). */
 int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t dtype,
                           const int32_t* iq, const int32_t* ik, const uint8_t* hard,
@@ -103,10 +109,10 @@ int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t
                           int32_t out_dtype, float* lse2, int32_t* lmax, int32_t* jarg,
                           void* stream);
 
-/* Hard backward on a workspace prepared by dism_hard_prepare for the same inputs: dsq, dsk
+/* Hard backward on a workspace prepared by dism_hard_prepare for the same labels: dsq, dsk
  * [B,N,H,R], dv [B,N,H,DV], rowtau [B,H,N] (caller-owned scratch) and dtau [H], all fp32,
- * deterministic (no atomics).  lse2 is the forward's log2 normalizer; lut/dlut share
- * lut_stride >= N+1.  Runs the four stages below in order.
+ * deterministic (no floating-point atomics).  lse2 is the forward's log2 normalizer;
+ * lut/dlut share lut_stride >= N+1.  Runs the five stages below in order.
  * Replaces cu.hard_backward (dism_v3/src/host/hard_backward.cpp:13-140). */
 int32_t dism_hard_backward(const void* sq, const void* sk, const void* v, const void* dout,
                            int32_t dtype, const int32_t* iq, const int32_t* ik,
@@ -116,17 +122,21 @@ int32_t dism_hard_backward(const void* sq, const void* sk, const void* v, const 
                            int32_t DV, void* workspace, int64_t workspace_bytes, float* dsq,
                            float* dsk, float* dv, float* rowtau, float* dtau, void* stream);
 
-/* Stages of dism_hard_backward, callable separately (same arguments).  Together they replace
- * the hard_dlog_weights / hard_backward / hard_tau_reduce launch sequence of
- * dism_v3/src/host/hard_backward.cpp:242-252:
- *   prepare: non-finite flag of dO, query records (position, labels, lse2, sq row, dO row);
- *   queries: query sweep -> dsq, rowtau;  keys: key sweep -> dsk, dv;
+/* Stages of dism_hard_backward, one kernel each, callable separately in this order (same
+ * arguments as above).  Together they replace the hard_dlog_weights / hard_backward /
+ * hard_tau_reduce launch sequence of dism_v3/src/host/hard_backward.cpp:242-252:
+ *   row_pairs:  corrections of the query rows' bigram pairs into the workspace;
+ *   queries:    label scan of the query rows -> dsq, rowtau (uses row_pairs);
+ *   keys:       label scan of the keys -> dsk, dv (length-1 part);
+ *   key_pairs:  adds the keys' bigram-pair corrections to dsk, dv in place;
  *   tau_reduce: fixed-order reduction rowtau -> dtau. */
-int32_t dism_hard_backward_prepare(const void* sq, const void* sk, const void* v,
-                                   const void* dout, int32_t dtype, const int32_t* iq,
-                                   const int32_t* ik, const float* lse2, int64_t B, int64_t N,
-                                   int64_t H, int32_t R, int32_t DV, void* workspace,
-                                   int64_t workspace_bytes, void* stream);
+int32_t dism_hard_backward_row_pairs(const void* sq, const void* sk, const void* v,
+                                     const void* dout, int32_t dtype, const int32_t* iq,
+                                     const int32_t* ik, const uint8_t* hard,
+                                     const int32_t* boundary, int32_t strip, const float* lut,
+                                     const float* dlut, int64_t lut_stride, const float* lse2,
+                                     int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
+                                     void* workspace, int64_t workspace_bytes, void* stream);
 int32_t dism_hard_backward_queries(const void* sq, const void* sk, const void* v,
                                    const void* dout, int32_t dtype, const int32_t* iq,
                                    const int32_t* ik, const uint8_t* hard,
@@ -142,6 +152,14 @@ int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, c
                                 int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
                                 void* workspace, int64_t workspace_bytes, float* dsk, float* dv,
                                 void* stream);
+int32_t dism_hard_backward_key_pairs(const void* sq, const void* sk, const void* v,
+                                     const void* dout, int32_t dtype, const int32_t* iq,
+                                     const int32_t* ik, const uint8_t* hard,
+                                     const int32_t* boundary, int32_t strip, const float* lut,
+                                     int64_t lut_stride, const float* lse2, int64_t B, int64_t N,
+                                     int64_t H, int32_t R, int32_t DV, void* workspace,
+                                     int64_t workspace_bytes, float* dsk, float* dv,
+                                     void* stream);
 int32_t dism_hard_tau_reduce(const float* rowtau, int64_t B, int64_t H, int64_t N, float* dtau,
                              void* stream);
 
