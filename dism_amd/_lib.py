@@ -74,7 +74,7 @@ def call(name, *args):
 
 
 def workspace_bytes(B, N, H, R, DV, dtype_code):
-    """Bytes of the caller-owned sweep workspace (raises for unsupported dimensions)."""
+    """Bytes of the caller-owned workspace (raises for unsupported dimensions)."""
     nbytes = load().dism_hard_workspace_bytes(B, N, H, R, DV, dtype_code)
     if nbytes < 0:
         raise RuntimeError(f"unsupported hard-core dimensions B={B} N={N} H={H} R={R} DV={DV}")

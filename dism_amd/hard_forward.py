@@ -61,8 +61,9 @@ def hard_dlog_weights(tau, stride):
 
 
 def prepare_workspace(sq, sk, v, idx_q, idx_k):
-    """Allocate the sweep workspace and fill it (label buckets, key records, non-finite
-    flags) for these inputs.  Returns the uint8 workspace tensor."""
+    """Allocate the workspace and fill it for these labels: the combined label order of
+    queries and keys, the bigram orders of each side and the bigram-pair plans.  Returns the
+    uint8 workspace tensor."""
     b, n, h, r, dv, dt = check_vectors(sq, sk, v)
     nbytes = _lib.workspace_bytes(b, n, h, r, dv, DTYPE_CODE[dt])
     ws = torch.empty((nbytes,), dtype=torch.uint8, device=sq.device)
