@@ -51,7 +51,7 @@ hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 //   pnb/prow: per query row bigram-pair count and record (layout: dism_launch.h)
 struct Layout {
     int64_t corder, clab, ctab, bpos[2], blab[2], bplab[2], btab[2], shift, tmp[3];
-    int64_t plo[2], pcnt[2], act[2], nact[2];
+    int64_t plo[2], pcnt[2], ccount[2], own[2], ocount;
     int64_t pnb, prow, total;
     int prow_stride;
 };
@@ -81,9 +81,10 @@ Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     for (int s = 0; s < 2; ++s) {
         L.plo[s] = take(BH * N * 4);
         L.pcnt[s] = take(BH * N * 4);
-        L.act[s] = take(BH * N * 4);
-        L.nact[s] = take(BH * 4);
+        L.ccount[s] = take(BH * ((N + 63) / 64) * 16);
+        L.own[s] = take(BH * N * 16);
     }
+    L.ocount = take(8 * 4);
     L.tmp[0] = take(BH * 2 * N * 4);
     L.tmp[1] = take(BH * N * 4);
     L.tmp[2] = take(BH * N * 4);
@@ -113,9 +114,10 @@ dism::Orders orders(const Layout& L, void* ws) {
     for (int s = 0; s < 2; ++s) {
         o.plo[s] = at<int32_t>(ws, L.plo[s]);
         o.pcnt[s] = at<int32_t>(ws, L.pcnt[s]);
-        o.act[s] = at<int32_t>(ws, L.act[s]);
-        o.nact[s] = at<int32_t>(ws, L.nact[s]);
+        o.ccount[s] = at<int32_t>(ws, L.ccount[s]);
+        o.own[s] = at<int4>(ws, L.own[s]);
     }
+    o.ocount = at<int32_t>(ws, L.ocount);
     return o;
 }
 
@@ -147,6 +149,8 @@ int32_t check_common(const void* sq, const void* sk, const void* v, int32_t dtyp
     if (!sq || !sk || !v || !iq || !ik || !ws)
         return fail(DISM_ERR_INVALID, "%s: null pointer", what);
     if (!dims_ok(B, N, H)) return fail(DISM_ERR_INVALID, "%s: positive dimensions required", what);
+    if (B * H * N > INT_MAX)
+        return fail(DISM_ERR_INVALID, "%s: B*H*N must be below 2^31", what);
     if (!rdv_ok(R, DV))
         return fail(DISM_ERR_UNSUPPORTED, "%s: unsupported R=%d DV=%d", what, R, DV);
     if (!dtype_ok(dtype))
@@ -230,7 +234,8 @@ int32_t dism_hard_boundary(const int32_t* iq, const int32_t* ik, const uint8_t* 
 
 int64_t dism_hard_workspace_bytes(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
                                   int32_t dtype) {
-    if (!dims_ok(B, N, H) || !rdv_ok(R, DV) || !dtype_ok(dtype)) return -1;
+    if (!dims_ok(B, N, H) || B * H * N > INT_MAX || !rdv_ok(R, DV) || !dtype_ok(dtype))
+        return -1;
     return layout(B, N, H, R, DV).total;
 }
 
@@ -280,9 +285,7 @@ int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t
     a.lse2 = lse2;
     a.lmax = lmax;
     a.jarg = jarg;
-    int32_t st2 = hip_status(dism::launch_pairs_stats(a, R, DV, dtype, S(stream)),
-                             "hard readout pairs");
-    if (st2) return st2;
+    int32_t st2;
     if ((st2 = hip_status(dism::launch_scan_forward(a, R, DV, dtype, S(stream)), "hard readout")))
         return st2;
     return hip_status(dism::launch_pairs_finish(a, R, DV, dtype, S(stream)),

@@ -31,7 +31,11 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
 template <typename T, int N>
 __device__ __forceinline__ void load_row(const T* p, float* out) {
     if constexpr (sizeof(T) == 2) {
-        if constexpr ((N * 2) % 16 == 0) {
+        if constexpr (N % 2 == 1) {
+            const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
+#pragma unroll
+            for (int c = 0; c < N; ++c) out[c] = __uint_as_float((uint32_t)q[c] << 16);
+        } else if constexpr ((N * 2) % 16 == 0) {
             const uint4* q = reinterpret_cast<const uint4*>(p);
 #pragma unroll
             for (int c = 0; c < N / 8; ++c) {
@@ -58,7 +62,10 @@ __device__ __forceinline__ void load_row(const T* p, float* out) {
             }
         }
     } else {
-        if constexpr ((N * 4) % 16 == 0) {
+        if constexpr (N % 2 == 1) {
+#pragma unroll
+            for (int c = 0; c < N; ++c) out[c] = p[c];
+        } else if constexpr ((N * 4) % 16 == 0) {
             const float4* q = reinterpret_cast<const float4*>(p);
 #pragma unroll
             for (int c = 0; c < N / 4; ++c) {

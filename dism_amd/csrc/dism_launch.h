@@ -28,14 +28,23 @@ struct Orders {
     int32_t* bplab[2];
     int32_t* btab[2];
     int32_t* shift;       // [B*H]
-    // bigram-pair plans (dism_pairs.hip), side 0 query rows, 1 keys, by bigram-order index t:
-    //   plo/pcnt: first partner index in the other side's bigram order and partner count;
-    //   act/nact: indices t with pcnt > 0 (in no particular order) and their count per row.
+    // bigram-pair plans (dism_pairs.hip), side 0 query rows, 1 keys:
+    //   plo/pcnt: by bigram-order index t, first partner index in the other side's bigram
+    //             order and partner count;
+    //   ccount:   per 64-owner chunk of a bigram order ([B*H*ceil(N/64)][4]), the owners of
+    //             each class, then (after the offsets pass) each class's first list slot;
+    //   own:      a record {bh, position, plo, pcnt} per owner with partners, classes
+    //             consecutive ([small][medium][large], (b,h)-major, bigram order within);
+    //   ocount:   [4*side + class] records per class.
     int32_t* plo[2];
     int32_t* pcnt[2];
-    int32_t* act[2];
-    int32_t* nact[2];     // [B*H]
+    int32_t* ccount[2];
+    int4* own[2];
+    int32_t* ocount;      // [8]
 };
+
+constexpr int OWNER_SMALL = 8;    // partner counts <= 8: 16 owners per wave, 4 lanes each
+constexpr int OWNER_MEDIUM = 32;  // <= 32: 4 owners per wave, 16 lanes each; more: 1 per wave
 
 struct SortArgs {
     const int32_t* lab[2];  // iq, ik  [B*H*N]
@@ -46,10 +55,9 @@ struct SortArgs {
 };
 
 // Per query row record (prow, valid when the row's bigram pair count pnb > 0):
-//   forward:  [m, key count, Lmax, argmax, pair range lo, hi, -, -, y[DV]]
+//   forward:  [-, key count, -, ..., y[DV] at PREC_Y] (y: the row's length-1 readout)
 //   backward: [cdq[R], cu, cvv, cw, cz]
-enum { PREC_M = 0, PREC_CNT = 1, PREC_LB = 2, PREC_JB = 3, PREC_LO = 4, PREC_HI = 5,
-       PREC_Y = 8 };
+enum { PREC_CNT = 1, PREC_Y = 8 };
 
 // Everything the pair and scan kernels of the hard core read or write.
 struct PathArgs {
@@ -96,7 +104,6 @@ hipError_t launch_fill_i32(int32_t* p, long count, int32_t value, hipStream_t s)
 hipError_t launch_sort(const SortArgs& a, hipStream_t s);
 // The following return hipErrorInvalidValue for an unsupported (R, DV, dtype).
 hipError_t launch_pair_plan(const PathArgs& a, hipStream_t s);
-hipError_t launch_pairs_stats(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_pairs_finish(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_scan_forward(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_pairs_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);

@@ -7,23 +7,29 @@
 // visits only them.  Each pair's length comes from the suffix walk (bounded by the composed
 // carry boundary when one is given).
 //
-// Mapping (MI355X): a wave takes OWNERS = 16 consecutive owners of a bigram order, four
-// lanes per owner ("slot").  The owners' partner lists are consumed in rounds of CK = 8
-// partners per owner:
-//   phase A  lane = (slot, sub): the round's pairs (two per lane) -- walk, exp2, dot
-//            products -- with the per-pair coefficients and partner readout rows put in LDS;
+// Mapping (MI355X): the plan kernel sorts the owners that have partners into three classes
+// by partner count; a wave takes 64/G owners of one class with G lanes per owner ("slot"):
+//   small  (cnt <= 8):  G = 8,  8 owners per wave;
+//   medium (cnt <= 32): G = 32, 2 owners per wave;
+//   large:              G = 64, 1 owner per wave.
+// An owner's partners are consumed in rounds of G (one round for all but the large class
+// beyond 64 partners), so a wave's dependent-load chain does not grow with the longest
+// partner list among many owners.  Per round:
+//   phase A  lane = (slot, sub): the round's pair c0 + sub -- walk, exp2, dot products (the
+//            owner's own DV-row staged in LDS) -- with the per-pair coefficients put in LDS;
 //   phase B  lane = (slot, column group): each slot folds its round's pairs into its own
-//            running sums in ascending partner order, all 16 owners at once (value-row
-//            segments are loaded straight from HBM, one 4-pair batch at a time).
-// Long partner lists of one owner take ceil(cnt/8) rounds; owners never wait for each other
-// pair by pair.  The longest-match statistics are order-free maxima (LDS atomics).
+//            running sums in ascending partner order (partner value rows are loaded straight
+//            from HBM, four pairs at a time).
+// The kernels are persistent: a fixed grid of waves strides over the items of all three
+// classes.  The longest-match statistics are order-free maxima (LDS atomics).
 // fp32 sequences (repeated by the CPU model), per owner over its pairs in ascending partner
 // position:
 //   forward rows: m = max(0, LUT[1], LUT[L]); p1 = exp2(LUT[1]-m); p = exp2(LUT[L]-m);
 //     dp = dp + p; s = chain(sq.sk); corr[d] = fma((p - p1)*s, v_j[d], corr[d]);
 //     den = (exp2(-m) + (float)(cnt - nb)*p1) + dp; out[d] = fma(p1, y[d], corr[d]) * (1/den)
 //   backward rows (l2 = lse2_i, cc = G[i+1]): P1 = exp2(LUT[1]-l2); q1 = P1*(G[1]-cc);
-//     p = exp2(LUT[L]-l2); dp = p-P1; s, e = chains; g = G[L]-cc; a = p*g - q1;
+//     p = exp2(LUT[L]-l2); dp = p-P1; s = chain(sq.sk); e = tree(dO_i.v_j) (below);
+//     g = G[L]-cc; a = p*g - q1;
 //     cdq[r] = fma(dp*e, sk[r], cdq[r]); cu = fma(dp*s, e, cu); cvv += a;
 //     cw = fma(a, s*e, cw); cz += dp
 //   backward keys: p = exp2(LUT[L]-l2_i); dp = p - exp2(LUT[1]-l2_i);
@@ -33,8 +39,8 @@
 
 namespace dism {
 
-constexpr int OWNERS = 16;  // owners per wave, 4 lanes each
-constexpr int CK = 8;       // partners per owner per round (2 per lane in phase A)
+constexpr int PAIR_SLOTS = 64;        // pairs per wave per round (one per lane)
+constexpr unsigned PAIR_GRID = 2048;  // workgroups of the persistent pair kernels
 
 // Partner range of owner t of side SIDE's bigram order (0: query rows with key partners
 // 1 <= j <= i; 1: keys with query partners i >= j): [lo, lo + cnt) of the other side's
@@ -71,9 +77,29 @@ __device__ __forceinline__ void partner_range(const PathArgs& a, int bh, long so
     cnt_out = hi - lo;
 }
 
-// Plan kernel: one lane per owner (both sides, grid = 2 * B*H * ceil(N/64) items): partner
-// range, pair count per query row (pnb, by position), and the owners with partners appended
-// to act[side] (one atomic per wave).
+
+// Match length of a bigram pair (i, j >= 1, q[i-1] == k[j-1] known): match_length's suffix
+// walk without its first comparison.
+__device__ __forceinline__ int pair_length(const int32_t* __restrict__ q,
+                                           const int32_t* __restrict__ k, int i, int j,
+                                           const int32_t* __restrict__ bound, int strip, int n) {
+    const int lo = bound ? (i / strip) * strip : 0;
+    int c = i - 1 >= lo ? 2 : 1;
+    while (i - c >= lo && j - c >= 0 && q[i - c] == k[j - c]) ++c;
+    if (bound && lo > 0 && i - c < lo && j - c >= 0) {
+        const int jj = j - c;
+        c += jj - bound[(long)(lo / strip - 1) * n + jj];
+    }
+    return c;
+}
+
+__device__ __forceinline__ int owner_class(int cnt) {
+    return cnt <= OWNER_SMALL ? 0 : cnt <= OWNER_MEDIUM ? 1 : 2;
+}
+
+// Plan, pass 1: one lane per owner (both sides, grid = 2 * B*H * ceil(N/64) items, one
+// 64-owner chunk each): partner range (plo/pcnt), pair count per query row (pnb, by
+// position), and the chunk's owners per class.
 __global__ __launch_bounds__(64 * WAVES) void pair_plan_kernel(PathArgs a) {
     const int n = a.n, lane = lane_id();
     const int per = (n + 63) / 64;
@@ -82,7 +108,8 @@ __global__ __launch_bounds__(64 * WAVES) void pair_plan_kernel(PathArgs a) {
     const int bh = (item >> 1) / per;
     if (bh >= a.B * a.H) return;
     const long so = (long)bh * n;
-    const int t = ((item >> 1) - bh * per) * 64 + lane;
+    const int chunk = (item >> 1) - bh * per;
+    const int t = chunk * 64 + lane;
     const bool own = t < n;
     const int tc = own ? t : n - 1;
     const int p = a.o.bpos[side][so + tc];
@@ -94,198 +121,292 @@ __global__ __launch_bounds__(64 * WAVES) void pair_plan_kernel(PathArgs a) {
         a.o.pcnt[side][so + t] = cnt;
         if (side == 0) a.pnb[so + p] = cnt;
     }
-    const unsigned long long m = __ballot(own && cnt > 0);
-    if (m) {
-        int base = 0;
-        if (lane == 0) base = atomicAdd(&a.o.nact[side][bh], __popcll(m));
-        base = __shfl(base, 0);
-        if (own && cnt > 0) {
-            const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
-            a.o.act[side][so + base + __popcll(m & below)] = t;
-        }
+    const int cls = owner_class(cnt);
+    const bool has = own && cnt > 0;
+    const int c0 = __popcll(__ballot(has && cls == 0));
+    const int c1 = __popcll(__ballot(has && cls == 1));
+    const int c2 = __popcll(__ballot(has && cls == 2));
+    if (lane == 0)
+        reinterpret_cast<int4*>(a.o.ccount[side])[(long)bh * per + chunk] =
+            make_int4(c0, c1, c2, 0);
+}
+
+// Plan, pass 2: one workgroup per side turns the chunk counts into list offsets (class
+// totals first, then chunks in (b,h)-major order) and writes the class totals.
+constexpr int OFFSET_THREADS = 1024;
+__global__ __launch_bounds__(OFFSET_THREADS) void pair_offsets_kernel(PathArgs a, long chunks) {
+    __shared__ int s_scan[3][OFFSET_THREADS];
+    const int side = blockIdx.x, tid = threadIdx.x;
+    int4* cc = reinterpret_cast<int4*>(a.o.ccount[side]);
+    const long per_t = (chunks + OFFSET_THREADS - 1) / OFFSET_THREADS;
+    const long c_lo = tid * per_t < chunks ? tid * per_t : chunks;
+    const long c_hi = c_lo + per_t < chunks ? c_lo + per_t : chunks;
+    int sum[3] = {0, 0, 0};
+    for (long c = c_lo; c < c_hi; ++c) {
+        const int4 x = cc[c];
+        sum[0] += x.x;
+        sum[1] += x.y;
+        sum[2] += x.z;
+    }
+#pragma unroll
+    for (int k = 0; k < 3; ++k) s_scan[k][tid] = sum[k];
+    __syncthreads();
+    for (int off = 1; off < OFFSET_THREADS; off <<= 1) {  // inclusive Hillis-Steele scan
+        int v[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) v[k] = tid >= off ? s_scan[k][tid - off] : 0;
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 3; ++k) s_scan[k][tid] += v[k];
+        __syncthreads();
+    }
+    const int t0 = s_scan[0][OFFSET_THREADS - 1], t1 = s_scan[1][OFFSET_THREADS - 1];
+    const int t2 = s_scan[2][OFFSET_THREADS - 1];
+    int run[3] = {s_scan[0][tid] - sum[0], t0 + s_scan[1][tid] - sum[1],
+                  t0 + t1 + s_scan[2][tid] - sum[2]};
+    for (long c = c_lo; c < c_hi; ++c) {
+        const int4 x = cc[c];
+        cc[c] = make_int4(run[0], run[1], run[2], 0);
+        run[0] += x.x;
+        run[1] += x.y;
+        run[2] += x.z;
+    }
+    if (tid == 0) {
+        a.o.ocount[4 * side + 0] = t0;
+        a.o.ocount[4 * side + 1] = t1;
+        a.o.ocount[4 * side + 2] = t2;
+    }
+}
+
+// Plan, pass 3: the owner records into their class lists (same grid as pass 1).
+__global__ __launch_bounds__(64 * WAVES) void pair_scatter_kernel(PathArgs a) {
+    const int n = a.n, lane = lane_id();
+    const int per = (n + 63) / 64;
+    const int item = xcd_work_item();
+    const int side = item & 1;
+    const int bh = (item >> 1) / per;
+    if (bh >= a.B * a.H) return;
+    const long so = (long)bh * n;
+    const int chunk = (item >> 1) - bh * per;
+    const int t = chunk * 64 + lane;
+    const bool own = t < n;
+    const long tc = so + (own ? t : n - 1);
+    const int p = a.o.bpos[side][tc];
+    const int lo = a.o.plo[side][tc];
+    const int cnt = own ? a.o.pcnt[side][tc] : 0;
+    const int4 off = reinterpret_cast<const int4*>(a.o.ccount[side])[(long)bh * per + chunk];
+    const int cls = owner_class(cnt);
+    const bool has = cnt > 0;
+    const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    const unsigned long long m0 = __ballot(has && cls == 0);
+    const unsigned long long m1 = __ballot(has && cls == 1);
+    const unsigned long long m2 = __ballot(has && cls == 2);
+    if (has) {
+        const unsigned long long m = cls == 0 ? m0 : cls == 1 ? m1 : m2;
+        const int base = cls == 0 ? off.x : cls == 1 ? off.y : off.z;
+        a.o.own[side][base + __popcll(m & below)] = make_int4(bh, p, lo, cnt);
     }
 }
 
 hipError_t launch_pair_plan(const PathArgs& a, hipStream_t s) {
-    const long items = 2L * ((a.n + 63) / 64) * a.B * a.H;
-    hipLaunchKernelGGL(pair_plan_kernel, dim3(grid_for(items)), dim3(64 * WAVES), 0, s, a);
+    const long chunks = ((a.n + 63) / 64) * (long)a.B * a.H;
+    const unsigned grid = grid_for(2 * chunks);
+    hipLaunchKernelGGL(pair_plan_kernel, dim3(grid), dim3(64 * WAVES), 0, s, a);
+    hipLaunchKernelGGL(pair_offsets_kernel, dim3(2), dim3(OFFSET_THREADS), 0, s, a, chunks);
+    hipLaunchKernelGGL(pair_scatter_kernel, dim3(grid), dim3(64 * WAVES), 0, s, a);
     return hipGetLastError();
 }
 
-struct Plan {
-    bool own;    // this lane (< OWNERS) holds an owner
-    int p;       // owner position
-    int lo;      // first partner index in the other side's bigram order
-    int cnt;     // partners
-    int maxcnt;  // wave-uniform maximum of cnt
+// Work of the persistent pair kernels of one side: items [0, i0) small class (8 owners
+// each), [i0, i01) medium (2 owners), [i01, total) large (1 owner).
+struct OwnerWork {
+    int i0, i01, total, n[3], base[3];
 };
-
-struct PairItem {
-    int bh, b, h;
-    long so, row0;
-    int k0;      // first entry of the wave in act[side]
-};
-
-// Work item = (b,h) row and a block of OWNERS entries of its active-owner list; items past
-// the list's end return at once.  grid = B*H * ceil(N/OWNERS) items.
 template <int SIDE>
-__device__ __forceinline__ bool pair_item(const PathArgs& a, PairItem& it, Plan& pl) {
-    const int per = (a.n + OWNERS - 1) / OWNERS;
-    const int item = xcd_work_item();
-    it.bh = item / per;
-    if (it.bh >= a.B * a.H || !a.hard[it.bh]) return false;
-    it.k0 = (item - it.bh * per) * OWNERS;
-    const int na = a.o.nact[SIDE][it.bh];
-    if (it.k0 >= na) return false;
-    it.b = it.bh / a.H;
-    it.h = it.bh - it.b * a.H;
-    it.so = (long)it.bh * a.n;
-    it.row0 = (long)it.b * a.n * a.H + it.h;
-    const int lane = lane_id();
-    pl.own = lane < OWNERS && it.k0 + lane < na;
-    const int t = a.o.act[SIDE][it.so + (pl.own ? it.k0 + lane : it.k0)];
-    pl.p = a.o.bpos[SIDE][it.so + t];
-    pl.lo = a.o.plo[SIDE][it.so + t];
-    pl.cnt = pl.own ? a.o.pcnt[SIDE][it.so + t] : 0;
-    int mx = pl.cnt;
+__device__ __forceinline__ OwnerWork owner_work(const PathArgs& a) {
+    const int32_t* c = a.o.ocount + 4 * SIDE;
+    OwnerWork w;
+    w.n[0] = c[0];
+    w.n[1] = c[1];
+    w.n[2] = c[2];
+    w.base[0] = 0;
+    w.base[1] = w.n[0];
+    w.base[2] = w.n[0] + w.n[1];
+    w.i0 = (w.n[0] + 7) / 8;
+    w.i01 = w.i0 + (w.n[1] + 1) / 2;
+    w.total = w.i01 + w.n[2];
+    return w;
+}
+
+// Owner of this lane's slot (G lanes per slot); soft rows hold no pairs.
+struct Slot {
+    int bh, h, p, lo, cnt, maxcnt;
+    bool hard;
+    long so, row0;
+};
+template <int SIDE, int G>
+__device__ __forceinline__ bool load_slot(const PathArgs& a, int base, int k0, int ncls,
+                                          Slot& s) {
+    const int sl = lane_id() / G;
+    const int k = k0 + sl;
+    const bool in = k < ncls;
+    const int4 r = a.o.own[SIDE][base + (in ? k : ncls - 1)];
+    const int b = r.x / a.H;
+    s.bh = r.x;
+    s.h = r.x - b * a.H;
+    s.p = r.y;
+    s.lo = r.z;
+    s.hard = a.hard[r.x] != 0;
+    s.cnt = in && s.hard ? r.w : 0;  // soft rows: no pairs (their carry boundary is unset)
+    s.so = (long)r.x * a.n;
+    s.row0 = (long)b * a.n * a.H + s.h;
+    int mx = s.cnt;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         const int v = __shfl_xor(mx, o);
         mx = v > mx ? v : mx;
     }
-    pl.maxcnt = __builtin_amdgcn_readfirstlane(mx);
-    return true;
+    s.maxcnt = __builtin_amdgcn_readfirstlane(mx);
+    return s.maxcnt > 0;
 }
 
-// ---------------------------------------------------------------------------------------
-// forward, pass 1 per query row: pair count, row shift m, longest match (ties -> largest j).
-template <typename T, int R, int DV>
-__global__ __launch_bounds__(64 * WAVES) void pairs_stats_kernel(PathArgs a) {
-    __shared__ unsigned s_m_all[WAVES][OWNERS];
-    __shared__ unsigned long long s_key_all[WAVES][OWNERS];
-    auto& s_m = s_m_all[wave_id()];
-    auto& s_key = s_key_all[wave_id()];
-    PairItem it;
-    Plan pl;
-    if (!pair_item<0>(a, it, pl)) return;
-    const int n = a.n, lane = lane_id();
-    const int32_t* kb = a.o.bpos[1] + it.so;
-    const int32_t* q = a.iq + it.so;
-    const int32_t* k = a.ik + it.so;
-    const int32_t* bnd = bound_of(a, it.bh);
-    const float* lut = a.lut + (long)it.h * a.lut_stride;
-    const float lut1 = lut[1];
-    const float m0 = lut1 > 0.0f ? lut1 : 0.0f;
-    if (lane < OWNERS) {
-        s_m[lane] = __float_as_uint(m0);
-        s_key[lane] = 0ull;
+// Runs `item(G-tag, list base, first owner, class size)` for every item of side SIDE this
+// wave strides over.
+template <int G> struct Lanes { static constexpr int value = G; };
+template <int SIDE, typename F>
+__device__ __forceinline__ void for_owner_items(const PathArgs& a, F&& item) {
+    const OwnerWork w = owner_work<SIDE>(a);
+    const int stride = (int)gridDim.x * WAVES;
+    for (int vi = (int)blockIdx.x * WAVES + wave_id(); vi < w.total; vi += stride) {
+        if (vi < w.i0) item(Lanes<8>{}, w.base[0], vi * 8, w.n[0]);
+        else if (vi < w.i01) item(Lanes<32>{}, w.base[1], (vi - w.i0) * 2, w.n[1]);
+        else item(Lanes<64>{}, w.base[2], vi - w.i01, w.n[2]);
     }
-    const int sl = lane >> 2, sub = lane & 3;
-    const int i = __shfl(pl.p, sl), lo = __shfl(pl.lo, sl), cnt = __shfl(pl.cnt, sl);
-    for (int c = 0; c < pl.maxcnt; c += CK) {
+}
+
+// Pairwise tree ((t0 + t1) + (t2 + t3)) + ... over products t[d] = a[d] * b[d].
+template <int N>
+__device__ __forceinline__ float tree_dot(const float (&a)[N], const float (&b)[N]) {
+    float t[N];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int kq = c + sub + 4 * u;
-            if (kq < cnt) {
-                const int j = kb[lo + kq];
-                const int L = match_length(q, k, i, j, bnd, a.strip, n);
-                const float lw = lut[L];
-                if (lw > m0) atomicMax(&s_m[sl], __float_as_uint(lw));
-                atomicMax(&s_key[sl], ((unsigned long long)(unsigned)L << 32) | (unsigned)j);
-            }
-        }
-    }
-    if (pl.own && pl.cnt > 0) {
-        float* rec = a.prow + (it.so + pl.p) * a.prow_stride;
-        const unsigned long long key = s_key[lane];
-        rec[PREC_M] = __uint_as_float(s_m[lane]);
-        rec[PREC_LB] = __int_as_float((int)(key >> 32));
-        rec[PREC_JB] = __int_as_float((int)(key & 0xffffffffu));
-    }
+    for (int d = 0; d < N; ++d) t[d] = a[d] * b[d];
+#pragma unroll
+    for (int sz = 1; sz < N; sz *= 2)
+#pragma unroll
+        for (int g = 0; g < N; g += 2 * sz) t[g] = t[g] + t[g + sz];
+    return t[0];
 }
 
 // ---------------------------------------------------------------------------------------
-// forward, pass 2 for rows with pairs (after the label scan wrote y and the key count).
-template <typename T, int R, int DV>
-__global__ __launch_bounds__(64 * WAVES) void pairs_finish_kernel(PathArgs a) {
-    constexpr int CPL = DV / 4;  // value columns per lane in phase B
-    __shared__ float s_cf_all[WAVES][OWNERS][CK];
-    __shared__ float s_p_all[WAVES][OWNERS][CK];
-    __shared__ int s_j_all[WAVES][OWNERS][CK];
-    auto& s_cf = s_cf_all[wave_id()];
-    auto& s_p = s_p_all[wave_id()];
-    auto& s_j = s_j_all[wave_id()];
-    PairItem it;
-    Plan pl;
-    if (!pair_item<0>(a, it, pl)) return;
-    const int n = a.n, lane = lane_id();
-    const int32_t* kb = a.o.bpos[1] + it.so;
-    const int32_t* q = a.iq + it.so;
-    const int32_t* k = a.ik + it.so;
-    const int32_t* bnd = bound_of(a, it.bh);
-    const float* lut = a.lut + (long)it.h * a.lut_stride;
+// forward, rows with pairs (after the label scan wrote y and the key count): sweep 1 finds
+// the row shift m and the longest match (ties -> largest j), sweep 2 folds the corrections.
+struct FinishLds {
+    float cf[PAIR_SLOTS];
+    float p[PAIR_SLOTS];
+    int j[PAIR_SLOTS];
+    unsigned m[8];
+    unsigned long long key[8];
+};
+
+template <typename T, int R, int DV, int G>
+__device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0, int ncls,
+                                            FinishLds& S) {
+    constexpr int CPL = DV >= G ? DV / G : 1;  // value columns per lane in phase B
+    Slot s;
+    if (!load_slot<0, G>(a, base, k0, ncls, s)) return;
+    const int n = a.n, lane = lane_id(), sl = lane / G, sub = lane % G;
+    const int i = s.p, lo = s.lo, cnt = s.cnt;
+    const int32_t* kb = a.o.bpos[1] + s.so;
+    const int32_t* q = a.iq + s.so;
+    const int32_t* k = a.ik + s.so;
+    const int32_t* bnd = bound_of(a, s.bh);
+    const float* lut = a.lut + (long)s.h * a.lut_stride;
     const T* sq = reinterpret_cast<const T*>(a.sq);
     const T* sk = reinterpret_cast<const T*>(a.sk);
     const T* v = reinterpret_cast<const T*>(a.v);
-
-    const int sl = lane >> 2, cg = lane & 3;
-    const int i = __shfl(pl.p, sl), lo = __shfl(pl.lo, sl), cnt = __shfl(pl.cnt, sl);
-    const float* rec = a.prow + (it.so + i) * a.prow_stride;
-    const float m = cnt > 0 ? rec[PREC_M] : 0.0f;
-    const float p1 = exp2_fp32(lut[1] - m);
+    const float lut1 = lut[1];
+    const float m0 = lut1 > 0.0f ? lut1 : 0.0f;
+    if (sub == 0) {
+        S.m[sl] = __float_as_uint(m0);
+        S.key[sl] = 0ull;
+    }
+    int j0 = 0, L0 = 1;  // round 0's partner and length, reused by sweep 2
+    for (int c0 = 0; c0 < s.maxcnt; c0 += G) {
+        const int kq = c0 + sub;
+        if (kq < cnt) {
+            const int j = kb[lo + kq];
+            const int L = pair_length(q, k, i, j, bnd, a.strip, n);
+            const float lw = lut[L];
+            if (lw > m0) atomicMax(&S.m[sl], __float_as_uint(lw));
+            atomicMax(&S.key[sl], ((unsigned long long)(unsigned)L << 32) | (unsigned)j);
+            if (c0 == 0) {
+                j0 = j;
+                L0 = L;
+            }
+        }
+    }
+    const float m = __uint_as_float(S.m[sl]);
+    const unsigned long long key = S.key[sl];
+    const float p1 = exp2_fp32(lut1 - m);
     float sqr[R];
-    load_row<T, R>(sq + (it.row0 + (long)i * a.H) * R, sqr);
+    load_row<T, R>(sq + (s.row0 + (long)i * a.H) * R, sqr);
+    const int cg = sub;
+    const bool cols = cg * CPL < DV;
     float dp = 0.0f, corr[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) corr[c] = 0.0f;
+    float* cf_s = S.cf + sl * G;
+    float* p_s = S.p + sl * G;
+    int* j_s = S.j + sl * G;
 
-    for (int c0 = 0; c0 < pl.maxcnt; c0 += CK) {
-        // phase A: pairs (slot, c0 + cg + 4u)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int kq = c0 + cg + 4 * u;
-            if (kq < cnt) {
-                const int j = kb[lo + kq];
-                const int L = match_length(q, k, i, j, bnd, a.strip, n);
-                const float p = exp2_fp32(lut[L] - m);
-                float skr[R];
-                load_row<T, R>(sk + (it.row0 + (long)j * a.H) * R, skr);
-                float s = 0.0f;
-#pragma unroll
-                for (int r = 0; r < R; ++r) s = __builtin_fmaf(sqr[r], skr[r], s);
-                s_cf[sl][cg + 4 * u] = (p - p1) * s;
-                s_p[sl][cg + 4 * u] = p;
-                s_j[sl][cg + 4 * u] = j;
+    for (int c0 = 0; c0 < s.maxcnt; c0 += G) {
+        // phase A: pair (slot, c0 + sub)
+        const int kq = c0 + sub;
+        if (kq < cnt) {
+            int j = j0, L = L0;
+            if (c0 > 0) {
+                j = kb[lo + kq];
+                L = pair_length(q, k, i, j, bnd, a.strip, n);
             }
+            const float p = exp2_fp32(lut[L] - m);
+            float skr[R];
+            load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
+            float sdot = 0.0f;
+#pragma unroll
+            for (int r = 0; r < R; ++r) sdot = __builtin_fmaf(sqr[r], skr[r], sdot);
+            cf_s[sub] = (p - p1) * sdot;
+            p_s[sub] = p;
+            j_s[sub] = j;
         }
-        // phase B: slot sl folds pairs c0 .. c0+7 in order, lane = column group cg
-        const int nv = cnt - c0 < CK ? cnt - c0 : CK;
+        // phase B: the slot folds its round's pairs in order, lane = column group cg
+        const int nv = cnt - c0 < G ? cnt - c0 : G;
+        if (cols) {
+            for (int h0 = 0; h0 < nv; h0 += 4) {
+                float vr[4][CPL];
 #pragma unroll
-        for (int h0 = 0; h0 < CK; h0 += 4) {
-            float vr[4][CPL];
+                for (int u = 0; u < 4; ++u) {
+                    const int jj = j_s[h0 + u < nv ? h0 + u : nv - 1];
+                    load_row<T, CPL>(v + (s.row0 + (long)jj * a.H) * DV + cg * CPL, vr[u]);
+                }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int j = s_j[sl][h0 + u];
-                if (h0 + u < nv)
-                    load_row<T, CPL>(v + (it.row0 + (long)j * a.H) * DV + cg * CPL, vr[u]);
-            }
+                for (int u = 0; u < 4; ++u) {
+                    if (h0 + u < nv) {
+                        dp = dp + p_s[h0 + u];
+                        const float cf = cf_s[h0 + u];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                if (h0 + u < nv) {
-                    dp = dp + s_p[sl][h0 + u];
-                    const float cf = s_cf[sl][h0 + u];
-#pragma unroll
-                    for (int c = 0; c < CPL; ++c) corr[c] = __builtin_fmaf(cf, vr[u][c], corr[c]);
+                        for (int c = 0; c < CPL; ++c)
+                            corr[c] = __builtin_fmaf(cf, vr[u][c], corr[c]);
+                    }
                 }
             }
         }
     }
-    if (cnt > 0) {
-        const int nb = cnt;
+    if (s.hard && cnt > 0 && cols) {
+        const float* rec = a.prow + (s.so + i) * a.prow_stride;
         const int kc = __float_as_int(rec[PREC_CNT]);
-        const float den = (exp2_fp32(-m) + (float)(kc - nb) * p1) + dp;
+        const float den = (exp2_fp32(-m) + (float)(kc - cnt) * p1) + dp;
         const float rden = 1.0f / den;
-        const long orow = it.row0 + (long)i * a.H;
+        const long orow = s.row0 + (long)i * a.H;
         const float* y = rec + PREC_Y + cg * CPL;
         if (a.out_dtype == DTYPE_F32) {
             float* o = reinterpret_cast<float*>(a.out) + orow * DV + cg * CPL;
@@ -293,120 +414,141 @@ __global__ __launch_bounds__(64 * WAVES) void pairs_finish_kernel(PathArgs a) {
             for (int c = 0; c < CPL; ++c) o[c] = __builtin_fmaf(p1, y[c], corr[c]) * rden;
         } else {
             uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + orow * DV + cg * CPL;
+            if constexpr (CPL == 1) {
+                o[0] = (uint16_t)f32_to_bf16_bits(__builtin_fmaf(p1, y[0], corr[0]) * rden);
+            } else {
 #pragma unroll
-            for (int c = 0; c < CPL; c += 2) {
-                const uint32_t w0 = f32_to_bf16_bits(__builtin_fmaf(p1, y[c], corr[c]) * rden);
-                const uint32_t w1 =
-                    f32_to_bf16_bits(__builtin_fmaf(p1, y[c + 1], corr[c + 1]) * rden);
-                reinterpret_cast<uint32_t*>(o)[c / 2] = w0 | (w1 << 16);
+                for (int c = 0; c < CPL; c += 2) {
+                    const uint32_t w0 =
+                        f32_to_bf16_bits(__builtin_fmaf(p1, y[c], corr[c]) * rden);
+                    const uint32_t w1 =
+                        f32_to_bf16_bits(__builtin_fmaf(p1, y[c + 1], corr[c + 1]) * rden);
+                    reinterpret_cast<uint32_t*>(o)[c / 2] = w0 | (w1 << 16);
+                }
             }
         }
         if (cg == 0) {
-            a.lse2[it.so + i] = m + log2_fp32(den);
-            if (a.lmax) a.lmax[it.so + i] = __float_as_int(rec[PREC_LB]);
-            if (a.jarg) a.jarg[it.so + i] = __float_as_int(rec[PREC_JB]);
+            a.lse2[s.so + i] = m + log2_fp32(den);
+            if (a.lmax) a.lmax[s.so + i] = (int)(key >> 32);
+            if (a.jarg) a.jarg[s.so + i] = (int)(key & 0xffffffffu);
         }
     }
 }
 
-// ---------------------------------------------------------------------------------------
-// backward, query rows: row corrections [cdq[R], cu, cvv, cw, cz] and the pair count.
 template <typename T, int R, int DV>
-__global__ __launch_bounds__(64 * WAVES) void pairs_rows_kernel(PathArgs a) {
-    constexpr int NF = 6;  // de, ds, e, av, se, dp
-    __shared__ float s_f_all[WAVES][OWNERS][CK][NF];
-    __shared__ float s_sk_all[WAVES][OWNERS][CK][R];
-    auto& s_f = s_f_all[wave_id()];
-    auto& s_sk = s_sk_all[wave_id()];
-    PairItem it;
-    Plan pl;
-    if (!pair_item<0>(a, it, pl)) return;
-    const int n = a.n, lane = lane_id();
-    const int32_t* kb = a.o.bpos[1] + it.so;
-    const int32_t* q = a.iq + it.so;
-    const int32_t* k = a.ik + it.so;
-    const int32_t* bnd = bound_of(a, it.bh);
-    const float* lut = a.lut + (long)it.h * a.lut_stride;
-    const float* glut = a.dlut + (long)it.h * a.lut_stride;
+__global__ __launch_bounds__(64 * WAVES) void pairs_finish_kernel(PathArgs a) {
+    __shared__ FinishLds s_all[WAVES];
+    FinishLds& S = s_all[wave_id()];
+    for_owner_items<0>(a, [&](auto g, int base, int k0, int ncls) {
+        finish_item<T, R, DV, decltype(g)::value>(a, base, k0, ncls, S);
+    });
+}
+
+// Rows and keys: the DV-dot e = dO_i . v_j of each pair is taken in phase B, where the slot's
+// lanes hold column groups: each lane's CPL contiguous columns as a pairwise tree of
+// products, then the pairwise tree over the slot's lanes (group_sum) -- together the
+// pairwise tree ((t0 + t1) + (t2 + t3)) + ... over all DV products t[d] = dO_i[d] * v_j[d].
+
+// ---------------------------------------------------------------------------------------
+// backward, query rows: row corrections [cdq[R], cu, cvv, cw, cz].
+template <int R>
+struct RowsLds {
+    float f[PAIR_SLOTS][4];  // dp, s, av, j (bits)
+    float sk[PAIR_SLOTS][R];
+};
+
+template <typename T, int R, int DV, int G>
+__device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, int ncls,
+                                          RowsLds<R>& S) {
+    constexpr int RL = (R + G - 1) / G;        // readout rows per lane in phase B
+    constexpr int CPL = DV >= G ? DV / G : 1;  // value columns per lane in phase B
+    constexpr int GE = DV >= G ? G : DV;       // lanes of a slot holding columns
+    Slot s;
+    if (!load_slot<0, G>(a, base, k0, ncls, s)) return;
+    const int n = a.n, lane = lane_id(), sl = lane / G, sub = lane % G;
+    const int i = s.p, lo = s.lo, cnt = s.cnt;
+    const int32_t* kb = a.o.bpos[1] + s.so;
+    const int32_t* q = a.iq + s.so;
+    const int32_t* k = a.ik + s.so;
+    const int32_t* bnd = bound_of(a, s.bh);
+    const float* lut = a.lut + (long)s.h * a.lut_stride;
+    const float* glut = a.dlut + (long)s.h * a.lut_stride;
     const T* sq = reinterpret_cast<const T*>(a.sq);
     const T* sk = reinterpret_cast<const T*>(a.sk);
     const T* v = reinterpret_cast<const T*>(a.v);
     const T* dout = reinterpret_cast<const T*>(a.dout);
 
-    const int sl = lane >> 2, cg = lane & 3;
-    const int i = __shfl(pl.p, sl), lo = __shfl(pl.lo, sl), cnt = __shfl(pl.cnt, sl);
-    const float l2 = a.lse2[it.so + i];
+    const float l2 = a.lse2[s.so + i];
     const float cc = glut[i + 1];
     const float P1 = exp2_fp32(lut[1] - l2);
     const float q1 = P1 * (glut[1] - cc);
-    const long qr = it.row0 + (long)i * a.H;
-    float sqr[R];
+    const long qr = s.row0 + (long)i * a.H;
+    const int col = (sub < GE ? sub : 0) * CPL;
+    float sqr[R], dor[CPL];
     load_row<T, R>(sq + qr * R, sqr);
-    constexpr int RL = (R + 3) / 4;  // readout rows handled per lane in phase B
+    load_row<T, CPL>(dout + qr * DV + col, dor);
     float cdq[RL], cu = 0.0f, cvv = 0.0f, cw = 0.0f, cz = 0.0f;
 #pragma unroll
     for (int x = 0; x < RL; ++x) cdq[x] = 0.0f;
+    const int sb = sl * G;
 
-    for (int c0 = 0; c0 < pl.maxcnt; c0 += CK) {
+    for (int c0 = 0; c0 < s.maxcnt; c0 += G) {
+        const int kq = c0 + sub;
+        if (kq < cnt) {
+            const int j = kb[lo + kq];
+            const int L = pair_length(q, k, i, j, bnd, a.strip, n);
+            float skr[R];
+            load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
+            float sdot = 0.0f;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int kq = c0 + cg + 4 * u;
-            if (kq < cnt) {
-                const int j = kb[lo + kq];
-                const int L = match_length(q, k, i, j, bnd, a.strip, n);
-                const long kr = it.row0 + (long)j * a.H;
-                float skr[R];
-                load_row<T, R>(sk + kr * R, skr);
-                float s = 0.0f;
+            for (int r = 0; r < R; ++r) sdot = __builtin_fmaf(sqr[r], skr[r], sdot);
+            const float p = exp2_fp32(lut[L] - l2);
+            float* f = S.f[sb + sub];
+            f[0] = p - P1;
+            f[1] = sdot;
+            f[2] = p * (glut[L] - cc) - q1;
+            f[3] = __int_as_float(j);
 #pragma unroll
-                for (int r = 0; r < R; ++r) s = __builtin_fmaf(sqr[r], skr[r], s);
-                float e = 0.0f;
-                constexpr int VC = DV < 32 ? DV : 32;
-#pragma unroll
-                for (int d0 = 0; d0 < DV; d0 += VC) {
-                    float dr[VC], vr[VC];
-                    load_row<T, VC>(dout + qr * DV + d0, dr);
-                    load_row<T, VC>(v + kr * DV + d0, vr);
-#pragma unroll
-                    for (int d = 0; d < VC; ++d) e = __builtin_fmaf(dr[d], vr[d], e);
-                }
-                const float p = exp2_fp32(lut[L] - l2);
-                const float dpv = p - P1;
-                const float av = p * (glut[L] - cc) - q1;
-                float* f = s_f[sl][cg + 4 * u];
-                f[0] = dpv * e;
-                f[1] = dpv * s;
-                f[2] = e;
-                f[3] = av;
-                f[4] = s * e;
-                f[5] = dpv;
-#pragma unroll
-                for (int r = 0; r < R; ++r) s_sk[sl][cg + 4 * u][r] = skr[r];
-            }
+            for (int r = 0; r < R; ++r) S.sk[sb + sub][r] = skr[r];
         }
-        const int nv = cnt - c0 < CK ? cnt - c0 : CK;
-        for (int u = 0; u < nv; ++u) {
-            const float* f = s_f[sl][u];
-            const float de = f[0];
+        const int nv = cnt - c0 < G ? cnt - c0 : G;
+        for (int h0 = 0; h0 < s.maxcnt - c0 && h0 < G; h0 += 4) {
+            float vr[4][CPL];
 #pragma unroll
-            for (int x = 0; x < RL; ++x) {
-                const int r = cg + 4 * x;
-                if (r < R) cdq[x] = __builtin_fmaf(de, s_sk[sl][u][r], cdq[x]);
+            for (int u = 0; u < 4; ++u) {
+                const int hu = h0 + u < nv ? h0 + u : (nv > 0 ? nv - 1 : 0);
+                const int j = __float_as_int(S.f[sb + hu][3]);
+                load_row<T, CPL>(v + (s.row0 + (long)(nv > 0 ? j : i) * a.H) * DV + col,
+                                 vr[u]);
             }
-            cu = __builtin_fmaf(f[1], f[2], cu);
-            cvv = cvv + f[3];
-            cw = __builtin_fmaf(f[3], f[4], cw);
-            cz = cz + f[5];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float e = group_sum<GE>(tree_dot<CPL>(dor, vr[u]));
+                if (h0 + u < nv) {
+                    const float* f = S.f[sb + h0 + u];
+                    const float dpv = f[0], sdot = f[1], av = f[2];
+                    const float de = dpv * e;
+#pragma unroll
+                    for (int x = 0; x < RL; ++x) {
+                        const int r = sub + G * x;
+                        if (r < R) cdq[x] = __builtin_fmaf(de, S.sk[sb + h0 + u][r], cdq[x]);
+                    }
+                    cu = __builtin_fmaf(dpv * sdot, e, cu);
+                    cvv = cvv + av;
+                    cw = __builtin_fmaf(av, sdot * e, cw);
+                    cz = cz + dpv;
+                }
+            }
         }
     }
-    if (cnt > 0) {
-        float* rec = a.prow + (it.so + i) * a.prow_stride;
+    if (s.hard && cnt > 0) {
+        float* rec = a.prow + (s.so + i) * a.prow_stride;
 #pragma unroll
         for (int x = 0; x < RL; ++x) {
-            const int r = cg + 4 * x;
+            const int r = sub + G * x;
             if (r < R) rec[r] = cdq[x];
         }
-        if (cg == 0) {
+        if (sub == 0) {
             rec[R] = cu;
             rec[R + 1] = cvv;
             rec[R + 2] = cw;
@@ -415,97 +557,96 @@ __global__ __launch_bounds__(64 * WAVES) void pairs_rows_kernel(PathArgs a) {
     }
 }
 
+template <typename T, int R, int DV>
+__global__ __launch_bounds__(64 * WAVES) void pairs_rows_kernel(PathArgs a) {
+    __shared__ RowsLds<R> s_all[WAVES];
+    RowsLds<R>& S = s_all[wave_id()];
+    for_owner_items<0>(a, [&](auto g, int base, int k0, int ncls) {
+        rows_item<T, R, DV, decltype(g)::value>(a, base, k0, ncls, S);
+    });
+}
+
 // ---------------------------------------------------------------------------------------
 // backward keys: adds the bigram-pair corrections to dSK and dV written by the key scan.
-template <typename T, int R, int DV>
-__global__ __launch_bounds__(64 * WAVES) void pairs_keys_kernel(PathArgs a) {
-    constexpr int CPL = DV / 4;
-    __shared__ float s_de_all[WAVES][OWNERS][CK];
-    __shared__ float s_ds_all[WAVES][OWNERS][CK];
-    __shared__ int s_i_all[WAVES][OWNERS][CK];
-    __shared__ float s_sq_all[WAVES][OWNERS][CK][R];
-    auto& s_de = s_de_all[wave_id()];
-    auto& s_ds = s_ds_all[wave_id()];
-    auto& s_i = s_i_all[wave_id()];
-    auto& s_sq = s_sq_all[wave_id()];
-    PairItem it;
-    Plan pl;
-    if (!pair_item<1>(a, it, pl)) return;
-    const int n = a.n, lane = lane_id();
-    const int32_t* qb = a.o.bpos[0] + it.so;
-    const int32_t* q = a.iq + it.so;
-    const int32_t* k = a.ik + it.so;
-    const int32_t* bnd = bound_of(a, it.bh);
-    const float* lut = a.lut + (long)it.h * a.lut_stride;
+template <int R>
+struct KeysLds {
+    float dp[PAIR_SLOTS];
+    float s[PAIR_SLOTS];
+    int i[PAIR_SLOTS];
+    float sq[PAIR_SLOTS][R];
+};
+
+template <typename T, int R, int DV, int G>
+__device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, int ncls,
+                                          KeysLds<R>& S) {
+    constexpr int CPL = DV >= G ? DV / G : 1;
+    constexpr int GE = DV >= G ? G : DV;
+    constexpr int RL = (R + G - 1) / G;
+    Slot s;
+    if (!load_slot<1, G>(a, base, k0, ncls, s)) return;
+    const int n = a.n, lane = lane_id(), sl = lane / G, sub = lane % G;
+    const int j = s.p, lo = s.lo, cnt = s.cnt;
+    const int32_t* qb = a.o.bpos[0] + s.so;
+    const int32_t* q = a.iq + s.so;
+    const int32_t* k = a.ik + s.so;
+    const int32_t* bnd = bound_of(a, s.bh);
+    const float* lut = a.lut + (long)s.h * a.lut_stride;
     const float lut1 = lut[1];
     const T* sq = reinterpret_cast<const T*>(a.sq);
     const T* sk = reinterpret_cast<const T*>(a.sk);
     const T* v = reinterpret_cast<const T*>(a.v);
     const T* dout = reinterpret_cast<const T*>(a.dout);
 
-    const int sl = lane >> 2, cg = lane & 3;
-    const int j = __shfl(pl.p, sl), lo = __shfl(pl.lo, sl), cnt = __shfl(pl.cnt, sl);
-    const long kr = it.row0 + (long)j * a.H;
-    float skr[R];
+    const long kr = s.row0 + (long)j * a.H;
+    const bool cols = sub < GE;
+    const int col = (cols ? sub : 0) * CPL;
+    float skr[R], vj[CPL];
     load_row<T, R>(sk + kr * R, skr);
-    constexpr int RL = (R + 3) / 4;
+    load_row<T, CPL>(v + kr * DV + col, vj);
     float cdk[RL], cdv[CPL];
 #pragma unroll
     for (int x = 0; x < RL; ++x) cdk[x] = 0.0f;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) cdv[c] = 0.0f;
+    const int sb = sl * G;
 
-    for (int c0 = 0; c0 < pl.maxcnt; c0 += CK) {
+    for (int c0 = 0; c0 < s.maxcnt; c0 += G) {
+        const int kq = c0 + sub;
+        if (kq < cnt) {
+            const int i = qb[lo + kq];
+            const int L = pair_length(q, k, i, j, bnd, a.strip, n);
+            const float l2 = a.lse2[s.so + i];
+            const float p = exp2_fp32(lut[L] - l2);
+            float sqr[R];
+            load_row<T, R>(sq + (s.row0 + (long)i * a.H) * R, sqr);
+            float sdot = 0.0f;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int kq = c0 + cg + 4 * u;
-            if (kq < cnt) {
-                const int i = qb[lo + kq];
-                const int L = match_length(q, k, i, j, bnd, a.strip, n);
-                const float l2 = a.lse2[it.so + i];
-                const float p = exp2_fp32(lut[L] - l2);
-                const float dpv = p - exp2_fp32(lut1 - l2);
-                const long qr = it.row0 + (long)i * a.H;
-                float sqr[R];
-                load_row<T, R>(sq + qr * R, sqr);
-                float s = 0.0f;
+            for (int r = 0; r < R; ++r) sdot = __builtin_fmaf(sqr[r], skr[r], sdot);
+            S.dp[sb + sub] = p - exp2_fp32(lut1 - l2);
+            S.s[sb + sub] = sdot;
+            S.i[sb + sub] = i;
 #pragma unroll
-                for (int r = 0; r < R; ++r) s = __builtin_fmaf(sqr[r], skr[r], s);
-                float e = 0.0f;
-                constexpr int VC = DV < 32 ? DV : 32;
-#pragma unroll
-                for (int d0 = 0; d0 < DV; d0 += VC) {
-                    float dr[VC], vr[VC];
-                    load_row<T, VC>(dout + qr * DV + d0, dr);
-                    load_row<T, VC>(v + kr * DV + d0, vr);
-#pragma unroll
-                    for (int d = 0; d < VC; ++d) e = __builtin_fmaf(dr[d], vr[d], e);
-                }
-                s_de[sl][cg + 4 * u] = dpv * e;
-                s_ds[sl][cg + 4 * u] = dpv * s;
-                s_i[sl][cg + 4 * u] = i;
-#pragma unroll
-                for (int r = 0; r < R; ++r) s_sq[sl][cg + 4 * u][r] = sqr[r];
-            }
+            for (int r = 0; r < R; ++r) S.sq[sb + sub][r] = sqr[r];
         }
-        const int nv = cnt - c0 < CK ? cnt - c0 : CK;
-#pragma unroll
-        for (int h0 = 0; h0 < CK; h0 += 4) {
+        const int nv = cnt - c0 < G ? cnt - c0 : G;
+        for (int h0 = 0; h0 < s.maxcnt - c0 && h0 < G; h0 += 4) {
             float dr[4][CPL];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const int i = s_i[sl][h0 + u];
-                if (h0 + u < nv)
-                    load_row<T, CPL>(dout + (it.row0 + (long)i * a.H) * DV + cg * CPL, dr[u]);
+                const int hu = h0 + u < nv ? h0 + u : (nv > 0 ? nv - 1 : 0);
+                const int ii = nv > 0 ? S.i[sb + hu] : j;
+                load_row<T, CPL>(dout + (s.row0 + (long)ii * a.H) * DV + col, dr[u]);
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
+                const float e = group_sum<GE>(tree_dot<CPL>(dr[u], vj));
                 if (h0 + u < nv) {
-                    const float de = s_de[sl][h0 + u], ds = s_ds[sl][h0 + u];
+                    const float dpv = S.dp[sb + h0 + u];
+                    const float de = dpv * e, ds = dpv * S.s[sb + h0 + u];
 #pragma unroll
                     for (int x = 0; x < RL; ++x) {
-                        const int r = cg + 4 * x;
-                        if (r < R) cdk[x] = __builtin_fmaf(de, s_sq[sl][h0 + u][r], cdk[x]);
+                        const int r = sub + G * x;
+                        if (r < R) cdk[x] = __builtin_fmaf(de, S.sq[sb + h0 + u][r], cdk[x]);
                     }
 #pragma unroll
                     for (int c = 0; c < CPL; ++c) cdv[c] = __builtin_fmaf(ds, dr[u][c], cdv[c]);
@@ -513,25 +654,34 @@ __global__ __launch_bounds__(64 * WAVES) void pairs_keys_kernel(PathArgs a) {
             }
         }
     }
-    if (cnt > 0) {
+    if (s.hard && cnt > 0) {
 #pragma unroll
         for (int x = 0; x < RL; ++x) {
-            const int r = cg + 4 * x;
+            const int r = sub + G * x;
             if (r < R) a.dsk[kr * R + r] = a.dsk[kr * R + r] + cdk[x];
         }
-        float* g = a.dv + kr * DV + cg * CPL;
+        if (cols) {
+            float* g = a.dv + kr * DV + col;
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) g[c] = g[c] + cdv[c];
+            for (int c = 0; c < CPL; ++c) g[c] = g[c] + cdv[c];
+        }
     }
+}
+
+template <typename T, int R, int DV>
+__global__ __launch_bounds__(64 * WAVES) void pairs_keys_kernel(PathArgs a) {
+    __shared__ KeysLds<R> s_all[WAVES];
+    KeysLds<R>& S = s_all[wave_id()];
+    for_owner_items<1>(a, [&](auto g, int base, int k0, int ncls) {
+        keys_item<T, R, DV, decltype(g)::value>(a, base, k0, ncls, S);
+    });
 }
 
 // ---------------------------------------------------------------------------------------
 #define DISM_PAIRS_LAUNCHER(NAME, KERNEL)                                                     \
     template <typename T, int R, int DV>                                                      \
     static hipError_t NAME##_go(const PathArgs& a, hipStream_t s) {                           \
-        const long items = (long)((a.n + OWNERS - 1) / OWNERS) * a.B * a.H;                   \
-        hipLaunchKernelGGL((KERNEL<T, R, DV>), dim3(grid_for(items)), dim3(64 * WAVES), 0, s, \
-                           a);                                                                \
+        hipLaunchKernelGGL((KERNEL<T, R, DV>), dim3(PAIR_GRID), dim3(64 * WAVES), 0, s, a);    \
         return hipGetLastError();                                                             \
     }                                                                                         \
     template <typename T, int R>                                                              \
@@ -560,7 +710,6 @@ __global__ __launch_bounds__(64 * WAVES) void pairs_keys_kernel(PathArgs a) {
         return hipErrorInvalidValue;                                                          \
     }
 
-DISM_PAIRS_LAUNCHER(pairs_stats, pairs_stats_kernel)
 DISM_PAIRS_LAUNCHER(pairs_finish, pairs_finish_kernel)
 DISM_PAIRS_LAUNCHER(pairs_rows, pairs_rows_kernel)
 DISM_PAIRS_LAUNCHER(pairs_keys, pairs_keys_kernel)

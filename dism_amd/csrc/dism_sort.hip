@@ -170,11 +170,7 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_kernel(SortArgs a) {
     int digits[4], nd = 0;
     for (int d = 0; d < 4; ++d)
         if ((used >> (8 * d)) & 255u) digits[nd++] = d;
-    if (tid == 0 && role == 0) {
-        a.o.shift[bh] = nd ? 8 * digits[nd - 1] : 0;
-        a.o.nact[0][bh] = 0;  // the pair plan appends to these
-        a.o.nact[1][bh] = 0;
-    }
+    if (tid == 0 && role == 0) a.o.shift[bh] = nd ? 8 * digits[nd - 1] : 0;
 
     if (role == 0) {
         // ---- combined label order of the 2N entries

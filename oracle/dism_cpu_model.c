@@ -486,6 +486,17 @@ static float rg_reduce(const float* a, const float* b, int DV, int R) {
     return t[0];
 }
 
+/* Pairwise tree ((t0 + t1) + (t2 + t3)) + ... over the products t[d] = a[d]*b[d], n a power
+ * of two <= 128: the bigram-pair DV-dot of the HIP pair kernels (lanes hold contiguous
+ * column groups, reduced in-lane and then across lanes by the same adjacent pairing). */
+static float tree_dot(const float* a, const float* b, int n) {
+    float t[128];
+    for (int d = 0; d < n; ++d) t[d] = a[d] * b[d];
+    for (int sz = 1; sz < n; sz *= 2)
+        for (int g = 0; g < n; g += 2 * sz) t[g] = t[g] + t[g + sz];
+    return t[0];
+}
+
 static float dot_chain(const float* a, const float* b, int n) {
     float s = 0.0f;
     for (int r = 0; r < n; ++r) s = fmaf(a[r], b[r], s);
@@ -621,7 +632,7 @@ void orc_forward(const float* sq, const float* sk, const float* v, const int32_t
  *   P1 = exp2(LUT[1]-l2); g1 = G[1]-c; q1 = P1*g1
  *   zq[r] = rg_reduce(dO_i, M_i[r]);  se0 = chain_r fma(sq_i[r], zq[r])
  *   for j in P (ascending): p = exp2(LUT[L]-l2); dp = p-P1; s = chain(sq_i.sk_j);
- *       e = chain(dO_i.v_j); g = G[L]-c; a = p*g - q1; de = dp*e; ds = dp*s;
+ *       e = tree(dO_i.v_j); g = G[L]-c; a = p*g - q1; de = dp*e; ds = dp*s;
  *       cdq[r] = fma(de, sk_j[r], cdq[r]); cu = fma(ds, e, cu); cvv = cvv + a;
  *       cw = fma(a, s*e, cw); cz = cz + dp
  *   dsq[r] = fma(P1, zq[r], cdq[r]); u = fma(P1, se0, cu); vv = fma(cnt, q1, cvv);
@@ -631,7 +642,7 @@ void orc_forward(const float* sq, const float* sk, const float* v, const int32_t
  *   N_j[r][d] = fma chain over valid queries, DESCENDING i, of (P1_i*sq_i[r]) * dO_i[d]
  *   dv0[d] = chain_r fma(sk_j[r], N[r][d]);  dsk0[r] = rg_reduce(N[r], v_j)
  *   for bigram queries i of j (ascending i): p = exp2(LUT[L]-l2_i); dp = p - P1_i;
- *       s = chain(sq_i.sk_j); e = chain(dO_i.v_j); cdk[r] = fma(dp*e, sq_i[r], cdk[r]);
+ *       s = chain(sq_i.sk_j); e = tree(dO_i.v_j); cdk[r] = fma(dp*e, sq_i[r], cdk[r]);
  *       cdv[d] = fma(dp*s, dO_i[d], cdv[d])
  *   dsk[r] = dsk0[r] + cdk[r];  dv[d] = dv0[d] + cdv[d]  (only for keys with bigram pairs). */
 void orc_backward(const float* sq, const float* sk, const float* v, const float* dout,
@@ -709,7 +720,7 @@ void orc_backward(const float* sq, const float* sk, const float* v, const float*
                         const float p = orc_exp2f(tab[L] - l2);
                         const float dp = p - P1;
                         const float s = dot_chain(sqi, skj, R);
-                        const float e = dot_chain(doi, v + krow * DV, DV);
+                        const float e = tree_dot(doi, v + krow * DV, DV);
                         const float g = gt[L] - c;
                         const float av = p * g - q1;
                         const float de = dp * e, ds = dp * s;
@@ -773,7 +784,7 @@ void orc_backward(const float* sq, const float* sk, const float* v, const float*
                         const float p = orc_exp2f(tab[L] - l2);
                         const float dp = p - P1;
                         const float s = dot_chain(sqi, skj, R);
-                        const float e = dot_chain(doi, vj, DV);
+                        const float e = tree_dot(doi, vj, DV);
                         const float de = dp * e, ds = dp * s;
                         for (int r = 0; r < R; ++r) cd[r] = fmaf(de, sqi[r], cd[r]);
                         for (int d = 0; d < DV; ++d) cd[R + d] = fmaf(ds, doi[d], cd[R + d]);
