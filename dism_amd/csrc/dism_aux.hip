@@ -136,50 +136,60 @@ __global__ __launch_bounds__(256) void chunk_kernel(const int32_t* __restrict__ 
 // "blocks of TAU_BLOCK consecutive (b, i) rows summed sequentially in double, then block
 // sums added sequentially in double", one workgroup per head.
 constexpr int TAU_BLOCK = 256;
-constexpr int TAU_GROUP = 64;          // blocks staged in LDS per round
 constexpr int TAU_THREADS = 1024;
+// One workgroup per head; each lane sums one block in order (contiguous rows are read as
+// float4 when the block lies inside one aligned (b, h) row), lane 0 adds the block sums in
+// order.  Rounds of TAU_THREADS blocks.
 __global__ __launch_bounds__(TAU_THREADS) void tau_reduce_kernel(const float* __restrict__ rowtau,
                                                                  int B, int H, long n,
                                                                  float* __restrict__ dtau) {
-    // Stage TAU_GROUP blocks with coalesced loads (row pitch TAU_BLOCK + 1 words keeps the
-    // per-block sequential reads below free of bank conflicts), then one lane per block sums
-    // its block in order; lane 0 adds the block sums in order.
-    __shared__ float tile[TAU_GROUP * (TAU_BLOCK + 1)];
-    __shared__ double part[TAU_GROUP];
-    const int h = blockIdx.x;
+    __shared__ double part[TAU_THREADS];
+    const int h = blockIdx.x, tid = threadIdx.x;
     const long total = (long)B * n;
     const long blocks = (total + TAU_BLOCK - 1) / TAU_BLOCK;
+    const bool rows4 = n % TAU_BLOCK == 0 && (reinterpret_cast<uintptr_t>(rowtau) & 15) == 0;
     double outer = 0.0;
-    for (long base = 0; base < blocks; base += TAU_GROUP) {
-        const long x0 = base * TAU_BLOCK;
-        for (int e = threadIdx.x; e < TAU_GROUP * TAU_BLOCK; e += TAU_THREADS) {
-            const long x = x0 + e;
-            float v = 0.0f;
-            if (x < total) {
-                const long b = x / n, i = x - b * n;
-                v = rowtau[(b * H + h) * n + i];
+    for (long base = 0; base < blocks; base += TAU_THREADS) {
+        const long blk = base + tid;
+        double inner = 0.0;
+        if (blk < blocks) {
+            const long x0 = blk * TAU_BLOCK;
+            if (rows4) {
+                const long b = x0 / n, i = x0 - b * n;
+                const float4* p = reinterpret_cast<const float4*>(rowtau + (b * H + h) * n + i);
+#pragma unroll 16
+                for (int u = 0; u < TAU_BLOCK / 4; ++u) {
+                    const float4 w = p[u];
+                    inner += (double)w.x;
+                    inner += (double)w.y;
+                    inner += (double)w.z;
+                    inner += (double)w.w;
+                }
+            } else {
+                const long cnt = total - x0 < TAU_BLOCK ? total - x0 : TAU_BLOCK;
+                for (long u = 0; u < cnt; ++u) {
+                    const long x = x0 + u, b = x / n, i = x - b * n;
+                    inner += (double)rowtau[(b * H + h) * n + i];
+                }
             }
-            tile[(e / TAU_BLOCK) * (TAU_BLOCK + 1) + (e % TAU_BLOCK)] = v;
+        }
+        part[tid] = inner;
+        __syncthreads();
+        if (tid == 0) {
+            const int cnt = blocks - base < TAU_THREADS ? (int)(blocks - base) : TAU_THREADS;
+            int u = 0;
+            for (; u + 8 <= cnt; u += 8) {  // batched LDS reads, adds in order
+                double x[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) x[t] = part[u + t];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) outer += x[t];
+            }
+            for (; u < cnt; ++u) outer += part[u];
         }
         __syncthreads();
-        if (threadIdx.x < TAU_GROUP) {
-            const long blk = base + threadIdx.x;
-            double inner = 0.0;
-            if (blk < blocks) {
-                const long cnt = total - blk * TAU_BLOCK < TAU_BLOCK ? total - blk * TAU_BLOCK
-                                                                       : TAU_BLOCK;
-                const float* row = tile + threadIdx.x * (TAU_BLOCK + 1);
-                for (long u = 0; u < cnt; ++u) inner += (double)row[u];
-            }
-            part[threadIdx.x] = inner;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const long cnt = blocks - base < TAU_GROUP ? blocks - base : TAU_GROUP;
-            for (long u = 0; u < cnt; ++u) outer += part[u];
-        }
     }
-    if (threadIdx.x == 0) dtau[h] = (float)outer;
+    if (tid == 0) dtau[h] = (float)outer;
 }
 
 // ---------------------------------------------------------------------------------------

@@ -51,7 +51,7 @@ hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 //   pnb/prow: per query row bigram-pair count and record (layout: dism_launch.h)
 struct Layout {
     int64_t corder, clab, ctab, bpos[2], blab[2], bplab[2], btab[2], shift, tmp[3];
-    int64_t plo[2], pcnt[2], ccount[2], own[2], ocount;
+    int64_t stage[2][2], bhcount[2], own[2], ocount, mode;
     int64_t pnb, prow, total;
     int prow_stride;
 };
@@ -79,12 +79,13 @@ Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     }
     L.shift = take(BH * 4);
     for (int s = 0; s < 2; ++s) {
-        L.plo[s] = take(BH * N * 4);
-        L.pcnt[s] = take(BH * N * 4);
-        L.ccount[s] = take(BH * ((N + 63) / 64) * 16);
+        L.stage[s][0] = take(BH * N * 16);
+        L.stage[s][1] = take(BH * N * 16);
+        L.bhcount[s] = take(BH * 16);
         L.own[s] = take(BH * N * 16);
     }
     L.ocount = take(8 * 4);
+    L.mode = take(BH * 4);
     L.tmp[0] = take(BH * 2 * N * 4);
     L.tmp[1] = take(BH * N * 4);
     L.tmp[2] = take(BH * N * 4);
@@ -112,12 +113,13 @@ dism::Orders orders(const Layout& L, void* ws) {
     }
     o.shift = at<int32_t>(ws, L.shift);
     for (int s = 0; s < 2; ++s) {
-        o.plo[s] = at<int32_t>(ws, L.plo[s]);
-        o.pcnt[s] = at<int32_t>(ws, L.pcnt[s]);
-        o.ccount[s] = at<int32_t>(ws, L.ccount[s]);
+        o.stage[s][0] = at<int4>(ws, L.stage[s][0]);
+        o.stage[s][1] = at<int4>(ws, L.stage[s][1]);
+        o.bhcount[s] = at<int32_t>(ws, L.bhcount[s]);
         o.own[s] = at<int4>(ws, L.own[s]);
     }
     o.ocount = at<int32_t>(ws, L.ocount);
+    o.mode = at<int32_t>(ws, L.mode);
     return o;
 }
 
@@ -254,9 +256,9 @@ int32_t dism_hard_prepare(const void* sq, const void* sk, const void* v, int32_t
     sa.n = (int)N;
     for (int t = 0; t < 3; ++t) sa.tmp[t] = at<int32_t>(workspace, L.tmp[t]);
     sa.o = orders(L, workspace);
-    if ((st = hip_status(dism::launch_sort(sa, S(stream)), "hard prepare"))) return st;
+    sa.pnb = at<int32_t>(workspace, L.pnb);
     dism::PathArgs pa = path(L, workspace, B, N, H, iq, ik, nullptr, nullptr, 0, nullptr, 0);
-    return hip_status(dism::launch_pair_plan(pa, S(stream)), "hard prepare plan");
+    return hip_status(dism::launch_prepare(sa, pa, S(stream)), "hard prepare");
 }
 
 int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t dtype,

@@ -28,21 +28,24 @@ struct Orders {
     int32_t* bplab[2];
     int32_t* btab[2];
     int32_t* shift;       // [B*H]
-    // bigram-pair plans (dism_pairs.hip), side 0 query rows, 1 keys:
-    //   plo/pcnt: by bigram-order index t, first partner index in the other side's bigram
-    //             order and partner count;
-    //   ccount:   per 64-owner chunk of a bigram order ([B*H*ceil(N/64)][4]), the owners of
-    //             each class, then (after the offsets pass) each class's first list slot;
-    //   own:      a record {bh, position, plo, pcnt} per owner with partners, classes
-    //             consecutive ([small][medium][large], (b,h)-major, bigram order within);
-    //   ocount:   [4*side + class] records per class.
-    int32_t* plo[2];
-    int32_t* pcnt[2];
-    int32_t* ccount[2];
+    // bigram-pair owners (dism_sort.hip / dism_pairs.hip), side 0 query rows, 1 keys: a
+    // record {bh, position, first partner index in the other side's bigram order, partner
+    // count} per owner with partners, by class (OWNER_SMALL / OWNER_MEDIUM bounds):
+    //   stage[side][0]: per (b,h) row (N slots at bh*N): small class from the front, large
+    //                   class from the back;  stage[side][1]: medium class from the front;
+    //   bhcount[side]:  [B*H][4] records of each class per row;
+    //   own[side]:      all records, classes consecutive ([small][medium][large]), rows in
+    //                   order inside a class;  ocount[4*side + class]: class totals.
+    //   mode[bh]:       1 when the row was prepared by the LDS-resident kernel (N <= PREP_N
+    //                   and labels that differ in one byte), 0 for the global-memory path.
+    int4* stage[2][2];
+    int32_t* bhcount[2];
     int4* own[2];
     int32_t* ocount;      // [8]
+    int32_t* mode;        // [B*H]
 };
 
+constexpr int PREP_N = 16384;     // longest row of the LDS-resident prepare kernel
 constexpr int OWNER_SMALL = 8;    // partner counts <= 8: 16 owners per wave, 4 lanes each
 constexpr int OWNER_MEDIUM = 32;  // <= 32: 4 owners per wave, 16 lanes each; more: 1 per wave
 
@@ -51,6 +54,7 @@ struct SortArgs {
     long BH;
     int n;
     int32_t* tmp[3];        // scratch: [B*H*2N] combined, [B*H*N] per bigram side
+    int32_t* pnb;           // [B*H*N] bigram pair count per query row (LDS-resident prepare)
     Orders o;
 };
 
@@ -101,9 +105,14 @@ hipError_t launch_chunk(const int32_t* summary, int32_t* out, long BH, long C, i
 hipError_t launch_tau_reduce(const float* rowtau, int B, int H, long n, float* dtau,
                              hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, long count, int32_t value, hipStream_t s);
+// Position orders and bigram-pair plans of a prepare call: the LDS-resident kernel for the
+// rows it can take, the global-memory sort and plan for the others, then the owner lists.
+hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s);
 hipError_t launch_sort(const SortArgs& a, hipStream_t s);
+hipError_t launch_prepare_lds(const SortArgs& a, hipStream_t s);
 // The following return hipErrorInvalidValue for an unsupported (R, DV, dtype).
 hipError_t launch_pair_plan(const PathArgs& a, hipStream_t s);
+hipError_t launch_owner_lists(const PathArgs& a, hipStream_t s);
 hipError_t launch_pairs_finish(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_scan_forward(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_pairs_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);

@@ -97,16 +97,17 @@ __device__ __forceinline__ int owner_class(int cnt) {
     return cnt <= OWNER_SMALL ? 0 : cnt <= OWNER_MEDIUM ? 1 : 2;
 }
 
-// Plan, pass 1: one lane per owner (both sides, grid = 2 * B*H * ceil(N/64) items, one
-// 64-owner chunk each): partner range (plo/pcnt), pair count per query row (pnb, by
-// position), and the chunk's owners per class.
+// Plan of the rows prepared in global memory (mode 0): one lane per owner (both sides,
+// grid = 2 * B*H * ceil(N/64) items, one 64-owner chunk each): partner range by binary
+// searches in the bigram orders, pair count per query row (pnb, by position), and the owner
+// record staged in its row's class list (one atomic per wave and class).
 __global__ __launch_bounds__(64 * WAVES) void pair_plan_kernel(PathArgs a) {
     const int n = a.n, lane = lane_id();
     const int per = (n + 63) / 64;
     const int item = xcd_work_item();
     const int side = item & 1;
     const int bh = (item >> 1) / per;
-    if (bh >= a.B * a.H) return;
+    if (bh >= a.B * a.H || a.o.mode[bh]) return;
     const long so = (long)bh * n;
     const int chunk = (item >> 1) - bh * per;
     const int t = chunk * 64 + lane;
@@ -117,104 +118,107 @@ __global__ __launch_bounds__(64 * WAVES) void pair_plan_kernel(PathArgs a) {
     if (own) {
         if (side == 0) partner_range<0>(a, bh, so, tc, p, lo, cnt);
         else partner_range<1>(a, bh, so, tc, p, lo, cnt);
-        a.o.plo[side][so + t] = lo;
-        a.o.pcnt[side][so + t] = cnt;
         if (side == 0) a.pnb[so + p] = cnt;
     }
     const int cls = owner_class(cnt);
     const bool has = own && cnt > 0;
-    const int c0 = __popcll(__ballot(has && cls == 0));
-    const int c1 = __popcll(__ballot(has && cls == 1));
-    const int c2 = __popcll(__ballot(has && cls == 2));
-    if (lane == 0)
-        reinterpret_cast<int4*>(a.o.ccount[side])[(long)bh * per + chunk] =
-            make_int4(c0, c1, c2, 0);
-}
-
-// Plan, pass 2: one workgroup per side turns the chunk counts into list offsets (class
-// totals first, then chunks in (b,h)-major order) and writes the class totals.
-constexpr int OFFSET_THREADS = 1024;
-__global__ __launch_bounds__(OFFSET_THREADS) void pair_offsets_kernel(PathArgs a, long chunks) {
-    __shared__ int s_scan[3][OFFSET_THREADS];
-    const int side = blockIdx.x, tid = threadIdx.x;
-    int4* cc = reinterpret_cast<int4*>(a.o.ccount[side]);
-    const long per_t = (chunks + OFFSET_THREADS - 1) / OFFSET_THREADS;
-    const long c_lo = tid * per_t < chunks ? tid * per_t : chunks;
-    const long c_hi = c_lo + per_t < chunks ? c_lo + per_t : chunks;
-    int sum[3] = {0, 0, 0};
-    for (long c = c_lo; c < c_hi; ++c) {
-        const int4 x = cc[c];
-        sum[0] += x.x;
-        sum[1] += x.y;
-        sum[2] += x.z;
-    }
-#pragma unroll
-    for (int k = 0; k < 3; ++k) s_scan[k][tid] = sum[k];
-    __syncthreads();
-    for (int off = 1; off < OFFSET_THREADS; off <<= 1) {  // inclusive Hillis-Steele scan
-        int v[3];
-#pragma unroll
-        for (int k = 0; k < 3; ++k) v[k] = tid >= off ? s_scan[k][tid - off] : 0;
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < 3; ++k) s_scan[k][tid] += v[k];
-        __syncthreads();
-    }
-    const int t0 = s_scan[0][OFFSET_THREADS - 1], t1 = s_scan[1][OFFSET_THREADS - 1];
-    const int t2 = s_scan[2][OFFSET_THREADS - 1];
-    int run[3] = {s_scan[0][tid] - sum[0], t0 + s_scan[1][tid] - sum[1],
-                  t0 + t1 + s_scan[2][tid] - sum[2]};
-    for (long c = c_lo; c < c_hi; ++c) {
-        const int4 x = cc[c];
-        cc[c] = make_int4(run[0], run[1], run[2], 0);
-        run[0] += x.x;
-        run[1] += x.y;
-        run[2] += x.z;
-    }
-    if (tid == 0) {
-        a.o.ocount[4 * side + 0] = t0;
-        a.o.ocount[4 * side + 1] = t1;
-        a.o.ocount[4 * side + 2] = t2;
-    }
-}
-
-// Plan, pass 3: the owner records into their class lists (same grid as pass 1).
-__global__ __launch_bounds__(64 * WAVES) void pair_scatter_kernel(PathArgs a) {
-    const int n = a.n, lane = lane_id();
-    const int per = (n + 63) / 64;
-    const int item = xcd_work_item();
-    const int side = item & 1;
-    const int bh = (item >> 1) / per;
-    if (bh >= a.B * a.H) return;
-    const long so = (long)bh * n;
-    const int chunk = (item >> 1) - bh * per;
-    const int t = chunk * 64 + lane;
-    const bool own = t < n;
-    const long tc = so + (own ? t : n - 1);
-    const int p = a.o.bpos[side][tc];
-    const int lo = a.o.plo[side][tc];
-    const int cnt = own ? a.o.pcnt[side][tc] : 0;
-    const int4 off = reinterpret_cast<const int4*>(a.o.ccount[side])[(long)bh * per + chunk];
-    const int cls = owner_class(cnt);
-    const bool has = cnt > 0;
+    const int4 rec = make_int4(bh, p, lo, cnt);
+    int32_t* counts = a.o.bhcount[side] + (long)bh * 4;
     const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
-    const unsigned long long m0 = __ballot(has && cls == 0);
-    const unsigned long long m1 = __ballot(has && cls == 1);
-    const unsigned long long m2 = __ballot(has && cls == 2);
-    if (has) {
-        const unsigned long long m = cls == 0 ? m0 : cls == 1 ? m1 : m2;
-        const int base = cls == 0 ? off.x : cls == 1 ? off.y : off.z;
-        a.o.own[side][base + __popcll(m & below)] = make_int4(bh, p, lo, cnt);
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const unsigned long long m = __ballot(has && cls == c);
+        if (!m) continue;
+        int base = 0;
+        if (lane == 0) base = atomicAdd(counts + c, __popcll(m));
+        base = __shfl(base, 0);
+        if (has && cls == c) {
+            const int k = base + __popcll(m & below);
+            if (c == 1) a.o.stage[side][1][so + k] = rec;
+            else a.o.stage[side][0][so + (c == 0 ? k : n - 1 - k)] = rec;
+        }
     }
 }
 
 hipError_t launch_pair_plan(const PathArgs& a, hipStream_t s) {
     const long chunks = ((a.n + 63) / 64) * (long)a.B * a.H;
-    const unsigned grid = grid_for(2 * chunks);
-    hipLaunchKernelGGL(pair_plan_kernel, dim3(grid), dim3(64 * WAVES), 0, s, a);
-    hipLaunchKernelGGL(pair_offsets_kernel, dim3(2), dim3(OFFSET_THREADS), 0, s, a, chunks);
-    hipLaunchKernelGGL(pair_scatter_kernel, dim3(grid), dim3(64 * WAVES), 0, s, a);
+    hipLaunchKernelGGL(pair_plan_kernel, dim3(grid_for(2 * chunks)), dim3(64 * WAVES), 0, s, a);
     return hipGetLastError();
+}
+
+// Owner lists: grid (B*H, 2 sides); workgroup (bh, side) finds its row's offset in each class
+// list (rows before it) and the class totals, then copies its staged records (and, for
+// query rows, their pair counts into pnb, whose other entries are zero).
+constexpr int LIST_THREADS = 256;
+__global__ __launch_bounds__(LIST_THREADS) void owner_lists_kernel(PathArgs a) {
+    __shared__ int s_red[LIST_THREADS / 64][8];
+    const int bh = blockIdx.x, side = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int BH = a.B * a.H, n = a.n;
+    const int32_t* cnt = a.o.bhcount[side];
+    int before[3] = {0, 0, 0}, total[3] = {0, 0, 0};
+    for (int r = tid; r < BH; r += LIST_THREADS) {
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const int v = cnt[(long)r * 4 + c];
+            total[c] += v;
+            if (r < bh) before[c] += v;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            before[c] += __shfl_xor(before[c], o);
+            total[c] += __shfl_xor(total[c], o);
+        }
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            s_red[tid >> 6][c] = before[c];
+            s_red[tid >> 6][4 + c] = total[c];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        before[c] = 0;
+        total[c] = 0;
+        for (int w = 0; w < LIST_THREADS / 64; ++w) {
+            before[c] += s_red[w][c];
+            total[c] += s_red[w][4 + c];
+        }
+    }
+    const int base[3] = {0, total[0], total[0] + total[1]};
+    const long so = (long)bh * n;
+    int4* own = a.o.own[side];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const int m = cnt[(long)bh * 4 + c];
+        const int4* src = a.o.stage[side][c == 1 ? 1 : 0] + so;
+        for (int k = tid; k < m; k += LIST_THREADS) {
+            const int4 rec = src[c == 2 ? n - 1 - k : k];
+            own[base[c] + before[c] + k] = rec;
+            if (side == 0) a.pnb[so + rec.y] = rec.w;  // pair count of the query row
+        }
+    }
+    if (bh == 0 && tid < 3) a.o.ocount[4 * side + tid] = total[tid];
+}
+
+hipError_t launch_owner_lists(const PathArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(owner_lists_kernel, dim3((unsigned)(a.B * a.H), 2), dim3(LIST_THREADS), 0,
+                       s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
+    hipError_t e;
+    if (pa.n <= PREP_N) e = launch_prepare_lds(sa, s);
+    else e = launch_fill_i32(sa.o.mode, sa.BH, 0, s);
+    if (e != hipSuccess) return e;
+    if ((e = launch_sort(sa, s)) != hipSuccess) return e;
+    if ((e = launch_pair_plan(pa, s)) != hipSuccess) return e;
+    return launch_owner_lists(pa, s);
 }
 
 // Work of the persistent pair kernels of one side: items [0, i0) small class (8 owners

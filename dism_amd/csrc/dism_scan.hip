@@ -50,8 +50,10 @@ struct Walk {
         return ord[idx(kk, e < WIN ? e : WIN - 1)];
     }
     __device__ __forceinline__ void begin(int lo_, int hi_) {
-        lo = lo_;
-        hi = hi_;
+        // wave-uniform bounds in scalar registers: the entry loops then branch on scalars
+        // instead of running as divergent loops with exec-mask bookkeeping
+        lo = __builtin_amdgcn_readfirstlane(lo_);
+        hi = __builtin_amdgcn_readfirstlane(hi_);
         nwin = (hi - lo + WIN - 1) / WIN;
         k = 0;
         entC = load(0);
@@ -90,10 +92,12 @@ __device__ __forceinline__ bool scan_item(const PathArgs& a, Item& it) {
 // Runs of equal labels inside the bucket's range [c0, c1) of the combined order.
 template <typename F>
 __device__ __forceinline__ void for_runs(const int32_t* clab, int c0, int c1, F&& run) {
-    int rs = c0;
+    int rs = __builtin_amdgcn_readfirstlane(c0);
+    c1 = __builtin_amdgcn_readfirstlane(c1);
     while (rs < c1) {
-        const uint32_t lbl = (uint32_t)clab[rs];
-        const int re = (uint32_t)clab[c1 - 1] == lbl ? c1 : upper_label(clab, rs + 1, c1, lbl);
+        const uint32_t lbl = (uint32_t)__builtin_amdgcn_readfirstlane(clab[rs]);
+        const int re = __builtin_amdgcn_readfirstlane(
+            (uint32_t)clab[c1 - 1] == lbl ? c1 : upper_label(clab, rs + 1, c1, lbl));
         run(rs, re);
         rs = re;
     }
@@ -191,7 +195,7 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
             for (int c = 0; c < COLS; ++c) M[r][c] = 0.0f;
         int carry_cnt = 0, carry_last = -1;
         do {
-            const int kk = wk.k, wn = wk.count(kk);
+            const int kk = wk.k, wn = __builtin_amdgcn_readfirstlane(wk.count(kk));
             // ---- lane-parallel: entry kind, key counts, row statistics, fp32 readout rows
             const int ent = wk.entC, p = ent >> 1;
             const bool ok = lane < wn, isq = ok && (ent & 1);
@@ -361,7 +365,7 @@ __global__ __launch_bounds__(64 * WAVES) void scan_rows_kernel(PathArgs a) {
         for (int t = 0; t < VPL; ++t) M[t] = 0.0f;
         int carry_cnt = 0;
         do {
-            const int kk = wk.k, wn = wk.count(kk);
+            const int kk = wk.k, wn = __builtin_amdgcn_readfirstlane(wk.count(kk));
             const int ent = wk.entC, p = ent >> 1;
             const bool ok = lane < wn, isq = ok && (ent & 1);
             const unsigned long long km = __ballot(ok && !isq), qm = __ballot(isq);
@@ -518,7 +522,7 @@ __global__ __launch_bounds__(64 * WAVES) void scan_keys_kernel(PathArgs a) {
 #pragma unroll
         for (int t = 0; t < VPL; ++t) Ng[t] = 0.0f;
         do {
-            const int kk = wk.k, wn = wk.count(kk);
+            const int kk = wk.k, wn = __builtin_amdgcn_readfirstlane(wk.count(kk));
             const int ent = wk.entC, p = ent >> 1;
             const bool ok = lane < wn, isq = ok && (ent & 1);
             const unsigned long long qm = __ballot(isq);

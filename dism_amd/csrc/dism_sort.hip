@@ -137,12 +137,90 @@ __device__ void sort_pass(int n, const int32_t* in, int32_t* out, int shift, Key
     __syncthreads();
 }
 
+// One stable counting-sort pass over m elements held in LDS: digit(x) is the 8-bit digit
+// of input element x, emit(x, dst) places it.  Per-wave contiguous segments and a scan over
+// (digit, wave) as in sort_pass; the histogram takes LDS atomic adds and the ranks inside a
+// 64-element group come from per-digit lane masks built with LDS atomic ORs (both
+// order-free, so the result is deterministic), instead of bit-by-bit ballot matching.
+template <typename Dig, typename Emit>
+__device__ void lds_pass(int m, Dig digit, Emit emit, int32_t* table, int (*wcnt)[RADIX],
+                         int* scan, unsigned long long (*lmask)[RADIX]) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int seg = ((m + SORT_WAVES - 1) / SORT_WAVES + 63) / 64 * 64;
+    const int beg = wave * seg;
+    const int end = beg + seg < m ? beg + seg : m;
+    const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    for (int e = tid; e < SORT_WAVES * RADIX; e += SORT_THREADS) {
+        (&wcnt[0][0])[e] = 0;
+        (&lmask[0][0])[e] = 0ull;
+    }
+    __syncthreads();
+    for (int x = beg + lane; x < end; x += 64) atomicAdd(&wcnt[wave][digit(x)], 1);
+    __syncthreads();
+    if (tid < RADIX) {
+        int tot = 0;
+        for (int w = 0; w < SORT_WAVES; ++w) tot += wcnt[w][tid];
+        scan[tid] = tot;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int v0 = scan[4 * tid], v1 = scan[4 * tid + 1], v2 = scan[4 * tid + 2],
+                  v3 = scan[4 * tid + 3];
+        const int sum = v0 + v1 + v2 + v3;
+        int inc = sum;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int t = __shfl_up(inc, off);
+            if (lane >= off) inc += t;
+        }
+        int ex = inc - sum;
+        scan[4 * tid] = ex;
+        ex += v0;
+        scan[4 * tid + 1] = ex;
+        ex += v1;
+        scan[4 * tid + 2] = ex;
+        ex += v2;
+        scan[4 * tid + 3] = ex;
+    }
+    __syncthreads();
+    if (tid < RADIX) {
+        int run = scan[tid];
+        for (int w = 0; w < SORT_WAVES; ++w) {
+            const int c = wcnt[w][tid];
+            wcnt[w][tid] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    for (int x0 = beg; x0 < end; x0 += 64) {
+        const int x = x0 + lane;
+        if (x < end) {
+            const int dig = digit(x);
+            atomicOr(&lmask[wave][dig], 1ull << lane);
+            __builtin_amdgcn_wave_barrier();
+            const unsigned long long eq = lmask[wave][dig];
+            const int rank = __popcll(eq & below);
+            const int dst = wcnt[wave][dig] + rank;
+            __builtin_amdgcn_wave_barrier();
+            if (rank == 0) {
+                wcnt[wave][dig] += __popcll(eq);
+                lmask[wave][dig] = 0ull;
+            }
+            __builtin_amdgcn_wave_barrier();
+            emit(x, dst);
+        }
+    }
+    if (table && tid <= RADIX) table[tid] = tid < RADIX ? scan[tid] : m;
+    __syncthreads();
+}
+
 // grid (BH, 3)
 __global__ __launch_bounds__(SORT_THREADS) void sort_kernel(SortArgs a) {
     __shared__ int wcnt[SORT_WAVES][RADIX];
     __shared__ int scan[RADIX];
     __shared__ uint32_t mask;
     const int bh = blockIdx.x, role = blockIdx.y, n = a.n, tid = threadIdx.x;
+    if (a.o.mode[bh]) return;  // prepared by prepare_lds_kernel
     const long off = (long)bh * n;
     const int32_t* __restrict__ lq = a.lab[0] + off;
     const int32_t* __restrict__ lk = a.lab[1] + off;
@@ -171,6 +249,7 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_kernel(SortArgs a) {
     for (int d = 0; d < 4; ++d)
         if ((used >> (8 * d)) & 255u) digits[nd++] = d;
     if (tid == 0 && role == 0) a.o.shift[bh] = nd ? 8 * digits[nd - 1] : 0;
+    if (role == 0 && tid < 8) a.o.bhcount[tid >> 2][(long)bh * 4 + (tid & 3)] = 0;  // plan appends
 
     if (role == 0) {
         // ---- combined label order of the 2N entries
@@ -237,6 +316,369 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_kernel(SortArgs a) {
                       last ? bplab : nullptr, prev_i, last ? btab : nullptr, wcnt, scan);
         in = out;
     }
+}
+
+// The same counting pass with every wave's elements already in registers: vd[g] holds
+// value | digit << 16 of element beg + 64 g + lane (digit RADIX past the end), so the input
+// order may be overwritten by emit.  Waves own at most 32 groups (m <= 32768).
+template <typename Emit>
+__device__ void reg_pass(int m, const uint32_t (&vd)[32], Emit emit, int (*wcnt)[RADIX],
+                         int* scan, unsigned long long (*lmask)[RADIX]) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int seg = ((m + SORT_WAVES - 1) / SORT_WAVES + 63) / 64 * 64;
+    const int beg = wave * seg;
+    const int end = beg + seg < m ? beg + seg : m;
+    const int groups = end > beg ? (end - beg + 63) / 64 : 0;
+    const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    for (int e = tid; e < SORT_WAVES * RADIX; e += SORT_THREADS) {
+        (&wcnt[0][0])[e] = 0;
+        (&lmask[0][0])[e] = 0ull;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < 32; ++g) {
+        const int dig = (int)(vd[g] >> 16);
+        if (g < groups && dig < RADIX) atomicAdd(&wcnt[wave][dig], 1);
+    }
+    __syncthreads();
+    if (tid < RADIX) {
+        int tot = 0;
+        for (int w = 0; w < SORT_WAVES; ++w) tot += wcnt[w][tid];
+        scan[tid] = tot;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int v0 = scan[4 * tid], v1 = scan[4 * tid + 1], v2 = scan[4 * tid + 2],
+                  v3 = scan[4 * tid + 3];
+        const int sum = v0 + v1 + v2 + v3;
+        int inc = sum;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int t = __shfl_up(inc, off);
+            if (lane >= off) inc += t;
+        }
+        int ex = inc - sum;
+        scan[4 * tid] = ex;
+        ex += v0;
+        scan[4 * tid + 1] = ex;
+        ex += v1;
+        scan[4 * tid + 2] = ex;
+        ex += v2;
+        scan[4 * tid + 3] = ex;
+    }
+    __syncthreads();
+    if (tid < RADIX) {
+        int run = scan[tid];
+        for (int w = 0; w < SORT_WAVES; ++w) {
+            const int c = wcnt[w][tid];
+            wcnt[w][tid] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < 32; ++g) {
+        if (g < groups) {
+            const int dig = (int)(vd[g] >> 16);
+            if (dig < RADIX) {
+                atomicOr(&lmask[wave][dig], 1ull << lane);
+                __builtin_amdgcn_wave_barrier();
+                const unsigned long long eq = lmask[wave][dig];
+                const int rank = __popcll(eq & below);
+                const int dst = wcnt[wave][dig] + rank;
+                __builtin_amdgcn_wave_barrier();
+                if (rank == 0) {
+                    wcnt[wave][dig] += __popcll(eq);
+                    lmask[wave][dig] = 0ull;
+                }
+                __builtin_amdgcn_wave_barrier();
+                emit((int)(vd[g] & 0xFFFFu), dst);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------------------
+// LDS-resident prepare: one (b,h) row per workgroup pair, for N <= PREP_N and labels that
+// differ in one byte only (the sign labels of up to 8 binarized features).  Everything the
+// pair kernels need is derived from two LDS sorts of the 2N entries e = 2p + s:
+//   y = 0  combined label order (as sort_kernel role 0), written out with coalesced stores;
+//   y = 1  the same order, then stably by the predecessor's label: the combined BIGRAM order
+//          (bigram (label[p-1], label[p]), then e).  In it a bigram group lists keys and
+//          queries merged in position order, so for a query row i (p >= 1) its partners are
+//          the keys j >= 1 of its group before it, and for a key j (p >= 1) the queries of its
+//          group after it.  Prefix counts over the order give each owner its partner range in
+//          the side's key / query list (no binary searches), then the owner records, the
+//          per-side bigram position lists and the pair counts per query row.
+// Each thread owns PREP_E = 2N/1024 consecutive entries of the bigram order (registers);
+// block scans combine the threads; outputs are staged in LDS and written coalesced.
+constexpr int PREP_E = 2 * PREP_N / SORT_THREADS;  // entries per thread
+
+// Block-wide exclusive scan over the threads, in thread order (rev = false) or reversed
+// thread order (rev = true), of an associative op with identity ident.  S is a small
+// aggregate of ints; shfl(S, lane) moves one.
+template <typename S, typename Op, typename Shfl>
+__device__ __forceinline__ S block_exscan(S x, Op op, S ident, Shfl shfl, S* lds, bool rev,
+                                          S* total) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int vl = rev ? 63 - lane : lane, vw = rev ? SORT_WAVES - 1 - wave : wave;
+    S inc = x;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const S y = shfl(inc, rev ? lane + off : lane - off);
+        if (vl >= off) inc = op(y, inc);
+    }
+    if (vl == 63) lds[vw] = inc;
+    __syncthreads();
+    S carry = ident, all = ident;
+    for (int w = 0; w < SORT_WAVES; ++w) {
+        if (w < vw) carry = op(carry, lds[w]);
+        all = op(all, lds[w]);
+    }
+    S ex = shfl(inc, rev ? lane + 1 : lane - 1);
+    if (vl == 0) ex = ident;
+    __syncthreads();
+    if (total) *total = all;
+    return op(carry, ex);
+}
+
+struct Seg {     // segmented count: f = a segment start lies inside, v = count after it
+    int f, v;
+};
+struct Cnt4 {
+    int x, y, z, w;
+};
+
+__global__ __launch_bounds__(SORT_THREADS) void prepare_lds_kernel(SortArgs a) {
+    // LDS pool: [dig 2N bytes | rank masks 32 KiB] [order 2N x u16] [digit counters]
+    //   after the sorts the first region holds a u16 per entry (partner counts, then the
+    //   pair counts per query row) and the order region the per-side position lists.
+    // Per-entry u16 arrays are padded by one slot per 32 entries (pad()): threads scan 32
+    // consecutive entries, and without the pad every lane of a wave would hit the same banks.
+    constexpr int DIG_BYTES = 2 * PREP_N;
+    constexpr int MASK_BYTES = SORT_WAVES * RADIX * 8;
+    constexpr int PADDED = 2 * PREP_N + 2 * PREP_N / 32;
+    constexpr int POOL = DIG_BYTES + MASK_BYTES > 2 * PADDED ? DIG_BYTES + MASK_BYTES : 2 * PADDED;
+    __shared__ __attribute__((aligned(16))) unsigned char pool[POOL];
+    __shared__ uint16_t s_ord[PADDED];
+    __shared__ int wcnt[SORT_WAVES][RADIX];
+    __shared__ int scan[RADIX];
+    __shared__ uint32_t mask;
+    __shared__ Cnt4 s_c4[SORT_WAVES];
+    __shared__ Seg s_seg[SORT_WAVES];
+    uint8_t* s_dig = pool;
+    auto s_mask = reinterpret_cast<unsigned long long (*)[RADIX]>(pool + DIG_BYTES);
+    uint16_t* s_cnt = reinterpret_cast<uint16_t*>(pool);  // after the sorts
+    auto pad = [](int c) { return c + (c >> 5); };
+    const int bh = blockIdx.x, role = blockIdx.y, n = a.n, tid = threadIdx.x;
+    const int n2 = 2 * n;
+    const long off = (long)bh * n;
+    const int32_t* __restrict__ lq = a.lab[0] + off;
+    const int32_t* __restrict__ lk = a.lab[1] + off;
+
+    if (tid == 0) mask = 0;
+    __syncthreads();
+    uint32_t m = 0;
+    for (int p = tid; p < n; p += SORT_THREADS) m |= (uint32_t)lq[p] | (uint32_t)lk[p];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m |= (uint32_t)__shfl_xor((int)m, o);
+    if ((tid & 63) == 0) atomicOr(&mask, m);
+    __syncthreads();
+    const uint32_t used = mask;
+    int nd = 0, dg = 0;
+    for (int d = 0; d < 4; ++d)
+        if ((used >> (8 * d)) & 255u) {
+            ++nd;
+            dg = d;
+        }
+    const bool lds_ok = nd == 1;
+    if (role == 0 && tid == 0) {
+        a.o.mode[bh] = lds_ok ? 1 : 0;
+        if (lds_ok) a.o.shift[bh] = 8 * dg;
+    }
+    if (!lds_ok) return;  // sort_kernel and pair_plan_kernel take this row
+    const int shift = 8 * dg;
+    for (int p = tid; p < n; p += SORT_THREADS) {
+        s_dig[2 * p] = (uint8_t)(((uint32_t)lk[p] >> shift) & 255u);
+        s_dig[2 * p + 1] = (uint8_t)(((uint32_t)lq[p] >> shift) & 255u);
+    }
+    __syncthreads();
+    // ---- combined label order
+    lds_pass(
+        n2, [&](int x) { return (int)s_dig[x]; },
+        [&](int x, int dst) { s_ord[pad(dst)] = (uint16_t)x; },
+        role == 0 ? a.o.ctab + (long)bh * (RADIX + 1) : nullptr, wcnt, scan, s_mask);
+    if (role == 0) {
+        int32_t* corder = a.o.corder + 2 * off;
+        int32_t* clab = a.o.clab + 2 * off;
+        for (int c = tid; c < n2; c += SORT_THREADS) {
+            const int e = s_ord[pad(c)];
+            corder[c] = e;
+            clab[c] = (int)((uint32_t)s_dig[e] << shift);
+        }
+        return;
+    }
+    // ---- combined bigram order: the label order, stably by the predecessor's label (each
+    // wave's segment of the label order moves to registers first)
+    {
+        const int lane = tid & 63, wave = tid >> 6;
+        const int seg = ((n2 + SORT_WAVES - 1) / SORT_WAVES + 63) / 64 * 64;
+        const int beg = wave * seg, end = beg + seg < n2 ? beg + seg : n2;
+        uint32_t vd[32];
+#pragma unroll
+        for (int g = 0; g < 32; ++g) {
+            const int x = beg + 64 * g + lane;
+            uint32_t w = (uint32_t)RADIX << 16;
+            if (x < end) {
+                const int e = s_ord[pad(x)];
+                w = (uint32_t)e | ((uint32_t)(e >= 2 ? s_dig[e - 2] : 0) << 16);
+            }
+            vd[g] = w;
+        }
+        reg_pass(n2, vd, [&](int e, int dst) { s_ord[pad(dst)] = (uint16_t)e; }, wcnt, scan, s_mask);
+    }
+
+    // ---- plan.  Each thread owns PREP_E consecutive entries c of the bigram order; its
+    // group-head flags are one register word (bit k: entry c0 + k starts a bigram group).
+    const int c0 = tid * PREP_E;
+    const int c1 = c0 + PREP_E < n2 ? c0 + PREP_E : n2;
+    uint32_t heads = 0;
+    {
+        auto big_of = [&](int e) {
+            return ((e >= 2 ? (int)s_dig[e - 2] : 0) << 8) | (int)s_dig[e];
+        };
+        int prev = c0 > 0 && c0 <= n2 ? big_of(s_ord[pad(c0 - 1)]) : -1;
+#pragma unroll 8
+        for (int c = c0; c < c1; ++c) {
+            const int b = big_of(s_ord[pad(c)]);
+            if (b != prev) heads |= 1u << (c - c0);
+            prev = b;
+        }
+    }
+    auto is_head = [&](int c) { return (heads >> (c - c0)) & 1u; };
+    // per-thread aggregates: keys, queries (p >= 1); segmented key count after the last head;
+    // queries before the first head
+    Cnt4 loc{0, 0, 0, 0};
+    Seg segk{0, 0}, segq{0, 0};
+    for (int c = c0; c < c1; ++c) {
+        const int e = s_ord[pad(c)];
+        const bool isk = e >= 2 && !(e & 1), isq = e >= 2 && (e & 1);
+        if (is_head(c)) {
+            segk.f = 1;
+            segk.v = 0;
+            segq.f = 1;
+        }
+        segk.v += isk;
+        if (!segq.f) segq.v += isq;
+        loc.x += isk;
+        loc.y += isq;
+    }
+    auto sh4 = [](Cnt4 v, int l) {
+        return Cnt4{__shfl(v.x, l), __shfl(v.y, l), __shfl(v.z, l), __shfl(v.w, l)};
+    };
+    auto add4 = [](Cnt4 p, Cnt4 q) { return Cnt4{p.x + q.x, p.y + q.y, p.z + q.z, p.w + q.w}; };
+    auto shs = [](Seg v, int l) { return Seg{__shfl(v.f, l), __shfl(v.v, l)}; };
+    auto segop = [](Seg p, Seg q) { return Seg{p.f | q.f, q.f ? q.v : p.v + q.v}; };
+    Cnt4 tot;
+    Seg dummy;
+    const Cnt4 rk = block_exscan(loc, add4, Cnt4{0, 0, 0, 0}, sh4, s_c4, false, &tot);
+    const Seg ck = block_exscan(segk, segop, Seg{0, 0}, shs, s_seg, false, &dummy);
+    const Seg cq = block_exscan(segq, segop, Seg{0, 0}, shs, s_seg, true, &dummy);
+    // partner counts into s_cnt: keys (queries after them in the group, backward), query
+    // rows (keys before them in the group, forward); per-thread class counts
+    {
+        int qa = cq.v;
+        for (int c = c1 - 1; c >= c0; --c) {
+            const int e = s_ord[pad(c)];
+            const bool isk = e >= 2 && !(e & 1), isq = e >= 2 && (e & 1);
+            s_cnt[pad(c)] = isk ? (uint16_t)qa : (uint16_t)0;
+            qa += isq;
+            if (is_head(c)) qa = 0;
+        }
+    }
+    Cnt4 cl{0, 0, 0, 0}, cl2{0, 0, 0, 0};  // classes of query rows, of keys
+    auto add_class = [](Cnt4& cc, int cnt) {
+        const int cls = cnt <= OWNER_SMALL ? 0 : cnt <= OWNER_MEDIUM ? 1 : 2;
+        cc.x += cls == 0;
+        cc.y += cls == 1;
+        cc.z += cls == 2;
+    };
+    {
+        int sk = ck.v;
+        for (int c = c0; c < c1; ++c) {
+            const int e = s_ord[pad(c)];
+            const bool isk = e >= 2 && !(e & 1), isq = e >= 2 && (e & 1);
+            if (is_head(c)) sk = 0;
+            if (isq) {
+                s_cnt[pad(c)] = (uint16_t)sk;
+                if (sk > 0) add_class(cl, sk);
+            } else if (isk) {
+                const int cnt = s_cnt[pad(c)];
+                if (cnt > 0) add_class(cl2, cnt);
+            }
+            sk += isk;
+        }
+    }
+    Cnt4 t0, t1;
+    Cnt4 r0 = block_exscan(cl, add4, Cnt4{0, 0, 0, 0}, sh4, s_c4, false, &t0);
+    Cnt4 r1 = block_exscan(cl2, add4, Cnt4{0, 0, 0, 0}, sh4, s_c4, false, &t1);
+    // owner records into the row's stage lists
+    {
+        int kr = rk.x, qr = rk.y, sk = ck.v;
+        for (int c = c0; c < c1; ++c) {
+            const int e = s_ord[pad(c)];
+            const bool isk = e >= 2 && !(e & 1), isq = e >= 2 && (e & 1);
+            if (is_head(c)) sk = 0;
+            const int cnt = s_cnt[pad(c)];
+            if ((isk || isq) && cnt > 0) {
+                const int lo = isq ? kr - sk : qr;
+                const int side = isq ? 0 : 1;  // 0: query rows, 1: keys
+                const int cls = cnt <= OWNER_SMALL ? 0 : cnt <= OWNER_MEDIUM ? 1 : 2;
+                int rank;
+                if (side == 0) rank = cls == 0 ? r0.x++ : cls == 1 ? r0.y++ : r0.z++;
+                else rank = cls == 0 ? r1.x++ : cls == 1 ? r1.y++ : r1.z++;
+                const int4 rec = make_int4(bh, e >> 1, lo, cnt);
+                if (cls == 1) a.o.stage[side][1][off + rank] = rec;
+                else a.o.stage[side][0][off + (cls == 0 ? rank : n - 1 - rank)] = rec;
+            }
+            kr += isk;
+            qr += isq;
+            sk += isk;
+        }
+    }
+    if (tid < 3) {
+        a.o.bhcount[0][(long)bh * 4 + tid] = tid == 0 ? t0.x : tid == 1 ? t0.y : t0.z;
+        a.o.bhcount[1][(long)bh * 4 + tid] = tid == 0 ? t1.x : tid == 1 ? t1.y : t1.z;
+    }
+    // per-side bigram position lists, written coalesced: wave-strided groups of 64 entries
+    // (two threads' ranges) take their ranks from the threads' prefix counts
+    int* s_rk = &wcnt[0][0];  // [SORT_THREADS][2]
+    s_rk[2 * tid] = rk.x;
+    s_rk[2 * tid + 1] = rk.y;
+    __syncthreads();
+    {
+        const int lane = tid & 63, wave = tid >> 6;
+        const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
+        int32_t* bq = a.o.bpos[0] + off;
+        int32_t* bk = a.o.bpos[1] + off;
+        for (int x0 = wave * 64; x0 < n2; x0 += 64 * SORT_WAVES) {
+            const int c = x0 + lane;
+            const int e = c < n2 ? s_ord[pad(c)] : 0;
+            const bool isk = e >= 2 && !(e & 1), isq = e >= 2 && (e & 1);
+            const unsigned long long km = __ballot(isk), qm = __ballot(isq);
+            const int tb = x0 / PREP_E;
+            if (isk) bk[s_rk[2 * tb] + __popcll(km & below)] = e >> 1;
+            if (isq) bq[s_rk[2 * tb + 1] + __popcll(qm & below)] = e >> 1;
+        }
+    }
+    // pair counts per query row: zeros here, the owner-list kernel writes the rows with pairs
+    for (int p = tid; p < n; p += SORT_THREADS) a.pnb[off + p] = 0;
+}
+
+hipError_t launch_prepare_lds(const SortArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(prepare_lds_kernel, dim3((unsigned)a.BH, 2), dim3(SORT_THREADS), 0, s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_sort(const SortArgs& a, hipStream_t s) {
