@@ -242,7 +242,7 @@ __device__ __forceinline__ OwnerWork owner_work(const PathArgs& a) {
     return w;
 }
 
-// Owner of this lane's slot (G lanes per slot); soft rows hold no pairs.
+// Owner of this lane's slot (G lanes per slot).
 struct Slot {
     int bh, h, p, lo, cnt, maxcnt;
     bool hard;
@@ -260,8 +260,8 @@ __device__ __forceinline__ bool load_slot(const PathArgs& a, int base, int k0, i
     s.h = r.x - b * a.H;
     s.p = r.y;
     s.lo = r.z;
-    s.hard = a.hard[r.x] != 0;
-    s.cnt = in && s.hard ? r.w : 0;  // soft rows: no pairs (their carry boundary is unset)
+    s.hard = a.hard[r.x] != 0;  // soft rows compute but write nothing (and walk unbounded:
+    s.cnt = in ? r.w : 0;       // their carry boundary is unset), off the dependent chain
     s.so = (long)r.x * a.n;
     s.row0 = (long)b * a.n * a.H + s.h;
     int mx = s.cnt;
@@ -312,10 +312,17 @@ struct FinishLds {
     unsigned long long key[8];
 };
 
+// 64-bit shuffle (xor pattern)
+__device__ __forceinline__ unsigned long long shfl_xor64(unsigned long long x, int m) {
+    const int lo = __shfl_xor((int)(uint32_t)x, m), hi = __shfl_xor((int)(uint32_t)(x >> 32), m);
+    return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
 template <typename T, int R, int DV, int G>
 __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0, int ncls,
                                             FinishLds& S) {
     constexpr int CPL = DV >= G ? DV / G : 1;  // value columns per lane in phase B
+    constexpr int GE = DV >= G ? G : DV;       // lanes of a slot holding columns
     Slot s;
     if (!load_slot<0, G>(a, base, k0, ncls, s)) return;
     const int n = a.n, lane = lane_id(), sl = lane / G, sub = lane % G;
@@ -323,101 +330,153 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
     const int32_t* kb = a.o.bpos[1] + s.so;
     const int32_t* q = a.iq + s.so;
     const int32_t* k = a.ik + s.so;
-    const int32_t* bnd = bound_of(a, s.bh);
+    const int32_t* bnd = s.hard ? bound_of(a, s.bh) : nullptr;
     const float* lut = a.lut + (long)s.h * a.lut_stride;
     const T* sq = reinterpret_cast<const T*>(a.sq);
     const T* sk = reinterpret_cast<const T*>(a.sk);
     const T* v = reinterpret_cast<const T*>(a.v);
+    const int cg = sub;
+    const bool cols = cg < GE;
+    const int col = (cols ? cg : 0) * CPL;
+    // owner-side loads first (they depend only on the owner record)
     const float lut1 = lut[1];
     const float m0 = lut1 > 0.0f ? lut1 : 0.0f;
-    if (sub == 0) {
-        S.m[sl] = __float_as_uint(m0);
-        S.key[sl] = 0ull;
-    }
-    int j0 = 0, L0 = 1;  // round 0's partner and length, reused by sweep 2
-    for (int c0 = 0; c0 < s.maxcnt; c0 += G) {
-        const int kq = c0 + sub;
-        if (kq < cnt) {
-            const int j = kb[lo + kq];
-            const int L = pair_length(q, k, i, j, bnd, a.strip, n);
-            const float lw = lut[L];
-            if (lw > m0) atomicMax(&S.m[sl], __float_as_uint(lw));
-            atomicMax(&S.key[sl], ((unsigned long long)(unsigned)L << 32) | (unsigned)j);
-            if (c0 == 0) {
-                j0 = j;
-                L0 = L;
-            }
-        }
-    }
-    const float m = __uint_as_float(S.m[sl]);
-    const unsigned long long key = S.key[sl];
-    const float p1 = exp2_fp32(lut1 - m);
     float sqr[R];
     load_row<T, R>(sq + (s.row0 + (long)i * a.H) * R, sqr);
-    const int cg = sub;
-    const bool cols = cg * CPL < DV;
+    const float* rec = a.prow + (s.so + i) * a.prow_stride;
+    const int kc = __float_as_int(rec[PREC_CNT]);
+    float y[CPL];
+    load_row<float, CPL>(rec + PREC_Y + col, y);
     float dp = 0.0f, corr[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) corr[c] = 0.0f;
-    float* cf_s = S.cf + sl * G;
-    float* p_s = S.p + sl * G;
-    int* j_s = S.j + sl * G;
+    float m;
+    unsigned long long key;
 
-    for (int c0 = 0; c0 < s.maxcnt; c0 += G) {
-        // phase A: pair (slot, c0 + sub)
-        const int kq = c0 + sub;
-        if (kq < cnt) {
-            int j = j0, L = L0;
-            if (c0 > 0) {
-                j = kb[lo + kq];
-                L = pair_length(q, k, i, j, bnd, a.strip, n);
-            }
-            const float p = exp2_fp32(lut[L] - m);
-            float skr[R];
-            load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
-            float sdot = 0.0f;
+    if (s.maxcnt <= G) {
+        // one round: a lane per partner, the slot's pairs in flight together; the longest
+        // match and the row shift by slot reductions, partner data to the column lanes by
+        // shuffles, partner value rows loaded as soon as the partners are known
+        const bool has = sub < cnt;
+        const int j = kb[has ? lo + sub : 0];
+        constexpr int UB = G <= 8 ? 4 : 16;  // partner rows loaded per batch
+        float vr[UB][CPL];                   // the first batch is issued with the partners
 #pragma unroll
-            for (int r = 0; r < R; ++r) sdot = __builtin_fmaf(sqr[r], skr[r], sdot);
-            cf_s[sub] = (p - p1) * sdot;
-            p_s[sub] = p;
-            j_s[sub] = j;
+        for (int u = 0; u < UB; ++u) {
+            const int jj = __shfl(j, sl * G + u);
+            load_row<T, CPL>(v + (s.row0 + (long)jj * a.H) * DV + col, vr[u]);
         }
-        // phase B: the slot folds its round's pairs in order, lane = column group cg
-        const int nv = cnt - c0 < G ? cnt - c0 : G;
-        if (cols) {
-            for (int h0 = 0; h0 < nv; h0 += 4) {
-                float vr[4][CPL];
+        float skr[R];
+        load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n) : 1;
+        const float lw = lut[L];
+        float mm = has && lw > m0 ? lw : m0;
+        key = has ? (((unsigned long long)(unsigned)L << 32) | (unsigned)j) : 0ull;
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int jj = j_s[h0 + u < nv ? h0 + u : nv - 1];
-                    load_row<T, CPL>(v + (s.row0 + (long)jj * a.H) * DV + cg * CPL, vr[u]);
+        for (int o = G / 2; o >= 1; o >>= 1) {
+            const float mo = __shfl_xor(mm, o);
+            mm = mo > mm ? mo : mm;
+            const unsigned long long ko = shfl_xor64(key, o);
+            key = ko > key ? ko : key;
+        }
+        m = mm;
+        const float p1 = exp2_fp32(lut1 - m);
+        const float p = exp2_fp32(lw - m);
+        float sdot = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) sdot = __builtin_fmaf(sqr[r], skr[r], sdot);
+        const float cf = (p - p1) * sdot;
+        for (int u0 = 0; u0 < s.maxcnt; u0 += UB) {
+            if (u0 > 0) {
+#pragma unroll
+                for (int u = 0; u < UB; ++u) {
+                    const int jj = __shfl(j, sl * G + u0 + u);
+                    load_row<T, CPL>(v + (s.row0 + (long)jj * a.H) * DV + col, vr[u]);
                 }
+            }
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    if (h0 + u < nv) {
-                        dp = dp + p_s[h0 + u];
-                        const float cf = cf_s[h0 + u];
+            for (int u = 0; u < UB; ++u) {
+                const float pu = __shfl(p, sl * G + u0 + u), cfu = __shfl(cf, sl * G + u0 + u);
+                if (u0 + u < cnt) {
+                    dp = dp + pu;
 #pragma unroll
-                        for (int c = 0; c < CPL; ++c)
-                            corr[c] = __builtin_fmaf(cf, vr[u][c], corr[c]);
+                    for (int c = 0; c < CPL; ++c) corr[c] = __builtin_fmaf(cfu, vr[u][c], corr[c]);
+                }
+            }
+        }
+    } else {
+        // several rounds: sweep 1 (row shift, longest match) over all partners, then sweep 2
+        if (sub == 0) {
+            S.m[sl] = __float_as_uint(m0);
+            S.key[sl] = 0ull;
+        }
+        for (int c0 = 0; c0 < s.maxcnt; c0 += G) {
+            const int kq = c0 + sub;
+            if (kq < cnt) {
+                const int j = kb[lo + kq];
+                const int L = pair_length(q, k, i, j, bnd, a.strip, n);
+                const float lw = lut[L];
+                if (lw > m0) atomicMax(&S.m[sl], __float_as_uint(lw));
+                atomicMax(&S.key[sl], ((unsigned long long)(unsigned)L << 32) | (unsigned)j);
+            }
+        }
+        m = __uint_as_float(S.m[sl]);
+        key = S.key[sl];
+        const float p1 = exp2_fp32(lut1 - m);
+        float* cf_s = S.cf + sl * G;
+        float* p_s = S.p + sl * G;
+        int* j_s = S.j + sl * G;
+        for (int c0 = 0; c0 < s.maxcnt; c0 += G) {
+            // phase A: pair (slot, c0 + sub)
+            const int kq = c0 + sub;
+            if (kq < cnt) {
+                const int j = kb[lo + kq];
+                const int L = pair_length(q, k, i, j, bnd, a.strip, n);
+                const float p = exp2_fp32(lut[L] - m);
+                float skr[R];
+                load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
+                float sdot = 0.0f;
+#pragma unroll
+                for (int r = 0; r < R; ++r) sdot = __builtin_fmaf(sqr[r], skr[r], sdot);
+                cf_s[sub] = (p - p1) * sdot;
+                p_s[sub] = p;
+                j_s[sub] = j;
+            }
+            // phase B: the slot folds its round's pairs in order, lane = column group cg
+            const int nv = cnt - c0 < G ? cnt - c0 : G;
+            if (cols) {
+                for (int h0 = 0; h0 < nv; h0 += 4) {
+                    float vr[4][CPL];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int jj = j_s[h0 + u < nv ? h0 + u : nv - 1];
+                        load_row<T, CPL>(v + (s.row0 + (long)jj * a.H) * DV + col, vr[u]);
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        if (h0 + u < nv) {
+                            dp = dp + p_s[h0 + u];
+                            const float cf = cf_s[h0 + u];
+#pragma unroll
+                            for (int c = 0; c < CPL; ++c)
+                                corr[c] = __builtin_fmaf(cf, vr[u][c], corr[c]);
+                        }
                     }
                 }
             }
         }
     }
     if (s.hard && cnt > 0 && cols) {
-        const float* rec = a.prow + (s.so + i) * a.prow_stride;
-        const int kc = __float_as_int(rec[PREC_CNT]);
+        const float p1 = exp2_fp32(lut1 - m);
         const float den = (exp2_fp32(-m) + (float)(kc - cnt) * p1) + dp;
         const float rden = 1.0f / den;
         const long orow = s.row0 + (long)i * a.H;
-        const float* y = rec + PREC_Y + cg * CPL;
         if (a.out_dtype == DTYPE_F32) {
-            float* o = reinterpret_cast<float*>(a.out) + orow * DV + cg * CPL;
+            float* o = reinterpret_cast<float*>(a.out) + orow * DV + col;
 #pragma unroll
             for (int c = 0; c < CPL; ++c) o[c] = __builtin_fmaf(p1, y[c], corr[c]) * rden;
         } else {
-            uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + orow * DV + cg * CPL;
+            uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + orow * DV + col;
             if constexpr (CPL == 1) {
                 o[0] = (uint16_t)f32_to_bf16_bits(__builtin_fmaf(p1, y[0], corr[0]) * rden);
             } else {
@@ -474,7 +533,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
     const int32_t* kb = a.o.bpos[1] + s.so;
     const int32_t* q = a.iq + s.so;
     const int32_t* k = a.ik + s.so;
-    const int32_t* bnd = bound_of(a, s.bh);
+    const int32_t* bnd = s.hard ? bound_of(a, s.bh) : nullptr;
     const float* lut = a.lut + (long)s.h * a.lut_stride;
     const float* glut = a.dlut + (long)s.h * a.lut_stride;
     const T* sq = reinterpret_cast<const T*>(a.sq);
@@ -496,6 +555,56 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
     for (int x = 0; x < RL; ++x) cdq[x] = 0.0f;
     const int sb = sl * G;
 
+    if (s.maxcnt <= G) {
+        // one round (see finish_item): partner value rows issued with the partners
+        const bool has = sub < cnt;
+        const int j = kb[has ? lo + sub : 0];
+        constexpr int UB = G <= 8 ? 4 : 16;
+        float vr[UB][CPL];
+#pragma unroll
+        for (int u = 0; u < UB; ++u) {
+            const int jj = __shfl(j, sb + u);
+            load_row<T, CPL>(v + (s.row0 + (long)jj * a.H) * DV + col, vr[u]);
+        }
+        float skr[R];
+        load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n) : 1;
+        float sdot = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) sdot = __builtin_fmaf(sqr[r], skr[r], sdot);
+        const float p = exp2_fp32(lut[L] - l2);
+        const float dpv = p - P1;
+        const float av = p * (glut[L] - cc) - q1;
+#pragma unroll
+        for (int r = 0; r < R; ++r) S.sk[sb + sub][r] = skr[r];
+        for (int u0 = 0; u0 < s.maxcnt; u0 += UB) {
+            if (u0 > 0) {
+#pragma unroll
+                for (int u = 0; u < UB; ++u) {
+                    const int jj = __shfl(j, sb + u0 + u);
+                    load_row<T, CPL>(v + (s.row0 + (long)jj * a.H) * DV + col, vr[u]);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < UB; ++u) {
+                const float e = group_sum<GE>(tree_dot<CPL>(dor, vr[u]));
+                const int src = sb + u0 + u;
+                const float dpu = __shfl(dpv, src), su = __shfl(sdot, src), avu = __shfl(av, src);
+                if (u0 + u < cnt) {
+                    const float de = dpu * e;
+#pragma unroll
+                    for (int x = 0; x < RL; ++x) {
+                        const int r = sub + G * x;
+                        if (r < R) cdq[x] = __builtin_fmaf(de, S.sk[src][r], cdq[x]);
+                    }
+                    cu = __builtin_fmaf(dpu * su, e, cu);
+                    cvv = cvv + avu;
+                    cw = __builtin_fmaf(avu, su * e, cw);
+                    cz = cz + dpu;
+                }
+            }
+        }
+    } else
     for (int c0 = 0; c0 < s.maxcnt; c0 += G) {
         const int kq = c0 + sub;
         if (kq < cnt) {
@@ -593,7 +702,7 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
     const int32_t* qb = a.o.bpos[0] + s.so;
     const int32_t* q = a.iq + s.so;
     const int32_t* k = a.ik + s.so;
-    const int32_t* bnd = bound_of(a, s.bh);
+    const int32_t* bnd = s.hard ? bound_of(a, s.bh) : nullptr;
     const float* lut = a.lut + (long)s.h * a.lut_stride;
     const float lut1 = lut[1];
     const T* sq = reinterpret_cast<const T*>(a.sq);
@@ -613,7 +722,64 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
 #pragma unroll
     for (int c = 0; c < CPL; ++c) cdv[c] = 0.0f;
     const int sb = sl * G;
+    // the key scan's dSK0 / dV0 of this key, read now and written back with the corrections
+    float dk0[RL], dv0[CPL];
+#pragma unroll
+    for (int x = 0; x < RL; ++x) {
+        const int r = sub + G * x;
+        dk0[x] = a.dsk[kr * R + (r < R ? r : 0)];
+    }
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) dv0[c] = a.dv[kr * DV + col + c];
 
+    if (s.maxcnt <= G) {
+        // one round (see finish_item): partner dO rows issued with the partners
+        const bool has = sub < cnt;
+        const int i = qb[has ? lo + sub : 0];
+        constexpr int UB = G <= 8 ? 4 : 16;
+        float dr[UB][CPL];
+#pragma unroll
+        for (int u = 0; u < UB; ++u) {
+            const int ii = __shfl(i, sb + u);
+            load_row<T, CPL>(dout + (s.row0 + (long)ii * a.H) * DV + col, dr[u]);
+        }
+        const float l2 = a.lse2[s.so + i];
+        float sqr[R];
+        load_row<T, R>(sq + (s.row0 + (long)i * a.H) * R, sqr);
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n) : 1;
+        const float p = exp2_fp32(lut[L] - l2);
+        float sdot = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) sdot = __builtin_fmaf(sqr[r], skr[r], sdot);
+        const float dpv = p - exp2_fp32(lut1 - l2);
+#pragma unroll
+        for (int r = 0; r < R; ++r) S.sq[sb + sub][r] = sqr[r];
+        for (int u0 = 0; u0 < s.maxcnt; u0 += UB) {
+            if (u0 > 0) {
+#pragma unroll
+                for (int u = 0; u < UB; ++u) {
+                    const int ii = __shfl(i, sb + u0 + u);
+                    load_row<T, CPL>(dout + (s.row0 + (long)ii * a.H) * DV + col, dr[u]);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < UB; ++u) {
+                const float e = group_sum<GE>(tree_dot<CPL>(dr[u], vj));
+                const int src = sb + u0 + u;
+                const float dpu = __shfl(dpv, src), su = __shfl(sdot, src);
+                if (u0 + u < cnt) {
+                    const float de = dpu * e, ds = dpu * su;
+#pragma unroll
+                    for (int x = 0; x < RL; ++x) {
+                        const int r = sub + G * x;
+                        if (r < R) cdk[x] = __builtin_fmaf(de, S.sq[src][r], cdk[x]);
+                    }
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) cdv[c] = __builtin_fmaf(ds, dr[u][c], cdv[c]);
+                }
+            }
+        }
+    } else
     for (int c0 = 0; c0 < s.maxcnt; c0 += G) {
         const int kq = c0 + sub;
         if (kq < cnt) {
@@ -662,12 +828,12 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
 #pragma unroll
         for (int x = 0; x < RL; ++x) {
             const int r = sub + G * x;
-            if (r < R) a.dsk[kr * R + r] = a.dsk[kr * R + r] + cdk[x];
+            if (r < R) a.dsk[kr * R + r] = dk0[x] + cdk[x];
         }
         if (cols) {
             float* g = a.dv + kr * DV + col;
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) g[c] = g[c] + cdv[c];
+            for (int c = 0; c < CPL; ++c) g[c] = dv0[c] + cdv[c];
         }
     }
 }
