@@ -202,6 +202,13 @@ def main():
                      "traffic": traffic, "alg_bytes_per_unit": per_unit[dom],
                      "launch_ms": kern_ms[dom]},
     }
+    valu = measured_valu(kernel_of[dom])
+    if valu is not None:  # the label scans are VALU-issue bound: the second ceiling
+        insts, peak = valu
+        rate = insts / (kern_ms[dom] / 1e3)
+        result["valu"] = {"kernel": kernel_of[dom], "insts_per_launch": insts,
+                          "achieved": rate / 1e9, "peak": peak / 1e9,
+                          "unit": "G wave64-instr/s", "frac": rate / peak}
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(q, k, v, do, args)
     print(json.dumps(result), flush=True)
@@ -216,6 +223,18 @@ def measured_traffic(kernel):
         with open(path) as f:
             t = json.load(f)
         return t["kernels"][kernel]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def measured_valu(kernel):
+    """(VALU wave-instructions per launch of `kernel`, peak issue rate) from the committed
+    rocprofv3 PMC summary (profiles/valu.json: SQ_INSTS_VALU), or None."""
+    path = os.path.join(ROOT, "profiles", "valu.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        return t["kernels"][kernel]["valu_insts"], t["peak_wave_insts_per_s"]
     except (OSError, KeyError, ValueError):
         return None
 

@@ -74,19 +74,19 @@ int32_t dism_hard_boundary(const int32_t* iq, const int32_t* ik, const uint8_t* 
                            int32_t* boundary, void* stream);
 
 /* Size in bytes of the caller-owned workspace for these dimensions (-1 for unsupported
- * dimensions).  It holds the position orders of dism_hard_prepare (combined label order of
- * queries and keys, bigram orders of each side), the bigram-pair plans, and one record per
- * query row (pair statistics / partial readout in the forward, row corrections in the
- * backward); about 4*B*H*N*(DV + 30) bytes.
+ * dimensions, or B*H*N >= 2^31).  It holds the position orders of dism_hard_prepare
+ * (combined label order of queries and keys, bigram position lists of each side), the
+ * bigram-pair owner records, and one record per query row (partial readout in the forward,
+ * row corrections in the backward); about 4*B*H*N*(DV + 48) bytes.
  * No reference counterpart: the reference keeps an O(B*H*N^2/32) int32 boundary instead. */
 int64_t dism_hard_workspace_bytes(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV,
                                   int32_t dtype);
 
 /* Preparation into `workspace` (labels only; the vectors are validated, not read):
- *   - per (b,h): stable radix sorts giving the combined label order of the 2N query/key
- *     entries and the bigram order (label[p-1], label[p]) of each side;
+ *   - per (b,h): stable sorts giving the combined label order of the 2N query/key entries
+ *     and the bigram order (label[p-1], label[p]) of the queries and of the keys;
  *   - per query row and per key: the range of its bigram partners (the pairs with match
- *     length >= 2) and the list of owners that have any.
+ *     length >= 2), and the owners that have any, listed by partner-count class.
  * A workspace prepared once serves dism_hard_readout and the backward entry points for the
  * same labels.  Replaces the summary + chunk passes that precede the reference readout
  * (dism_v3/python/flash_dism/hard_forward.py:36-40). */
