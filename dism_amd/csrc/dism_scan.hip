@@ -238,18 +238,8 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
             for (int e = 0; e < wn; ++e) {
                 float rr[R];
                 lds_row_f32<R>(&s_r[e][0], rr);
-                if (!((qm >> e) & 1)) {
-                    const unsigned char* row = vbuf + slot * RB;
-                    ++slot;
-                    float vv[COLS];
-#pragma unroll
-                    for (int c = 0; c < COLS; ++c)
-                        vv[c] = lane + 64 * c < DV ? lds_elem<T>(row, lane + 64 * c) : 0.0f;
-#pragma unroll
-                    for (int r = 0; r < R; ++r)
-#pragma unroll
-                        for (int c = 0; c < COLS; ++c) M[r][c] = __builtin_fmaf(rr[r], vv[c], M[r][c]);
-                } else {
+                const bool qe = (qm >> e) & 1;
+                if (qe) {
                     float y[COLS];
 #pragma unroll
                     for (int c = 0; c < COLS; ++c) {
@@ -270,6 +260,21 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
                         for (int c = 0; c < COLS; ++c)
                             if (lane + 64 * c < DV) rec[lane + 64 * c] = y[c];
                     }
+                }
+                // two one-sided branches kept apart (an if/else made the compiler copy the
+                // running matrix on every entry): read M, then update M in place
+                asm volatile("" ::: "memory");
+                if (!qe) {
+                    const unsigned char* row = vbuf + slot * RB;
+                    ++slot;
+                    float vv[COLS];
+#pragma unroll
+                    for (int c = 0; c < COLS; ++c)
+                        vv[c] = lane + 64 * c < DV ? lds_elem<T>(row, lane + 64 * c) : 0.0f;
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+#pragma unroll
+                        for (int c = 0; c < COLS; ++c) M[r][c] = __builtin_fmaf(rr[r], vv[c], M[r][c]);
                 }
             }
             if (!wk.rotate()) break;
@@ -399,11 +404,8 @@ __global__ __launch_bounds__(64 * WAVES) void scan_rows_kernel(PathArgs a) {
                 const unsigned char* row = vbuf + e * RB + gl * VPL * (int)sizeof(T);
                 float vals[VPL];
                 lds_vals<T, VPL>(row, vals);
-                if (!((qm >> e) & 1)) {
-                    const float s = s_r[e][rl];
-#pragma unroll
-                    for (int t = 0; t < VPL; ++t) M[t] = __builtin_fmaf(s, vals[t], M[t]);
-                } else {
+                const bool qe = (qm >> e) & 1;
+                if (qe) {
                     float part = 0.0f;
 #pragma unroll
                     for (int t = 0; t < VPL; ++t) part = __builtin_fmaf(vals[t], M[t], part);
@@ -421,6 +423,12 @@ __global__ __launch_bounds__(64 * WAVES) void scan_rows_kernel(PathArgs a) {
                     for (int r = 0; r < R; ++r)
                         se0 = __builtin_fmaf(sqr[r], readlane_f(zq, r * G), se0);
                     se0v = lane == e ? se0 : se0v;
+                }
+                asm volatile("" ::: "memory");  // one-sided branches (see scan_forward_kernel)
+                if (!qe) {
+                    const float s = s_r[e][rl];
+#pragma unroll
+                    for (int t = 0; t < VPL; ++t) M[t] = __builtin_fmaf(s, vals[t], M[t]);
                 }
             }
             if (isq) {
@@ -460,6 +468,11 @@ __global__ __launch_bounds__(64 * WAVES) void scan_keys_kernel(PathArgs a) {
     auto& s_v = s_v_all[wave_id()];
     __shared__ __attribute__((aligned(16))) float s_r_all[WAVES][WIN][R];
     auto& s_r = s_r_all[wave_id()];
+    // N in row-group order for one key's dSK: written column-wise, read as row-group segments
+    // (rows padded by 4 floats: the 8-float segments of consecutive rows then fall on
+    // different banks)
+    __shared__ __attribute__((aligned(16))) float s_t_all[WAVES][R][DV + 4];
+    auto& s_t = s_t_all[wave_id()];
     Item it;
     if (!scan_item(a, it)) return;
     const int lane = lane_id(), rl = lane / G, gl = lane % G;
@@ -514,13 +527,11 @@ __global__ __launch_bounds__(64 * WAVES) void scan_keys_kernel(PathArgs a) {
         if (wk.nwin > 1) issue(1, wk.entN);
         wait_vm0();
 
-        float Nd[R][COLS], Ng[VPL];
+        float Nd[R][COLS];
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int c = 0; c < COLS; ++c) Nd[r][c] = 0.0f;
-#pragma unroll
-        for (int t = 0; t < VPL; ++t) Ng[t] = 0.0f;
         do {
             const int kk = wk.k, wn = __builtin_amdgcn_readfirstlane(wk.count(kk));
             const int ent = wk.entC, p = ent >> 1;
@@ -540,23 +551,12 @@ __global__ __launch_bounds__(64 * WAVES) void scan_keys_kernel(PathArgs a) {
             const unsigned char* vbuf = s_v[kk & 1];
             for (int e = 0; e < wn; ++e) {
                 const unsigned char* row = vbuf + e * RB;
-                float vg[VPL];
-                lds_vals<T, VPL>(row + gl * VPL * (int)sizeof(T), vg);
-                float vd[COLS];
-#pragma unroll
-                for (int c = 0; c < COLS; ++c)
-                    vd[c] = lane + 64 * c < DV ? lds_elem<T>(row, lane + 64 * c) : 0.0f;
                 float rr[R];
                 lds_row_f32<R>(&s_r[e][0], rr);
-                if ((qm >> e) & 1) {
-#pragma unroll
-                    for (int r = 0; r < R; ++r)
-#pragma unroll
-                        for (int c = 0; c < COLS; ++c) Nd[r][c] = __builtin_fmaf(rr[r], vd[c], Nd[r][c]);
-                    const float ar = s_r[e][rl];
-#pragma unroll
-                    for (int t = 0; t < VPL; ++t) Ng[t] = __builtin_fmaf(ar, vg[t], Ng[t]);
-                } else {
+                const bool qe = (qm >> e) & 1;
+                if (!qe) {
+                    // key: dV0 = sk . N (lane-local); dSK0 = N . v over d, from N moved to the
+                    // row-group layout through LDS (lane = r*G + g takes N[r][gV .. gV+V))
                     const int j = readlane_i(p, e);
                     const long krow = it.row0 + (long)j * a.H;
 #pragma unroll
@@ -564,13 +564,34 @@ __global__ __launch_bounds__(64 * WAVES) void scan_keys_kernel(PathArgs a) {
                         float y = 0.0f;
 #pragma unroll
                         for (int r = 0; r < R; ++r) y = __builtin_fmaf(rr[r], Nd[r][c], y);
-                        if (lane + 64 * c < DV) a.dv[krow * DV + lane + 64 * c] = y;
+                        if (lane + 64 * c < DV) {
+                            a.dv[krow * DV + lane + 64 * c] = y;
+#pragma unroll
+                            for (int r = 0; r < R; ++r) s_t[r][lane + 64 * c] = Nd[r][c];
+                        }
                     }
+                    float vg[VPL], ng[VPL];
+                    lds_vals<T, VPL>(row + gl * VPL * (int)sizeof(T), vg);
+                    lds_row_f32<VPL>(&s_t[rl][gl * VPL], ng);
                     float part = 0.0f;
 #pragma unroll
-                    for (int t = 0; t < VPL; ++t) part = __builtin_fmaf(Ng[t], vg[t], part);
+                    for (int t = 0; t < VPL; ++t) part = __builtin_fmaf(ng[t], vg[t], part);
                     const float dk = group_sum<G>(part);
                     if (gl == 0) a.dsk[krow * R + rl] = dk;
+                }
+                // keeps the two one-sided branches apart (an if/else here made the compiler
+                // copy the running matrix on every entry)
+                asm volatile("" ::: "memory");
+                if (qe) {
+                    // query: N += a (x) dO (column layout, lane = d)
+                    float vd[COLS];
+#pragma unroll
+                    for (int c = 0; c < COLS; ++c)
+                        vd[c] = lane + 64 * c < DV ? lds_elem<T>(row, lane + 64 * c) : 0.0f;
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+#pragma unroll
+                        for (int c = 0; c < COLS; ++c) Nd[r][c] = __builtin_fmaf(rr[r], vd[c], Nd[r][c]);
                 }
             }
             if (!wk.rotate()) break;

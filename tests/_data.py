@@ -66,3 +66,23 @@ def flags(b, h):
 
 def taus(h):
     return np.linspace(-0.5, 0.5, h).astype(np.float32)
+
+
+def copied_spans(q, k, frac=0.10, lo=32, hi=512, seed=20261204):
+    """BASELINE configs[3] generator: starting at t=0 and stepping forward, copy spans of length
+    U[lo, hi] from an earlier source s0 (s0 + len <= t0) until `frac` of the positions are
+    covered: q[:, t0:t0+len] := k[:, s0:s0+len] (all batch rows and heads alike), so queries
+    match earlier keys with long suffixes.  q, k: [B, T, H, d] float arrays, modified in place."""
+    rng = np.random.default_rng(seed)
+    T = q.shape[1]
+    covered, t0 = 0, 0
+    while covered < frac * T:
+        ln = int(rng.integers(lo, hi + 1))
+        t0 = int(rng.integers(t0 + ln, min(T - ln, t0 + 4 * hi) + 1)) if t0 + ln <= T - ln else T
+        if t0 + ln > T:
+            break
+        s0 = int(rng.integers(0, t0 - ln + 1))
+        q[:, t0:t0 + ln] = k[:, s0:s0 + ln]
+        covered += ln
+        t0 += ln
+    return covered
