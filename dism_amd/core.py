@@ -1,44 +1,81 @@
-"""Differentiable hard core (autograd) on the MI355X library.
+"""Differentiable hard core (autograd, torch.compile) on the MI355X library.
 
-The hard-row part of the reference's training op: _MixedCore / dism_core_hybrid
-(dism_v3/python/flash_dism/hard_training.py:343-409) add the hard output to the soft core's
-output and, in backward, add backward_hard_recompute's FP32 gradients.  This build has no soft
-core, so ``dism_core_hard`` is the all-hard specialisation: forward_hard in forward, the
-hard backward in backward.  Unlike the reference default (which re-runs the forward in
-backward), the forward's O(B*H*N) log2 normalizer and its carry boundary are saved, so the
-backward does not recompute the forward.
+The reference's training op is _MixedCore / dism_core_hybrid
+(dism_v3/python/flash_dism/hard_training.py:343-409): the soft core's output plus the hard
+output, and in backward the soft gradients plus backward_hard_recompute's FP32 gradients.  The
+soft core skips hard rows (dism_v3/include/forward/producer.cuh:18), so on rows that are all
+hard the op is exactly the hard core.  This build implements that part:
+
+* ``hard_core`` / ``hard_core_backward`` -- torch.library custom operators (``dism_amd::``)
+  with fake (meta) implementations and a registered autograd formula, so the op is opaque to
+  torch.compile the way the reference registers its cores (flash_dism/compiler.py:143-181).
+  Unlike the reference default (which re-runs the forward in backward), the forward's
+  workspace and O(B*H*N) log2 normalizer are saved, so the backward does not recompute it.
+* ``dism_core_hard(sq, sk, v, idx_q, idx_k, hard, tau)`` -- the hard core with autograd;
+  soft rows give zero output and zero gradients.
+* ``dism_core(q, k, sq, sk, v, q_lse, k_lse, idx_q, idx_k, direction, hard, rtau, *, ctas=0,
+  _lse_preabsorbed=False)`` -- the reference's signature (flash_dism/backward.py:41); rows must
+  all be hard (soft rows need the soft DISM core, which this build does not provide, and raise).
 """
 import torch
+from torch import Tensor
 
+from . import _lib
+from ._checks import DTYPE_CODE, check_ctas, require
 from .hard_backward import backward_hard
 from .hard_forward import _forward_core
 
 
-class HardCore(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, sq, sk, v, idx_q, idx_k, hard, tau):
-        iq = idx_q.to(torch.int32).contiguous()
-        ik = idx_k.to(torch.int32).contiguous()
-        sq_c, sk_c, v_c = sq.contiguous(), sk.contiguous(), v.contiguous()
-        hard_c, tau_c = hard.contiguous(), tau.detach().float().contiguous()
-        out, lse2, lut, carry, strip, _, _, ws = _forward_core(
-            sq_c, sk_c, v_c, iq, ik, hard_c, tau_c, None, None, False)
-        ctx.save_for_backward(sq_c, sk_c, v_c, iq, ik, hard_c, tau_c, lse2, lut, ws,
-                              *(() if carry is None else (carry,)))
-        ctx.strip = strip
-        ctx.has_carry = carry is not None
-        return out
+@torch.library.custom_op("dism_amd::hard_core", mutates_args=())
+def hard_core(sq: Tensor, sk: Tensor, v: Tensor, idx_q: Tensor, idx_k: Tensor, hard: Tensor,
+              tau: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Forward: (O in the vectors' dtype, lse2 fp32 [B,H,N], LUT fp32 [H,N+1], workspace)."""
+    out, lse2, lut, _, _, _, _, ws = _forward_core(sq, sk, v, idx_q, idx_k, hard, tau, 0, None,
+                                                   False)
+    return out, lse2, lut, ws
 
-    @staticmethod
-    @torch.autograd.function.once_differentiable
-    def backward(ctx, dout):
-        saved = ctx.saved_tensors
-        sq, sk, v, iq, ik, hard, tau, lse2, lut, ws = saved[:10]
-        carry = saved[10] if ctx.has_carry else None
-        dout = dout.to(sq.dtype).contiguous()
-        state = dict(log_weights=lut, tau=tau, carry=carry, carry_strip=ctx.strip, workspace=ws)
-        dsq, dsk, dv, dtau = backward_hard(sq, sk, v, dout, iq, ik, hard, lse2, state)
-        return dsq, dsk, dv, None, None, None, dtau
+
+@hard_core.register_fake
+def _hard_core_fake(sq, sk, v, idx_q, idx_k, hard, tau):
+    b, n, h, r = sq.shape
+    dv = v.shape[3]
+    nbytes = _lib.workspace_bytes(b, n, h, r, dv, DTYPE_CODE[sq.dtype])
+    return (v.new_empty((b, n, h, dv)), sq.new_empty((b, h, n), dtype=torch.float32),
+            sq.new_empty((h, n + 1), dtype=torch.float32),
+            sq.new_empty((nbytes,), dtype=torch.uint8))
+
+
+@torch.library.custom_op("dism_amd::hard_core_backward", mutates_args=())
+def hard_core_backward(sq: Tensor, sk: Tensor, v: Tensor, dout: Tensor, idx_q: Tensor,
+                       idx_k: Tensor, hard: Tensor, tau: Tensor, lse2: Tensor, lut: Tensor,
+                       workspace: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Backward on the forward's workspace: (dSQ, dSK, dV, dtau), all fp32."""
+    state = dict(log_weights=lut, tau=tau, carry=None, carry_strip=0, workspace=workspace)
+    return tuple(backward_hard(sq, sk, v, dout.to(sq.dtype).contiguous(), idx_q, idx_k, hard,
+                               lse2, state))
+
+
+@hard_core_backward.register_fake
+def _hard_core_backward_fake(sq, sk, v, dout, idx_q, idx_k, hard, tau, lse2, lut, workspace):
+    f32 = dict(dtype=torch.float32)
+    return (sq.new_empty(sq.shape, **f32), sk.new_empty(sk.shape, **f32),
+            v.new_empty(v.shape, **f32), tau.new_empty(tau.shape, **f32))
+
+
+def _setup_context(ctx, inputs, output):
+    sq, sk, v, idx_q, idx_k, hard, tau = inputs
+    _, lse2, lut, ws = output
+    ctx.save_for_backward(sq, sk, v, idx_q, idx_k, hard, tau, lse2, lut, ws)
+
+
+def _hard_core_autograd(ctx, dout, _dlse2, _dlut, _dws):
+    sq, sk, v, idx_q, idx_k, hard, tau, lse2, lut, ws = ctx.saved_tensors
+    dsq, dsk, dv, dtau = hard_core_backward(sq, sk, v, dout, idx_q, idx_k, hard, tau, lse2,
+                                            lut, ws)
+    return dsq, dsk, dv, None, None, None, dtau
+
+
+hard_core.register_autograd(_hard_core_autograd, setup_context=_setup_context)
 
 
 def dism_core_hard(sq, sk, v, idx_q, idx_k, hard, tau):
@@ -46,5 +83,48 @@ def dism_core_hard(sq, sk, v, idx_q, idx_k, hard, tau):
 
     sq, sk [B,N,H,R], v [B,N,H,DV] (bf16 or f32), labels [B,H,N] int, hard [B,H] bool,
     tau [H] (natural-log match coefficient).  Returns O [B,N,H,DV] in the vectors' dtype.
+    Soft rows give zero output and zero gradients.
     """
-    return HardCore.apply(sq, sk, v, idx_q, idx_k, hard, tau)
+    iq = idx_q.to(torch.int32).contiguous()
+    ik = idx_k.to(torch.int32).contiguous()
+    return hard_core(sq.contiguous(), sk.contiguous(), v.contiguous(), iq, ik, hard.contiguous(),
+                     tau.float().contiguous())[0]
+
+
+def dism_core(q, k, sq, sk, v, q_lse, k_lse, idx_q, idx_k, direction, hard, rtau, *, ctas=0,
+              _lse_preabsorbed=False):
+    """Differentiable core with the reference's signature (flash_dism/backward.py:41-54) for
+    sequences that are all hard: O = hard output (the soft core skips hard rows), gradients
+    for sq, sk, v and rtau; q, k, q_lse, k_lse receive zero gradients.  Soft rows raise
+    NotImplementedError (they need the soft core).  ``rtau`` is the natural-log coefficient,
+    used as is (no softplus), as in the reference's hard path."""
+    check_ctas(ctas)
+    b, n, h = sq.shape[0], sq.shape[1], sq.shape[2]
+    require(tuple(q.shape[:3]) == (b, n, h) and tuple(k.shape[:3]) == (b, n, h),
+            "q/k must match sq/sk in [B,N,H]")
+    require(tuple(q_lse.shape) == (b, h, n) and tuple(k_lse.shape) == (b, h, n),
+            "q_lse/k_lse must be [B,H,N]")
+    require(tuple(direction.shape) == (b, h), "direction must be [B,H]")
+    require(isinstance(hard, torch.Tensor) and tuple(hard.shape) == (b, h),
+            "fixed hard must be [B,H]")
+    # (a host read of the flags; skipped inside a compiled graph, where soft rows give zeros)
+    if not torch.compiler.is_compiling() and not bool(hard.all()):
+        raise NotImplementedError(
+            "soft rows need the soft DISM core, which the MI355X hard core does not provide")
+    out = dism_core_hard(sq, sk, v, idx_q, idx_k, hard, rtau)
+    return _SoftOperands.apply(out, q, k, q_lse, k_lse)
+
+
+class _SoftOperands(torch.autograd.Function):
+    """Identity on O; zero gradients for the soft core's operands (q, k, q_lse, k_lse), which
+    all-hard rows do not read."""
+
+    @staticmethod
+    def forward(ctx, out, q, k, q_lse, k_lse):
+        ctx.save_for_backward(q, k, q_lse, k_lse)
+        return out.view_as(out)
+
+    @staticmethod
+    def backward(ctx, grad):
+        return (grad, *(torch.zeros_like(t) if ctx.needs_input_grad[i + 1] else None
+                        for i, t in enumerate(ctx.saved_tensors)))

@@ -1,0 +1,78 @@
+"""torch.library registration of the hard core (CPU: fake/meta shapes and argument checks;
+GPU: eager vs torch.compile, reference-signature core)."""
+import numpy as np
+import pytest
+import torch
+
+import dism_amd
+
+
+def _fake_inputs(b=2, n=512, h=3, r=8, dv=64, dtype=torch.bfloat16):
+    sq = torch.empty(b, n, h, r, dtype=dtype)
+    v = torch.empty(b, n, h, dv, dtype=dtype)
+    lab = torch.empty(b, h, n, dtype=torch.int32)
+    return sq, sq.clone(), v, lab, lab.clone(), torch.empty(b, h, dtype=torch.bool), torch.empty(h)
+
+
+def test_fake_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from dism_amd import _lib
+    with FakeTensorMode():
+        sq, sk, v, iq, ik, hard, tau = _fake_inputs()
+        out, lse2, lut, ws = torch.ops.dism_amd.hard_core(sq, sk, v, iq, ik, hard, tau)
+        assert out.shape == v.shape and out.dtype == torch.bfloat16
+        assert lse2.shape == (2, 3, 512) and lse2.dtype == torch.float32
+        assert lut.shape == (3, 513)
+        assert ws.shape == (_lib.workspace_bytes(2, 512, 3, 8, 64, 0),) and ws.dtype == torch.uint8
+        g = torch.ops.dism_amd.hard_core_backward(sq, sk, v, out, iq, ik, hard, tau, lse2, lut, ws)
+        assert [t.shape for t in g] == [sq.shape, sk.shape, v.shape, tau.shape]
+        assert all(t.dtype == torch.float32 for t in g)
+
+
+def test_reference_signature_checks_cpu():
+    sq, sk, v, iq, ik, _, tau = _fake_inputs(b=1, n=256, h=2)
+    sq, sk, v = torch.zeros_like(sq), torch.zeros_like(sk), torch.zeros_like(v)
+    q, k = sq.clone(), sk.clone()
+    lse = torch.zeros(1, 2, 256)
+    hard = torch.ones(1, 2, dtype=torch.bool)
+    direction = torch.zeros(1, 2, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="q_lse/k_lse"):
+        dism_amd.dism_core(q, k, sq, sk, v, lse[:, :1], lse, iq, ik, direction, hard, tau)
+    with pytest.raises(NotImplementedError, match="soft rows"):
+        dism_amd.dism_core(q, k, sq, sk, v, lse, lse, iq, ik, direction, ~hard, tau)
+    with pytest.raises(RuntimeError, match="CUDA"):  # the product path never computes on the host
+        dism_amd.dism_core(q, k, sq, sk, v, lse, lse, iq, ik, direction, hard, tau)
+
+
+@pytest.mark.gpu
+def test_compiled_matches_eager():
+    from tests._data import labels, taus, vectors
+    n, b, h = 512, 2, 3
+    sq, sk, v = vectors(n, b, h)
+    q, k = labels(n, "alphabet4", b, h)
+    d = torch.device("cuda")
+    dout = torch.from_numpy(np.random.default_rng(5).standard_normal(v.shape).astype(np.float32))
+    dout = dout.to(d, torch.bfloat16)
+    iq, ik = torch.from_numpy(q).to(d), torch.from_numpy(k).to(d)
+    hard = torch.ones((b, h), dtype=torch.bool, device=d)
+
+    def run(fn):
+        leaves = [torch.from_numpy(a).to(d, torch.bfloat16).requires_grad_() for a in (sq, sk, v)]
+        tau = torch.from_numpy(taus(h)).to(d).requires_grad_()
+        qs = leaves[0].detach().clone().requires_grad_()
+        lse = torch.zeros((b, h, n), device=d, requires_grad=True)
+        direction = torch.zeros((b, h), dtype=torch.uint8, device=d)
+        out = fn(qs, leaves[1].detach(), *leaves, lse, lse.detach(), iq, ik, direction, hard, tau)
+        out.backward(dout)
+        return out.detach(), [t.grad for t in leaves] + [tau.grad, qs.grad, lse.grad]
+
+    eager = run(dism_amd.dism_core)
+    compiled = run(torch.compile(dism_amd.dism_core, backend="aot_eager", fullgraph=True))
+    assert torch.equal(eager[0], compiled[0])
+    for a, c in zip(eager[1], compiled[1]):
+        assert torch.equal(a, c)
+    assert not eager[1][4].any() and not eager[1][5].any()  # soft operands: zero gradients
+    # the reference-signature core is the hard core on all-hard rows
+    ref = dism_amd.dism_core_hard(*(torch.from_numpy(a).to(d, torch.bfloat16) for a in (sq, sk, v)),
+                                  iq, ik, hard, torch.from_numpy(taus(h)).to(d))
+    assert torch.equal(ref, eager[0])
