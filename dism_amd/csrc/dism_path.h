@@ -170,6 +170,45 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
+// Sums x[r] over the 64 lanes for every r at once.  The high lane bits go first (32, 16, ...,
+// down to G = 64/R), each step pairing lane l with lane l ^ m and halving the values a lane
+// holds (lanes with bit m set keep the upper half); then group_sum's adjacent tree runs over
+// the G lanes of a group.  Lane l ends with the sum for r = l / G (complete where l % G == 0):
+//   t[l] = x_r at lane l;  for m = 32, 16, ..., G: t[l] = t[l] + t[l + m] (l < m);
+//   then ((t0 + t1) + (t2 + t3)) + ... over t[0 .. G).
+template <int H, int M, int R>
+__device__ __forceinline__ void transpose_step(float (&x)[R]) {
+    if constexpr (H >= 1) {
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const float a = x[i], b = x[i + H];
+            if constexpr (M == 32) {
+                const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(a),
+                                                                __float_as_uint(b), false, false);
+                x[i] = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+            } else if constexpr (M == 16) {
+                const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(a),
+                                                                __float_as_uint(b), false, false);
+                x[i] = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+            } else {
+                const bool up = lane_id() & M;
+                const float keep = up ? b : a, send = up ? a : b;
+                if constexpr (M == 8)
+                    x[i] = keep + dpp<0x128>(send);  // row_ror:8 = lane ^ 8 within a row
+                else
+                    x[i] = keep + __shfl_xor(send, M);
+            }
+        }
+        transpose_step<H / 2, M / 2, R>(x);
+    }
+}
+
+template <int R>
+__device__ __forceinline__ float lane_transpose_sum(float (&x)[R]) {
+    transpose_step<R / 2, 32, R>(x);
+    return group_sum<64 / R>(x[0]);
+}
+
 // LDS readers below take generic pointers into __shared__ arrays; after inlining the
 // compiler sees the LDS origin and emits ds_read instructions.
 // NV consecutive elements of T (aligned to NV * sizeof(T) or 16 bytes)

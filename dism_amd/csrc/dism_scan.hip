@@ -24,8 +24,9 @@
 // fp32 sequences (the CPU model repeats them):
 //   M, N: fma chains over the group's entries in merge order (N in DESCENDING position);
 //   y[d] = chain_r fma(sq[r], M[r][d]);  dv0[d] = chain_r fma(sk[r], N[r][d]);
-//   zq[r] = tree_g(chain_t fma(dO[gV+t], M[r][gV+t])),  dsk0[r] = tree_g(chain_t
-//   fma(N[r][gV+t], v[gV+t])) with V = VPL, tree_g the pairwise tree over g = 0..G-1.
+//   zq[r] = tree_g(chain_t fma(dO[gV+t], M[r][gV+t])) with V = VPL, tree_g the pairwise tree
+//   over g = 0..G-1;  dsk0[r] = lane tree (lane_transpose_sum) of the per-lane terms
+//   fma(N[r][l+64], v[l+64], N[r][l]*v[l]) (DV = 128) or N[r][l]*v[l] (0 beyond DV).
 #include "dism_path.h"
 
 namespace dism {
@@ -456,23 +457,18 @@ __global__ __launch_bounds__(64 * WAVES) void scan_rows_kernel(PathArgs a) {
 // ---------------------------------------------------------------------------------------
 // backward, keys: the length-1 parts dSK0, dV0 (pair corrections are added afterwards by the
 // key pair kernel).  Merge in DESCENDING position order: a query at the key's own position
-// comes before the key.  N is kept in both layouts: column (for dV) and row-group (for dSK).
+// comes before the key.  N is kept in the column layout (lane = d); dSK0 reduces over lanes.
 template <typename T, int R, int DV>
 __global__ __launch_bounds__(64 * WAVES) void scan_keys_kernel(PathArgs a) {
     using G_ = Geo<T, DV>;
     constexpr int WIN = G_::WIN, RB = G_::RB, NI = G_::NI;
     constexpr int COLS = (DV + 63) / 64;
     constexpr int W = words_of(sizeof(T), R);
-    constexpr int G = 64 / R, VPL = DV / G;
+    constexpr int G = 64 / R;
     __shared__ __attribute__((aligned(16))) unsigned char s_v_all[WAVES][2][WBYTES];
     auto& s_v = s_v_all[wave_id()];
     __shared__ __attribute__((aligned(16))) float s_r_all[WAVES][WIN][R];
     auto& s_r = s_r_all[wave_id()];
-    // N in row-group order for one key's dSK: written column-wise, read as row-group segments
-    // (rows padded by 4 floats: the 8-float segments of consecutive rows then fall on
-    // different banks)
-    __shared__ __attribute__((aligned(16))) float s_t_all[WAVES][R][DV + 4];
-    auto& s_t = s_t_all[wave_id()];
     Item it;
     if (!scan_item(a, it)) return;
     const int lane = lane_id(), rl = lane / G, gl = lane % G;
@@ -554,29 +550,31 @@ __global__ __launch_bounds__(64 * WAVES) void scan_keys_kernel(PathArgs a) {
                 float rr[R];
                 lds_row_f32<R>(&s_r[e][0], rr);
                 const bool qe = (qm >> e) & 1;
+                // the entry's value row in the column layout (v for a key, dO for a query)
+                float vd[COLS];
+#pragma unroll
+                for (int c = 0; c < COLS; ++c)
+                    vd[c] = lane + 64 * c < DV ? lds_elem<T>(row, lane + 64 * c) : 0.0f;
                 if (!qe) {
-                    // key: dV0 = sk . N (lane-local); dSK0 = N . v over d, from N moved to the
-                    // row-group layout through LDS (lane = r*G + g takes N[r][gV .. gV+V))
+                    // key: dV0 = sk . N (lane-local); dSK0 = N . v over d, from per-lane
+                    // partial products summed across the wave by lane_transpose_sum
                     const int j = readlane_i(p, e);
                     const long krow = it.row0 + (long)j * a.H;
+                    float part[R];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        part[r] = Nd[r][0] * vd[0];
+#pragma unroll
+                        for (int c = 1; c < COLS; ++c) part[r] = __builtin_fmaf(Nd[r][c], vd[c], part[r]);
+                    }
 #pragma unroll
                     for (int c = 0; c < COLS; ++c) {
                         float y = 0.0f;
 #pragma unroll
                         for (int r = 0; r < R; ++r) y = __builtin_fmaf(rr[r], Nd[r][c], y);
-                        if (lane + 64 * c < DV) {
-                            a.dv[krow * DV + lane + 64 * c] = y;
-#pragma unroll
-                            for (int r = 0; r < R; ++r) s_t[r][lane + 64 * c] = Nd[r][c];
-                        }
+                        if (lane + 64 * c < DV) a.dv[krow * DV + lane + 64 * c] = y;
                     }
-                    float vg[VPL], ng[VPL];
-                    lds_vals<T, VPL>(row + gl * VPL * (int)sizeof(T), vg);
-                    lds_row_f32<VPL>(&s_t[rl][gl * VPL], ng);
-                    float part = 0.0f;
-#pragma unroll
-                    for (int t = 0; t < VPL; ++t) part = __builtin_fmaf(ng[t], vg[t], part);
-                    const float dk = group_sum<G>(part);
+                    const float dk = lane_transpose_sum<R>(part);
                     if (gl == 0) a.dsk[krow * R + rl] = dk;
                 }
                 // keeps the two one-sided branches apart (an if/else here made the compiler
@@ -584,10 +582,6 @@ __global__ __launch_bounds__(64 * WAVES) void scan_keys_kernel(PathArgs a) {
                 asm volatile("" ::: "memory");
                 if (qe) {
                     // query: N += a (x) dO (column layout, lane = d)
-                    float vd[COLS];
-#pragma unroll
-                    for (int c = 0; c < COLS; ++c)
-                        vd[c] = lane + 64 * c < DV ? lds_elem<T>(row, lane + 64 * c) : 0.0f;
 #pragma unroll
                     for (int r = 0; r < R; ++r)
 #pragma unroll

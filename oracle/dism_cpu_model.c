@@ -486,6 +486,26 @@ static float rg_reduce(const float* a, const float* b, int DV, int R) {
     return t[0];
 }
 
+/* Lane-tree reduction of sum_d a[d]*b[d] (DV <= 128) for readout width R, G = 64/R: lane l
+ * holds the term fma(a[l+64], b[l+64], a[l]*b[l]) (DV = 128), a[l]*b[l] (l < DV) or 0; the
+ * high lane bits are paired first, t[l] = t[l] + t[l+m] for m = 32, 16, ..., G, then the G
+ * remaining partials form the pairwise tree ((t0 + t1) + (t2 + t3)) + ...  This is the order
+ * of the HIP column-layout reduction (lane = d) with its transposing butterfly. */
+static float lane_reduce(const float* a, const float* b, int DV, int R) {
+    float t[64];
+    const int G = 64 / R;
+    for (int l = 0; l < 64; ++l) {
+        float x = l < DV ? a[l] * b[l] : 0.0f;
+        if (l + 64 < DV) x = fmaf(a[l + 64], b[l + 64], x);
+        t[l] = x;
+    }
+    for (int m = 32; m >= G; m /= 2)
+        for (int l = 0; l < m; ++l) t[l] = t[l] + t[l + m];
+    for (int sz = 1; sz < G; sz *= 2)
+        for (int g = 0; g < G; g += 2 * sz) t[g] = t[g] + t[g + sz];
+    return t[0];
+}
+
 /* Pairwise tree ((t0 + t1) + (t2 + t3)) + ... over the products t[d] = a[d]*b[d], n a power
  * of two <= 128: the bigram-pair DV-dot of the HIP pair kernels (lanes hold contiguous
  * column groups, reduced in-lane and then across lanes by the same adjacent pairing). */
@@ -640,7 +660,7 @@ void orc_forward(const float* sq, const float* sk, const float* v, const int32_t
  *   f = exp2(-l2); mass = z+f; mean = fma(-f, c, vv)/mass; rowtau = fma(-u, mean, w)/mass
  * Per key j (valid queries i >= j of the same label):
  *   N_j[r][d] = fma chain over valid queries, DESCENDING i, of (P1_i*sq_i[r]) * dO_i[d]
- *   dv0[d] = chain_r fma(sk_j[r], N[r][d]);  dsk0[r] = rg_reduce(N[r], v_j)
+ *   dv0[d] = chain_r fma(sk_j[r], N[r][d]);  dsk0[r] = lane_reduce(N[r], v_j)
  *   for bigram queries i of j (ascending i): p = exp2(LUT[L]-l2_i); dp = p - P1_i;
  *       s = chain(sq_i.sk_j); e = tree(dO_i.v_j); cdk[r] = fma(dp*e, sq_i[r], cdk[r]);
  *       cdv[d] = fma(dp*s, dO_i[d], cdv[d])
@@ -792,7 +812,7 @@ void orc_backward(const float* sq, const float* sk, const float* v, const float*
                     }
                 /* corrections are added only to keys that have bigram pairs */
                 for (int r = 0; r < R; ++r) {
-                    const float base = rg_reduce(M + (long)r * DV, vj, DV, R);
+                    const float base = lane_reduce(M + (long)r * DV, vj, DV, R);
                     dsk[krow * R + r] = npair ? base + cd[r] : base;
                 }
                 for (int d = 0; d < DV; ++d) {
