@@ -250,6 +250,25 @@ __device__ __forceinline__ float lds_elem(const unsigned char* row, int d) {
 }
 
 // R fp32 values at p (broadcast read when p is uniform)
+// R consecutive fp32 values to global memory (16-byte stores where R allows; rows of R
+// floats start at multiples of R floats)
+template <int R>
+__device__ __forceinline__ void store_row_f32(float* p, const float (&x)[R]) {
+    if constexpr (R % 4 == 0) {
+#pragma unroll
+        for (int c = 0; c < R / 4; ++c)
+            reinterpret_cast<float4*>(p)[c] = make_float4(x[4 * c], x[4 * c + 1], x[4 * c + 2],
+                                                          x[4 * c + 3]);
+    } else if constexpr (R % 2 == 0) {
+#pragma unroll
+        for (int c = 0; c < R / 2; ++c)
+            reinterpret_cast<float2*>(p)[c] = make_float2(x[2 * c], x[2 * c + 1]);
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) p[r] = x[r];
+    }
+}
+
 template <int R>
 __device__ __forceinline__ void lds_row_f32(const float* p, float (&out)[R]) {
     if constexpr (R % 4 == 0) {

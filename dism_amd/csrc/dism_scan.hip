@@ -301,8 +301,8 @@ __global__ __launch_bounds__(64 * WAVES) void scan_rows_kernel(PathArgs a) {
     auto& s_v = s_v_all[wave_id()];
     __shared__ __attribute__((aligned(16))) float s_r_all[WAVES][WIN][R];
     auto& s_r = s_r_all[wave_id()];
-    __shared__ __attribute__((aligned(16))) float s_c_all[WAVES][WIN][R];
-    auto& s_c = s_c_all[wave_id()];
+    __shared__ __attribute__((aligned(16))) float s_z_all[WAVES][WIN][R];
+    auto& s_z = s_z_all[wave_id()];
     Item it;
     if (!scan_item(a, it)) return;
     const int lane = lane_id(), rl = lane / G, gl = lane % G;
@@ -385,10 +385,7 @@ __global__ __launch_bounds__(64 * WAVES) void scan_rows_kernel(PathArgs a) {
                 for (int r = 0; r < R; ++r) rr[r] = word_elem<T>(wC, r);
                 if (ok) {
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        s_r[lane][r] = rr[r];
-                        s_c[lane][r] = has ? __uint_as_float(xC[3 + r]) : 0.0f;
-                    }
+                    for (int r = 0; r < R; ++r) s_r[lane][r] = rr[r];
                 }
             }
             const float l2 = __uint_as_float(xC[0]);
@@ -400,30 +397,19 @@ __global__ __launch_bounds__(64 * WAVES) void scan_rows_kernel(PathArgs a) {
             const float cw = has ? __uint_as_float(xC[5 + R]) : 0.0f;
             const float cz = has ? __uint_as_float(xC[6 + R]) : 0.0f;
             const unsigned char* vbuf = s_v[kk & 1];
-            float se0v = 0.0f;
             for (int e = 0; e < wn; ++e) {
                 const unsigned char* row = vbuf + e * RB + gl * VPL * (int)sizeof(T);
                 float vals[VPL];
                 lds_vals<T, VPL>(row, vals);
                 const bool qe = (qm >> e) & 1;
                 if (qe) {
+                    // zq[r] of this query to LDS; dSQ and the tau terms are finished
+                    // lane-parallel (one query per lane) after the window
                     float part = 0.0f;
 #pragma unroll
                     for (int t = 0; t < VPL; ++t) part = __builtin_fmaf(vals[t], M[t], part);
                     const float zq = group_sum<G>(part);
-                    if (gl == 0) {
-                        const float P1e = readlane_f(P1, e);
-                        const int i = readlane_i(p, e);
-                        a.dsq[(it.row0 + (long)i * a.H) * R + rl] =
-                            __builtin_fmaf(P1e, zq, s_c[e][rl]);
-                    }
-                    float sqr[R];
-                    lds_row_f32<R>(&s_r[e][0], sqr);
-                    float se0 = 0.0f;
-#pragma unroll
-                    for (int r = 0; r < R; ++r)
-                        se0 = __builtin_fmaf(sqr[r], readlane_f(zq, r * G), se0);
-                    se0v = lane == e ? se0 : se0v;
+                    if (gl == 0) s_z[e][rl] = zq;
                 }
                 asm volatile("" ::: "memory");  // one-sided branches (see scan_forward_kernel)
                 if (!qe) {
@@ -432,7 +418,19 @@ __global__ __launch_bounds__(64 * WAVES) void scan_rows_kernel(PathArgs a) {
                     for (int t = 0; t < VPL; ++t) M[t] = __builtin_fmaf(s, vals[t], M[t]);
                 }
             }
+            asm volatile("" ::: "memory");
             if (isq) {
+                float zq[R], rr[R], g[R];
+                lds_row_f32<R>(&s_z[lane][0], zq);
+#pragma unroll
+                for (int r = 0; r < R; ++r) rr[r] = word_elem<T>(wC, r);
+                float se0v = 0.0f;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    se0v = __builtin_fmaf(rr[r], zq[r], se0v);
+                    g[r] = __builtin_fmaf(P1, zq[r], has ? __uint_as_float(xC[3 + r]) : 0.0f);
+                }
+                store_row_f32<R>(a.dsq + (it.row0 + (long)p * a.H) * R, g);
                 const float fc = (float)cnt;
                 const float uu = __builtin_fmaf(P1, se0v, cu);
                 const float vv = __builtin_fmaf(fc, q1, cvv);
