@@ -29,8 +29,8 @@ def check_ctas(ctas):
 
 def check_layout(layout):
     if layout is not None:
-        raise NotImplementedError(
-            "packed varlen layouts are not implemented by the MI355X hard core yet")
+        from .varlen import VarlenLayout
+        require(isinstance(layout, VarlenLayout), "layout must be a VarlenLayout")
 
 
 def check_graph_choice(choice):

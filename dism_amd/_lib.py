@@ -32,6 +32,12 @@ SIGNATURES = {
     "dism_hard_backward_key_pairs": [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _I64, _P,
                                      _I64, _I64, _I64, _I32, _I32, _P, _I64, _P, _P, _P],
     "dism_hard_tau_reduce": [_P, _I64, _I64, _I64, _P, _P],
+    "dism_hard_packed_prepare": [_P, _P, _P, _I32, _P, _P, _P, _I64, _I64, _I64, _I32, _I32,
+                                 _P, _I64, _P],
+    "dism_hard_packed_readout": [_P, _P, _P, _I32, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32,
+                                 _I32, _P, _I64, _P, _I32, _P, _P, _P, _P],
+    "dism_hard_packed_backward": [_P, _P, _P, _P, _I32, _P, _I64, _P, _P, _I64, _I64, _P, _I64,
+                                  _I64, _I32, _I32, _P, _I64, _P, _P, _P, _P, _P, _P],
 }
 
 _lib = None
@@ -60,6 +66,8 @@ def load():
         lib.dism_abi_version.argtypes = []
         lib.dism_hard_workspace_bytes.restype = ctypes.c_int64
         lib.dism_hard_workspace_bytes.argtypes = [_I64, _I64, _I64, _I32, _I32, _I32]
+        lib.dism_hard_packed_workspace_bytes.restype = ctypes.c_int64
+        lib.dism_hard_packed_workspace_bytes.argtypes = [_I64, _I64, _I32, _I32, _I32]
         _lib = lib
     return _lib
 
@@ -78,4 +86,12 @@ def workspace_bytes(B, N, H, R, DV, dtype_code):
     nbytes = load().dism_hard_workspace_bytes(B, N, H, R, DV, dtype_code)
     if nbytes < 0:
         raise RuntimeError(f"unsupported hard-core dimensions B={B} N={N} H={H} R={R} DV={DV}")
+    return nbytes
+
+
+def packed_workspace_bytes(N, H, R, DV, dtype_code):
+    """Bytes of a packed (varlen) call's workspace (raises for unsupported dimensions)."""
+    nbytes = load().dism_hard_packed_workspace_bytes(N, H, R, DV, dtype_code)
+    if nbytes < 0:
+        raise RuntimeError(f"unsupported packed hard-core dimensions N={N} H={H} R={R} DV={DV}")
     return nbytes

@@ -23,7 +23,8 @@ from torch import Tensor
 from . import _lib
 from ._checks import DTYPE_CODE, check_ctas, require
 from .hard_backward import backward_hard
-from .hard_forward import _forward_core
+from .hard_forward import _forward_core, _packed_forward_core, hard_dlog_weights
+from .varlen import VarlenLayout, packed_backward
 
 
 @torch.library.custom_op("dism_amd::hard_core", mutates_args=())
@@ -78,40 +79,85 @@ def _hard_core_autograd(ctx, dout, _dlse2, _dlut, _dws):
 hard_core.register_autograd(_hard_core_autograd, setup_context=_setup_context)
 
 
-def dism_core_hard(sq, sk, v, idx_q, idx_k, hard, tau):
+class _PackedHardCore(torch.autograd.Function):
+    """Packed batch-1 hard core (VarlenLayout): forward keeps the workspace, LUT and log2
+    normalizer; backward runs the packed backward on them (no recompute)."""
+
+    @staticmethod
+    def forward(ctx, sq, sk, v, iq, ik, hard, tau, layout):
+        out, lse2, lut, _, _, ws = _packed_forward_core(sq, sk, v, iq, ik, hard, tau, layout,
+                                                        None, False)
+        ctx.layout = layout
+        ctx.save_for_backward(sq, sk, v, iq, ik, hard, tau, lse2, lut, ws)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        sq, sk, v, iq, ik, hard, tau, lse2, lut, ws = ctx.saved_tensors
+        dlut = hard_dlog_weights(tau, lut.shape[1])
+        dsq, dsk, dv, dtau = packed_backward(sq, sk, v, dout.to(sq.dtype).contiguous(), iq, ik,
+                                             hard, lse2, lut, dlut, ctx.layout, workspace=ws)
+        return dsq, dsk, dv, None, None, None, dtau, None
+
+
+def dism_core_hard(sq, sk, v, idx_q, idx_k, hard, tau, *, layout=None):
     """Hard-only DISM core with autograd: O = hard readout; grads for sq, sk, v and tau.
 
     sq, sk [B,N,H,R], v [B,N,H,DV] (bf16 or f32), labels [B,H,N] int, hard [B,H] bool,
     tau [H] (natural-log match coefficient).  Returns O [B,N,H,DV] in the vectors' dtype.
-    Soft rows give zero output and zero gradients.
+    Soft rows give zero output and zero gradients.  ``layout`` (VarlenLayout) selects packed
+    batch-1 execution with hard [training_rows, H].
     """
     iq = idx_q.to(torch.int32).contiguous()
     ik = idx_k.to(torch.int32).contiguous()
+    if layout is not None:
+        return _PackedHardCore.apply(sq.contiguous(), sk.contiguous(), v.contiguous(), iq, ik,
+                                     hard.contiguous(), tau.float().contiguous(), layout)
     return hard_core(sq.contiguous(), sk.contiguous(), v.contiguous(), iq, ik, hard.contiguous(),
                      tau.float().contiguous())[0]
 
 
-def dism_core(q, k, sq, sk, v, q_lse, k_lse, idx_q, idx_k, direction, hard, rtau, *, ctas=0,
-              _lse_preabsorbed=False):
-    """Differentiable core with the reference's signature (flash_dism/backward.py:41-54) for
-    sequences that are all hard: O = hard output (the soft core skips hard rows), gradients
-    for sq, sk, v and rtau; q, k, q_lse, k_lse receive zero gradients.  Soft rows raise
-    NotImplementedError (they need the soft core).  ``rtau`` is the natural-log coefficient,
-    used as is (no softplus), as in the reference's hard path."""
+def dism_core(q, k, sq, sk, v, q_lse, k_lse, idx_q, idx_k, direction, hard, rtau, *,
+              cu_seqlens=None, layout=None, ctas=0, hard_planner=None, _lse_preabsorbed=False):
+    """Differentiable core with the reference's signature (flash_dism/__init__.py:20-40,
+    backward.py:41-54) for sequences that are all hard: O = hard output (the soft core skips
+    hard rows), gradients for sq, sk, v and rtau; q, k, q_lse, k_lse receive zero gradients.
+    Soft rows raise NotImplementedError (they need the soft core).  ``rtau`` is the natural-log
+    coefficient, used as is (no softplus), as in the reference's hard path.  ``cu_seqlens`` or
+    ``layout`` selects packed batch-1 execution (hard [training_rows, H])."""
+    if hard_planner is not None:
+        raise NotImplementedError("the asynchronous hard planner is not part of the MI355X "
+                                  "hard core")
+    packed = cu_seqlens is not None or layout is not None
+    if packed:
+        if ctas:
+            raise ValueError("ctas is only supported for fixed-length execution")
+        if cu_seqlens is not None:
+            if layout is not None:
+                raise ValueError("provide either layout or cu_seqlens, not both")
+            layout = VarlenLayout.from_cu_seqlens(cu_seqlens, sq.shape[1])
     check_ctas(ctas)
     b, n, h = sq.shape[0], sq.shape[1], sq.shape[2]
     require(tuple(q.shape[:3]) == (b, n, h) and tuple(k.shape[:3]) == (b, n, h),
             "q/k must match sq/sk in [B,N,H]")
     require(tuple(q_lse.shape) == (b, h, n) and tuple(k_lse.shape) == (b, h, n),
             "q_lse/k_lse must be [B,H,N]")
-    require(tuple(direction.shape) == (b, h), "direction must be [B,H]")
-    require(isinstance(hard, torch.Tensor) and tuple(hard.shape) == (b, h),
-            "fixed hard must be [B,H]")
+    if packed:
+        require(b == 1, "packed execution needs batch 1")
+        require(isinstance(hard, torch.Tensor) and hard.dim() == 2 and hard.shape[1] == h,
+                "hard must be contiguous bool [training_rows,H]; token-level masks are "
+                "unsupported")
+        require(direction.dim() == 2 and direction.shape[1] == h,
+                "direction must be [training_rows,H]")
+    else:
+        require(tuple(direction.shape) == (b, h), "direction must be [B,H]")
+        require(isinstance(hard, torch.Tensor) and tuple(hard.shape) == (b, h),
+                "fixed hard must be [B,H]")
     # (a host read of the flags; skipped inside a compiled graph, where soft rows give zeros)
     if not torch.compiler.is_compiling() and not bool(hard.all()):
         raise NotImplementedError(
             "soft rows need the soft DISM core, which the MI355X hard core does not provide")
-    out = dism_core_hard(sq, sk, v, idx_q, idx_k, hard, rtau)
+    out = dism_core_hard(sq, sk, v, idx_q, idx_k, hard, rtau, layout=layout)
     return _SoftOperands.apply(out, q, k, q_lse, k_lse)
 
 

@@ -169,7 +169,7 @@ int32_t check_common(const void* sq, const void* sk, const void* v, int32_t dtyp
 extern "C" {
 
 const char* dism_last_error(void) { return g_error.c_str(); }
-int32_t dism_abi_version(void) { return 3; }
+int32_t dism_abi_version(void) { return 4; }
 
 int32_t dism_sign_labels(const void* x, int32_t dtype, int64_t B, int64_t N, int64_t H, int32_t d,
                          int32_t* labels, void* stream) {
@@ -432,6 +432,218 @@ int32_t dism_hard_backward(const void* sq, const void* sk, const void* v, const 
                                       workspace_bytes, dsk, dv, stream);
     if (st) return st;
     return dism_hard_tau_reduce(rowtau, B, H, N, dtau, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------------
+// Packed (varlen) batch-1 layouts: the fixed-length workspace of (B = 1, N, H) followed by the
+// document-tagged labels, the document start of every token and all-ones row flags
+// (dism_packed.hip).
+namespace {
+
+struct PackedLayout {
+    Layout base;
+    int64_t tq, tk, dstart, dindex, ones, total;
+};
+
+PackedLayout packed_layout(int64_t N, int64_t H, int32_t R, int32_t DV) {
+    PackedLayout P;
+    P.base = layout(1, N, H, R, DV);
+    int64_t o = P.base.total;
+    P.tq = o;
+    o += align256(H * N * 4);
+    P.tk = o;
+    o += align256(H * N * 4);
+    P.dstart = o;
+    o += align256(N * 4);
+    P.dindex = o;
+    o += align256(N * 4);
+    P.ones = o;
+    o += align256(H);
+    P.total = o;
+    return P;
+}
+
+int32_t check_packed(const void* sq, const void* sk, const void* v, int32_t dtype, int64_t N,
+                     int64_t H, int32_t R, int32_t DV, const void* ws, int64_t ws_bytes,
+                     const char* what) {
+    if (!sq || !sk || !v || !ws) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
+    if (!dims_ok(1, N, H)) return fail(DISM_ERR_INVALID, "%s: positive dimensions required", what);
+    if (H * N > INT_MAX) return fail(DISM_ERR_INVALID, "%s: H*N must be below 2^31", what);
+    if (!rdv_ok(R, DV))
+        return fail(DISM_ERR_UNSUPPORTED, "%s: unsupported R=%d DV=%d", what, R, DV);
+    if (!dtype_ok(dtype))
+        return fail(DISM_ERR_UNSUPPORTED, "%s: vector dtype must be bf16 or f32", what);
+    if (!aligned16(sq) || !aligned16(sk) || !aligned16(v))
+        return fail(DISM_ERR_INVALID, "%s: vector tensors must be 16-byte aligned", what);
+    if (ws_bytes < packed_layout(N, H, R, DV).total)
+        return fail(DISM_ERR_INVALID, "%s: workspace too small", what);
+    return DISM_OK;
+}
+
+int32_t check_rows(const uint8_t* hard, int64_t rows, int64_t N, const float* lut,
+                   int64_t lut_stride, int64_t max_length, const char* what) {
+    if (!hard || !lut) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
+    if (rows <= 0 || N % rows != 0 || (N / rows) % 256 != 0)
+        return fail(DISM_ERR_INVALID,
+                    "packed hard rows must evenly divide tokens into 256-aligned training rows");
+    if (max_length <= 0 || max_length > N)
+        return fail(DISM_ERR_INVALID, "%s: invalid longest document length", what);
+    if (lut_stride < max_length + 1)
+        return fail(DISM_ERR_INVALID, "hard log-weight table is too short");
+    return DISM_OK;
+}
+
+dism::PathArgs packed_path(const PackedLayout& P, void* ws, int64_t N, int64_t H,
+                           const float* lut, int64_t lut_stride) {
+    dism::PathArgs a = path(P.base, ws, 1, N, H, at<int32_t>(ws, P.tq), at<int32_t>(ws, P.tk),
+                            at<uint8_t>(ws, P.ones), nullptr, 0, lut, lut_stride);
+    a.dstart = at<int32_t>(ws, P.dstart);
+    return a;
+}
+
+dism::PackedZero packed_zero(const uint8_t* hard, int64_t rows, int64_t N, int64_t H, int32_t R,
+                             int32_t DV) {
+    dism::PackedZero z{};
+    z.hard = hard;
+    z.row_tokens = N / rows;
+    z.H = H;
+    z.n = N;
+    z.R = R;
+    z.DV = DV;
+    return z;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t dism_hard_packed_workspace_bytes(int64_t N, int64_t H, int32_t R, int32_t DV,
+                                         int32_t dtype) {
+    if (!dims_ok(1, N, H) || H * N > INT_MAX || !rdv_ok(R, DV) || !dtype_ok(dtype)) return -1;
+    return packed_layout(N, H, R, DV).total;
+}
+
+int32_t dism_hard_packed_prepare(const void* sq, const void* sk, const void* v, int32_t dtype,
+                                 const int32_t* iq, const int32_t* ik,
+                                 const int32_t* cu_seqlens, int64_t docs, int64_t N, int64_t H,
+                                 int32_t R, int32_t DV, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+    const char* what = "packed hard prepare";
+    int32_t st = check_packed(sq, sk, v, dtype, N, H, R, DV, workspace, workspace_bytes, what);
+    if (st) return st;
+    if (!iq || !ik || !cu_seqlens) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
+    if (docs <= 0 || docs > N) return fail(DISM_ERR_INVALID, "%s: invalid document count", what);
+    if (2 * N * docs > ((int64_t)1 << 32))
+        return fail(DISM_ERR_INVALID, "%s: 2 * N * documents must not exceed 2^32", what);
+    const PackedLayout P = packed_layout(N, H, R, DV);
+    int32_t* tq = at<int32_t>(workspace, P.tq);
+    int32_t* tk = at<int32_t>(workspace, P.tk);
+    int32_t* dindex = at<int32_t>(workspace, P.dindex);
+    hipStream_t s = S(stream);
+    // document of every token, then dense label ranks from a label sort of the raw labels
+    dism::SortArgs raw{};
+    raw.lab[0] = iq;
+    raw.lab[1] = ik;
+    raw.BH = H;
+    raw.n = (int)N;
+    for (int t = 0; t < 3; ++t) raw.tmp[t] = at<int32_t>(workspace, P.base.tmp[t]);
+    raw.o = orders(P.base, workspace);
+    raw.pnb = at<int32_t>(workspace, P.base.pnb);
+    if ((st = hip_status(dism::launch_packed_docs(cu_seqlens, (int)docs, H, N,
+                                                  at<int32_t>(workspace, P.dstart), dindex,
+                                                  at<uint8_t>(workspace, P.ones), s), what)) ||
+        (st = hip_status(dism::launch_fill_i32(raw.o.mode, H, 0, s), what)) ||
+        (st = hip_status(dism::launch_sort_labels(raw, s), what)) ||
+        (st = hip_status(dism::launch_packed_tags(raw.o.corder, raw.o.clab, dindex, (int)docs, H,
+                                                  N, tq, tk, s), what)))
+        return st;
+    dism::SortArgs sa{};
+    sa.lab[0] = tq;
+    sa.lab[1] = tk;
+    sa.BH = H;
+    sa.n = (int)N;
+    for (int t = 0; t < 3; ++t) sa.tmp[t] = at<int32_t>(workspace, P.base.tmp[t]);
+    sa.o = orders(P.base, workspace);
+    sa.pnb = at<int32_t>(workspace, P.base.pnb);
+    const dism::PathArgs pa = packed_path(P, workspace, N, H, nullptr, 0);
+    return hip_status(dism::launch_prepare(sa, pa, s), what);
+}
+
+int32_t dism_hard_packed_readout(const void* sq, const void* sk, const void* v, int32_t dtype,
+                                 const uint8_t* hard, int64_t rows, const float* lut,
+                                 int64_t lut_stride, int64_t max_length, int64_t N, int64_t H,
+                                 int32_t R, int32_t DV, void* workspace, int64_t workspace_bytes,
+                                 void* out, int32_t out_dtype, float* lse2, int32_t* lmax,
+                                 int32_t* jarg, void* stream) {
+    const char* what = "packed hard readout";
+    int32_t st = check_packed(sq, sk, v, dtype, N, H, R, DV, workspace, workspace_bytes, what);
+    if (st) return st;
+    if ((st = check_rows(hard, rows, N, lut, lut_stride, max_length, what))) return st;
+    if (!out || !lse2) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
+    if (!dtype_ok(out_dtype))
+        return fail(DISM_ERR_UNSUPPORTED, "%s: output dtype must be bf16 or f32", what);
+    if (!aligned16(out)) return fail(DISM_ERR_INVALID, "%s: output must be 16-byte aligned", what);
+    const PackedLayout P = packed_layout(N, H, R, DV);
+    dism::PathArgs a = packed_path(P, workspace, N, H, lut, lut_stride);
+    a.sq = sq;
+    a.sk = sk;
+    a.v = v;
+    a.out = out;
+    a.out_dtype = out_dtype;
+    a.lse2 = lse2;
+    a.lmax = lmax;
+    a.jarg = jarg;
+    if ((st = hip_status(dism::launch_scan_forward(a, R, DV, dtype, S(stream)), what))) return st;
+    if ((st = hip_status(dism::launch_pairs_finish(a, R, DV, dtype, S(stream)), what))) return st;
+    dism::PackedZero z = packed_zero(hard, rows, N, H, R, DV);
+    z.out = out;
+    z.out_dtype = out_dtype;
+    z.lse2 = lse2;
+    z.lmax = lmax;
+    z.jarg = jarg;
+    return hip_status(dism::launch_packed_soft_zero(z, S(stream)), what);
+}
+
+int32_t dism_hard_packed_backward(const void* sq, const void* sk, const void* v,
+                                  const void* dout, int32_t dtype, const uint8_t* hard,
+                                  int64_t rows, const float* lut, const float* dlut,
+                                  int64_t lut_stride, int64_t max_length, const float* lse2,
+                                  int64_t N, int64_t H, int32_t R, int32_t DV, void* workspace,
+                                  int64_t workspace_bytes, float* dsq, float* dsk, float* dv,
+                                  float* rowtau, float* dtau, void* stream) {
+    const char* what = "packed hard backward";
+    int32_t st = check_packed(sq, sk, v, dtype, N, H, R, DV, workspace, workspace_bytes, what);
+    if (st) return st;
+    if ((st = check_rows(hard, rows, N, lut, lut_stride, max_length, what))) return st;
+    if (!dout || !dlut || !lse2 || !dsq || !dsk || !dv || !rowtau || !dtau)
+        return fail(DISM_ERR_INVALID, "%s: null pointer", what);
+    if (!aligned16(dout)) return fail(DISM_ERR_INVALID, "%s: dO must be 16-byte aligned", what);
+    const PackedLayout P = packed_layout(N, H, R, DV);
+    dism::PathArgs a = packed_path(P, workspace, N, H, lut, lut_stride);
+    a.sq = sq;
+    a.sk = sk;
+    a.v = v;
+    a.dout = dout;
+    a.dlut = dlut;
+    a.lse2 = const_cast<float*>(lse2);
+    a.dsq = dsq;
+    a.dsk = dsk;
+    a.dv = dv;
+    a.rowtau = rowtau;
+    hipStream_t s = S(stream);
+    if ((st = hip_status(dism::launch_pairs_rows(a, R, DV, dtype, s), what))) return st;
+    if ((st = hip_status(dism::launch_scan_rows(a, R, DV, dtype, s), what))) return st;
+    if ((st = hip_status(dism::launch_scan_keys(a, R, DV, dtype, s), what))) return st;
+    if ((st = hip_status(dism::launch_pairs_keys(a, R, DV, dtype, s), what))) return st;
+    dism::PackedZero z = packed_zero(hard, rows, N, H, R, DV);
+    z.dsq = dsq;
+    z.dsk = dsk;
+    z.dv = dv;
+    z.rowtau = rowtau;
+    if ((st = hip_status(dism::launch_packed_soft_zero(z, s), what))) return st;
+    return hip_status(dism::launch_tau_reduce(rowtau, 1, (int)H, N, dtau, s), what);
 }
 
 }  // extern "C"

@@ -91,6 +91,26 @@ struct PathArgs {
     float* dsk;
     float* dv;               // [B,N,H,DV] fp32
     float* rowtau;           // [B,H,N]
+    // packed layouts (B = 1, dism_packed.hip): start of each token's document, or null for
+    // fixed-length rows.  Walks stop at the query's document start, the pair plan drops the
+    // diagonal pair at a document start, and G[i+1] uses the document-local position.
+    const int32_t* dstart;   // [N]
+};
+
+// Outputs a packed call zeroes on soft training rows (null pointers are skipped).
+struct PackedZero {
+    const uint8_t* hard;     // [rows, H]
+    long row_tokens, H, n;
+    int R, DV;
+    void* out;
+    int out_dtype;
+    float* lse2;
+    int32_t* lmax;
+    int32_t* jarg;
+    float* dsq;
+    float* dsk;
+    float* dv;
+    float* rowtau;
 };
 
 hipError_t launch_sign_labels(const void* x, int dtype, long B, long N, long H, int d,
@@ -105,10 +125,19 @@ hipError_t launch_chunk(const int32_t* summary, int32_t* out, long BH, long C, i
 hipError_t launch_tau_reduce(const float* rowtau, int B, int H, long n, float* dtau,
                              hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, long count, int32_t value, hipStream_t s);
+hipError_t launch_packed_docs(const int32_t* cu, int docs, long H, long n, int32_t* dstart,
+                              int32_t* dindex, uint8_t* ones, hipStream_t s);
+hipError_t launch_packed_tags(const int32_t* corder, const int32_t* clab,
+                              const int32_t* dindex, int docs, long H, long n, int32_t* tq,
+                              int32_t* tk, hipStream_t s);
+hipError_t launch_packed_soft_zero(const PackedZero& z, hipStream_t s);
 // Position orders and bigram-pair plans of a prepare call: the LDS-resident kernel for the
 // rows it can take, the global-memory sort and plan for the others, then the owner lists.
 hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s);
 hipError_t launch_sort(const SortArgs& a, hipStream_t s);
+// only the combined label order (corder, clab, ctab) of every row, global-memory path (the
+// rows' mode must be 0)
+hipError_t launch_sort_labels(const SortArgs& a, hipStream_t s);
 hipError_t launch_prepare_lds(const SortArgs& a, hipStream_t s);
 // The following return hipErrorInvalidValue for an unsupported (R, DV, dtype).
 hipError_t launch_pair_plan(const PathArgs& a, hipStream_t s);

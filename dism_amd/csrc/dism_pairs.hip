@@ -56,6 +56,9 @@ __device__ __forceinline__ void partner_range(const PathArgs& a, int bh, long so
                      (uint32_t)a.o.bplab[SIDE][so + t], (uint32_t)a.o.blab[SIDE][so + t], lo,
                      hi);
         const int32_t* ob = a.o.bpos[OTHER] + so;
+        // packed rows: the diagonal pair (p, p) at a document start p has predecessors in
+        // the previous document and is not a bigram pair
+        const bool dstart = a.dstart && a.dstart[p] == p;
         if (SIDE == 0) {
             if (lo < hi && ob[lo] == 0) ++lo;  // key 0 has no predecessor
             int l = lo, r = hi;                // keys j <= i
@@ -64,6 +67,7 @@ __device__ __forceinline__ void partner_range(const PathArgs& a, int bh, long so
                 if (ob[mid] <= p) l = mid + 1; else r = mid;
             }
             hi = l;
+            if (dstart && hi > lo && ob[hi - 1] == p) --hi;
         } else {
             int l = lo, r = hi;                // queries i >= j
             while (l < r) {
@@ -71,6 +75,7 @@ __device__ __forceinline__ void partner_range(const PathArgs& a, int bh, long so
                 if (ob[mid] < p) l = mid + 1; else r = mid;
             }
             lo = l;
+            if (dstart && lo < hi && ob[lo] == p) ++lo;
         }
     }
     lo_out = lo;
@@ -80,10 +85,13 @@ __device__ __forceinline__ void partner_range(const PathArgs& a, int bh, long so
 
 // Match length of a bigram pair (i, j >= 1, q[i-1] == k[j-1] known): match_length's suffix
 // walk without its first comparison.
+// dlo: start of the query's document (0 for fixed-length rows; packed calls have no carry
+// boundary).
 __device__ __forceinline__ int pair_length(const int32_t* __restrict__ q,
                                            const int32_t* __restrict__ k, int i, int j,
-                                           const int32_t* __restrict__ bound, int strip, int n) {
-    const int lo = bound ? (i / strip) * strip : 0;
+                                           const int32_t* __restrict__ bound, int strip, int n,
+                                           int dlo) {
+    const int lo = bound ? (i / strip) * strip : dlo;
     int c = i - 1 >= lo ? 2 : 1;
     while (i - c >= lo && j - c >= 0 && q[i - c] == k[j - c]) ++c;
     if (bound && lo > 0 && i - c < lo && j - c >= 0) {
@@ -213,7 +221,7 @@ hipError_t launch_owner_lists(const PathArgs& a, hipStream_t s) {
 
 hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
     hipError_t e;
-    if (pa.n <= PREP_N) e = launch_prepare_lds(sa, s);
+    if (pa.n <= PREP_N && !pa.dstart) e = launch_prepare_lds(sa, s);
     else e = launch_fill_i32(sa.o.mode, sa.BH, 0, s);
     if (e != hipSuccess) return e;
     if ((e = launch_sort(sa, s)) != hipSuccess) return e;
@@ -368,7 +376,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
         }
         float skr[R];
         load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
-        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n) : 1;
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, doc_start(a, i)) : 1;
         const float lw = lut[L];
         float mm = has && lw > m0 ? lw : m0;
         key = has ? (((unsigned long long)(unsigned)L << 32) | (unsigned)j) : 0ull;
@@ -414,7 +422,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
             const int kq = c0 + sub;
             if (kq < cnt) {
                 const int j = kb[lo + kq];
-                const int L = pair_length(q, k, i, j, bnd, a.strip, n);
+                const int L = pair_length(q, k, i, j, bnd, a.strip, n, doc_start(a, i));
                 const float lw = lut[L];
                 if (lw > m0) atomicMax(&S.m[sl], __float_as_uint(lw));
                 atomicMax(&S.key[sl], ((unsigned long long)(unsigned)L << 32) | (unsigned)j);
@@ -431,7 +439,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
             const int kq = c0 + sub;
             if (kq < cnt) {
                 const int j = kb[lo + kq];
-                const int L = pair_length(q, k, i, j, bnd, a.strip, n);
+                const int L = pair_length(q, k, i, j, bnd, a.strip, n, doc_start(a, i));
                 const float p = exp2_fp32(lut[L] - m);
                 float skr[R];
                 load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
@@ -542,7 +550,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
     const T* dout = reinterpret_cast<const T*>(a.dout);
 
     const float l2 = a.lse2[s.so + i];
-    const float cc = glut[i + 1];
+    const float cc = glut[i - doc_start(a, i) + 1];
     const float P1 = exp2_fp32(lut[1] - l2);
     const float q1 = P1 * (glut[1] - cc);
     const long qr = s.row0 + (long)i * a.H;
@@ -568,7 +576,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
         }
         float skr[R];
         load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
-        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n) : 1;
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, doc_start(a, i)) : 1;
         float sdot = 0.0f;
 #pragma unroll
         for (int r = 0; r < R; ++r) sdot = __builtin_fmaf(sqr[r], skr[r], sdot);
@@ -609,7 +617,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
         const int kq = c0 + sub;
         if (kq < cnt) {
             const int j = kb[lo + kq];
-            const int L = pair_length(q, k, i, j, bnd, a.strip, n);
+            const int L = pair_length(q, k, i, j, bnd, a.strip, n, doc_start(a, i));
             float skr[R];
             load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
             float sdot = 0.0f;
@@ -746,7 +754,7 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
         const float l2 = a.lse2[s.so + i];
         float sqr[R];
         load_row<T, R>(sq + (s.row0 + (long)i * a.H) * R, sqr);
-        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n) : 1;
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, doc_start(a, i)) : 1;
         const float p = exp2_fp32(lut[L] - l2);
         float sdot = 0.0f;
 #pragma unroll
@@ -784,7 +792,7 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
         const int kq = c0 + sub;
         if (kq < cnt) {
             const int i = qb[lo + kq];
-            const int L = pair_length(q, k, i, j, bnd, a.strip, n);
+            const int L = pair_length(q, k, i, j, bnd, a.strip, n, doc_start(a, i));
             const float l2 = a.lse2[s.so + i];
             const float p = exp2_fp32(lut[L] - l2);
             float sqr[R];

@@ -77,6 +77,11 @@ __device__ __forceinline__ float load_elem(const T* p, long idx) {
     }
 }
 
+// start of position p's document: 0 for fixed-length rows, dstart[p] for packed layouts
+__device__ __forceinline__ int doc_start(const PathArgs& a, int p) {
+    return a.dstart ? a.dstart[p] : 0;
+}
+
 // first index in [lo, hi) whose unsigned label is >= x (lower) / > x (upper)
 __device__ __forceinline__ int lower_label(const int32_t* lab, int lo, int hi, uint32_t x) {
     while (lo < hi) {

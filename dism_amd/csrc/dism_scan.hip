@@ -345,7 +345,7 @@ __global__ __launch_bounds__(64 * WAVES) void scan_rows_kernel(PathArgs a) {
             load_words<W>((isq ? sq : sk) + (it.row0 + (long)p * a.H) * R, wN);
             // row statistics only for query entries, corrections only for rows with pairs
             xN[0] = isq ? __float_as_uint(a.lse2[it.so + p]) : 0u;
-            xN[1] = isq ? __float_as_uint(glut[p + 1]) : 0u;
+            xN[1] = isq ? __float_as_uint(glut[p - doc_start(a, p) + 1]) : 0u;
             xN[2] = isq ? (uint32_t)a.pnb[it.so + p] : 0u;
             const float* rec = a.prow + (it.so + p) * a.prow_stride;
             const bool has = isq && xN[2] > 0;

@@ -686,4 +686,9 @@ hipError_t launch_sort(const SortArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+hipError_t launch_sort_labels(const SortArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(sort_kernel, dim3((unsigned)a.BH, 1), dim3(SORT_THREADS), 0, s, a);
+    return hipGetLastError();
+}
+
 }  // namespace dism

@@ -15,7 +15,9 @@ import torch
 from . import _lib
 from ._checks import (DTYPE_CODE, check_ctas, check_graph_choice, check_labels, check_layout,
                       check_tensor, check_vectors, require)
-from .hard_forward import _forward_core, hard_dlog_weights, prepare_workspace
+from .hard_forward import (_forward_core, _packed_forward_core, hard_dlog_weights,
+                           prepare_workspace)
+from .varlen import packed_backward
 
 
 def _stream(t):
@@ -28,11 +30,16 @@ def backward_hard(sq, sk, v, dout, idx_q, idx_k, hard, normalizer, state, *, lay
     """Return dSQ, dSK, dV, d(tau) (all FP32) for sequence-hard rows; soft rows get zeros.
 
     ``state`` comes from forward_hard(..., save_state=True) on the same inputs; ``normalizer``
-    is that call's log2 normalizer.  tau is the natural-log coefficient.
+    is that call's log2 normalizer.  tau is the natural-log coefficient.  ``layout`` selects
+    packed batch-1 execution (hard [training_rows, H]); soft training rows get zeros and dtau
+    sums the hard documents.
     """
     check_ctas(ctas)
     check_layout(layout)
     check_graph_choice(_graph_choice)
+    if layout is not None:
+        return _packed_backward_hard(sq, sk, v, dout, idx_q, idx_k, hard, normalizer, state,
+                                     layout)
     b, n, h, r, dv, dt = check_vectors(sq, sk, v, extra=(("dO", dout),))
     check_labels(idx_q, idx_k, b, h, n, sq.device)
     check_tensor(hard, torch.bool, (b, h), "sequence hard flags", sq.device)
@@ -49,9 +56,7 @@ def backward_hard(sq, sk, v, dout, idx_q, idx_k, hard, normalizer, state, *, lay
         check_tensor(carry, torch.int32, (b, h, (n - 1) // 32, n), "integer boundary", sq.device)
     else:
         carry, strip = None, 0
-    tau = state.get("tau")
-    if tau is None:  # reference state: recover tau from LUT[:,1] = tau / ln 2
-        tau = (lut[:, 1].double() * math.log(2.0)).float().contiguous()
+    tau = _state_tau(state, lut)
     dlut = hard_dlog_weights(tau, n + 1)
     ws = state.get("workspace")
     if ws is None or ws.numel() < _lib.workspace_bytes(b, n, h, r, dv, DTYPE_CODE[dt]):
@@ -71,6 +76,24 @@ def backward_hard(sq, sk, v, dout, idx_q, idx_k, hard, normalizer, state, *, lay
     return dsq, dsk, dvv, dtau
 
 
+def _state_tau(state, lut):
+    tau = state.get("tau")
+    if tau is None:  # reference state: recover tau from LUT[:,1] = tau / ln 2
+        tau = (lut[:, 1].double() * math.log(2.0)).float().contiguous()
+    return tau
+
+
+def _packed_backward_hard(sq, sk, v, dout, idx_q, idx_k, hard, normalizer, state, layout):
+    require(isinstance(state, dict) and "log_weights" in state, "invalid hard forward state")
+    lut = state["log_weights"]
+    require(isinstance(lut, torch.Tensor) and lut.dim() == 2,
+            "log weight LUT: invalid device, dtype, shape or stride")
+    dlut = hard_dlog_weights(_state_tau(state, lut), lut.shape[1])
+    ws = state.get("workspace") if state.get("layout") is layout else None
+    return packed_backward(sq, sk, v, dout, idx_q, idx_k, hard, normalizer, lut, dlut, layout,
+                           workspace=ws)
+
+
 @torch.no_grad()
 def backward_hard_recompute(sq, sk, v, dout, iq, ik, hard, tau, *, layout=None, ctas=0,
                             _graph_choice=None):
@@ -81,6 +104,22 @@ def backward_hard_recompute(sq, sk, v, dout, iq, ik, hard, tau, *, layout=None, 
     q, k = [x.to(torch.int32).contiguous() for x in (iq, ik)]
     check_ctas(ctas)
     check_graph_choice(_graph_choice)
+    if layout is not None:
+        # reference host checks of the packed fallback (hard_backward.py:41-51)
+        n = sq.shape[1]
+        if sq.shape[0] != 1 or hard.ndim != 2 or n % hard.shape[0] or layout.tokens != n:
+            raise ValueError("invalid packed fallback rows")
+        row_n = n // hard.shape[0]
+        if any(start // row_n != (start + length - 1) // row_n
+               for start, length in layout.spans()):
+            raise ValueError("document crosses original hard row")
+        flags, t = hard.contiguous(), tau.contiguous()
+        _, norm, lut, _, _, ws = _packed_forward_core(a, b_, c, q, k, flags, t, layout, None,
+                                                      False)
+        dlut = hard_dlog_weights(t, lut.shape[1])
+        result = packed_backward(a, b_, c, do, q, k, flags, norm, lut, dlut, layout,
+                                 workspace=ws)
+        return dict(zip(("sq_vec", "sk_vec", "v", "rtau"), result))
     _, norm, lut, carry, strip, _, _, ws = _forward_core(a, b_, c, q, k, hard.contiguous(),
                                                          tau.contiguous(), None, None, False)
     state = dict(log_weights=lut, tau=tau.contiguous(), carry=carry, carry_strip=strip,

@@ -23,6 +23,7 @@ from . import _lib
 from ._checks import (DTYPE_CODE, check_ctas, check_graph_choice, check_hard, check_labels,
                       check_layout, check_tensor, check_vectors, require)
 from .summary import hard_boundary, hard_chunk_scan, summarize_hard
+from .varlen import VarlenLayout, packed_readout
 
 DEFAULT_CARRY_STRIP = int(os.environ.get("DISM_HARD_CARRY_STRIP", "0"))
 
@@ -119,9 +120,28 @@ def hard_readout(sq, sk, v, idx_q, idx_k, hard, boundary, log_weights, *, layout
     check_ctas(ctas)
     check_layout(layout)
     check_graph_choice(_graph_choice)
+    if layout is not None:
+        # the packed readout recomputes lengths from the labels; the boundary is validated
+        check_tensor(boundary, torch.int32, (layout.forward_elements * sq.shape[2],),
+                     "packed hard boundary", sq.device)
+        out, lse2, _, _, _ = packed_readout(sq, sk, v, idx_q, idx_k, hard, log_weights, layout,
+                                            sq.dtype, False)
+        return out, lse2
     out, lse2, _, _, _ = _readout(sq, sk, v, idx_q, idx_k, hard, boundary, 32, log_weights,
                                   sq.dtype, False)
     return out, lse2
+
+
+def _packed_forward_core(sq, sk, v, idx_q, idx_k, hard, tau, layout, out_dtype, matches):
+    """Packed LUT + readout; returns (out, lse2, lut, lmax, jarg, workspace)."""
+    b, n, h, _, _, dt = check_vectors(sq, sk, v)
+    require(isinstance(tau, torch.Tensor) and tau.is_cuda and tau.dtype == torch.float32 and
+            tau.shape == (h,) and tau.is_contiguous(), "tau must be contiguous CUDA FP32 [H]")
+    require(isinstance(layout, VarlenLayout), "layout must be a VarlenLayout")
+    lut = hard_log_weights(tau, layout.longest)
+    out, lse2, lmax, jarg, ws = packed_readout(sq, sk, v, idx_q, idx_k, hard, lut, layout,
+                                               out_dtype or dt, matches)
+    return out, lse2, lut, lmax, jarg, ws
 
 
 def _forward_core(sq, sk, v, idx_q, idx_k, hard, tau, carry_strip, out_dtype, matches):
@@ -149,12 +169,28 @@ def forward_hard(sq, sk, v, idx_q, idx_k, hard, tau, *, layout=None, ctas=0, sav
 
     Returns (O, lse2) or, with save_state, (O, lse2, dict(summary, boundary, log_weights,
     tau, strip, carry, carry_strip, workspace)); with return_matches a further
-    dict(length, index).
+    dict(length, index).  ``layout`` (a VarlenLayout) selects packed batch-1 execution: B = 1,
+    hard [training_rows, H], documents never matched against each other; the LUT then covers
+    the longest document and the saved summary/boundary use the reference's flat packed
+    format.
     O has the vectors' dtype unless out_dtype is given.
     """
     check_ctas(ctas)
     check_layout(layout)
     check_graph_choice(_graph_choice)
+    if layout is not None:
+        out, lse2, lut, lmax, jarg, ws = _packed_forward_core(
+            sq, sk, v, idx_q, idx_k, hard, tau, layout, out_dtype, return_matches)
+        result = [out, lse2]
+        if save_state:
+            summary = summarize_hard(idx_q, idx_k, hard, layout=layout)
+            boundary = hard_chunk_scan(summary, layout=layout, heads=sq.shape[2])
+            result.append(dict(summary=summary, boundary=boundary, log_weights=lut, tau=tau,
+                               strip=32, carry=None, carry_strip=0, workspace=ws,
+                               layout=layout))
+        if return_matches:
+            result.append(dict(length=lmax, index=jarg))
+        return tuple(result)
     out, lse2, lut, carry, strip, lmax, jarg, ws = _forward_core(
         sq, sk, v, idx_q, idx_k, hard, tau, carry_strip, out_dtype, return_matches)
     result = [out, lse2]

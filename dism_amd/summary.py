@@ -40,12 +40,17 @@ def summarize_hard(idx_q, idx_k, hard, *, layout=None, ctas=0, _graph_choice=Non
     R[c,j] is the largest mismatching key coordinate on the diagonal segment ending at
     (32c+31, j) within this 32-row strip, or -1 if none.  Only causal hard entries are
     computed; others are -1.  Reference: dism_v3/python/flash_dism/summary.py:5-17.
+    With ``layout`` (B = 1, hard [training_rows, H]) the result is the reference's flat packed
+    format [forward_elements * H], each document summarised on its own.
     """
     b, h, n = _check_label_pair(idx_q, idx_k)
-    _check_flags(hard, b, h, idx_q.device)
     check_ctas(ctas)
     check_layout(layout)
     check_graph_choice(_graph_choice)
+    if layout is not None:
+        from .varlen import packed_summary
+        return packed_summary(idx_q, idx_k, hard, layout)
+    _check_flags(hard, b, h, idx_q.device)
     out = torch.empty((b, h, (n - 1) // 32, n), dtype=torch.int32, device=idx_q.device)
     with torch.cuda.device(idx_q.device):
         _lib.call("dism_hard_summary", idx_q.data_ptr(), idx_k.data_ptr(), hard.data_ptr(),
@@ -63,6 +68,9 @@ def hard_chunk_scan(summary, *, layout=None, heads=0, _graph_choice=None, inplac
             "hard summary must be contiguous CUDA int32")
     check_layout(layout)
     check_graph_choice(_graph_choice)
+    if layout is not None:
+        from .varlen import packed_chunk
+        return packed_chunk(summary, layout, heads, inplace)
     require(summary.dim() == 4, "fixed hard summary must be [B,H,C,N]")
     bh = summary.shape[0] * summary.shape[1]
     require(0 < bh <= 65535 and (heads == 0 or heads == summary.shape[1]),

@@ -163,6 +163,54 @@ int32_t dism_hard_backward_key_pairs(const void* sq, const void* sk, const void*
 int32_t dism_hard_tau_reduce(const float* rowtau, int64_t B, int64_t H, int64_t N, float* dtau,
                              void* stream);
 
+/* ---- Packed (varlen) batch-1 layouts.  One token sequence of N tokens (B = 1) holds the
+ * documents [cu_seqlens[d], cu_seqlens[d+1]), d < docs (device int32 [docs+1], 0 = first,
+ * N = last, strictly increasing: the caller drops empty documents); matches never cross a
+ * document.  Hard flags are per training row: hard [rows, H] with N/rows tokens per row (a
+ * multiple of 256), and no document crosses a training row (the caller checks the offsets on
+ * the host, as the reference's layout does).  Soft training rows get zero outputs and
+ * gradients.  Labels are any int32 values; 2 * N * docs <= 2^32 (documents are told apart by
+ * tagging dense label ranks).  max_length is the longest document; the LUT covers lengths
+ * 0..max_length.
+ * Replaces the packed branches of cu.hard_readout / cu.hard_backward, which take the layout
+ * table of dism_v3/python/flash_dism/varlen.py:9-51 (dism_v3/src/host/hard_forward.cpp:55-80,
+ * dism_v3/src/host/hard_backward.cpp:54-93). */
+
+/* Workspace bytes of a packed call (-1 for unsupported dimensions): the fixed-length
+ * workspace of (1, N, H) plus the tagged labels and per-token document starts. */
+int64_t dism_hard_packed_workspace_bytes(int64_t N, int64_t H, int32_t R, int32_t DV,
+                                         int32_t dtype);
+
+/* Ranks and tags the labels iq, ik [1,H,N] by document and prepares the workspace as
+ * dism_hard_prepare does.  The readout and backward below read the labels from the
+ * workspace. */
+int32_t dism_hard_packed_prepare(const void* sq, const void* sk, const void* v, int32_t dtype,
+                                 const int32_t* iq, const int32_t* ik,
+                                 const int32_t* cu_seqlens, int64_t docs, int64_t N, int64_t H,
+                                 int32_t R, int32_t DV, void* workspace,
+                                 int64_t workspace_bytes, void* stream);
+
+/* Packed readout: O [1,N,H,DV], lse2 [1,H,N] (and optional lmax/jarg, key indices global),
+ * equal per document to dism_hard_readout on that document alone.
+ * Replaces cu.hard_readout with a layout table (dism_v3/src/host/hard_forward.cpp:55-80). */
+int32_t dism_hard_packed_readout(const void* sq, const void* sk, const void* v, int32_t dtype,
+                                 const uint8_t* hard, int64_t rows, const float* lut,
+                                 int64_t lut_stride, int64_t max_length, int64_t N, int64_t H,
+                                 int32_t R, int32_t DV, void* workspace, int64_t workspace_bytes,
+                                 void* out, int32_t out_dtype, float* lse2, int32_t* lmax,
+                                 int32_t* jarg, void* stream);
+
+/* Packed backward (all five stages, then dtau over all hard documents).  The centring
+ * constant of query i is G[i - start + 1] with the document-local position.
+ * Replaces cu.hard_backward with a layout table (dism_v3/src/host/hard_backward.cpp:54-93). */
+int32_t dism_hard_packed_backward(const void* sq, const void* sk, const void* v,
+                                  const void* dout, int32_t dtype, const uint8_t* hard,
+                                  int64_t rows, const float* lut, const float* dlut,
+                                  int64_t lut_stride, int64_t max_length, const float* lse2,
+                                  int64_t N, int64_t H, int32_t R, int32_t DV, void* workspace,
+                                  int64_t workspace_bytes, float* dsq, float* dsk, float* dv,
+                                  float* rowtau, float* dtau, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,12 +35,13 @@ def test_header_symbols_exported(lib):
 def test_python_signatures_cover_header(lib):
     from dism_amd import _lib
     declared = set(_declared())
-    special = {"dism_last_error", "dism_abi_version", "dism_hard_workspace_bytes"}
+    special = {"dism_last_error", "dism_abi_version", "dism_hard_workspace_bytes",
+               "dism_hard_packed_workspace_bytes"}
     assert declared - special == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
 
 
 def test_version_and_workspace(lib):
-    assert lib.dism_abi_version() == 3
+    assert lib.dism_abi_version() == 4
     ws = lib.dism_hard_workspace_bytes(4, 16384, 16, 8, 64, 0)
     assert ws > 4 * 16384 * 16 * 64 * 4  # holds one fp32 readout row per query
     assert ws % 256 == 0
@@ -48,6 +49,10 @@ def test_version_and_workspace(lib):
     assert lib.dism_hard_workspace_bytes(4, 16384, 16, 8, 48, 0) == -1   # DV unsupported
     assert lib.dism_hard_workspace_bytes(0, 16384, 16, 8, 64, 0) == -1   # empty
     assert lib.dism_hard_workspace_bytes(4, 16384, 16, 8, 64, 7) == -1   # dtype
+    packed = lib.dism_hard_packed_workspace_bytes(16384, 16, 8, 64, 0)
+    assert packed > lib.dism_hard_workspace_bytes(1, 16384, 16, 8, 64, 0)
+    assert packed % 256 == 0
+    assert lib.dism_hard_packed_workspace_bytes(16384, 16, 8, 48, 0) == -1
 
 
 def test_host_validation_without_launch(lib):
