@@ -10,8 +10,10 @@ from .labels import sign_labels
 from .summary import hard_boundary, hard_chunk_scan, summarize_hard
 from .core import dism_core, dism_core_hard, hard_core, hard_core_backward
 from .varlen import VarlenLayout
+from .inference import HardDismDecoder, HardDismPrefill, PreparedHardPrefill
 
 __all__ = ["forward_hard", "hard_readout", "hard_log_weights", "hard_dlog_weights",
            "backward_hard", "backward_hard_recompute", "summarize_hard", "hard_chunk_scan",
            "hard_boundary", "sign_labels", "dism_core", "dism_core_hard", "hard_core",
-           "hard_core_backward", "VarlenLayout"]
+           "hard_core_backward", "VarlenLayout", "HardDismPrefill", "PreparedHardPrefill",
+           "HardDismDecoder"]

@@ -38,6 +38,19 @@ SIGNATURES = {
                                  _I32, _P, _I64, _P, _I32, _P, _P, _P, _P],
     "dism_hard_packed_backward": [_P, _P, _P, _P, _I32, _P, _I64, _P, _P, _I64, _I64, _P, _I64,
                                   _I64, _I32, _I32, _P, _I64, _P, _P, _P, _P, _P, _P],
+    "dism_hard_prefill": [_P, _P, _P, _I32, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32,
+                          _P, _I64, _P, _P, _P],
+    "dism_decoder_init": [_P, _I64, _I64, _I32, _I32, _I64, _I32, _I32, _P],
+    "dism_decoder_step": [_P, _I64, _I64, _I64, _I32, _I32, _I64, _I32, _I32, _I64, _P, _P, _P,
+                          _P, _P, _P, _P, _I64, _P, _P, _P],
+}
+
+# entry points returning a size (int64, -1 = unsupported) rather than a status
+SIZE_SIGNATURES = {
+    "dism_hard_workspace_bytes": [_I64, _I64, _I64, _I32, _I32, _I32],
+    "dism_hard_packed_workspace_bytes": [_I64, _I64, _I32, _I32, _I32],
+    "dism_hard_prefill_workspace_bytes": [_I64, _I64, _I64, _I32, _I32, _I32],
+    "dism_decoder_state_bytes": [_I64, _I32, _I32, _I64, _I32, _I32],
 }
 
 _lib = None
@@ -64,10 +77,10 @@ def load():
         lib.dism_last_error.argtypes = []
         lib.dism_abi_version.restype = ctypes.c_int32
         lib.dism_abi_version.argtypes = []
-        lib.dism_hard_workspace_bytes.restype = ctypes.c_int64
-        lib.dism_hard_workspace_bytes.argtypes = [_I64, _I64, _I64, _I32, _I32, _I32]
-        lib.dism_hard_packed_workspace_bytes.restype = ctypes.c_int64
-        lib.dism_hard_packed_workspace_bytes.argtypes = [_I64, _I64, _I32, _I32, _I32]
+        for name, args in SIZE_SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int64
         _lib = lib
     return _lib
 
@@ -94,4 +107,12 @@ def packed_workspace_bytes(N, H, R, DV, dtype_code):
     nbytes = load().dism_hard_packed_workspace_bytes(N, H, R, DV, dtype_code)
     if nbytes < 0:
         raise RuntimeError(f"unsupported packed hard-core dimensions N={N} H={H} R={R} DV={DV}")
+    return nbytes
+
+
+def size(name, *args):
+    """Call a size entry point (SIZE_SIGNATURES); raise for unsupported dimensions."""
+    nbytes = getattr(load(), name)(*args)
+    if nbytes < 0:
+        raise RuntimeError(f"{name}: unsupported dimensions {args}")
     return nbytes

@@ -647,3 +647,173 @@ int32_t dism_hard_packed_backward(const void* sq, const void* sk, const void* v,
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------------------
+// Inference: prefill with query resets, and the incremental decoder (dism_decode.hip).
+namespace {
+
+struct DecoderLayout {
+    int64_t meta, qlab, klab, skh, vh, slot_label, slot_cnt, slot_last, M, slot_blocks, pool,
+        scratch, total;
+    int bcap, pool_blocks;
+};
+
+bool decoder_dims_ok(int64_t rows, int32_t R, int32_t DV, int64_t cap, int32_t slots,
+                     int32_t dtype) {
+    return rows > 0 && rows <= 65535 && rdv_ok(R, DV) && dtype_ok(dtype) && cap > 0 &&
+           cap <= (1 << 24) && slots >= 64 && slots <= (1 << 20) && (slots & (slots - 1)) == 0;
+}
+
+DecoderLayout decoder_layout(int64_t rows, int32_t R, int32_t DV, int64_t cap, int32_t slots,
+                             int32_t dtype) {
+    DecoderLayout D;
+    const int64_t esz = dtype == DISM_BF16 ? 2 : 4;
+    D.bcap = (int)((cap + dism::LIST_BLOCK - 1) / dism::LIST_BLOCK);
+    D.pool_blocks = D.bcap + slots;
+    int64_t o = 0;
+    auto take = [&](int64_t bytes) {
+        int64_t a = o;
+        o += align256(bytes);
+        return a;
+    };
+    D.meta = take(rows * 4 * 4);
+    D.qlab = take(rows * cap * 4);
+    D.klab = take(rows * cap * 4);
+    D.skh = take(rows * cap * R * esz);
+    D.vh = take(rows * cap * DV * esz);
+    D.slot_label = take(rows * slots * 4);
+    D.slot_cnt = take(rows * slots * 4);
+    D.slot_last = take(rows * slots * 4);
+    D.M = take(rows * slots * (int64_t)R * DV * 4);
+    D.slot_blocks = take(rows * slots * (int64_t)D.bcap * 4);
+    D.pool = take(rows * (int64_t)D.pool_blocks * dism::LIST_BLOCK * 4);
+    D.scratch = take(rows * cap * 4);
+    D.total = o;
+    return D;
+}
+
+int64_t prefill_extra(int64_t B, int64_t N, int64_t H) {
+    return align256(B * H) + align256(B * H * N * 4);
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t dism_hard_prefill_workspace_bytes(int64_t B, int64_t N, int64_t H, int32_t R,
+                                          int32_t DV, int32_t dtype) {
+    if (!dims_ok(B, N, H) || B * H * N > INT_MAX || !rdv_ok(R, DV) || !dtype_ok(dtype))
+        return -1;
+    return layout(B, N, H, R, DV).total + prefill_extra(B, N, H);
+}
+
+int32_t dism_hard_prefill(const void* sq, const void* sk, const void* v, int32_t dtype,
+                          const int32_t* iq, const int32_t* ik, const uint8_t* reset,
+                          const float* lut, int64_t lut_stride, int64_t B, int64_t N, int64_t H,
+                          int32_t R, int32_t DV, void* workspace, int64_t workspace_bytes,
+                          float* out, float* lse2, void* stream) {
+    const char* what = "hard prefill";
+    int32_t st = check_common(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
+                              workspace_bytes, what);
+    if (st) return st;
+    if (!lut || !out || !lse2) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
+    if (lut_stride < N + 1) return fail(DISM_ERR_INVALID, "hard log-weight table is too short");
+    if (!aligned16(out)) return fail(DISM_ERR_INVALID, "%s: output must be 16-byte aligned", what);
+    const Layout L = layout(B, N, H, R, DV);
+    if (workspace_bytes < L.total + prefill_extra(B, N, H))
+        return fail(DISM_ERR_INVALID, "%s: workspace too small", what);
+    uint8_t* ones = at<uint8_t>(workspace, L.total);
+    int32_t* wlo = at<int32_t>(workspace, L.total + align256(B * H));
+    hipStream_t s = S(stream);
+    // all-hard row flags (bytes of one, a fill kernel), then the reset starts
+    if ((st = hip_status(dism::launch_fill_i32(reinterpret_cast<int32_t*>(ones),
+                                               align256(B * H) / 4, 0x01010101, s), what)))
+        return st;
+    if (reset && (st = hip_status(dism::launch_reset_starts(reset, B * H, N, wlo, s), what)))
+        return st;
+    if ((st = dism_hard_prepare(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
+                                workspace_bytes, stream)))
+        return st;
+    dism::PathArgs a = path(L, workspace, B, N, H, iq, ik, ones, nullptr, 0, lut, lut_stride);
+    a.wlo = reset ? wlo : nullptr;
+    a.sq = sq;
+    a.sk = sk;
+    a.v = v;
+    a.out = out;
+    a.out_dtype = DISM_F32;
+    a.lse2 = lse2;
+    if ((st = hip_status(dism::launch_scan_forward(a, R, DV, dtype, s), what))) return st;
+    return hip_status(dism::launch_pairs_finish(a, R, DV, dtype, s), what);
+}
+
+int64_t dism_decoder_state_bytes(int64_t rows, int32_t R, int32_t DV, int64_t capacity,
+                                 int32_t slots, int32_t dtype) {
+    if (!decoder_dims_ok(rows, R, DV, capacity, slots, dtype)) return -1;
+    return decoder_layout(rows, R, DV, capacity, slots, dtype).total;
+}
+
+int32_t dism_decoder_init(void* state, int64_t state_bytes, int64_t rows, int32_t R, int32_t DV,
+                          int64_t capacity, int32_t slots, int32_t dtype, void* stream) {
+    const char* what = "decoder init";
+    if (!state) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
+    if (!decoder_dims_ok(rows, R, DV, capacity, slots, dtype))
+        return fail(DISM_ERR_INVALID, "%s: invalid decoder dimensions", what);
+    const DecoderLayout D = decoder_layout(rows, R, DV, capacity, slots, dtype);
+    if (state_bytes < D.total) return fail(DISM_ERR_INVALID, "%s: state too small", what);
+    // zero every section (a fill kernel, not a memset node: safe under graph capture)
+    return hip_status(dism::launch_fill_i32(static_cast<int32_t*>(state), D.total / 4, 0,
+                                            S(stream)), what);
+}
+
+int32_t dism_decoder_step(void* state, int64_t state_bytes, int64_t B, int64_t H, int32_t R,
+                          int32_t DV, int64_t capacity, int32_t slots, int32_t dtype, int64_t n,
+                          const int32_t* iq, const int32_t* ik, const uint8_t* reset,
+                          const void* sq, const void* sk, const void* v, const float* lut,
+                          int64_t lut_stride, float* out, float* lse2, void* stream) {
+    const char* what = "decoder step";
+    if (!state || !iq || !ik || !sk || !v) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
+    const int64_t rows = B * H;
+    if (B <= 0 || H <= 0 || !decoder_dims_ok(rows, R, DV, capacity, slots, dtype))
+        return fail(DISM_ERR_INVALID, "%s: invalid decoder dimensions", what);
+    if (n <= 0 || n > capacity) return fail(DISM_ERR_INVALID, "%s: invalid token count", what);
+    if (out && (!sq || !lut)) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
+    if (out && lut_stride < capacity + 1)
+        return fail(DISM_ERR_INVALID, "hard log-weight table is too short");
+    const DecoderLayout D = decoder_layout(rows, R, DV, capacity, slots, dtype);
+    if (state_bytes < D.total) return fail(DISM_ERR_INVALID, "%s: state too small", what);
+    dism::DecodeArgs a{};
+    a.rows = (int)rows;
+    a.H = (int)H;
+    a.cap = (int)capacity;
+    a.slots = slots;
+    a.bcap = D.bcap;
+    a.R = R;
+    a.DV = DV;
+    a.meta = at<int32_t>(state, D.meta);
+    a.qlab = at<int32_t>(state, D.qlab);
+    a.klab = at<int32_t>(state, D.klab);
+    a.skh = at<void>(state, D.skh);
+    a.vh = at<void>(state, D.vh);
+    a.slot_label = at<int32_t>(state, D.slot_label);
+    a.slot_cnt = at<int32_t>(state, D.slot_cnt);
+    a.slot_last = at<int32_t>(state, D.slot_last);
+    a.M = at<float>(state, D.M);
+    a.slot_blocks = at<int32_t>(state, D.slot_blocks);
+    a.pool = at<int32_t>(state, D.pool);
+    a.scratch = at<int32_t>(state, D.scratch);
+    a.pool_blocks = D.pool_blocks;
+    a.n = (int)n;
+    a.iq = iq;
+    a.ik = ik;
+    a.reset = reset;
+    a.sq = sq;
+    a.sk = sk;
+    a.v = v;
+    a.lut = out ? lut : nullptr;
+    a.lut_stride = lut_stride;
+    a.out = out;
+    a.lse2 = out ? lse2 : nullptr;
+    return hip_status(dism::launch_decode(a, dtype, S(stream)), what);
+}
+
+}  // extern "C"

@@ -95,6 +95,9 @@ struct PathArgs {
     // fixed-length rows.  Walks stop at the query's document start, the pair plan drops the
     // diagonal pair at a document start, and G[i+1] uses the document-local position.
     const int32_t* dstart;   // [N]
+    // query resets (inference prefill): per query the last reset position at or before it;
+    // walks from that query stop there.  [B*H*N] or null.
+    const int32_t* wlo;
 };
 
 // Outputs a packed call zeroes on soft training rows (null pointers are skipped).
@@ -112,6 +115,44 @@ struct PackedZero {
     float* dv;
     float* rowtau;
 };
+
+// Incremental decoder (dism_decode.hip): state sections of one caller-owned buffer and the
+// tokens of one call.
+constexpr int LIST_BLOCK = 64;  // key positions per block of a label's position list
+struct DecodeArgs {
+    int rows, H, cap, slots, bcap;
+    int R, DV;
+    // state (one caller-owned buffer, dism_capi.cpp: decoder layout)
+    int32_t* meta;        // [rows][4] position, pool blocks used, last reset, error
+    int32_t* qlab;        // [rows][cap]
+    int32_t* klab;        // [rows][cap]
+    void* skh;            // [rows][cap][R]
+    void* vh;             // [rows][cap][DV]
+    int32_t* slot_label;  // [rows][slots]
+    int32_t* slot_cnt;    // [rows][slots] keys of the label (0: empty slot)
+    int32_t* slot_last;   // [rows][slots]
+    float* M;             // [rows][slots][R*DV]
+    int32_t* slot_blocks; // [rows][slots][bcap]
+    int32_t* pool;        // [rows][pool_blocks * 64]
+    int32_t* scratch;     // [rows][cap] walk lengths of the current query's candidates
+    int pool_blocks;
+    // this call's tokens: n per row, inputs in the training layouts with N = n
+    int n;
+    const int32_t* iq;    // [B,H,n]
+    const int32_t* ik;
+    const uint8_t* reset; // [B,H,n] or null
+    const void* sq;       // [B,n,H,R] (null for prime)
+    const void* sk;
+    const void* v;        // [B,n,H,DV]
+    const float* lut;     // [H, lut_stride]
+    long lut_stride;
+    float* out;           // [B,n,H,DV] fp32, null for prime (keys only)
+    float* lse2;          // [B,H,n] or null
+};
+
+hipError_t launch_decode(const DecodeArgs& a, int dtype, hipStream_t s);
+hipError_t launch_reset_starts(const uint8_t* reset, long rows, long n, int32_t* wlo,
+                               hipStream_t s);
 
 hipError_t launch_sign_labels(const void* x, int dtype, long B, long N, long H, int d,
                               int32_t* out, hipStream_t s);

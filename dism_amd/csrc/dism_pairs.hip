@@ -85,8 +85,8 @@ __device__ __forceinline__ void partner_range(const PathArgs& a, int bh, long so
 
 // Match length of a bigram pair (i, j >= 1, q[i-1] == k[j-1] known): match_length's suffix
 // walk without its first comparison.
-// dlo: start of the query's document (0 for fixed-length rows; packed calls have no carry
-// boundary).
+// dlo: the lowest query position the walk may reach (walk_lo: document start, last reset;
+// calls with either have no carry boundary).
 __device__ __forceinline__ int pair_length(const int32_t* __restrict__ q,
                                            const int32_t* __restrict__ k, int i, int j,
                                            const int32_t* __restrict__ bound, int strip, int n,
@@ -376,7 +376,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
         }
         float skr[R];
         load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
-        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, doc_start(a, i)) : 1;
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i)) : 1;
         const float lw = lut[L];
         float mm = has && lw > m0 ? lw : m0;
         key = has ? (((unsigned long long)(unsigned)L << 32) | (unsigned)j) : 0ull;
@@ -422,7 +422,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
             const int kq = c0 + sub;
             if (kq < cnt) {
                 const int j = kb[lo + kq];
-                const int L = pair_length(q, k, i, j, bnd, a.strip, n, doc_start(a, i));
+                const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i));
                 const float lw = lut[L];
                 if (lw > m0) atomicMax(&S.m[sl], __float_as_uint(lw));
                 atomicMax(&S.key[sl], ((unsigned long long)(unsigned)L << 32) | (unsigned)j);
@@ -439,7 +439,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
             const int kq = c0 + sub;
             if (kq < cnt) {
                 const int j = kb[lo + kq];
-                const int L = pair_length(q, k, i, j, bnd, a.strip, n, doc_start(a, i));
+                const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i));
                 const float p = exp2_fp32(lut[L] - m);
                 float skr[R];
                 load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
@@ -576,7 +576,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
         }
         float skr[R];
         load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
-        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, doc_start(a, i)) : 1;
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i)) : 1;
         float sdot = 0.0f;
 #pragma unroll
         for (int r = 0; r < R; ++r) sdot = __builtin_fmaf(sqr[r], skr[r], sdot);
@@ -617,7 +617,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
         const int kq = c0 + sub;
         if (kq < cnt) {
             const int j = kb[lo + kq];
-            const int L = pair_length(q, k, i, j, bnd, a.strip, n, doc_start(a, i));
+            const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i));
             float skr[R];
             load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
             float sdot = 0.0f;
@@ -754,7 +754,7 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
         const float l2 = a.lse2[s.so + i];
         float sqr[R];
         load_row<T, R>(sq + (s.row0 + (long)i * a.H) * R, sqr);
-        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, doc_start(a, i)) : 1;
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i)) : 1;
         const float p = exp2_fp32(lut[L] - l2);
         float sdot = 0.0f;
 #pragma unroll
@@ -792,7 +792,7 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
         const int kq = c0 + sub;
         if (kq < cnt) {
             const int i = qb[lo + kq];
-            const int L = pair_length(q, k, i, j, bnd, a.strip, n, doc_start(a, i));
+            const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i));
             const float l2 = a.lse2[s.so + i];
             const float p = exp2_fp32(lut[L] - l2);
             float sqr[R];

@@ -82,6 +82,17 @@ __device__ __forceinline__ int doc_start(const PathArgs& a, int p) {
     return a.dstart ? a.dstart[p] : 0;
 }
 
+// lowest query position a suffix walk from query p may reach: its document start (packed
+// rows) and its last query reset (prefill with resets); row offset so = bh * n
+__device__ __forceinline__ int walk_lo(const PathArgs& a, long so, int p) {
+    int lo = doc_start(a, p);
+    if (a.wlo) {
+        const int r = a.wlo[so + p];
+        lo = r > lo ? r : lo;
+    }
+    return lo;
+}
+
 // first index in [lo, hi) whose unsigned label is >= x (lower) / > x (upper)
 __device__ __forceinline__ int lower_label(const int32_t* lab, int lo, int hi, uint32_t x) {
     while (lo < hi) {

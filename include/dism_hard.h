@@ -211,6 +211,53 @@ int32_t dism_hard_packed_backward(const void* sq, const void* sk, const void* v,
                                   int64_t workspace_bytes, float* dsq, float* dsk, float* dv,
                                   float* rowtau, float* dtau, void* stream);
 
+/* ---- Inference (all rows hard, FP32 outputs).
+ * Query resets follow the reference inference oracle (dism_v3/tests/test_sam_inference.py:9-29):
+ * reset[b,h,i] = 1 starts query i's match afresh (its suffix walk stops at i); stored keys
+ * stay visible. */
+
+/* Workspace bytes of dism_hard_prefill (-1 for unsupported dimensions). */
+int64_t dism_hard_prefill_workspace_bytes(int64_t B, int64_t N, int64_t H, int32_t R,
+                                          int32_t DV, int32_t dtype);
+
+/* Hard prefill: out [B,N,H,DV] fp32 and lse2 [B,H,N] for labels iq, ik [B,H,N] with optional
+ * query resets [B,H,N] (uint8, NULL = none): prepare + readout of the training forward, every
+ * row hard.  lut_stride >= N + 1.  Replaces HardDismPrefill's plan + execute
+ * (dism_v3/python/flash_dism/inference/prefill_batch.py:67-118, README.md:229-292); equal
+ * bit for bit to dism_hard_readout's fp32 output when there are no resets. */
+int32_t dism_hard_prefill(const void* sq, const void* sk, const void* v, int32_t dtype,
+                          const int32_t* iq, const int32_t* ik, const uint8_t* reset,
+                          const float* lut, int64_t lut_stride, int64_t B, int64_t N, int64_t H,
+                          int32_t R, int32_t DV, void* workspace, int64_t workspace_bytes,
+                          float* out, float* lse2, void* stream);
+
+/* Incremental decoder state bytes for rows = B*H, capacity positions and `slots` label-table
+ * entries per row (a power of two >= 64; at least twice the distinct key labels a row will
+ * see), vectors cached in dtype (-1 for unsupported dimensions).  The first rows*4 int32 of
+ * the state are, per row: position, list blocks used, last query reset, error flag (1 when
+ * the label table overflowed).  No reference counterpart for the layout: the reference keeps
+ * suffix-automaton snapshots (inference/runtime.py, gpu_runtime.py). */
+int64_t dism_decoder_state_bytes(int64_t rows, int32_t R, int32_t DV, int64_t capacity,
+                                 int32_t slots, int32_t dtype);
+
+/* Zeroes a decoder state (a fill kernel on the stream). */
+int32_t dism_decoder_init(void* state, int64_t state_bytes, int64_t rows, int32_t R, int32_t DV,
+                          int64_t capacity, int32_t slots, int32_t dtype, void* stream);
+
+/* Appends n tokens to every row: labels iq, ik [B,H,n], optional resets [B,H,n], vectors sq,
+ * sk [B,n,H,R], v [B,n,H,DV] in the state's dtype.  Each token's key is added before its
+ * query is read (a token matches itself).  out [B,n,H,DV] fp32 (and optional lse2 [B,H,n])
+ * receive the outputs, equal bit for bit to the training forward's fp32 output at those
+ * positions; out = NULL primes the state with keys only (sq and lut may then be NULL).
+ * lut [H, lut_stride] with lut_stride >= capacity + 1.  The caller keeps position + n <=
+ * capacity.  Replaces HardDismDecoder.append / prime
+ * (dism_v3/python/flash_dism/inference/api.py:63-95). */
+int32_t dism_decoder_step(void* state, int64_t state_bytes, int64_t B, int64_t H, int32_t R,
+                          int32_t DV, int64_t capacity, int32_t slots, int32_t dtype, int64_t n,
+                          const int32_t* iq, const int32_t* ik, const uint8_t* reset,
+                          const void* sq, const void* sk, const void* v, const float* lut,
+                          int64_t lut_stride, float* out, float* lse2, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

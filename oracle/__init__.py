@@ -67,6 +67,9 @@ def lib():
         L.orc_backward.argtypes = [P, P, P, P, P, P, P, P, P, i64, P, i32, i64, i32, i32, i32,
                                    P, P, P, P, i32]
         L.orc_forward_direct.argtypes = L.orc_forward.argtypes
+        L.orc_forward_reset.argtypes = L.orc_forward.argtypes + [P]
+        L.orc_suffix_walk_from.restype = i64
+        L.orc_suffix_walk_from.argtypes = [P, P, i64, i64, i64]
         L.orc_backward_direct.argtypes = L.orc_backward.argtypes
         L.orc_tau_reduce.argtypes = [P, i32, i32, i64, i64, P]
         _lib = L
@@ -151,11 +154,21 @@ def suffix_walk(q, k, i, j):
     return lib().orc_suffix_walk(_p(q), _p(k), i, j)
 
 
-def forward(sq, sk, v, iq, ik, hard, lut, threads=0, direct=False):
+def reset_starts(reset):
+    """[B,H,N] bool query resets -> int32 [B,H,N]: last reset position at or before each
+    query (0 where none)."""
+    reset = np.asarray(reset, dtype=bool)
+    pos = np.where(reset, np.arange(reset.shape[-1], dtype=np.int64), 0)
+    return np.ascontiguousarray(np.maximum.accumulate(pos, axis=-1).astype(np.int32))
+
+
+def forward(sq, sk, v, iq, ik, hard, lut, threads=0, direct=False, reset=None):
     """CPU model forward.  Returns (O fp32 [B,N,H,DV], lse2 [B,H,N], Lmax, argmax).
 
     direct=False: the decomposed fp32 sequence the HIP kernels reproduce bit for bit;
-    direct=True: the pairwise definition (same mathematics, other fp32 association)."""
+    direct=True: the pairwise definition (same mathematics, other fp32 association).
+    reset: optional [B,H,N] bool query resets (inference semantics: a reset query's match
+    starts afresh at that query; keys stay)."""
     sq, sk, v, lut = _f32(sq), _f32(sk), _f32(v), _f32(lut)
     iq, ik = _i32(iq), _i32(ik)
     B, N, H, R = sq.shape
@@ -164,10 +177,14 @@ def forward(sq, sk, v, iq, ik, hard, lut, threads=0, direct=False):
     lse2 = np.empty((B, H, N), dtype=np.float32)
     lmax = np.empty((B, H, N), dtype=np.int32)
     jarg = np.empty((B, H, N), dtype=np.int32)
-    fn = lib().orc_forward_direct if direct else lib().orc_forward
-    fn(_p(sq), _p(sk), _p(v), _p(iq), _p(ik), _p(_flags(hard)), _p(lut),
-                      lut.shape[1], B, N, H, R, DV, _p(out), _p(lse2), _p(lmax), _p(jarg),
-                      threads)
+    args = (_p(sq), _p(sk), _p(v), _p(iq), _p(ik), _p(_flags(hard)), _p(lut), lut.shape[1], B,
+            N, H, R, DV, _p(out), _p(lse2), _p(lmax), _p(jarg), threads)
+    if reset is not None:
+        assert not direct
+        wlo = reset_starts(reset)
+        lib().orc_forward_reset(*args, _p(wlo))
+    else:
+        (lib().orc_forward_direct if direct else lib().orc_forward)(*args)
     return out, lse2, lmax, jarg
 
 

@@ -36,8 +36,10 @@ def dense_lengths(iq, ik):
     return np.tril(out)
 
 
-def _scores(iq, ik, tau):
-    """logM + softplus recurrence (dism_v3_ref.py:41-52) for one (b,h)."""
+def _scores(iq, ik, tau, reset=None):
+    """logM + softplus recurrence (dism_v3_ref.py:41-52) for one (b,h).  reset [N] bool: the
+    predecessor score of a reset query is -inf (inference oracle,
+    dism_v3/tests/test_sam_inference.py:19-21)."""
     n = iq.shape[0]
     logm = np.where(iq[:, None] == ik[None, :], 0.0, -np.inf) + tau
     rows = []
@@ -45,6 +47,8 @@ def _scores(iq, ik, tau):
     prev = np.full(n, -np.inf)
     for i in range(n):
         x = np.concatenate(([-np.inf], prev[:-1]))
+        if reset is not None and reset[i]:
+            x = np.full(n, -np.inf)
         with np.errstate(over="ignore", invalid="ignore"):
             sig = np.where(x > 20.0, 1.0, 1.0 / (1.0 + np.exp(-x)))
         alphas.append(np.where(np.isneginf(x), 0.0, sig))
@@ -55,8 +59,8 @@ def _scores(iq, ik, tau):
     return np.where(causal, w, -np.inf), np.stack(alphas)
 
 
-def _bh_forward(sq, sk, v, iq, ik, tau):
-    w, _ = _scores(iq, ik, tau)
+def _bh_forward(sq, sk, v, iq, ik, tau, reset=None):
+    w, _ = _scores(iq, ik, tau, reset)
     zmax = np.maximum(w.max(-1, keepdims=True), 0.0)
     with np.errstate(invalid="ignore"):
         ew = np.exp(w - zmax)
@@ -69,9 +73,10 @@ def _bh_forward(sq, sk, v, iq, ik, tau):
     return num / den, lse2
 
 
-def dense_forward(sq, sk, v, iq, ik, hard, tau):
+def dense_forward(sq, sk, v, iq, ik, hard, tau, reset=None):
     """sq,sk [B,N,H,R], v [B,N,H,DV] (any float), iq/ik [B,H,N] int, hard [B,H] bool,
-    tau [H].  Returns (O [B,N,H,DV] float64, lse2 [B,H,N] float64); soft rows are zero."""
+    tau [H], optional query resets [B,H,N] bool.  Returns (O [B,N,H,DV] float64,
+    lse2 [B,H,N] float64); soft rows are zero."""
     sq, sk, v = (np.asarray(x, dtype=np.float64) for x in (sq, sk, v))
     B, N, H, _ = sq.shape
     out = np.zeros(v.shape, dtype=np.float64)
@@ -81,7 +86,7 @@ def dense_forward(sq, sk, v, iq, ik, hard, tau):
             if not hard[b, h]:
                 continue
             o, l2 = _bh_forward(sq[b, :, h], sk[b, :, h], v[b, :, h], iq[b, h], ik[b, h],
-                                float(tau[h]))
+                                float(tau[h]), None if reset is None else reset[b, h])
             out[b, :, h] = o
             lse2[b, h] = l2
     return out, lse2

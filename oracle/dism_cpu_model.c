@@ -267,6 +267,15 @@ long orc_suffix_walk(const int32_t* q, const int32_t* k, long i, long j) {
     return c;
 }
 
+/* The walk of a query whose match was reset at position lo <= i (the reference inference
+ * oracle masks the predecessor score of a reset query, test_sam_inference.py:19-21): the
+ * query side never reaches below lo. */
+long orc_suffix_walk_from(const int32_t* q, const int32_t* k, long i, long j, long lo) {
+    long c = 0;
+    while (i - c >= lo && j - c >= 0 && q[i - c] == k[j - c]) ++c;
+    return c;
+}
+
 /* ---------------- forward ----------------
  * Vectors fp32 BNHD (bf16 inputs widened exactly by the caller), labels BHN, hard [B*H].
  * Per row i:
@@ -544,10 +553,37 @@ static long label_lb(const int32_t* lab, const int32_t* ord, long N, uint32_t x)
  *   den = (exp2(-m) + (float)(cnt - |P|) * p1) + dp
  *   y[d] = chain_r fma(sq_i[r], M_i[r][d])
  *   out[d] = fma(p1, y[d], corr[d]) * (1/den);  lse2 = m + log2(den). */
+static void forward_impl(const float* sq, const float* sk, const float* v, const int32_t* iq,
+                         const int32_t* ik, const uint8_t* hard, const float* lut,
+                         long lut_stride, int B, long N, int H, int R, int DV, float* out,
+                         float* lse2, int32_t* lmax, int32_t* jarg, int threads,
+                         const int32_t* wlo);
+
 void orc_forward(const float* sq, const float* sk, const float* v, const int32_t* iq,
                  const int32_t* ik, const uint8_t* hard, const float* lut, long lut_stride,
                  int B, long N, int H, int R, int DV, float* out, float* lse2, int32_t* lmax,
                  int32_t* jarg, int threads) {
+    forward_impl(sq, sk, v, iq, ik, hard, lut, lut_stride, B, N, H, R, DV, out, lse2, lmax,
+                 jarg, threads, NULL);
+}
+
+/* orc_forward with query resets: wlo [B*H*N] holds, per query, the last reset position at or
+ * before it (0 without one); walks of that query stop there.  Bigram pairs are still every
+ * key whose (previous, current) labels equal the query's; a pair cut by a reset has L = 1. */
+void orc_forward_reset(const float* sq, const float* sk, const float* v, const int32_t* iq,
+                       const int32_t* ik, const uint8_t* hard, const float* lut,
+                       long lut_stride, int B, long N, int H, int R, int DV, float* out,
+                       float* lse2, int32_t* lmax, int32_t* jarg, int threads,
+                       const int32_t* wlo) {
+    forward_impl(sq, sk, v, iq, ik, hard, lut, lut_stride, B, N, H, R, DV, out, lse2, lmax,
+                 jarg, threads, wlo);
+}
+
+static void forward_impl(const float* sq, const float* sk, const float* v, const int32_t* iq,
+                         const int32_t* ik, const uint8_t* hard, const float* lut,
+                         long lut_stride, int B, long N, int H, int R, int DV, float* out,
+                         float* lse2, int32_t* lmax, int32_t* jarg, int threads,
+                         const int32_t* wlo) {
 #ifdef _OPENMP
     if (threads > 0) omp_set_num_threads(threads);
 #pragma omp parallel for schedule(dynamic, 1)
@@ -608,7 +644,9 @@ void orc_forward(const float* sq, const float* sk, const float* v, const int32_t
                         const long j = ko[x];
                         if (j >= 1 && k[j - 1] == q[i - 1]) {
                             pj[np] = (int32_t)j;
-                            pl[np] = (int32_t)orc_suffix_walk(q, k, i, j);
+                            pl[np] = (int32_t)(wlo ? orc_suffix_walk_from(
+                                                         q, k, i, j, wlo[(long)bh * N + i])
+                                                   : orc_suffix_walk(q, k, i, j));
                             ++np;
                         }
                     }

@@ -306,3 +306,32 @@ def test_tau_reduce_order():
                 inner += x
             outer += inner
         assert out[h] == np.float32(outer)
+
+
+def test_forward_with_query_resets_pinned_by_fp64():
+    """orc_forward_reset (inference resets) against the FP64 restatement of the reference's
+    inference oracle (dism_v3/tests/test_sam_inference.py:9-29, predecessor score -inf at a
+    reset query); without resets it is orc_forward exactly, and resets do change the result."""
+    from oracle import dense
+    rng = np.random.default_rng(83)
+    b, h, n, r, dv = 2, 2, 79, 16, 32
+    for alphabet in (1, 4):
+        iq = rng.integers(0, alphabet, (b, h, n)).astype(np.int32)
+        ik = rng.integers(0, alphabet, (b, h, n)).astype(np.int32)
+        sq, sk, v = (oracle.bf16_round(rng.standard_normal((b, n, h, c)) * 0.2)
+                     for c in (r, r, dv))
+        tau = np.array([0.0, 0.35], dtype=np.float32)
+        hard = np.ones((b, h), bool)
+        lut = oracle.log_weights(tau, n)
+        reset = np.zeros((b, h, n), bool)
+        reset[..., 17::19] = True
+        got, l2, _, _ = oracle.forward(sq, sk, v, iq, ik, hard, lut, reset=reset)
+        ref, l2d = dense.dense_forward(sq, sk, v, iq, ik, hard, tau, reset=reset)
+        np.testing.assert_allclose(got, ref, atol=2e-6, rtol=2e-4)
+        np.testing.assert_allclose(l2, l2d, atol=2e-5, rtol=2e-6)
+        plain = oracle.forward(sq, sk, v, iq, ik, hard, lut)[0]
+        none = oracle.forward(sq, sk, v, iq, ik, hard, lut, reset=np.zeros_like(reset))[0]
+        assert np.array_equal(plain.view(np.uint32), none.view(np.uint32))
+        assert np.abs(plain - got).max() > 1e-3
+    starts = oracle.reset_starts(np.array([[[0, 1, 0, 0, 1, 0]]], bool))
+    assert starts.tolist() == [[[0, 1, 1, 1, 4, 4]]]
