@@ -38,6 +38,7 @@ SIGNATURES = {
                                  _I32, _P, _I64, _P, _I32, _P, _P, _P, _P],
     "dism_hard_packed_backward": [_P, _P, _P, _P, _I32, _P, _I64, _P, _P, _I64, _I64, _P, _I64,
                                   _I64, _I32, _I32, _P, _I64, _P, _P, _P, _P, _P, _P],
+    "dism_vocab_labels": [_P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P],
     "dism_hard_prefill": [_P, _P, _P, _I32, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32,
                           _P, _I64, _P, _P, _P],
     "dism_decoder_init": [_P, _I64, _I64, _I32, _I32, _I64, _I32, _I32, _P],

@@ -24,3 +24,36 @@ def sign_labels(x):
         _lib.call("dism_sign_labels", x.data_ptr(), DTYPE_CODE[x.dtype], b, n, h, d,
                   out.data_ptr(), torch.cuda.current_stream(x.device).cuda_stream)
     return out
+
+
+@torch.no_grad()
+def vocab_labels(x, vocab, *, return_exact_count=False):
+    """Codebook argmax labels (the general label producer): x bf16 [B,N,H,D] (CUDA),
+    vocab bf16 [H,V,D] or shared [V,D], D in {32, 64, 128} -> int32 [B,H,N] with
+    labels[b,h,n] = argmax_v x[b,n,h] . vocab[h,v] in exact arithmetic, first index on ties
+    (reference dism_v3/python/flash_dism/reference/dism_v3_ref.py:159-162).  Scores run on the
+    matrix cores; tokens whose top-two margin lies within the certified fp32 error bound are
+    rescored in fp64.  With return_exact_count, also returns how many tokens were rescored."""
+    require(isinstance(x, torch.Tensor) and x.is_cuda and x.dim() == 4 and x.is_contiguous()
+            and x.dtype == torch.bfloat16, "x must be contiguous CUDA bf16 [B,N,H,D]")
+    b, n, h, d = x.shape
+    require(isinstance(vocab, torch.Tensor) and vocab.device == x.device and
+            vocab.dtype == torch.bfloat16 and vocab.is_contiguous() and vocab.dim() in (2, 3),
+            "vocabulary must be contiguous CUDA bf16 [H,V,D] or [V,D]")
+    require(vocab.shape[-1] == d and (vocab.dim() == 2 or vocab.shape[0] == h) and
+            vocab.shape[-2] > 0, "invalid vocabulary/channel size")
+    require(d in (32, 64, 128), "invalid vocabulary/channel size")
+    v = vocab.shape[-2]
+    out = torch.empty((b, h, n), dtype=torch.int32, device=x.device)
+    count = torch.zeros((1,), dtype=torch.int32, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.call("dism_vocab_labels", x.data_ptr(), vocab.data_ptr(),
+                  0 if vocab.dim() == 2 else v * d, b, n, h, v, d, out.data_ptr(),
+                  count.data_ptr(), torch.cuda.current_stream(x.device).cuda_stream)
+    return (out, count) if return_exact_count else out
+
+
+def vocab_argmax_labels(q, k, q_vocab, k_vocab):
+    """(idx_q, idx_k) = codebook argmax labels of q against q_vocab and of k against k_vocab,
+    the hard labels of dism_v3/python/flash_dism/reference/dism_v3_ref.py:159-162."""
+    return vocab_labels(q, q_vocab), vocab_labels(k, k_vocab)

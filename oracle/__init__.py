@@ -68,6 +68,7 @@ def lib():
                                    P, P, P, P, i32]
         L.orc_forward_direct.argtypes = L.orc_forward.argtypes
         L.orc_forward_reset.argtypes = L.orc_forward.argtypes + [P]
+        L.orc_vocab_labels.argtypes = [P, P, i64, i32, i64, i32, i64, i32, P]
         L.orc_suffix_walk_from.restype = i64
         L.orc_suffix_walk_from.argtypes = [P, P, i64, i64, i64]
         L.orc_backward_direct.argtypes = L.orc_backward.argtypes
@@ -207,3 +208,16 @@ def backward(sq, sk, v, dout, iq, ik, hard, lut, dlut, lse2, threads=0, block=25
     dtau = np.empty(H, dtype=np.float32)
     lib().orc_tau_reduce(_p(rowtau), B, H, N, block, _p(dtau))
     return dsq, dsk, dv, dtau, rowtau
+
+
+def vocab_labels(x, vocab):
+    """Exact codebook argmax labels [B,H,N] (first index on ties): x [B,N,H,D] floats (bf16
+    values), vocab [H,V,D] or shared [V,D]."""
+    x = _f32(x)
+    vocab = _f32(vocab)
+    B, N, H, D = x.shape
+    V = vocab.shape[-2]
+    vhs = 0 if vocab.ndim == 2 else V * D
+    out = np.empty((B, H, N), dtype=np.int32)
+    lib().orc_vocab_labels(_p(x), _p(vocab), vhs, B, N, H, V, D, _p(out))
+    return out

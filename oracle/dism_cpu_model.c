@@ -863,3 +863,26 @@ void orc_backward(const float* sq, const float* sk, const float* v, const float*
         free(qo); free(ko); free(M); free(zq); free(cd); free(a);
     }
 }
+
+/* ---------------- vocabulary labels ----------------
+ * labels[b,h,n] = argmax_v sum_d x[b,n,h,d] * vocab[h*vhs + v*D + d], summed in d order in
+ * double (products of bf16 values are exact; for ordinary inputs so is the sum), first index
+ * on ties -- the argmax of dism_v3/python/flash_dism/reference/dism_v3_ref.py:159-162 (torch
+ * argmax returns the first maximal index) evaluated exactly. */
+void orc_vocab_labels(const float* x, const float* vocab, long vhs, int B, long N, int H, long V,
+                      int D, int32_t* labels) {
+    for (int b = 0; b < B; ++b)
+        for (long n = 0; n < N; ++n)
+            for (int h = 0; h < H; ++h) {
+                const float* xt = x + (((long)b * N + n) * H + h) * D;
+                double best = -INFINITY;
+                long bi = 0;
+                for (long v = 0; v < V; ++v) {
+                    const float* e = vocab + (long)h * vhs + v * D;
+                    double s = 0.0;
+                    for (int d = 0; d < D; ++d) s += (double)xt[d] * (double)e[d];
+                    if (s > best) { best = s; bi = v; }
+                }
+                labels[((long)b * H + h) * N + n] = (int32_t)bi;
+            }
+}
