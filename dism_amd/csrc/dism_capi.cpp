@@ -822,20 +822,20 @@ extern "C" {
 
 int32_t dism_vocab_labels(const void* x, const void* vocab, int64_t vocab_head_stride, int64_t B,
                           int64_t N, int64_t H, int64_t V, int32_t D, int32_t* labels,
-                          int32_t* exact_count, void* stream) {
+                          int32_t* scratch, void* stream) {
     const char* what = "vocabulary labels";
-    if (!x || !vocab || !labels) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
-    if (B <= 0 || N <= 0 || H <= 0 || V <= 0 || V > INT_MAX || N > INT_MAX ||
-        B * H * ((N + 31) / 32) > ((int64_t)1 << 40))
+    if (!x || !vocab || !labels || !scratch)
+        return fail(DISM_ERR_INVALID, "%s: null pointer", what);
+    if (B <= 0 || N <= 0 || H <= 0 || V <= 0 || V > INT_MAX || B * H * N >= INT_MAX)
         return fail(DISM_ERR_INVALID, "%s: positive dimensions required", what);
     if (D != 32 && D != 64 && D != 128)
         return fail(DISM_ERR_UNSUPPORTED, "invalid vocabulary/channel size");
     if (vocab_head_stride != 0 && vocab_head_stride < V * D)
         return fail(DISM_ERR_INVALID, "%s: invalid vocabulary head stride", what);
-    if ((reinterpret_cast<uintptr_t>(x) & 7) || (reinterpret_cast<uintptr_t>(vocab) & 7))
-        return fail(DISM_ERR_INVALID, "%s: inputs must be 8-byte aligned", what);
+    if ((reinterpret_cast<uintptr_t>(x) & 7) || (reinterpret_cast<uintptr_t>(vocab) & 15))
+        return fail(DISM_ERR_INVALID, "%s: x must be 8-byte and vocab 16-byte aligned", what);
     return hip_status(dism::launch_vocab_argmax(x, vocab, vocab_head_stride, (int)B, (int)N,
-                                                (int)H, (int)V, D, labels, exact_count,
+                                                (int)H, (int)V, D, labels, scratch,
                                                 S(stream)),
                       what);
 }

@@ -154,9 +154,10 @@ hipError_t launch_decode(const DecodeArgs& a, int dtype, hipStream_t s);
 hipError_t launch_reset_starts(const uint8_t* reset, long rows, long n, int32_t* wlo,
                                hipStream_t s);
 
-// x, vocab: bf16
+// x, vocab: bf16; list: caller scratch [1 + 2H + B*H*N] (count of fp64-rescored tokens, per
+// head vocabulary statistics, the rescored tokens)
 hipError_t launch_vocab_argmax(const void* x, const void* vocab, long vhs, int B, int N, int H,
-                               int V, int D, int32_t* labels, int32_t* exact, hipStream_t s);
+                               int V, int D, int32_t* labels, int32_t* list, hipStream_t s);
 hipError_t launch_sign_labels(const void* x, int dtype, long B, long N, long H, int d,
                               int32_t* out, hipStream_t s);
 hipError_t launch_log_weights(const float* tau, int H, long stride, float* out, hipStream_t s);

@@ -45,12 +45,12 @@ def vocab_labels(x, vocab, *, return_exact_count=False):
     require(d in (32, 64, 128), "invalid vocabulary/channel size")
     v = vocab.shape[-2]
     out = torch.empty((b, h, n), dtype=torch.int32, device=x.device)
-    count = torch.zeros((1,), dtype=torch.int32, device=x.device)
+    scratch = torch.empty((1 + 2 * h + b * h * n,), dtype=torch.int32, device=x.device)
     with torch.cuda.device(x.device):
         _lib.call("dism_vocab_labels", x.data_ptr(), vocab.data_ptr(),
                   0 if vocab.dim() == 2 else v * d, b, n, h, v, d, out.data_ptr(),
-                  count.data_ptr(), torch.cuda.current_stream(x.device).cuda_stream)
-    return (out, count) if return_exact_count else out
+                  scratch.data_ptr(), torch.cuda.current_stream(x.device).cuda_stream)
+    return (out, scratch[:1]) if return_exact_count else out
 
 
 def vocab_argmax_labels(q, k, q_vocab, k_vocab):

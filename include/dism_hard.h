@@ -46,13 +46,14 @@ int32_t dism_sign_labels(const void* x, int32_t dtype, int64_t B, int64_t N, int
  * exact arithmetic, first index on ties; x bf16 [B,N,H,D], vocab bf16 [H,V,D] with head stride
  * vocab_head_stride elements (0 = one shared [V,D] table), D in {32,64,128}.  Matrix-core
  * scores with a certified error bound; tokens whose top-two margin is within the bound are
- * rescored in fp64.  exact_count (nullable) is incremented per rescored token.  Replaces the
+ * listed in scratch (caller-owned int32 [1 + 2H + B*H*N]: scratch[0] = how many) and
+ * rescored in fp64 by a second kernel.  B*H*N < 2^31.  Replaces the
  * label output of the Triton interpolation (dism_v3/python/flash_dism/emb_kernel.py:83-108,
  * :155-156) and the oracle argmax (dism_v3/python/flash_dism/reference/dism_v3_ref.py:159-162);
  * the interpolated embeddings and LSE belong to the soft path. */
 int32_t dism_vocab_labels(const void* x, const void* vocab, int64_t vocab_head_stride, int64_t B,
                           int64_t N, int64_t H, int64_t V, int32_t D, int32_t* labels,
-                          int32_t* exact_count, void* stream);
+                          int32_t* scratch, void* stream);
 
 /* log2 geometric weight table lut[h, l] = log2 sum_{s=1..l} e^{s tau_h}, lut[h,0] = -1e6,
  * l in [0, max_length].  Replaces cu.hard_log_weights (dism_v3/src/host/hard_forward.cpp:11-23,
