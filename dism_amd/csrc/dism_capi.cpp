@@ -58,6 +58,35 @@ struct Layout {
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
+// Side stream of the calling thread on the current device (default priority, non-blocking)
+// with its fork/join events, created on first use and kept for the thread's lifetime: the
+// only state the library keeps.  Null if HIP cannot create them (callers then run serially).
+struct SideStream {
+    hipStream_t stream = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+
+SideStream* side_stream() {
+    constexpr int MAX_DEVICES = 64;
+    thread_local SideStream cache[MAX_DEVICES];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
+    SideStream& c = cache[dev];
+    if (!c.stream) {
+        if (hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking) != hipSuccess) {
+            c.stream = nullptr;
+            return nullptr;
+        }
+        if (hipEventCreateWithFlags(&c.fork, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&c.join, hipEventDisableTiming) != hipSuccess) {
+            hipStreamDestroy(c.stream);
+            c.stream = nullptr;
+            return nullptr;
+        }
+    }
+    return &c;
+}
+
 Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     Layout L;
     const int64_t BH = B * H;
@@ -415,23 +444,42 @@ int32_t dism_hard_backward(const void* sq, const void* sk, const void* v, const 
                            int32_t DV, void* workspace, int64_t workspace_bytes, float* dsq,
                            float* dsk, float* dv, float* rowtau, float* dtau, void* stream) {
     if (!dtau) return fail(DISM_ERR_INVALID, "hard backward: null pointer");
+    // the key chain (keys -> key pairs) and the query-row chain (row pairs -> queries -> tau)
+    // are independent: the key chain runs on a side stream, forked from and joined back into
+    // the caller's stream (the row pairs are enqueued first so their persistent grid starts
+    // first)
+    SideStream* side = side_stream();
+    const hipStream_t s = S(stream);
+    void* ks = stream;
+    if (side) {
+        if (hipEventRecord(side->fork, s) != hipSuccess ||
+            hipStreamWaitEvent(side->stream, side->fork, 0) != hipSuccess)
+            side = nullptr;
+        else
+            ks = side->stream;
+    }
     int32_t st = dism_hard_backward_row_pairs(sq, sk, v, dout, dtype, iq, ik, hard, boundary,
                                               strip, lut, dlut, lut_stride, lse2, B, N, H, R, DV,
                                               workspace, workspace_bytes, stream);
-    if (st) return st;
-    st = dism_hard_backward_queries(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
-                                    dlut, lut_stride, lse2, B, N, H, R, DV, workspace,
-                                    workspace_bytes, dsq, rowtau, stream);
-    if (st) return st;
-    st = dism_hard_backward_keys(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
-                                 lut_stride, lse2, B, N, H, R, DV, workspace, workspace_bytes,
-                                 dsk, dv, stream);
-    if (st) return st;
-    st = dism_hard_backward_key_pairs(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip, lut,
-                                      lut_stride, lse2, B, N, H, R, DV, workspace,
-                                      workspace_bytes, dsk, dv, stream);
-    if (st) return st;
-    return dism_hard_tau_reduce(rowtau, B, H, N, dtau, stream);
+    if (!st)
+        st = dism_hard_backward_keys(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip,
+                                     lut, lut_stride, lse2, B, N, H, R, DV, workspace,
+                                     workspace_bytes, dsk, dv, ks);
+    if (!st)
+        st = dism_hard_backward_key_pairs(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip,
+                                          lut, lut_stride, lse2, B, N, H, R, DV, workspace,
+                                          workspace_bytes, dsk, dv, ks);
+    if (!st)
+        st = dism_hard_backward_queries(sq, sk, v, dout, dtype, iq, ik, hard, boundary, strip,
+                                        lut, dlut, lut_stride, lse2, B, N, H, R, DV, workspace,
+                                        workspace_bytes, dsq, rowtau, stream);
+    if (!st) st = dism_hard_tau_reduce(rowtau, B, H, N, dtau, stream);
+    if (side) {  // join even after an error, so the caller's stream never runs ahead
+        const bool joined = hipEventRecord(side->join, side->stream) == hipSuccess &&
+                            hipStreamWaitEvent(s, side->join, 0) == hipSuccess;
+        if (!st && !joined) return fail(DISM_ERR_HIP, "hard backward: stream join failed");
+    }
+    return st;
 }
 
 }  // extern "C"

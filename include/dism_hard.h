@@ -4,8 +4,9 @@
  * Library: dism_amd/libdism_hip.so (gfx950).  Every entry point takes raw device pointers,
  * sizes and a HIP stream (passed as void*, a hipStream_t; NULL = default stream), enqueues
  * its kernels on that stream and returns without synchronising.  The caller allocates all
- * outputs; the library owns no device memory and keeps no mutable global state, so calls
- * on different streams or threads are independent.  Return value: 0 on success, otherwise
+ * outputs; the library owns no device memory and keeps no mutable global state beyond one
+ * side stream and two events per calling thread and device (dism_hard_backward), so calls on
+ * different streams or threads are independent.  Return value: 0 on success, otherwise
  * a DISM_ERR_* code with a thread-local message from dism_last_error().
  *
  * Layouts follow the reference: vectors BNHD ([B,N,H,R] / [B,N,H,DV], contiguous), labels
@@ -125,7 +126,10 @@ int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t
 /* Hard backward on a workspace prepared by dism_hard_prepare for the same labels: dsq, dsk
  * [B,N,H,R], dv [B,N,H,DV], rowtau [B,H,N] (caller-owned scratch) and dtau [H], all fp32,
  * deterministic (no floating-point atomics).  lse2 is the forward's log2 normalizer;
- * lut/dlut share lut_stride >= N+1.  Runs the five stages below in order.
+ * lut/dlut share lut_stride >= N+1.  Runs the five stages below: the key chain (keys, key
+ * pairs) on a side stream of the calling thread (default priority, created on first use and
+ * kept; forked from and joined back into `stream`, so the call stays asynchronous and
+ * capturable), the query-row chain (row pairs, queries, tau reduce) on `stream`.
  * Replaces cu.hard_backward (dism_v3/src/host/hard_backward.cpp:13-140). */
 int32_t dism_hard_backward(const void* sq, const void* sk, const void* v, const void* dout,
                            int32_t dtype, const int32_t* iq, const int32_t* ik,

@@ -76,3 +76,42 @@ def test_compiled_matches_eager():
     ref = dism_amd.dism_core_hard(*(torch.from_numpy(a).to(d, torch.bfloat16) for a in (sq, sk, v)),
                                   iq, ik, hard, torch.from_numpy(taus(h)).to(d))
     assert torch.equal(ref, eager[0])
+
+
+@pytest.mark.gpu
+def test_forward_backward_graph_replay():
+    """forward_hard + backward_hard (whose key chain forks onto the library's side stream)
+    captured in a HIP graph: every replay, with eager work and synchronisations in between,
+    equals the eager results bit for bit (reference test_hard_forward.py:160-172 replays its
+    readout the same way)."""
+    import numpy as np
+    import torch
+    import dism_amd
+    from tests._data import labels, taus, vectors
+    b, n, h = 2, 1024, 4
+    q, k = labels(n, "alphabet4", b=b, h=h)
+    sq, sk, v = vectors(n, b=b, h=h)
+    do = np.random.default_rng(1).standard_normal(v.shape).astype(np.float32)
+    dev = lambda a, dt=None: torch.from_numpy(np.ascontiguousarray(a)).cuda().to(  # noqa
+        dt or torch.from_numpy(np.ascontiguousarray(a)).dtype)
+    tq, tk, tv, tdo = (dev(a, torch.bfloat16) for a in (sq, sk, v, do))
+    iq, ik = dev(q), dev(k)
+    hard, tau = dev(np.ones((b, h), bool)), dev(taus(h))
+
+    def run():
+        out, lse2, state = dism_amd.forward_hard(tq, tk, tv, iq, ik, hard, tau, save_state=True)
+        return (out, lse2) + tuple(dism_amd.backward_hard(tq, tk, tv, tdo, iq, ik, hard, lse2,
+                                                          state))
+
+    eager = [t.clone() for t in run()]  # also creates the side stream outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = run()
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(captured, eager):
+            assert torch.equal(got, want), i
+        run()  # eager work between replays
+        torch.cuda.synchronize()
