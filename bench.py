@@ -57,6 +57,9 @@ def main():
     ap.add_argument("--carry-strip", type=int, default=0,
                     help="composed carry boundary strip height (0 = off)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--workload", default="train", choices=("train", "decode", "vocab"),
+                    help="train: the BASELINE metric (default); decode: prefill + token-by-token "
+                         "decoding at the nanochat layer shape; vocab: codebook argmax labels")
     ap.add_argument("--streams", type=int, default=2, choices=(1, 2),
                     help="2: the backward's key chain runs concurrently on a side stream")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
@@ -80,6 +83,10 @@ def main():
     import dism_amd
     from dism_amd import _lib
     from dism_amd._checks import DTYPE_CODE
+    if args.workload == "decode":
+        return bench_decode(args)
+    if args.workload == "vocab":
+        return bench_vocab(args)
 
     dev = torch.device("cuda:0")
     B, T, H, D, DV = args.B, args.T, args.H, args.dqk, args.dv
@@ -267,6 +274,78 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(q, k, v, do, args)
     print(json.dumps(result), flush=True)
+
+
+def _time(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def bench_decode(args):
+    """Inference at the nanochat layer shape (B=8, H=10, d_qk=8, d_v=128,
+    bf16): prefill of a 2048-token prompt, then decoding 256 tokens one at a time after priming
+    with the prompt.  Prints one JSON line (decode tokens/s over the B*H rows, prefill time)."""
+    import torch
+    import dism_amd
+    B, H, R, DV, P, G = 8, 10, 8, 128, 2048, 256
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(20261205)
+    x = lambda *s: torch.randn(*s, generator=g).to(dev, torch.bfloat16)  # noqa: E731
+    sq, sk, v = x(B, P + G, H, R), x(B, P + G, H, R), x(B, P + G, H, DV)
+    iq, ik = dism_amd.sign_labels(sq), dism_amd.sign_labels(sk)
+    tau = [0.5] * H
+    with dism_amd.HardDismPrefill() as engine:
+        prep = engine.prepare(iq[..., :P], ik[..., :P], tau)
+        psq, psk, pv = (t[:, :P].contiguous() for t in (sq, sk, v))
+        pre_ms = _time(lambda: prep.execute(psq, psk, pv), args.steps, args.warmup)
+    dec = dism_amd.HardDismDecoder(B, H, R, DV, P + G, tau, label_slots=512,
+                                   check_errors=False)
+    dec.prime(iq[..., :P], ik[..., :P], sk[:, :P], v[:, :P])
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for t in range(P, P + G):
+        dec.append(iq[..., t:t + 1], ik[..., t:t + 1], sq[:, t:t + 1], sk[:, t:t + 1],
+                   v[:, t:t + 1])
+    e.record()
+    torch.cuda.synchronize()
+    step_ms = s.elapsed_time(e) / G
+    dec._check()
+    print(json.dumps({"metric": "hard DISM decode step latency (one token, all B*H rows)",
+                      "value": step_ms * 1e3, "unit": "us/token", "higher_is_better": False,
+                      "decode_tokens_per_s": B / (step_ms / 1e3),
+                      "prefill_ms": pre_ms, "prefill_tokens_per_s": B * P / (pre_ms / 1e3),
+                      "config": {"workload": "BASELINE configs[4] shape, inference", "B": B,
+                                 "H": H, "d_qk": R, "d_v": DV, "prompt": P, "decoded": G},
+                      "data": "synthetic N(0,1) bf16 vectors, sign labels"}), flush=True)
+
+
+def bench_vocab(args):
+    """Codebook argmax labels (the general label producer) for q at configs[2]'s token count
+    (B=4, T=16384, H=16) with D=64, V=512 per-head codebooks."""
+    import torch
+    import dism_amd
+    B, T, H, D, V = 4, 16384, 16, 64, 512
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(20261206)
+    x = torch.randn(B, T, H, D, generator=g).to(dev, torch.bfloat16)
+    voc = torch.randn(H, V, D, generator=g).to(dev, torch.bfloat16)
+    ms = _time(lambda: dism_amd.vocab_labels(x, voc), args.steps, args.warmup)
+    flops = 2.0 * B * T * H * V * D
+    print(json.dumps({"metric": "codebook argmax labels", "value": B * T * H / (ms / 1e3),
+                      "unit": "tokens/s", "ms": ms, "mfma_tflops": flops / (ms / 1e3) / 1e12,
+                      "mfma_peak_tflops": 2500.0, "config": {"B": B, "T": T, "H": H, "D": D,
+                                                             "V": V},
+                      "data": "synthetic N(0,1) bf16"}), flush=True)
 
 
 def measured_traffic(kernel):
