@@ -299,10 +299,11 @@ __device__ __forceinline__ void lds_row_f32(const float* p, float (&out)[R]) {
     }
 }
 
-template <typename T, int DV>
+template <typename T, int DV, int WB = WBYTES>
 struct Geo {
     static constexpr int RB = DV * (int)sizeof(T);
-    static constexpr int WIN = WBYTES / RB < 64 ? WBYTES / RB : 64;
+    static constexpr int BYTES = WB;  // one window buffer
+    static constexpr int WIN = WB / RB < 64 ? WB / RB : 64;
     static constexpr int NI = WIN * RB / 1024;
     static_assert((WIN * RB) % 1024 == 0, "window must be whole 1 KiB DMA blocks");
 };

@@ -458,12 +458,12 @@ __global__ __launch_bounds__(64 * WAVES) void scan_rows_kernel(PathArgs a) {
 // comes before the key.  N is kept in the column layout (lane = d); dSK0 reduces over lanes.
 template <typename T, int R, int DV>
 __global__ __launch_bounds__(64 * WAVES) void scan_keys_kernel(PathArgs a) {
-    using G_ = Geo<T, DV>;
+    using G_ = Geo<T, DV, WBYTES / 2>;  // half windows: 70 VGPRs, LDS allows 7 waves/SIMD
     constexpr int WIN = G_::WIN, RB = G_::RB, NI = G_::NI;
     constexpr int COLS = (DV + 63) / 64;
     constexpr int W = words_of(sizeof(T), R);
     constexpr int G = 64 / R;
-    __shared__ __attribute__((aligned(16))) unsigned char s_v_all[WAVES][2][WBYTES];
+    __shared__ __attribute__((aligned(16))) unsigned char s_v_all[WAVES][2][G_::BYTES];
     auto& s_v = s_v_all[wave_id()];
     __shared__ __attribute__((aligned(16))) float s_r_all[WAVES][WIN][R];
     auto& s_r = s_r_all[wave_id()];
