@@ -42,6 +42,8 @@ SIGNATURES = {
     "dism_hard_prefill": [_P, _P, _P, _I32, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32,
                           _P, _I64, _P, _P, _P],
     "dism_decoder_init": [_P, _I64, _I64, _I32, _I32, _I64, _I32, _I32, _P],
+    "dism_decoder_prime": [_P, _I64, _I64, _I64, _I32, _I32, _I64, _I32, _I32, _I64, _P, _P,
+                           _P, _P, _P, _P, _I64, _P],
     "dism_decoder_step": [_P, _I64, _I64, _I64, _I32, _I32, _I64, _I32, _I32, _I64, _P, _P, _P,
                           _P, _P, _P, _P, _I64, _P, _P, _P],
 }
@@ -52,6 +54,7 @@ SIZE_SIGNATURES = {
     "dism_hard_packed_workspace_bytes": [_I64, _I64, _I32, _I32, _I32],
     "dism_hard_prefill_workspace_bytes": [_I64, _I64, _I64, _I32, _I32, _I32],
     "dism_decoder_state_bytes": [_I64, _I32, _I32, _I64, _I32, _I32],
+    "dism_decoder_prime_workspace_bytes": [_I64, _I64, _I64, _I32, _I32, _I32],
 }
 
 _lib = None

@@ -740,6 +740,32 @@ DecoderLayout decoder_layout(int64_t rows, int32_t R, int32_t DV, int64_t cap, i
     return D;
 }
 
+dism::DecodeArgs decode_args(void* state, const DecoderLayout& D, int64_t rows, int64_t H,
+                             int32_t R, int32_t DV, int64_t capacity, int32_t slots) {
+    dism::DecodeArgs a{};
+    a.rows = (int)rows;
+    a.H = (int)H;
+    a.cap = (int)capacity;
+    a.slots = slots;
+    a.bcap = D.bcap;
+    a.R = R;
+    a.DV = DV;
+    a.meta = at<int32_t>(state, D.meta);
+    a.qlab = at<int32_t>(state, D.qlab);
+    a.klab = at<int32_t>(state, D.klab);
+    a.skh = at<void>(state, D.skh);
+    a.vh = at<void>(state, D.vh);
+    a.slot_label = at<int32_t>(state, D.slot_label);
+    a.slot_cnt = at<int32_t>(state, D.slot_cnt);
+    a.slot_last = at<int32_t>(state, D.slot_last);
+    a.M = at<float>(state, D.M);
+    a.slot_blocks = at<int32_t>(state, D.slot_blocks);
+    a.pool = at<int32_t>(state, D.pool);
+    a.scratch = at<int32_t>(state, D.scratch);
+    a.pool_blocks = D.pool_blocks;
+    return a;
+}
+
 int64_t prefill_extra(int64_t B, int64_t N, int64_t H) {
     return align256(B * H) + align256(B * H * N * 4);
 }
@@ -829,27 +855,7 @@ int32_t dism_decoder_step(void* state, int64_t state_bytes, int64_t B, int64_t H
         return fail(DISM_ERR_INVALID, "hard log-weight table is too short");
     const DecoderLayout D = decoder_layout(rows, R, DV, capacity, slots, dtype);
     if (state_bytes < D.total) return fail(DISM_ERR_INVALID, "%s: state too small", what);
-    dism::DecodeArgs a{};
-    a.rows = (int)rows;
-    a.H = (int)H;
-    a.cap = (int)capacity;
-    a.slots = slots;
-    a.bcap = D.bcap;
-    a.R = R;
-    a.DV = DV;
-    a.meta = at<int32_t>(state, D.meta);
-    a.qlab = at<int32_t>(state, D.qlab);
-    a.klab = at<int32_t>(state, D.klab);
-    a.skh = at<void>(state, D.skh);
-    a.vh = at<void>(state, D.vh);
-    a.slot_label = at<int32_t>(state, D.slot_label);
-    a.slot_cnt = at<int32_t>(state, D.slot_cnt);
-    a.slot_last = at<int32_t>(state, D.slot_last);
-    a.M = at<float>(state, D.M);
-    a.slot_blocks = at<int32_t>(state, D.slot_blocks);
-    a.pool = at<int32_t>(state, D.pool);
-    a.scratch = at<int32_t>(state, D.scratch);
-    a.pool_blocks = D.pool_blocks;
+    dism::DecodeArgs a = decode_args(state, D, rows, H, R, DV, capacity, slots);
     a.n = (int)n;
     a.iq = iq;
     a.ik = ik;
@@ -886,6 +892,61 @@ int32_t dism_vocab_labels(const void* x, const void* vocab, int64_t vocab_head_s
                                                 (int)H, (int)V, D, labels, scratch,
                                                 S(stream)),
                       what);
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int64_t dism_decoder_prime_workspace_bytes(int64_t B, int64_t n, int64_t H, int32_t R,
+                                           int32_t DV, int32_t dtype) {
+    const int64_t npad = (n + 255) / 256 * 256;
+    if (n <= 0 || !dims_ok(B, npad, H) || B * H * npad > INT_MAX || !rdv_ok(R, DV) ||
+        !dtype_ok(dtype))
+        return -1;
+    return layout(B, npad, H, R, DV).total + 2 * align256(B * H * npad * 4);
+}
+
+int32_t dism_decoder_prime(void* state, int64_t state_bytes, int64_t B, int64_t H, int32_t R,
+                           int32_t DV, int64_t capacity, int32_t slots, int32_t dtype, int64_t n,
+                           const int32_t* iq, const int32_t* ik, const uint8_t* reset,
+                           const void* sk, const void* v, void* workspace,
+                           int64_t workspace_bytes, void* stream) {
+    const char* what = "decoder prime";
+    if (!state || !iq || !ik || !sk || !v || !workspace)
+        return fail(DISM_ERR_INVALID, "%s: null pointer", what);
+    const int64_t rows = B * H;
+    if (B <= 0 || H <= 0 || !decoder_dims_ok(rows, R, DV, capacity, slots, dtype))
+        return fail(DISM_ERR_INVALID, "%s: invalid decoder dimensions", what);
+    if (n <= 0 || n > capacity) return fail(DISM_ERR_INVALID, "%s: invalid token count", what);
+    const int64_t need = dism_decoder_prime_workspace_bytes(B, n, H, R, DV, dtype);
+    if (need < 0 || workspace_bytes < need)
+        return fail(DISM_ERR_INVALID, "%s: workspace too small", what);
+    if (!aligned16(sk) || !aligned16(v))
+        return fail(DISM_ERR_INVALID, "%s: vectors must be 16-byte aligned", what);
+    const DecoderLayout D = decoder_layout(rows, R, DV, capacity, slots, dtype);
+    if (state_bytes < D.total) return fail(DISM_ERR_INVALID, "%s: state too small", what);
+    const int64_t npad = (n + 255) / 256 * 256;
+    const Layout L = layout(B, npad, H, R, DV);
+    int32_t* pq = at<int32_t>(workspace, L.total);
+    int32_t* pk = at<int32_t>(workspace, L.total + align256(rows * npad * 4));
+    hipStream_t s = S(stream);
+    int32_t st;
+    if ((st = hip_status(dism::launch_pad_labels(iq, rows, n, npad, pq, s), what)) ||
+        (st = hip_status(dism::launch_pad_labels(ik, rows, n, npad, pk, s), what)))
+        return st;
+    // combined label order of the padded prompt (the vectors are validated, not read)
+    if ((st = dism_hard_prepare(sk, sk, v, dtype, pq, pk, B, npad, H, R, DV, workspace,
+                                workspace_bytes, stream)))
+        return st;
+    dism::DecodeArgs a = decode_args(state, D, rows, H, R, DV, capacity, slots);
+    a.n = (int)n;
+    a.iq = iq;
+    a.ik = ik;
+    a.reset = reset;
+    a.sk = sk;
+    a.v = v;
+    return hip_status(dism::launch_prime(a, orders(L, workspace), (int)npad, dtype, s), what);
 }
 
 }  // extern "C"

@@ -246,6 +246,149 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_kernel(DecodeArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Parallel prime: the decoder state of a whole prompt (keys only) from the prompt's combined
+// label order (dism_hard_prepare on the prompt, padded past n; entries at positions >= n are
+// skipped).  One wave per (row, top-digit bucket) as in the label scans; for every label
+// group with keys it claims a table slot (atomic CAS of the slot's key count, so groups of
+// one row never collide), takes list blocks from the row's pool (atomic add), writes the key
+// positions in ascending order and folds M over the keys in position order -- the fp32
+// chain of the serial key steps, so the state decodes exactly like a serially primed one.
+// History rows, labels and the last reset are written per position.
+template <typename T, int R, int DV>
+__global__ __launch_bounds__(64 * DEC_WAVES) void prime_kernel(DecodeArgs a, Orders o,
+                                                               int npad) {
+    constexpr int COLS = (DV + 63) / 64;
+    const int lane = lane_id();
+    const long item = (long)blockIdx.x * DEC_WAVES + wave_id();
+    const int bh = (int)(item >> 8), bucket = (int)(item & 255);
+    if (bh >= a.rows) return;
+    const int h = bh % a.H, b = bh / a.H;
+    const long so = (long)bh * npad, cap = a.cap;
+    const int32_t* corder = o.corder + 2 * so;
+    const int32_t* clab = o.clab + 2 * so;
+    const int c0 = o.ctab[(long)bh * 257 + bucket], c1 = o.ctab[(long)bh * 257 + bucket + 1];
+    int32_t* meta = a.meta + (long)bh * 4;
+    int32_t* qlab = a.qlab + bh * cap;
+    int32_t* klab = a.klab + bh * cap;
+    T* skh = reinterpret_cast<T*>(a.skh) + bh * cap * R;
+    T* vh = reinterpret_cast<T*>(a.vh) + bh * cap * DV;
+    int32_t* slot_label = a.slot_label + (long)bh * a.slots;
+    int32_t* slot_cnt = a.slot_cnt + (long)bh * a.slots;
+    int32_t* slot_last = a.slot_last + (long)bh * a.slots;
+    float* Mrow = a.M + (long)bh * a.slots * (R * DV);
+    int32_t* blocks = a.slot_blocks + (long)bh * a.slots * a.bcap;
+    int32_t* pool = a.pool + (long)bh * a.pool_blocks * LIST_BLOCK;
+    const T* sk_in = reinterpret_cast<const T*>(a.sk);
+    const T* v_in = reinterpret_cast<const T*>(a.v);
+    const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    // history and resets, lane-parallel over the bucket's entries
+    for (int x = c0 + lane; x < c1; x += 64) {
+        const int e = corder[x], p = e >> 1;
+        if (p >= a.n) continue;
+        const long lrow = (long)bh * a.n + p, irow = ((long)b * a.n + p) * a.H + h;
+        if (e & 1) {
+            qlab[p] = a.iq[lrow];
+            if (a.reset && a.reset[lrow]) atomicMax(meta + 2, p);
+        } else {
+            klab[p] = a.ik[lrow];
+            for (int r = 0; r < R; ++r) skh[(long)p * R + r] = sk_in[irow * R + r];
+            for (int d = 0; d < DV; ++d) vh[(long)p * DV + d] = v_in[irow * DV + d];
+        }
+    }
+    int rs = __builtin_amdgcn_readfirstlane(c0);
+    const int ce = __builtin_amdgcn_readfirstlane(c1);
+    while (rs < ce) {
+        const uint32_t lbl = (uint32_t)__builtin_amdgcn_readfirstlane(clab[rs]);
+        const int re = __builtin_amdgcn_readfirstlane(
+            (uint32_t)clab[ce - 1] == lbl ? ce : upper_label(clab, rs + 1, ce, lbl));
+        // keys of the group (entries 2p, p < n), in position order
+        int nk = 0;
+        for (int x0 = rs; x0 < re; x0 += 64) {
+            const int x = x0 + lane;
+            const int e = x < re ? corder[x] : 1;
+            nk += __popcll(__ballot(!(e & 1) && (e >> 1) < a.n));
+        }
+        if (nk > 0) {
+            const int32_t label = (int32_t)lbl;
+            int s = -1;
+            if (lane == 0) {  // claim the first free slot on the label's probe sequence
+                const uint32_t mask = (uint32_t)a.slots - 1u, h0 = label_hash(label);
+                for (int t = 0; t < a.slots; ++t) {
+                    const int idx = (int)((h0 + (uint32_t)t) & mask);
+                    if (atomicCAS(slot_cnt + idx, 0, nk) == 0) {
+                        s = idx;
+                        break;
+                    }
+                }
+                if (s < 0) atomicExch(meta + 3, 1);
+            }
+            s = __shfl(s, 0);
+            if (s >= 0) {
+                const int nb = (nk + LIST_BLOCK - 1) / LIST_BLOCK;
+                int base = 0;
+                if (lane == 0) base = atomicAdd(meta + 1, nb);
+                base = __shfl(base, 0);
+                int32_t* sb = blocks + (long)s * a.bcap;
+                for (int t = lane; t < nb; t += 64) sb[t] = base + t;
+                float M[R][COLS];
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int c = 0; c < COLS; ++c) M[r][c] = 0.0f;
+                int kseen = 0, last = 0;
+                for (int x0 = rs; x0 < re; x0 += 64) {
+                    const int x = x0 + lane;
+                    const int e = x < re ? corder[x] : 1;
+                    const bool isk = !(e & 1) && (e >> 1) < a.n;
+                    const unsigned long long km = __ballot(isk);
+                    if (isk) {
+                        const int xi = kseen + __popcll(km & below);
+                        pool[(long)(base + xi / LIST_BLOCK) * LIST_BLOCK + xi % LIST_BLOCK] =
+                            e >> 1;
+                    }
+                    // M over this window's keys, in order
+                    unsigned long long mm = km;
+                    while (mm) {
+                        const int l = __ffsll((long long)mm) - 1;
+                        mm &= mm - 1;
+                        const int p = readlane_i(e, l) >> 1;
+                        const long irow = ((long)b * a.n + p) * a.H + h;
+                        float skr[R];
+#pragma unroll
+                        for (int r = 0; r < R; ++r) skr[r] = load_elem<T>(sk_in, irow * R + r);
+#pragma unroll
+                        for (int c = 0; c < COLS; ++c) {
+                            const int d = lane + 64 * c;
+                            const float vd = d < DV ? load_elem<T>(v_in, irow * DV + d) : 0.0f;
+#pragma unroll
+                            for (int r = 0; r < R; ++r)
+                                M[r][c] = __builtin_fmaf(skr[r], vd, M[r][c]);
+                        }
+                        last = p;
+                    }
+                    kseen += __popcll(km);
+                }
+                float* Ms = Mrow + (long)s * (R * DV);
+#pragma unroll
+                for (int c = 0; c < COLS; ++c) {
+                    const int d = lane + 64 * c;
+                    if (d < DV) {
+#pragma unroll
+                        for (int r = 0; r < R; ++r) Ms[r * DV + d] = M[r][c];
+                    }
+                }
+                if (lane == 0) {
+                    slot_label[s] = label;
+                    slot_last[s] = last;
+                }
+            }
+        }
+        rs = re;
+    }
+    if (item == (long)bh * 256 && lane == 0) meta[0] = a.n;  // one writer per row
+}
+
 template <typename T, int R>
 static hipError_t decode_dv(const DecodeArgs& a, hipStream_t s) {
     const unsigned grid = (unsigned)((a.rows + DEC_WAVES - 1) / DEC_WAVES);
@@ -271,10 +414,65 @@ static hipError_t decode_r(const DecodeArgs& a, hipStream_t s) {
     }
 }
 
+template <typename T, int R>
+static hipError_t prime_dv(const DecodeArgs& a, const Orders& o, int npad, hipStream_t s) {
+    const unsigned grid = (unsigned)((256L * a.rows + DEC_WAVES - 1) / DEC_WAVES);
+    const dim3 block(64 * DEC_WAVES);
+    switch (a.DV) {
+        case 32:
+            hipLaunchKernelGGL((prime_kernel<T, R, 32>), dim3(grid), block, 0, s, a, o, npad);
+            break;
+        case 64:
+            hipLaunchKernelGGL((prime_kernel<T, R, 64>), dim3(grid), block, 0, s, a, o, npad);
+            break;
+        case 128:
+            hipLaunchKernelGGL((prime_kernel<T, R, 128>), dim3(grid), block, 0, s, a, o, npad);
+            break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t prime_r(const DecodeArgs& a, const Orders& o, int npad, hipStream_t s) {
+    switch (a.R) {
+        case 2: return prime_dv<T, 2>(a, o, npad, s);
+        case 4: return prime_dv<T, 4>(a, o, npad, s);
+        case 8: return prime_dv<T, 8>(a, o, npad, s);
+        case 16: return prime_dv<T, 16>(a, o, npad, s);
+        case 32: return prime_dv<T, 32>(a, o, npad, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_prime(const DecodeArgs& a, const Orders& o, int npad, int dtype,
+                        hipStream_t s) {
+    if (dtype == DTYPE_BF16) return prime_r<bf16_t>(a, o, npad, s);
+    if (dtype == DTYPE_F32) return prime_r<float>(a, o, npad, s);
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_decode(const DecodeArgs& a, int dtype, hipStream_t s) {
     if (dtype == DTYPE_BF16) return decode_r<bf16_t>(a, s);
     if (dtype == DTYPE_F32) return decode_r<float>(a, s);
     return hipErrorInvalidValue;
+}
+
+// rows of n labels -> rows of npad labels (0 past n)
+__global__ __launch_bounds__(256) void pad_labels_kernel(const int32_t* __restrict__ src,
+                                                         long rows, long n, long npad,
+                                                         int32_t* __restrict__ dst) {
+    const long x = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= rows * npad) return;
+    const long r = x / npad, p = x - r * npad;
+    dst[x] = p < n ? src[r * n + p] : 0;
+}
+
+hipError_t launch_pad_labels(const int32_t* src, long rows, long n, long npad, int32_t* dst,
+                             hipStream_t s) {
+    hipLaunchKernelGGL(pad_labels_kernel, dim3((unsigned)((rows * npad + 255) / 256)), dim3(256),
+                       0, s, src, rows, n, npad, dst);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------------------

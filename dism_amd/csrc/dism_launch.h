@@ -151,6 +151,11 @@ struct DecodeArgs {
 };
 
 hipError_t launch_decode(const DecodeArgs& a, int dtype, hipStream_t s);
+hipError_t launch_pad_labels(const int32_t* src, long rows, long n, long npad, int32_t* dst,
+                             hipStream_t s);
+// keys-only state of a whole prompt of a.n tokens from its combined label order (rows of npad)
+hipError_t launch_prime(const DecodeArgs& a, const Orders& o, int npad, int dtype,
+                        hipStream_t s);
 hipError_t launch_reset_starts(const uint8_t* reset, long rows, long n, int32_t* wlo,
                                hipStream_t s);
 

@@ -265,12 +265,29 @@ class HardDismDecoder:
         return out
 
     @torch.no_grad()
-    def prime(self, idx_q, idx_k, sk, v, *, reset=None):
-        """Initialize from a complete prefill history; compute outputs separately."""
+    def prime(self, idx_q, idx_k, sk, v, *, reset=None, serial=False):
+        """Initialize from a complete prefill history; compute outputs separately.  The state
+        is built in parallel over (row, label) (dism_decoder_prime); serial=True appends the
+        prompt's keys one token at a time instead (the same state, for tests)."""
         if self.position:
             raise ValueError("prime requires empty cache")
         n, iq, ik, rs = self._prepare(idx_q, idx_k, sk, v, reset)
-        self._step(n, iq, ik, rs, None, sk.contiguous(), v.contiguous(), None, None)
+        if serial:
+            self._step(n, iq, ik, rs, None, sk.contiguous(), v.contiguous(), None, None)
+            return
+        sk, v = sk.contiguous(), v.contiguous()
+        nbytes = _lib.size("dism_decoder_prime_workspace_bytes", self.batch, n, self.heads,
+                           self.r, self.dv, self._code)
+        ws = torch.empty((nbytes,), dtype=torch.uint8, device=self.device)
+        with torch.cuda.device(self.device):
+            _lib.call("dism_decoder_prime", self.state.data_ptr(), self.state.numel(),
+                      self.batch, self.heads, self.r, self.dv, self.capacity, self.slots,
+                      self._code, n, iq.data_ptr(), ik.data_ptr(),
+                      0 if rs is None else rs.data_ptr(), sk.data_ptr(), v.data_ptr(),
+                      ws.data_ptr(), nbytes, _stream(self.device))
+        self.position += n
+        if self.check_errors:
+            self._check()
 
     def memory_stats(self):
         meta = self.state[:self.rows * 16].view(torch.int32).view(self.rows, 4).cpu()

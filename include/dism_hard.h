@@ -275,6 +275,22 @@ int32_t dism_decoder_step(void* state, int64_t state_bytes, int64_t B, int64_t H
                           const void* sq, const void* sk, const void* v, const float* lut,
                           int64_t lut_stride, float* out, float* lse2, void* stream);
 
+/* Workspace bytes of dism_decoder_prime for an n-token prompt (-1 for unsupported sizes). */
+int64_t dism_decoder_prime_workspace_bytes(int64_t B, int64_t n, int64_t H, int32_t R,
+                                           int32_t DV, int32_t dtype);
+
+/* Primes a freshly initialised decoder state with an n-token prompt (keys only) in parallel:
+ * the prompt's combined label order (dism_hard_prepare, rows padded to 256), then one wave per
+ * (row, label bucket) builds each label's running matrix, count, last key and position list
+ * with the same fp32 sequence as n single-token key steps, so decoding from it gives the
+ * same outputs bit for bit.  Inputs as dism_decoder_step (no sq).  Replaces
+ * HardDismDecoder.prime (dism_v3/python/flash_dism/inference/api.py:87-95). */
+int32_t dism_decoder_prime(void* state, int64_t state_bytes, int64_t B, int64_t H, int32_t R,
+                           int32_t DV, int64_t capacity, int32_t slots, int32_t dtype, int64_t n,
+                           const int32_t* iq, const int32_t* ik, const uint8_t* reset,
+                           const void* sk, const void* v, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

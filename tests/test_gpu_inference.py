@@ -162,3 +162,34 @@ def test_decoder_validation_and_overflow():
             engine(iq.long(), ik, sq, sk, v, TAU)
     with pytest.raises(ValueError, match="chunk_size"):
         HardDismPrefill(chunk_size=7)
+
+
+@pytest.mark.parametrize("pattern", ["random", "repeat", "wide"])
+def test_parallel_prime_equals_serial_prime(pattern):
+    """The parallel prime (label order -> per-label running matrices and key lists) decodes
+    exactly like the token-by-token key steps: odd prompt length, a query reset inside the
+    prompt, labels spanning the int32 range ('wide', where padding label 0 is also real)."""
+    from dism_amd.inference import HardDismDecoder
+    b, h, n, r, dv, start = 2, 3, 700, 8, 64, 333
+    rng = np.random.default_rng(21)
+    if pattern == "wide":
+        pool = np.array([np.iinfo(np.int32).min, -7, 0, 5, np.iinfo(np.int32).max], np.int32)
+        iq, ik = (pool[rng.integers(0, 5, (b, h, n))] for _ in range(2))
+    else:
+        iq, ik, *_ = sam_inputs(pattern, b=b, h=h, n=n, alphabet=16)
+    sq, sk, v = (oracle.bf16_round(rng.standard_normal((b, n, h, c)) * 0.3) for c in (r, r, dv))
+    reset = np.zeros((b, h, n), dtype=bool)
+    reset[..., 100] = True
+    tau = np.array([0.5, 0.0, 1.5], dtype=np.float32)
+    want, _ = cpu_model(iq, ik, sq, sk, v, tau, reset)
+    t = to_dev(iq, ik, sq, sk, v)
+    rs = dev(reset)
+    outs = []
+    for serial in (False, True):
+        dec = HardDismDecoder(b, h, r, dv, n, list(tau), label_slots=64)
+        dec.prime(t[0][..., :start], t[1][..., :start], t[3][:, :start], t[4][:, :start],
+                  reset=rs[..., :start], serial=serial)
+        outs.append(dec.append(t[0][..., start:], t[1][..., start:], t[2][:, start:],
+                               t[3][:, start:], t[4][:, start:], reset=rs[..., start:]))
+    assert torch.equal(outs[0], outs[1])
+    assert_bits(host(outs[0]), want[:, start:], "decode after parallel prime")
