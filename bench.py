@@ -318,11 +318,14 @@ def bench_decode(args):
         dec.prime(piq, pik, psk2, pv2)
     prime_ms = _time(fresh_prime, args.steps, args.warmup)  # includes the state's zero fill
     torch.cuda.synchronize()
+    # per-token inputs as a model step produces them (fresh contiguous tensors)
+    toks = [tuple(x[..., t:t + 1].contiguous() if x.dim() == 3 else x[:, t:t + 1].contiguous()
+                  for x in (iq, ik, sq, sk, v)) for t in range(P, P + G)]
+    torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
-    for t in range(P, P + G):
-        dec.append(iq[..., t:t + 1], ik[..., t:t + 1], sq[:, t:t + 1], sk[:, t:t + 1],
-                   v[:, t:t + 1])
+    for tk in toks:
+        dec.append(*tk)
     e.record()
     torch.cuda.synchronize()
     step_ms = s.elapsed_time(e) / G
