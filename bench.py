@@ -4,7 +4,8 @@ A step is one training pass of the hard DISM op over one synthetic batch of the 
 configuration (B=4, H=16, T=16384, d_qk=8, d_v=64, bf16, periodic
 component on 25% of the heads):
     labels (sign binarizer, q and k) -> log2 weight table -> [carry boundary, off by default]
-    -> prepare (position orders, bigram-pair plans) -> readout -> dlog table
+    -> forward (position orders and bigram-pair plans, the bigram half on a side stream
+    overlapping the length-1 label scan; then the pair corrections) -> dlog table
     -> row pairs -> query-row scan (dSQ, tau terms) -> tau reduction, with the key scan (dV,
     dSK) -> key pairs chain on a side stream (--streams 2, the default; joined each step).
 Inputs are resident in HBM before timing.  Prints ONE JSON line.  The timed region records
@@ -105,8 +106,11 @@ def main():
     dvv = torch.empty((B, T, H, DV), dtype=torch.float32, device=dev)
     rowtau = torch.empty((B, H, T), dtype=torch.float32, device=dev)
     dtau = torch.empty((H,), dtype=torch.float32, device=dev)
-    names = ["labels", "lut", "carry", "prepare", "readout", "dlut", "row_pairs", "queries",
-             "keys", "key_pairs", "tau_reduce"]
+    # with a side stream the forward is one call (dism_hard_forward: the bigram half of the
+    # prepare overlaps the length-1 label scan); else prepare and readout run as two stages
+    fused = args.streams == 2
+    names = ["labels", "lut", "carry"] + (["forward"] if fused else ["prepare", "readout"]) + \
+        ["dlut", "row_pairs", "queries", "keys", "key_pairs", "tau_reduce"]
     side = torch.cuda.Stream(device=dev) if args.streams == 2 else None
     fork, join = torch.cuda.Event(), torch.cuda.Event()
     out = torch.empty((B, T, H, DV), dtype=torch.bfloat16, device=dev)
@@ -135,15 +139,20 @@ def main():
             if strip > 0 else None
         cp = 0 if carry is None else carry.data_ptr()
         mark("carry", 1)
-        mark("prepare", 0)
         vec = (tq.data_ptr(), tk.data_ptr(), tv.data_ptr())
-        _lib.call("dism_hard_prepare", *vec, code, qp, kp, B, T, H, D, DV, W, nbytes, S)
-        mark("prepare", 1)
-        mark("readout", 0)
-        _lib.call("dism_hard_readout", *vec, code, qp, kp, hp, cp, strip, lut.data_ptr(),
-                  n + 1, B, T, H, D, DV, W, nbytes, out.data_ptr(), code, lse2.data_ptr(), 0, 0,
-                  S)
-        mark("readout", 1)
+        rd = (*vec, code, qp, kp, hp, cp, strip, lut.data_ptr(), n + 1, B, T, H, D, DV, W,
+              nbytes, out.data_ptr(), code, lse2.data_ptr(), 0, 0, S)
+        if fused:
+            mark("forward", 0)
+            _lib.call("dism_hard_forward", *rd)
+            mark("forward", 1)
+        else:
+            mark("prepare", 0)
+            _lib.call("dism_hard_prepare", *vec, code, qp, kp, B, T, H, D, DV, W, nbytes, S)
+            mark("prepare", 1)
+            mark("readout", 0)
+            _lib.call("dism_hard_readout", *rd)
+            mark("readout", 1)
         bw = (*vec, tdo.data_ptr(), code, qp, kp, hp, cp, strip, lut.data_ptr())
         if side is not None:
             fork.record(stream)  # the forward's outputs are ready

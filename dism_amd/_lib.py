@@ -21,6 +21,8 @@ SIGNATURES = {
     "dism_hard_prepare": [_P, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _I32, _I32, _P, _I64, _P],
     "dism_hard_readout": [_P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _I64, _I64, _I64, _I64,
                           _I32, _I32, _P, _I64, _P, _I32, _P, _P, _P, _P],
+    "dism_hard_forward": [_P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _I64, _I64, _I64, _I64,
+                          _I32, _I32, _P, _I64, _P, _I32, _P, _P, _P, _P],
     "dism_hard_backward": [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _P, _I64, _P, _I64,
                            _I64, _I64, _I32, _I32, _P, _I64, _P, _P, _P, _P, _P, _P],
     "dism_hard_backward_row_pairs": [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _P, _I64,

@@ -198,7 +198,7 @@ int32_t check_common(const void* sq, const void* sk, const void* v, int32_t dtyp
 extern "C" {
 
 const char* dism_last_error(void) { return g_error.c_str(); }
-int32_t dism_abi_version(void) { return 4; }
+int32_t dism_abi_version(void) { return 5; }
 
 int32_t dism_sign_labels(const void* x, int32_t dtype, int64_t B, int64_t N, int64_t H, int32_t d,
                          int32_t* labels, void* stream) {
@@ -321,6 +321,73 @@ int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t
         return st2;
     return hip_status(dism::launch_pairs_finish(a, R, DV, dtype, S(stream)),
                       "hard readout pairs");
+}
+
+int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t dtype,
+                          const int32_t* iq, const int32_t* ik, const uint8_t* hard,
+                          const int32_t* boundary, int32_t strip, const float* lut,
+                          int64_t lut_stride, int64_t B, int64_t N, int64_t H, int32_t R,
+                          int32_t DV, void* workspace, int64_t workspace_bytes, void* out,
+                          int32_t out_dtype, float* lse2, int32_t* lmax, int32_t* jarg,
+                          void* stream) {
+    int32_t st = check_common(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
+                              workspace_bytes, "hard forward");
+    if (st) return st;
+    if (!hard || !lut || !out || !lse2) return fail(DISM_ERR_INVALID, "hard forward: null pointer");
+    if (!dtype_ok(out_dtype))
+        return fail(DISM_ERR_UNSUPPORTED, "hard forward: output dtype must be bf16 or f32");
+    if (lut_stride < N + 1) return fail(DISM_ERR_INVALID, "hard log-weight table is too short");
+    if (boundary && strip < 1) return fail(DISM_ERR_INVALID, "invalid hard boundary strip");
+    if (!aligned16(out)) return fail(DISM_ERR_INVALID, "hard forward: output must be 16-byte aligned");
+    const Layout L = layout(B, N, H, R, DV);
+    dism::SortArgs sa{};
+    sa.lab[0] = iq;
+    sa.lab[1] = ik;
+    sa.BH = B * H;
+    sa.n = (int)N;
+    for (int t = 0; t < 3; ++t) sa.tmp[t] = at<int32_t>(workspace, L.tmp[t]);
+    sa.o = orders(L, workspace);
+    sa.pnb = at<int32_t>(workspace, L.pnb);
+    dism::PathArgs a = path(L, workspace, B, N, H, iq, ik, hard, boundary, strip, lut, lut_stride);
+    a.sq = sq;
+    a.sk = sk;
+    a.v = v;
+    a.out = out;
+    a.out_dtype = out_dtype;
+    a.lse2 = lse2;
+    a.lmax = lmax;
+    a.jarg = jarg;
+    // The label order (what the length-1 scan needs) and the bigram half of the prepare (what
+    // only the pair kernels need) are independent: the bigram half runs on a side stream while
+    // the scan takes the rows prepared in LDS, counting their bigram partners itself (phase
+    // 1); after the join the scan takes the remaining rows from the plan's counts (phase 2),
+    // then the pair kernels run.  Without a side stream the same launches run in order.
+    SideStream* side = side_stream();
+    const hipStream_t s = S(stream);
+    hipStream_t ps = s;
+    if (side) {
+        if (hipEventRecord(side->fork, s) != hipSuccess ||
+            hipStreamWaitEvent(side->stream, side->fork, 0) != hipSuccess)
+            side = nullptr;
+        else
+            ps = side->stream;
+    }
+    hipError_t e = dism::launch_prepare_labels(sa, a, s);
+    if (e == hipSuccess) e = dism::launch_prepare_pairs(sa, a, ps);
+    if (e == hipSuccess) {
+        a.fwd_phase = 1;
+        e = dism::launch_scan_forward(a, R, DV, dtype, s);
+    }
+    bool joined = true;
+    if (side)  // join even after an error, so the caller's stream never runs ahead
+        joined = hipEventRecord(side->join, side->stream) == hipSuccess &&
+                 hipStreamWaitEvent(s, side->join, 0) == hipSuccess;
+    if ((st = hip_status(e, "hard forward"))) return st;
+    if (!joined) return fail(DISM_ERR_HIP, "hard forward: stream join failed");
+    a.fwd_phase = 2;
+    if ((st = hip_status(dism::launch_scan_forward(a, R, DV, dtype, s), "hard forward")))
+        return st;
+    return hip_status(dism::launch_pairs_finish(a, R, DV, dtype, s), "hard forward pairs");
 }
 
 }  // extern "C"

@@ -56,6 +56,7 @@ struct SortArgs {
     int32_t* tmp[3];        // scratch: [B*H*2N] combined, [B*H*N] per bigram side
     int32_t* pnb;           // [B*H*N] bigram pair count per query row (LDS-resident prepare)
     Orders o;
+    int role_base;          // first role of a launch (blockIdx.y + role_base)
 };
 
 // Per query row record (prow, valid when the row's bigram pair count pnb > 0):
@@ -98,6 +99,10 @@ struct PathArgs {
     // query resets (inference prefill): per query the last reset position at or before it;
     // walks from that query stop there.  [B*H*N] or null.
     const int32_t* wlo;
+    // forward label scan: 0 = every row, pair counts from pnb; 1 = rows prepared in LDS
+    // (mode 1) with the pair counts computed in the scan (the plan may still be running on
+    // another stream); 2 = the remaining rows (mode 0), from pnb
+    int fwd_phase;
 };
 
 // Outputs a packed call zeroes on soft training rows (null pointers are skipped).
@@ -184,11 +189,15 @@ hipError_t launch_packed_soft_zero(const PackedZero& z, hipStream_t s);
 // Position orders and bigram-pair plans of a prepare call: the LDS-resident kernel for the
 // rows it can take, the global-memory sort and plan for the others, then the owner lists.
 hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s);
-hipError_t launch_sort(const SortArgs& a, hipStream_t s);
+// the two independent halves of launch_prepare: the combined label order (what the label
+// scans need) and the bigram orders, pair plans and owner lists (what the pair kernels need)
+hipError_t launch_prepare_labels(const SortArgs& sa, const PathArgs& pa, hipStream_t s);
+hipError_t launch_prepare_pairs(const SortArgs& sa, const PathArgs& pa, hipStream_t s);
+hipError_t launch_sort(const SortArgs& a, int role0, int roles, hipStream_t s);
 // only the combined label order (corder, clab, ctab) of every row, global-memory path (the
 // rows' mode must be 0)
 hipError_t launch_sort_labels(const SortArgs& a, hipStream_t s);
-hipError_t launch_prepare_lds(const SortArgs& a, hipStream_t s);
+hipError_t launch_prepare_lds(const SortArgs& a, int role0, int roles, hipStream_t s);
 // The following return hipErrorInvalidValue for an unsupported (R, DV, dtype).
 hipError_t launch_pair_plan(const PathArgs& a, hipStream_t s);
 hipError_t launch_owner_lists(const PathArgs& a, hipStream_t s);

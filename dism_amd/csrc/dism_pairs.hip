@@ -219,12 +219,32 @@ hipError_t launch_owner_lists(const PathArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
-    hipError_t e;
-    if (pa.n <= PREP_N && !pa.dstart) e = launch_prepare_lds(sa, s);
-    else e = launch_fill_i32(sa.o.mode, sa.BH, 0, s);
+// The rows the LDS-resident kernel can take (N <= PREP_N, unpacked) run role 0 / role 1 of
+// prepare_lds_kernel; the global-memory sort takes the others (its roles 0 / 1-2).  Both
+// halves write the same row modes, so they may run on different streams.
+static bool lds_rows(const PathArgs& pa) { return pa.n <= PREP_N && !pa.dstart; }
+
+hipError_t launch_prepare_labels(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
+    hipError_t e = lds_rows(pa) ? launch_prepare_lds(sa, 0, 1, s)
+                                : launch_fill_i32(sa.o.mode, sa.BH, 0, s);
     if (e != hipSuccess) return e;
-    if ((e = launch_sort(sa, s)) != hipSuccess) return e;
+    return launch_sort(sa, 0, 1, s);
+}
+
+hipError_t launch_prepare_pairs(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
+    hipError_t e = lds_rows(pa) ? launch_prepare_lds(sa, 1, 1, s)
+                                : launch_fill_i32(sa.o.mode, sa.BH, 0, s);
+    if (e != hipSuccess) return e;
+    if ((e = launch_sort(sa, 1, 2, s)) != hipSuccess) return e;
+    if ((e = launch_pair_plan(pa, s)) != hipSuccess) return e;
+    return launch_owner_lists(pa, s);
+}
+
+hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
+    hipError_t e = lds_rows(pa) ? launch_prepare_lds(sa, 0, 2, s)
+                                : launch_fill_i32(sa.o.mode, sa.BH, 0, s);
+    if (e != hipSuccess) return e;
+    if ((e = launch_sort(sa, 0, 3, s)) != hipSuccess) return e;
     if ((e = launch_pair_plan(pa, s)) != hipSuccess) return e;
     return launch_owner_lists(pa, s);
 }

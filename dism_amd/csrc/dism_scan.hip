@@ -120,8 +120,18 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
     auto& s_r = s_r_all[wave_id()];
     __shared__ int s_slot_all[WAVES][WIN];
     auto& s_slot = s_slot_all[wave_id()];
+    // predecessor-label histogram of the current label group's keys, two 16-bit counts per
+    // word (one-byte labels), for the pair counts computed here (fwd_phase 1)
+    __shared__ uint32_t s_h_all[WAVES][128];
+    uint32_t* s_h = s_h_all[wave_id()];
     Item it;
     if (!scan_item(a, it)) return;
+    // fwd_phase 1: rows prepared in LDS (one-byte labels), pair counts from the histogram;
+    // 2: the other rows, pair counts from the plan (pnb); 0: every row from pnb
+    const int mode = a.fwd_phase ? a.o.mode[it.bh] : 0;
+    if ((a.fwd_phase == 1 && !mode) || (a.fwd_phase == 2 && mode)) return;
+    const bool hist_nb = a.fwd_phase == 1;
+    const int lshift = hist_nb ? a.o.shift[it.bh] : 0;
     const int lane = lane_id();
     const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
     const int32_t* corder = a.o.corder + 2 * it.so;
@@ -165,12 +175,17 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
         wk.begin(rs, re);
         // per-lane data of window k+1 (issued one window ahead) and of window k
         uint32_t wN[W];
-        int nbN = 0;
+        int nbN = 0;  // pair count of the query row, or the predecessor's label byte (-1: none)
         auto issue = [&](int kk, int ent) {  // readout words, pair count, key rows -> s_v
             const int p = ent >> 1;
             const bool isq = ent & 1;
             load_words<W>((isq ? sq : sk) + (it.row0 + (long)p * a.H) * R, wN);
-            nbN = isq ? a.pnb[it.so + p] : 0;
+            if (hist_nb)
+                nbN = p >= 1 ? (int)(((uint32_t)(isq ? a.iq : a.ik)[it.so + p - 1] >> lshift) &
+                                     255u)
+                             : -1;
+            else
+                nbN = isq ? a.pnb[it.so + p] : 0;
             const bool ok = lane < wk.count(kk);
             const unsigned long long km = __ballot(ok && !isq);
             const int nk = __popcll(km);
@@ -195,6 +210,10 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
 #pragma unroll
             for (int c = 0; c < COLS; ++c) M[r][c] = 0.0f;
         int carry_cnt = 0, carry_last = -1;
+        if (hist_nb) {
+            for (int x = lane; x < 128; x += 64) s_h[x] = 0u;
+            asm volatile("" ::: "memory");
+        }
         do {
             const int kk = wk.k, wn = __builtin_amdgcn_readfirstlane(wk.count(kk));
             // ---- lane-parallel: entry kind, key counts, row statistics, fp32 readout rows
@@ -215,7 +234,26 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
                     for (int r = 0; r < R; ++r) s_r[lane][r] = rr[r];
                 }
             }
-            const int nb = nbC;
+            int nb = nbC;
+            if (hist_nb) {
+                // bigram partners of a query: the group's keys before it (j >= 1) whose
+                // predecessor label equals the query's -- earlier windows from the histogram,
+                // this window's from the lanes before it; then this window's keys join the
+                // histogram
+                const int pl = nbC;
+                int c = 0;
+                if (isq && pl >= 0) c = (int)((s_h[pl >> 1] >> (16 * (pl & 1))) & 0xffffu);
+                unsigned long long kv = __ballot(ok && !isq && pl >= 0);
+                while (kv) {
+                    const int l = __ffsll((long long)kv) - 1;
+                    kv &= kv - 1;
+                    if (isq && l < lane && pl == readlane_i(pl, l)) ++c;
+                }
+                nb = isq ? c : 0;
+                asm volatile("" ::: "memory");
+                if (ok && !isq && pl >= 0) atomicAdd(&s_h[pl >> 1], 1u << (16 * (pl & 1)));
+                asm volatile("" ::: "memory");
+            }
             const float m = (cnt > 0 && lut1 > 0.0f) ? lut1 : 0.0f;
             const float p1 = exp2_fp32(lut1 - m);
             const float den = exp2_fp32(-m) + (float)cnt * p1;

@@ -219,7 +219,7 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_kernel(SortArgs a) {
     __shared__ int wcnt[SORT_WAVES][RADIX];
     __shared__ int scan[RADIX];
     __shared__ uint32_t mask;
-    const int bh = blockIdx.x, role = blockIdx.y, n = a.n, tid = threadIdx.x;
+    const int bh = blockIdx.x, role = (int)blockIdx.y + a.role_base, n = a.n, tid = threadIdx.x;
     if (a.o.mode[bh]) return;  // prepared by prepare_lds_kernel
     const long off = (long)bh * n;
     const int32_t* __restrict__ lq = a.lab[0] + off;
@@ -248,8 +248,10 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_kernel(SortArgs a) {
     int digits[4], nd = 0;
     for (int d = 0; d < 4; ++d)
         if ((used >> (8 * d)) & 255u) digits[nd++] = d;
-    if (tid == 0 && role == 0) a.o.shift[bh] = nd ? 8 * digits[nd - 1] : 0;
-    if (role == 0 && tid < 8) a.o.bhcount[tid >> 2][(long)bh * 4 + (tid & 3)] = 0;  // plan appends
+    // every role writes the same shift (the roles may run on different streams); role 1
+    // clears the plan's per-row class counts (the plan appends to them after roles 1 and 2)
+    if (tid == 0) a.o.shift[bh] = nd ? 8 * digits[nd - 1] : 0;
+    if (role == 1 && tid < 8) a.o.bhcount[tid >> 2][(long)bh * 4 + (tid & 3)] = 0;
 
     if (role == 0) {
         // ---- combined label order of the 2N entries
@@ -471,7 +473,7 @@ __global__ __launch_bounds__(SORT_THREADS) void prepare_lds_kernel(SortArgs a) {
     auto s_mask = reinterpret_cast<unsigned long long (*)[RADIX]>(pool + DIG_BYTES);
     uint16_t* s_cnt = reinterpret_cast<uint16_t*>(pool);  // after the sorts
     auto pad = [](int c) { return c + (c >> 5); };
-    const int bh = blockIdx.x, role = blockIdx.y, n = a.n, tid = threadIdx.x;
+    const int bh = blockIdx.x, role = (int)blockIdx.y + a.role_base, n = a.n, tid = threadIdx.x;
     const int n2 = 2 * n;
     const long off = (long)bh * n;
     const int32_t* __restrict__ lq = a.lab[0] + off;
@@ -493,7 +495,7 @@ __global__ __launch_bounds__(SORT_THREADS) void prepare_lds_kernel(SortArgs a) {
             dg = d;
         }
     const bool lds_ok = nd == 1;
-    if (role == 0 && tid == 0) {
+    if (tid == 0) {  // both roles write the same values (they may run on different streams)
         a.o.mode[bh] = lds_ok ? 1 : 0;
         if (lds_ok) a.o.shift[bh] = 8 * dg;
     }
@@ -676,19 +678,22 @@ __global__ __launch_bounds__(SORT_THREADS) void prepare_lds_kernel(SortArgs a) {
     for (int p = tid; p < n; p += SORT_THREADS) a.pnb[off + p] = 0;
 }
 
-hipError_t launch_prepare_lds(const SortArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(prepare_lds_kernel, dim3((unsigned)a.BH, 2), dim3(SORT_THREADS), 0, s, a);
+hipError_t launch_prepare_lds(const SortArgs& a, int role0, int roles, hipStream_t s) {
+    SortArgs b = a;
+    b.role_base = role0;
+    hipLaunchKernelGGL(prepare_lds_kernel, dim3((unsigned)a.BH, (unsigned)roles),
+                       dim3(SORT_THREADS), 0, s, b);
     return hipGetLastError();
 }
 
-hipError_t launch_sort(const SortArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(sort_kernel, dim3((unsigned)a.BH, 3), dim3(SORT_THREADS), 0, s, a);
+hipError_t launch_sort(const SortArgs& a, int role0, int roles, hipStream_t s) {
+    SortArgs b = a;
+    b.role_base = role0;
+    hipLaunchKernelGGL(sort_kernel, dim3((unsigned)a.BH, (unsigned)roles), dim3(SORT_THREADS), 0,
+                       s, b);
     return hipGetLastError();
 }
 
-hipError_t launch_sort_labels(const SortArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(sort_kernel, dim3((unsigned)a.BH, 1), dim3(SORT_THREADS), 0, s, a);
-    return hipGetLastError();
-}
+hipError_t launch_sort_labels(const SortArgs& a, hipStream_t s) { return launch_sort(a, 0, 1, s); }
 
 }  // namespace dism

@@ -88,8 +88,11 @@ def _readout(sq, sk, v, idx_q, idx_k, hard, boundary, strip, log_weights, out_dt
     if boundary is not None:
         check_tensor(boundary, torch.int32, (b, h, (n - 1) // strip, n), "hard boundary",
                      sq.device)
-    if workspace is None:
-        workspace = prepare_workspace(sq, sk, v, idx_q, idx_k)
+    entry = "dism_hard_readout"
+    if workspace is None:  # prepare and read out in one call (the prepare's halves overlap)
+        nbytes = _lib.workspace_bytes(b, n, h, r, dv, DTYPE_CODE[dt])
+        workspace = torch.empty((nbytes,), dtype=torch.uint8, device=sq.device)
+        entry = "dism_hard_forward"
     out = torch.empty((b, n, h, dv), dtype=out_dtype, device=sq.device)
     lse2 = torch.empty((b, h, n), dtype=torch.float32, device=sq.device)
     lmax = jarg = None
@@ -98,7 +101,7 @@ def _readout(sq, sk, v, idx_q, idx_k, hard, boundary, strip, log_weights, out_dt
         jarg = torch.empty((b, h, n), dtype=torch.int32, device=sq.device)
     ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
     with torch.cuda.device(sq.device):
-        _lib.call("dism_hard_readout", sq.data_ptr(), sk.data_ptr(), v.data_ptr(),
+        _lib.call(entry, sq.data_ptr(), sk.data_ptr(), v.data_ptr(),
                   DTYPE_CODE[dt], idx_q.data_ptr(), idx_k.data_ptr(), hard.data_ptr(),
                   ptr(boundary), strip if boundary is not None else 0, log_weights.data_ptr(),
                   log_weights.shape[1], b, n, h, r, dv, workspace.data_ptr(),

@@ -123,6 +123,21 @@ int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t
                           int32_t out_dtype, float* lse2, int32_t* lmax, int32_t* jarg,
                           void* stream);
 
+/* dism_hard_prepare followed by dism_hard_readout, in one call with the same arguments as
+ * dism_hard_readout (the workspace need not be prepared; it is on return, for the backward).
+ * The bigram half of the preparation runs on the calling thread's side stream (see
+ * dism_hard_backward), overlapped with the length-1 label scan, and is joined back into
+ * `stream` before the pair kernels.  Outputs are bit-identical to the two-call sequence.
+ * Replaces the forward_hard chain summary -> chunk -> readout
+ * (dism_v3/python/flash_dism/hard_forward.py:36-47). */
+int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t dtype,
+                          const int32_t* iq, const int32_t* ik, const uint8_t* hard,
+                          const int32_t* boundary, int32_t strip, const float* lut,
+                          int64_t lut_stride, int64_t B, int64_t N, int64_t H, int32_t R,
+                          int32_t DV, void* workspace, int64_t workspace_bytes, void* out,
+                          int32_t out_dtype, float* lse2, int32_t* lmax, int32_t* jarg,
+                          void* stream);
+
 /* Hard backward on a workspace prepared by dism_hard_prepare for the same labels: dsq, dsk
  * [B,N,H,R], dv [B,N,H,DV], rowtau [B,H,N] (caller-owned scratch) and dtau [H], all fp32,
  * deterministic (no floating-point atomics).  lse2 is the forward's log2 normalizer;
