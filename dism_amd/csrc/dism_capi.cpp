@@ -669,7 +669,6 @@ int32_t dism_hard_packed_prepare(const void* sq, const void* sk, const void* v, 
     if ((st = hip_status(dism::launch_packed_docs(cu_seqlens, (int)docs, H, N,
                                                   at<int32_t>(workspace, P.dstart), dindex,
                                                   at<uint8_t>(workspace, P.ones), s), what)) ||
-        (st = hip_status(dism::launch_fill_i32(raw.o.mode, H, 0, s), what)) ||
         (st = hip_status(dism::launch_sort_labels(raw, s), what)) ||
         (st = hip_status(dism::launch_packed_tags(raw.o.corder, raw.o.clab, dindex, (int)docs, H,
                                                   N, tq, tk, s), what)))

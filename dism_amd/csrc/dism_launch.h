@@ -57,6 +57,7 @@ struct SortArgs {
     int32_t* pnb;           // [B*H*N] bigram pair count per query row (LDS-resident prepare)
     Orders o;
     int role_base;          // first role of a launch (blockIdx.y + role_base)
+    int lds_rows;           // rows with one label byte go to prepare_lds_kernel (sort skips them)
 };
 
 // Per query row record (prow, valid when the row's bigram pair count pnb > 0):

@@ -219,32 +219,43 @@ hipError_t launch_owner_lists(const PathArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// The rows the LDS-resident kernel can take (N <= PREP_N, unpacked) run role 0 / role 1 of
-// prepare_lds_kernel; the global-memory sort takes the others (its roles 0 / 1-2).  Both
-// halves write the same row modes, so they may run on different streams.
+// The rows the LDS-resident kernel can take (N <= PREP_N, unpacked, one label byte) run role
+// 0 / role 1 of prepare_lds_kernel; the global-memory sort takes the others (its roles 0 /
+// 1-2), deciding which from the labels as prepare_lds_kernel does.  Every kernel that decides
+// writes the same row modes, so the halves may run on different streams.  The bigram half
+// starts with its short kernels (sort and plan exit early on one-byte rows), so that on a
+// busy device the long LDS kernel is the last to wait for free compute units.
 static bool lds_rows(const PathArgs& pa) { return pa.n <= PREP_N && !pa.dstart; }
 
+static SortArgs sort_args(const SortArgs& sa, const PathArgs& pa) {
+    SortArgs b = sa;
+    b.lds_rows = lds_rows(pa) ? 1 : 0;
+    return b;
+}
+
 hipError_t launch_prepare_labels(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
-    hipError_t e = lds_rows(pa) ? launch_prepare_lds(sa, 0, 1, s)
-                                : launch_fill_i32(sa.o.mode, sa.BH, 0, s);
+    const SortArgs b = sort_args(sa, pa);
+    hipError_t e = hipSuccess;
+    if (b.lds_rows) e = launch_prepare_lds(b, 0, 1, s);
     if (e != hipSuccess) return e;
-    return launch_sort(sa, 0, 1, s);
+    return launch_sort(b, 0, 1, s);
 }
 
 hipError_t launch_prepare_pairs(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
-    hipError_t e = lds_rows(pa) ? launch_prepare_lds(sa, 1, 1, s)
-                                : launch_fill_i32(sa.o.mode, sa.BH, 0, s);
+    const SortArgs b = sort_args(sa, pa);
+    hipError_t e = launch_sort(b, 1, 2, s);
+    if (e == hipSuccess) e = launch_pair_plan(pa, s);
+    if (e == hipSuccess && b.lds_rows) e = launch_prepare_lds(b, 1, 1, s);
     if (e != hipSuccess) return e;
-    if ((e = launch_sort(sa, 1, 2, s)) != hipSuccess) return e;
-    if ((e = launch_pair_plan(pa, s)) != hipSuccess) return e;
     return launch_owner_lists(pa, s);
 }
 
 hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
-    hipError_t e = lds_rows(pa) ? launch_prepare_lds(sa, 0, 2, s)
-                                : launch_fill_i32(sa.o.mode, sa.BH, 0, s);
+    const SortArgs b = sort_args(sa, pa);
+    hipError_t e = hipSuccess;
+    if (b.lds_rows) e = launch_prepare_lds(b, 0, 2, s);
     if (e != hipSuccess) return e;
-    if ((e = launch_sort(sa, 0, 3, s)) != hipSuccess) return e;
+    if ((e = launch_sort(b, 0, 3, s)) != hipSuccess) return e;
     if ((e = launch_pair_plan(pa, s)) != hipSuccess) return e;
     return launch_owner_lists(pa, s);
 }

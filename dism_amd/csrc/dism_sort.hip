@@ -220,7 +220,6 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_kernel(SortArgs a) {
     __shared__ int scan[RADIX];
     __shared__ uint32_t mask;
     const int bh = blockIdx.x, role = (int)blockIdx.y + a.role_base, n = a.n, tid = threadIdx.x;
-    if (a.o.mode[bh]) return;  // prepared by prepare_lds_kernel
     const long off = (long)bh * n;
     const int32_t* __restrict__ lq = a.lab[0] + off;
     const int32_t* __restrict__ lk = a.lab[1] + off;
@@ -248,9 +247,16 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_kernel(SortArgs a) {
     int digits[4], nd = 0;
     for (int d = 0; d < 4; ++d)
         if ((used >> (8 * d)) & 255u) digits[nd++] = d;
-    // every role writes the same shift (the roles may run on different streams); role 1
-    // clears the plan's per-row class counts (the plan appends to them after roles 1 and 2)
-    if (tid == 0) a.o.shift[bh] = nd ? 8 * digits[nd - 1] : 0;
+    // rows with one label byte are prepare_lds_kernel's when it runs (lds_rows): the same
+    // test it makes.  Every role writes the row's mode and shift (the same values
+    // prepare_lds_kernel writes; the roles may run on different streams); role 1 clears the
+    // plan's per-row class counts (the plan appends to them after roles 1 and 2)
+    const bool lds = a.lds_rows && nd == 1;
+    if (tid == 0) {
+        a.o.mode[bh] = lds ? 1 : 0;
+        a.o.shift[bh] = nd ? 8 * digits[nd - 1] : 0;
+    }
+    if (lds) return;
     if (role == 1 && tid < 8) a.o.bhcount[tid >> 2][(long)bh * 4 + (tid & 3)] = 0;
 
     if (role == 0) {
