@@ -320,7 +320,7 @@ template <int SIDE, typename F>
 __device__ __forceinline__ void for_owner_items(const PathArgs& a, F&& item) {
     const OwnerWork w = owner_work<SIDE>(a);
     const int stride = (int)gridDim.x * WAVES;
-    for (int vi = (int)blockIdx.x * WAVES + wave_id(); vi < w.total; vi += stride) {
+    for (int vi = (int)blockIdx.x * WAVES + wave_id_v(); vi < w.total; vi += stride) {
         if (vi < w.i0) item(Lanes<8>{}, w.base[0], vi * 8, w.n[0]);
         else if (vi < w.i01) item(Lanes<32>{}, w.base[1], (vi - w.i0) * 2, w.n[1]);
         else item(Lanes<64>{}, w.base[2], vi - w.i01, w.n[2]);
@@ -540,7 +540,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
 template <typename T, int R, int DV>
 __global__ __launch_bounds__(64 * WAVES) void pairs_finish_kernel(PathArgs a) {
     __shared__ FinishLds s_all[WAVES];
-    FinishLds& S = s_all[wave_id()];
+    FinishLds& S = s_all[wave_id_v()];
     for_owner_items<0>(a, [&](auto g, int base, int k0, int ncls) {
         finish_item<T, R, DV, decltype(g)::value>(a, base, k0, ncls, S);
     });
@@ -712,7 +712,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
 template <typename T, int R, int DV>
 __global__ __launch_bounds__(64 * WAVES) void pairs_rows_kernel(PathArgs a) {
     __shared__ RowsLds<R> s_all[WAVES];
-    RowsLds<R>& S = s_all[wave_id()];
+    RowsLds<R>& S = s_all[wave_id_v()];
     for_owner_items<0>(a, [&](auto g, int base, int k0, int ncls) {
         rows_item<T, R, DV, decltype(g)::value>(a, base, k0, ncls, S);
     });
@@ -880,7 +880,7 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
 template <typename T, int R, int DV>
 __global__ __launch_bounds__(64 * WAVES) void pairs_keys_kernel(PathArgs a) {
     __shared__ KeysLds<R> s_all[WAVES];
-    KeysLds<R>& S = s_all[wave_id()];
+    KeysLds<R>& S = s_all[wave_id_v()];
     for_owner_items<1>(a, [&](auto g, int base, int k0, int ncls) {
         keys_item<T, R, DV, decltype(g)::value>(a, base, k0, ncls, S);
     });

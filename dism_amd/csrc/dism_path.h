@@ -13,7 +13,14 @@ namespace dism {
 // each wave owns one work item and its own slice of the workgroup's LDS.
 constexpr int WAVES = 4;
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
-__device__ __forceinline__ int wave_id() { return (int)(threadIdx.x >> 6); }
+// (uniform across the wave: read into a scalar register, so that everything derived from it,
+// row bases and LDS offsets, is scalar arithmetic)
+__device__ __forceinline__ int wave_id() {
+    return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+// the same index as a vector value (the pair kernels: scalar row bases there raise the
+// register count of pairs_keys_kernel past an occupancy step)
+__device__ __forceinline__ int wave_id_v() { return (int)(threadIdx.x >> 6); }
 
 // Work item of this wave with an XCD-contiguous mapping: workgroups are dispatched
 // round-robin over the 8 XCDs, so consecutive work items (same (b,h) row, whose labels and
