@@ -18,7 +18,7 @@ LIB = os.path.join(HERE, "libdism_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("DISM_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["dism_aux.hip", "dism_sort.hip", "dism_pairs.hip", "dism_scan.hip",
+SOURCES = ["dism_aux.hip", "dism_sort.hip", "dism_msort.hip", "dism_pairs.hip", "dism_scan.hip",
            "dism_packed.hip", "dism_decode.hip", "dism_vocab.hip", "dism_capi.cpp"]
 
 FLAGS = [

@@ -51,8 +51,8 @@ hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 //   pnb/prow: per query row bigram-pair count and record (layout: dism_launch.h)
 struct Layout {
     int64_t corder, clab, ctab, bpos[2], blab[2], bplab[2], btab[2], shift, tmp[3];
-    int64_t stage[2][2], bhcount[2], own[2], ocount, mode;
-    int64_t pnb, prow, total;
+    int64_t stage[2][2], bhcount[2], own[2], ocount, mode, onebyte;
+    int64_t pnb, prow, mcount, mdig, total;
     int prow_stride;
 };
 
@@ -115,6 +115,9 @@ Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     }
     L.ocount = take(8 * 4);
     L.mode = take(BH * 4);
+    L.onebyte = take(BH * 4);
+    L.mcount = take(3 * BH * 256 * dism::MSORT_SEGMENTS * 4);
+    L.mdig = take(BH * (32 + 8) * 4);
     L.tmp[0] = take(BH * 2 * N * 4);
     L.tmp[1] = take(BH * N * 4);
     L.tmp[2] = take(BH * N * 4);
@@ -149,6 +152,9 @@ dism::Orders orders(const Layout& L, void* ws) {
     }
     o.ocount = at<int32_t>(ws, L.ocount);
     o.mode = at<int32_t>(ws, L.mode);
+    o.onebyte = at<int32_t>(ws, L.onebyte);
+    o.mcount = at<int32_t>(ws, L.mcount);
+    o.mdig = at<int32_t>(ws, L.mdig);
     return o;
 }
 

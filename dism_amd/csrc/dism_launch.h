@@ -43,9 +43,16 @@ struct Orders {
     int4* own[2];
     int32_t* ocount;      // [8]
     int32_t* mode;        // [B*H]
+    int32_t* onebyte;     // [B*H] 1 when the row's labels differ in at most one byte (shift)
+    // multi-block sort (dism_msort.hip): digit counts [3*B*H][256][MSORT_SEGMENTS] (the
+    // combined order's rows, then the bigram orders' rows), per-row partial label-bit masks
+    // [B*H][32], then per-row digit lists [B*H][8]
+    int32_t* mcount;
+    int32_t* mdig;
 };
 
 constexpr int PREP_N = 16384;     // longest row of the LDS-resident prepare kernel
+constexpr int MSORT_SEGMENTS = 32;  // most workgroups per row of the multi-block sort
 constexpr int OWNER_SMALL = 8;    // partner counts <= 8: 16 owners per wave, 4 lanes each
 constexpr int OWNER_MEDIUM = 32;  // <= 32: 4 owners per wave, 16 lanes each; more: 1 per wave
 
@@ -100,9 +107,10 @@ struct PathArgs {
     // query resets (inference prefill): per query the last reset position at or before it;
     // walks from that query stop there.  [B*H*N] or null.
     const int32_t* wlo;
-    // forward label scan: 0 = every row, pair counts from pnb; 1 = rows prepared in LDS
-    // (mode 1) with the pair counts computed in the scan (the plan may still be running on
-    // another stream); 2 = the remaining rows (mode 0), from pnb
+    // forward label scan: 0 = every row, pair counts from pnb; 1 = rows whose labels differ
+    // in one byte (onebyte), with the pair counts computed in the scan (the plan may still be
+    // running on another stream); 2 = the remaining rows, from pnb.  Phases 1/2 only for
+    // fixed-length rows (dstart null).
     int fwd_phase;
 };
 
@@ -195,6 +203,10 @@ hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s)
 hipError_t launch_prepare_labels(const SortArgs& sa, const PathArgs& pa, hipStream_t s);
 hipError_t launch_prepare_pairs(const SortArgs& sa, const PathArgs& pa, hipStream_t s);
 hipError_t launch_sort(const SortArgs& a, int role0, int roles, hipStream_t s);
+// multi-block sorts (rows the LDS-resident kernel cannot take): the combined label order, and
+// the bigram orders of both sides (each also lists the rows' digits, mode and shift)
+hipError_t launch_msort_labels(const SortArgs& a, hipStream_t s);
+hipError_t launch_msort_pairs(const SortArgs& a, hipStream_t s);
 // only the combined label order (corder, clab, ctab) of every row, global-memory path (the
 // rows' mode must be 0)
 hipError_t launch_sort_labels(const SortArgs& a, hipStream_t s);

@@ -235,29 +235,37 @@ static SortArgs sort_args(const SortArgs& sa, const PathArgs& pa) {
 
 hipError_t launch_prepare_labels(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
     const SortArgs b = sort_args(sa, pa);
-    hipError_t e = hipSuccess;
-    if (b.lds_rows) e = launch_prepare_lds(b, 0, 1, s);
-    if (e != hipSuccess) return e;
-    return launch_sort(b, 0, 1, s);
+    if (!b.lds_rows) return launch_msort_labels(b, s);
+    const hipError_t e = launch_prepare_lds(b, 0, 1, s);
+    return e != hipSuccess ? e : launch_sort(b, 0, 1, s);
 }
 
 hipError_t launch_prepare_pairs(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
     const SortArgs b = sort_args(sa, pa);
-    hipError_t e = launch_sort(b, 1, 2, s);
-    if (e == hipSuccess) e = launch_pair_plan(pa, s);
-    if (e == hipSuccess && b.lds_rows) e = launch_prepare_lds(b, 1, 1, s);
-    if (e != hipSuccess) return e;
-    return launch_owner_lists(pa, s);
+    hipError_t e;
+    if (!b.lds_rows) {
+        e = launch_msort_pairs(b, s);
+        if (e == hipSuccess) e = launch_pair_plan(pa, s);
+    } else {
+        e = launch_sort(b, 1, 2, s);
+        if (e == hipSuccess) e = launch_pair_plan(pa, s);
+        if (e == hipSuccess) e = launch_prepare_lds(b, 1, 1, s);
+    }
+    return e != hipSuccess ? e : launch_owner_lists(pa, s);
 }
 
 hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
     const SortArgs b = sort_args(sa, pa);
-    hipError_t e = hipSuccess;
-    if (b.lds_rows) e = launch_prepare_lds(b, 0, 2, s);
-    if (e != hipSuccess) return e;
-    if ((e = launch_sort(b, 0, 3, s)) != hipSuccess) return e;
-    if ((e = launch_pair_plan(pa, s)) != hipSuccess) return e;
-    return launch_owner_lists(pa, s);
+    if (!b.lds_rows) {
+        const hipError_t e = launch_prepare_labels(sa, pa, s);
+        return e != hipSuccess ? e : launch_prepare_pairs(sa, pa, s);
+    }
+    // one stream: both LDS roles in one grid (64-block roles side by side), then the sort
+    // for the other rows, the plan and the owner lists
+    hipError_t e = launch_prepare_lds(b, 0, 2, s);
+    if (e == hipSuccess) e = launch_sort(b, 0, 3, s);
+    if (e == hipSuccess) e = launch_pair_plan(pa, s);
+    return e != hipSuccess ? e : launch_owner_lists(pa, s);
 }
 
 // Work of the persistent pair kernels of one side: items [0, i0) small class (8 owners

@@ -126,10 +126,10 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
     uint32_t* s_h = s_h_all[wave_id()];
     Item it;
     if (!scan_item(a, it)) return;
-    // fwd_phase 1: rows prepared in LDS (one-byte labels), pair counts from the histogram;
+    // fwd_phase 1: rows whose labels differ in one byte, pair counts from the histogram;
     // 2: the other rows, pair counts from the plan (pnb); 0: every row from pnb
-    const int mode = a.fwd_phase ? a.o.mode[it.bh] : 0;
-    if ((a.fwd_phase == 1 && !mode) || (a.fwd_phase == 2 && mode)) return;
+    const int onebyte = a.fwd_phase ? a.o.onebyte[it.bh] : 0;
+    if ((a.fwd_phase == 1 && !onebyte) || (a.fwd_phase == 2 && onebyte)) return;
     const bool hist_nb = a.fwd_phase == 1;
     const int lshift = hist_nb ? a.o.shift[it.bh] : 0;
     const int lane = lane_id();

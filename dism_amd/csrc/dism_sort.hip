@@ -255,6 +255,7 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_kernel(SortArgs a) {
     if (tid == 0) {
         a.o.mode[bh] = lds ? 1 : 0;
         a.o.shift[bh] = nd ? 8 * digits[nd - 1] : 0;
+        a.o.onebyte[bh] = nd <= 1 ? 1 : 0;
     }
     if (lds) return;
     if (role == 1 && tid < 8) a.o.bhcount[tid >> 2][(long)bh * 4 + (tid & 3)] = 0;
@@ -503,6 +504,7 @@ __global__ __launch_bounds__(SORT_THREADS) void prepare_lds_kernel(SortArgs a) {
     const bool lds_ok = nd == 1;
     if (tid == 0) {  // both roles write the same values (they may run on different streams)
         a.o.mode[bh] = lds_ok ? 1 : 0;
+        a.o.onebyte[bh] = nd <= 1 ? 1 : 0;
         if (lds_ok) a.o.shift[bh] = 8 * dg;
     }
     if (!lds_ok) return;  // sort_kernel and pair_plan_kernel take this row
@@ -700,6 +702,6 @@ hipError_t launch_sort(const SortArgs& a, int role0, int roles, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_sort_labels(const SortArgs& a, hipStream_t s) { return launch_sort(a, 0, 1, s); }
+hipError_t launch_sort_labels(const SortArgs& a, hipStream_t s) { return launch_msort_labels(a, s); }
 
 }  // namespace dism
