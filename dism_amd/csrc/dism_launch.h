@@ -53,8 +53,8 @@ struct Orders {
 
 constexpr int PREP_N = 16384;     // longest row of the LDS-resident prepare kernel
 constexpr int MSORT_SEGMENTS = 32;  // most workgroups per row of the multi-block sort
-constexpr int OWNER_SMALL = 8;    // partner counts <= 8: 16 owners per wave, 4 lanes each
-constexpr int OWNER_MEDIUM = 32;  // <= 32: 4 owners per wave, 16 lanes each; more: 1 per wave
+constexpr int OWNER_SMALL = 4;    // partner counts <= 4: 16 owners per wave, 4 lanes each
+constexpr int OWNER_MEDIUM = 16;  // <= 16: 4 owners per wave, 16 lanes each; more: 1 per wave
 
 struct SortArgs {
     const int32_t* lab[2];  // iq, ik  [B*H*N]

@@ -9,9 +9,10 @@
 //
 // Mapping (MI355X): the plan kernel sorts the owners that have partners into three classes
 // by partner count; a wave takes 64/G owners of one class with G lanes per owner ("slot"):
-//   small  (cnt <= 8):  G = 8,  8 owners per wave;
-//   medium (cnt <= 32): G = 32, 2 owners per wave;
+//   small  (cnt <= 4):  G = 4,  16 owners per wave;
+//   medium (cnt <= 16): G = 16, 4 owners per wave;
 //   large:              G = 64, 1 owner per wave.
+// (With 256 symbols and long rows, most owners have one partner and few more than four.)
 // An owner's partners are consumed in rounds of G (one round for all but the large class
 // beyond 64 partners), so a wave's dependent-load chain does not grow with the longest
 // partner list among many owners.  Per round:
@@ -19,7 +20,7 @@
 //            owner's own DV-row staged in LDS) -- with the per-pair coefficients put in LDS;
 //   phase B  lane = (slot, column group): each slot folds its round's pairs into its own
 //            running sums in ascending partner order (partner value rows are loaded straight
-//            from HBM, four pairs at a time).
+//            from HBM, a few pairs at a time).
 // The kernels are persistent: a fixed grid of waves strides over the items of all three
 // classes.  The longest-match statistics are order-free maxima (LDS atomics).
 // fp32 sequences (repeated by the CPU model), per owner over its pairs in ascending partner
@@ -40,6 +41,20 @@
 namespace dism {
 
 constexpr int PAIR_SLOTS = 64;        // pairs per wave per round (one per lane)
+// Lanes per owner of the small and medium classes: at least the class's partner bound (so
+// its owners finish in one round); wider slots where the kernel's per-lane value registers
+// (DV / lanes columns, several rows at a time) would not fit otherwise (the key kernel, which
+// also keeps its own row and two accumulators per column, and DV = 128).
+__host__ __device__ constexpr int lanes_small(int dv, bool keys) {
+    return keys || dv >= 128 ? 8 : OWNER_SMALL;
+}
+__host__ __device__ constexpr int lanes_medium(int dv) { return dv >= 128 ? 32 : OWNER_MEDIUM; }
+constexpr int LANES_SMALL_MIN = OWNER_SMALL;  // most small-class slots per wave: 64 / 4
+// partner rows per batch of the one-round path and per step of the ordered accumulation:
+// about 32 registers of row values per lane
+__host__ __device__ constexpr int row_batch(int cpl, int cap) {
+    return 32 / cpl < 2 ? 2 : (32 / cpl > cap ? cap : 32 / cpl);
+}
 constexpr unsigned PAIR_GRID = 2048;  // workgroups of the persistent pair kernels
 
 // Partner range of owner t of side SIDE's bigram order (0: query rows with key partners
@@ -268,12 +283,12 @@ hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s)
     return e != hipSuccess ? e : launch_owner_lists(pa, s);
 }
 
-// Work of the persistent pair kernels of one side: items [0, i0) small class (8 owners
-// each), [i0, i01) medium (2 owners), [i01, total) large (1 owner).
+// Work of the persistent pair kernels of one side: items [0, i0) small class (16 owners
+// each), [i0, i01) medium (4 owners), [i01, total) large (1 owner).
 struct OwnerWork {
     int i0, i01, total, n[3], base[3];
 };
-template <int SIDE>
+template <int SIDE, int GS, int GM>
 __device__ __forceinline__ OwnerWork owner_work(const PathArgs& a) {
     const int32_t* c = a.o.ocount + 4 * SIDE;
     OwnerWork w;
@@ -283,8 +298,8 @@ __device__ __forceinline__ OwnerWork owner_work(const PathArgs& a) {
     w.base[0] = 0;
     w.base[1] = w.n[0];
     w.base[2] = w.n[0] + w.n[1];
-    w.i0 = (w.n[0] + 7) / 8;
-    w.i01 = w.i0 + (w.n[1] + 1) / 2;
+    w.i0 = (w.n[0] + 64 / GS - 1) / (64 / GS);
+    w.i01 = w.i0 + (w.n[1] + 64 / GM - 1) / (64 / GM);
     w.total = w.i01 + w.n[2];
     return w;
 }
@@ -324,13 +339,14 @@ __device__ __forceinline__ bool load_slot(const PathArgs& a, int base, int k0, i
 // Runs `item(G-tag, list base, first owner, class size)` for every item of side SIDE this
 // wave strides over.
 template <int G> struct Lanes { static constexpr int value = G; };
-template <int SIDE, typename F>
+template <int SIDE, int GS, int GM, typename F>
 __device__ __forceinline__ void for_owner_items(const PathArgs& a, F&& item) {
-    const OwnerWork w = owner_work<SIDE>(a);
+    static_assert(OWNER_SMALL <= GS && OWNER_MEDIUM <= GM, "owner classes must fit their lanes");
+    const OwnerWork w = owner_work<SIDE, GS, GM>(a);
     const int stride = (int)gridDim.x * WAVES;
     for (int vi = (int)blockIdx.x * WAVES + wave_id_v(); vi < w.total; vi += stride) {
-        if (vi < w.i0) item(Lanes<8>{}, w.base[0], vi * 8, w.n[0]);
-        else if (vi < w.i01) item(Lanes<32>{}, w.base[1], (vi - w.i0) * 2, w.n[1]);
+        if (vi < w.i0) item(Lanes<GS>{}, w.base[0], vi * (64 / GS), w.n[0]);
+        else if (vi < w.i01) item(Lanes<GM>{}, w.base[1], (vi - w.i0) * (64 / GM), w.n[1]);
         else item(Lanes<64>{}, w.base[2], vi - w.i01, w.n[2]);
     }
 }
@@ -355,8 +371,8 @@ struct FinishLds {
     float cf[PAIR_SLOTS];
     float p[PAIR_SLOTS];
     int j[PAIR_SLOTS];
-    unsigned m[8];
-    unsigned long long key[8];
+    unsigned m[64 / LANES_SMALL_MIN];
+    unsigned long long key[64 / LANES_SMALL_MIN];
 };
 
 // 64-bit shuffle (xor pattern)
@@ -406,7 +422,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
         // shuffles, partner value rows loaded as soon as the partners are known
         const bool has = sub < cnt;
         const int j = kb[has ? lo + sub : 0];
-        constexpr int UB = G <= 8 ? 4 : 16;  // partner rows loaded per batch
+        constexpr int UB = row_batch(CPL, 16);  // partner rows loaded per batch
         float vr[UB][CPL];                   // the first batch is issued with the partners
 #pragma unroll
         for (int u = 0; u < UB; ++u) {
@@ -492,15 +508,16 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
             // phase B: the slot folds its round's pairs in order, lane = column group cg
             const int nv = cnt - c0 < G ? cnt - c0 : G;
             if (cols) {
-                for (int h0 = 0; h0 < nv; h0 += 4) {
-                    float vr[4][CPL];
+                constexpr int HB = row_batch(CPL, 4);
+                for (int h0 = 0; h0 < nv; h0 += HB) {
+                    float vr[HB][CPL];
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
+                    for (int u = 0; u < HB; ++u) {
                         const int jj = j_s[h0 + u < nv ? h0 + u : nv - 1];
                         load_row<T, CPL>(v + (s.row0 + (long)jj * a.H) * DV + col, vr[u]);
                     }
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
+                    for (int u = 0; u < HB; ++u) {
                         if (h0 + u < nv) {
                             dp = dp + p_s[h0 + u];
                             const float cf = cf_s[h0 + u];
@@ -549,7 +566,8 @@ template <typename T, int R, int DV>
 __global__ __launch_bounds__(64 * WAVES) void pairs_finish_kernel(PathArgs a) {
     __shared__ FinishLds s_all[WAVES];
     FinishLds& S = s_all[wave_id_v()];
-    for_owner_items<0>(a, [&](auto g, int base, int k0, int ncls) {
+    constexpr int GS = lanes_small(DV, false), GM = lanes_medium(DV);
+    for_owner_items<0, GS, GM>(a, [&](auto g, int base, int k0, int ncls) {
         finish_item<T, R, DV, decltype(g)::value>(a, base, k0, ncls, S);
     });
 }
@@ -606,7 +624,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
         // one round (see finish_item): partner value rows issued with the partners
         const bool has = sub < cnt;
         const int j = kb[has ? lo + sub : 0];
-        constexpr int UB = G <= 8 ? 4 : 16;
+        constexpr int UB = row_batch(CPL, 16);
         float vr[UB][CPL];
 #pragma unroll
         for (int u = 0; u < UB; ++u) {
@@ -672,17 +690,18 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
             for (int r = 0; r < R; ++r) S.sk[sb + sub][r] = skr[r];
         }
         const int nv = cnt - c0 < G ? cnt - c0 : G;
-        for (int h0 = 0; h0 < s.maxcnt - c0 && h0 < G; h0 += 4) {
-            float vr[4][CPL];
+        constexpr int HB = row_batch(CPL, 4);
+        for (int h0 = 0; h0 < s.maxcnt - c0 && h0 < G; h0 += HB) {
+            float vr[HB][CPL];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < HB; ++u) {
                 const int hu = h0 + u < nv ? h0 + u : (nv > 0 ? nv - 1 : 0);
                 const int j = __float_as_int(S.f[sb + hu][3]);
                 load_row<T, CPL>(v + (s.row0 + (long)(nv > 0 ? j : i) * a.H) * DV + col,
                                  vr[u]);
             }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < HB; ++u) {
                 const float e = group_sum<GE>(tree_dot<CPL>(dor, vr[u]));
                 if (h0 + u < nv) {
                     const float* f = S.f[sb + h0 + u];
@@ -721,7 +740,8 @@ template <typename T, int R, int DV>
 __global__ __launch_bounds__(64 * WAVES) void pairs_rows_kernel(PathArgs a) {
     __shared__ RowsLds<R> s_all[WAVES];
     RowsLds<R>& S = s_all[wave_id_v()];
-    for_owner_items<0>(a, [&](auto g, int base, int k0, int ncls) {
+    constexpr int GS = lanes_small(DV, false), GM = lanes_medium(DV);
+    for_owner_items<0, GS, GM>(a, [&](auto g, int base, int k0, int ncls) {
         rows_item<T, R, DV, decltype(g)::value>(a, base, k0, ncls, S);
     });
 }
@@ -783,7 +803,7 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
         // one round (see finish_item): partner dO rows issued with the partners
         const bool has = sub < cnt;
         const int i = qb[has ? lo + sub : 0];
-        constexpr int UB = G <= 8 ? 4 : 16;
+        constexpr int UB = row_batch(CPL, 16);
         float dr[UB][CPL];
 #pragma unroll
         for (int u = 0; u < UB; ++u) {
@@ -846,16 +866,17 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
             for (int r = 0; r < R; ++r) S.sq[sb + sub][r] = sqr[r];
         }
         const int nv = cnt - c0 < G ? cnt - c0 : G;
-        for (int h0 = 0; h0 < s.maxcnt - c0 && h0 < G; h0 += 4) {
-            float dr[4][CPL];
+        constexpr int HB = row_batch(CPL, 4);
+        for (int h0 = 0; h0 < s.maxcnt - c0 && h0 < G; h0 += HB) {
+            float dr[HB][CPL];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < HB; ++u) {
                 const int hu = h0 + u < nv ? h0 + u : (nv > 0 ? nv - 1 : 0);
                 const int ii = nv > 0 ? S.i[sb + hu] : j;
                 load_row<T, CPL>(dout + (s.row0 + (long)ii * a.H) * DV + col, dr[u]);
             }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < HB; ++u) {
                 const float e = group_sum<GE>(tree_dot<CPL>(dr[u], vj));
                 if (h0 + u < nv) {
                     const float dpv = S.dp[sb + h0 + u];
@@ -889,7 +910,8 @@ template <typename T, int R, int DV>
 __global__ __launch_bounds__(64 * WAVES) void pairs_keys_kernel(PathArgs a) {
     __shared__ KeysLds<R> s_all[WAVES];
     KeysLds<R>& S = s_all[wave_id_v()];
-    for_owner_items<1>(a, [&](auto g, int base, int k0, int ncls) {
+    constexpr int GS = lanes_small(DV, true), GM = lanes_medium(DV);
+    for_owner_items<1, GS, GM>(a, [&](auto g, int base, int k0, int ncls) {
         keys_item<T, R, DV, decltype(g)::value>(a, base, k0, ncls, S);
     });
 }
