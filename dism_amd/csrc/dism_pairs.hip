@@ -108,7 +108,27 @@ __device__ __forceinline__ int pair_length(const int32_t* __restrict__ q,
                                            int dlo) {
     const int lo = bound ? (i / strip) * strip : dlo;
     int c = i - 1 >= lo ? 2 : 1;
-    while (i - c >= lo && j - c >= 0 && q[i - c] == k[j - c]) ++c;
+    if (c == 2) {
+        // the walk compares WALK_PF label pairs per step, all loads in flight together
+        // (clamped indices; a comparison counts only while both positions are in range), so
+        // the usual short match costs one round trip instead of one per label
+        constexpr int WALK_PF = 4;
+        for (;;) {
+            int qv[WALK_PF], kv[WALK_PF];
+#pragma unroll
+            for (int u = 0; u < WALK_PF; ++u) {
+                const int iq = i - c - u, jk = j - c - u;
+                qv[u] = q[iq > 0 ? iq : 0];
+                kv[u] = k[jk > 0 ? jk : 0];
+            }
+            int run = 0;
+#pragma unroll
+            for (int u = 0; u < WALK_PF; ++u)
+                if (run == u && i - c - u >= lo && j - c - u >= 0 && qv[u] == kv[u]) ++run;
+            c += run;
+            if (run < WALK_PF) break;
+        }
+    }
     if (bound && lo > 0 && i - c < lo && j - c >= 0) {
         const int jj = j - c;
         c += jj - bound[(long)(lo / strip - 1) * n + jj];
