@@ -243,7 +243,10 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
                 const int pl = nbC;
                 int c = 0;
                 if (isq && pl >= 0) c = (int)((s_h[pl >> 1] >> (16 * (pl & 1))) & 0xffffu);
+                // only keys before the window's last query can count
+                const unsigned long long qv = __ballot(isq && pl >= 0);
                 unsigned long long kv = __ballot(ok && !isq && pl >= 0);
+                kv = qv ? kv & (~0ull >> __clzll(qv)) : 0ull;  // lanes up to the last query
                 while (kv) {
                     const int l = __ffsll((long long)kv) - 1;
                     kv &= kv - 1;
