@@ -270,9 +270,10 @@ static SortArgs sort_args(const SortArgs& sa, const PathArgs& pa) {
 
 hipError_t launch_prepare_labels(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
     const SortArgs b = sort_args(sa, pa);
+    // prepare_lds_kernel role 0 orders every row: in LDS, or in global memory for rows whose
+    // labels differ in more than one byte
     if (!b.lds_rows) return launch_msort_labels(b, s);
-    const hipError_t e = launch_prepare_lds(b, 0, 1, s);
-    return e != hipSuccess ? e : launch_sort(b, 0, 1, s);
+    return launch_prepare_lds(b, 0, 1, s);
 }
 
 hipError_t launch_prepare_pairs(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
@@ -295,10 +296,10 @@ hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s)
         const hipError_t e = launch_prepare_labels(sa, pa, s);
         return e != hipSuccess ? e : launch_prepare_pairs(sa, pa, s);
     }
-    // one stream: both LDS roles in one grid (64-block roles side by side), then the sort
-    // for the other rows, the plan and the owner lists
+    // one stream: both LDS roles in one grid (64-block roles side by side), then the bigram
+    // sorts of the other rows, the plan and the owner lists
     hipError_t e = launch_prepare_lds(b, 0, 2, s);
-    if (e == hipSuccess) e = launch_sort(b, 0, 3, s);
+    if (e == hipSuccess) e = launch_sort(b, 1, 2, s);
     if (e == hipSuccess) e = launch_pair_plan(pa, s);
     return e != hipSuccess ? e : launch_owner_lists(pa, s);
 }

@@ -214,6 +214,43 @@ __device__ void lds_pass(int m, Dig digit, Emit emit, int32_t* table, int (*wcnt
     __syncthreads();
 }
 
+// Combined label order of row bh's 2N entries in global memory (LSD passes over the row's nd
+// used label bytes digits[], low first): corder / clab / ctab.  One 1024-thread workgroup;
+// wcnt and scan are LDS scratch.
+__device__ void label_order_global(const SortArgs& a, int bh, int nd, const int* digits,
+                                   int (*wcnt)[RADIX], int* scan) {
+    const int n = a.n, tid = threadIdx.x;
+    const long off = (long)bh * n;
+    const int32_t* __restrict__ lq = a.lab[0] + off;
+    const int32_t* __restrict__ lk = a.lab[1] + off;
+    const int n2 = 2 * n;
+    int32_t* corder = a.o.corder + 2 * off;
+    int32_t* clab = a.o.clab + 2 * off;
+    int32_t* ctab = a.o.ctab + (long)bh * (RADIX + 1);
+    int32_t* tmp = a.tmp[0] + 2 * off;
+    auto lab_of = [&](int v) -> uint32_t {
+        return (uint32_t)((v & 1) ? lq[v >> 1] : lk[v >> 1]);
+    };
+    auto lab_out = [&](int v) -> int { return (int)lab_of(v); };
+    auto none = [&](int) -> int { return 0; };
+    if (nd == 0) {
+        for (int x = tid; x < n2; x += SORT_THREADS) {
+            corder[x] = x;
+            clab[x] = (int)lab_of(x);
+        }
+        if (tid <= RADIX) ctab[tid] = tid == 0 ? 0 : n2;
+        return;
+    }
+    const int32_t* in = nullptr;
+    for (int k = 0; k < nd; ++k) {
+        const bool last = k == nd - 1;
+        int32_t* out = ((nd - 1 - k) & 1) ? tmp : corder;
+        sort_pass(n2, in, out, 8 * digits[k], lab_of, last ? clab : nullptr, lab_out,
+                  nullptr, none, last ? ctab : nullptr, wcnt, scan);
+        in = out;
+    }
+}
+
 // grid (BH, 3)
 __global__ __launch_bounds__(SORT_THREADS) void sort_kernel(SortArgs a) {
     __shared__ int wcnt[SORT_WAVES][RADIX];
@@ -261,33 +298,7 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_kernel(SortArgs a) {
     if (role == 1 && tid < 8) a.o.bhcount[tid >> 2][(long)bh * 4 + (tid & 3)] = 0;
 
     if (role == 0) {
-        // ---- combined label order of the 2N entries
-        const int n2 = 2 * n;
-        int32_t* corder = a.o.corder + 2 * off;
-        int32_t* clab = a.o.clab + 2 * off;
-        int32_t* ctab = a.o.ctab + (long)bh * (RADIX + 1);
-        int32_t* tmp = a.tmp[0] + 2 * off;
-        auto lab_of = [&](int v) -> uint32_t {
-            return (uint32_t)((v & 1) ? lq[v >> 1] : lk[v >> 1]);
-        };
-        auto lab_out = [&](int v) -> int { return (int)lab_of(v); };
-        auto none = [&](int) -> int { return 0; };
-        if (nd == 0) {
-            for (int x = tid; x < n2; x += SORT_THREADS) {
-                corder[x] = x;
-                clab[x] = (int)lab_of(x);
-            }
-            if (tid <= RADIX) ctab[tid] = tid == 0 ? 0 : n2;
-            return;
-        }
-        const int32_t* in = nullptr;
-        for (int k = 0; k < nd; ++k) {
-            const bool last = k == nd - 1;
-            int32_t* out = ((nd - 1 - k) & 1) ? tmp : corder;
-            sort_pass(n2, in, out, 8 * digits[k], lab_of, last ? clab : nullptr, lab_out,
-                      nullptr, none, last ? ctab : nullptr, wcnt, scan);
-            in = out;
-        }
+        label_order_global(a, bh, nd, digits, wcnt, scan);
         return;
     }
 
@@ -505,9 +516,20 @@ __global__ __launch_bounds__(SORT_THREADS) void prepare_lds_kernel(SortArgs a) {
     if (tid == 0) {  // both roles write the same values (they may run on different streams)
         a.o.mode[bh] = lds_ok ? 1 : 0;
         a.o.onebyte[bh] = nd <= 1 ? 1 : 0;
-        if (lds_ok) a.o.shift[bh] = 8 * dg;
+        a.o.shift[bh] = 8 * dg;  // the top used byte (0 without any)
     }
-    if (!lds_ok) return;  // sort_kernel and pair_plan_kernel take this row
+    if (!lds_ok) {
+        // the global-memory path takes this row: its combined label order here (the LDS
+        // pool as the passes' scratch), the bigram orders in sort_kernel roles 1-2
+        if (role == 0) {
+            int digits[4], k = 0;
+            for (int d = 0; d < 4; ++d)
+                if ((used >> (8 * d)) & 255u) digits[k++] = d;
+            label_order_global(a, bh, nd, digits, reinterpret_cast<int (*)[RADIX]>(pool),
+                               reinterpret_cast<int*>(pool) + SORT_WAVES * RADIX);
+        }
+        return;
+    }
     const int shift = 8 * dg;
     for (int p = tid; p < n; p += SORT_THREADS) {
         s_dig[2 * p] = (uint8_t)(((uint32_t)lk[p] >> shift) & 255u);
