@@ -192,10 +192,50 @@ __global__ __launch_bounds__(TAU_THREADS) void tau_reduce_kernel(const float* __
     if (tid == 0) dtau[h] = (float)outer;
 }
 
+// bf16 rows of d = 8 (16 bytes), H <= 64: a workgroup takes 64 positions x all H heads of one
+// batch entry.  Loads run over (position, head) with the head fastest, one contiguous H*16-byte
+// block per position; the labels go through LDS so that the stores run over positions, one
+// contiguous 256-byte run per head.
+constexpr int LAB_P = 64;
+__global__ __launch_bounds__(256) void sign_labels_tile_kernel(const uint4* __restrict__ x,
+                                                               long N, int H,
+                                                               int32_t* __restrict__ out) {
+    __shared__ int32_t s_lab[64][LAB_P + 1];
+    const long tiles = (N + LAB_P - 1) / LAB_P;
+    const long b = blockIdx.x / tiles, n0 = (blockIdx.x - b * tiles) * LAB_P;
+    const int tid = threadIdx.x, cnt = LAB_P * H;
+    for (int t = tid; t < cnt; t += 256) {
+        const int nl = t / H, h = t - nl * H;
+        int32_t lab = 0;
+        if (n0 + nl < N) {
+            const uint4 w = x[(b * N + n0 + nl) * H + h];
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float v = (k & 1) ? __uint_as_float(ws[k >> 1] & 0xFFFF0000u)
+                                        : __uint_as_float(ws[k >> 1] << 16);
+                if (v > 0.0f) lab |= (1 << k);
+            }
+        }
+        s_lab[h][nl] = lab;
+    }
+    __syncthreads();
+    for (int t = tid; t < cnt; t += 256) {
+        const int h = t / LAB_P, nl = t - h * LAB_P;
+        if (n0 + nl < N) out[(b * H + h) * N + n0 + nl] = s_lab[h][nl];
+    }
+}
+
 // ---------------------------------------------------------------------------------------
 hipError_t launch_sign_labels(const void* x, int dtype, long B, long N, long H, int d,
                               int32_t* out, hipStream_t s) {
     long total = B * H * N;
+    if (dtype == DTYPE_BF16 && d == 8 && H <= 64 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        const long tiles = (N + LAB_P - 1) / LAB_P;
+        hipLaunchKernelGGL(sign_labels_tile_kernel, dim3((unsigned)(B * tiles)), dim3(256), 0, s,
+                           (const uint4*)x, N, (int)H, out);
+        return hipGetLastError();
+    }
     dim3 grid((unsigned)((total + 255) / 256));
     if (dtype == DTYPE_BF16)
         hipLaunchKernelGGL(sign_labels_kernel<bf16_t>, grid, dim3(256), 0, s,

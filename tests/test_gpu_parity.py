@@ -121,6 +121,18 @@ def test_sign_labels_exact():
                 "labels bf16")
 
 
+@pytest.mark.parametrize("b,n,h", [(1, 1, 1), (3, 100, 16), (2, 130, 64), (1, 70, 65)])
+def test_sign_labels_tiled_shapes(b, n, h):
+    """bf16 d = 8 rows take the tiled kernel (64 positions x all heads per workgroup) for
+    H <= 64; ragged position counts, one position, and H = 65 (the per-token kernel)."""
+    import dism_amd
+    rng = np.random.default_rng(b * 1000 + n + h)
+    x = oracle.bf16_round(rng.standard_normal((b, n, h, 8)).astype(np.float32))
+    x[0, 0, 0, :] = 0.0
+    assert_bits(host(dism_amd.sign_labels(dev(x, torch.bfloat16))), oracle.sign_labels(x),
+                f"labels bf16 {b}x{n}x{h}")
+
+
 # ---------------------------------------------------------------- forward
 def _inputs(n, pattern, b=2, h=3, r=8, dv=64):
     q, k = labels(n, pattern, b, h)
