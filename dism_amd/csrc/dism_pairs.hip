@@ -396,6 +396,29 @@ struct FinishLds {
     unsigned long long key[64 / LANES_SMALL_MIN];
 };
 
+// N consecutive row elements of type T held as raw 32-bit words: bf16 pairs stay packed
+// (unpacked at use) when N is even, otherwise the values are converted at load.
+template <typename T, int N>
+struct RawRow {
+    static constexpr bool PACKED = sizeof(T) == 2 && N % 2 == 0;
+    static constexpr int W = PACKED ? N / 2 : N;
+    uint32_t w[W];
+    __device__ __forceinline__ void load(const T* p) {
+        if constexpr (PACKED) {
+            load_words<W>(p, w);
+        } else {
+            float f[N];
+            load_row<T, N>(p, f);
+#pragma unroll
+            for (int c = 0; c < N; ++c) w[c] = __float_as_uint(f[c]);
+        }
+    }
+    __device__ __forceinline__ float at(int c) const {
+        if constexpr (PACKED) return word_elem<T>(w, c);
+        else return __uint_as_float(w[c]);
+    }
+};
+
 // 64-bit shuffle (xor pattern)
 __device__ __forceinline__ unsigned long long shfl_xor64(unsigned long long x, int m) {
     const int lo = __shfl_xor((int)(uint32_t)x, m), hi = __shfl_xor((int)(uint32_t)(x >> 32), m);
@@ -443,12 +466,15 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
         // shuffles, partner value rows loaded as soon as the partners are known
         const bool has = sub < cnt;
         const int j = kb[has ? lo + sub : 0];
-        constexpr int UB = row_batch(CPL, 16);  // partner rows loaded per batch
-        float vr[UB][CPL];                   // the first batch is issued with the partners
+        // partner rows loaded per batch, held as raw words (bf16 pairs unpacked at use, so a
+        // batch holds twice the rows); the first batch is issued with the partners
+        using RB_ = RawRow<T, CPL>;
+        constexpr int UB = row_batch(RB_::W, 16);
+        RB_ vr[UB];
 #pragma unroll
         for (int u = 0; u < UB; ++u) {
             const int jj = __shfl(j, sl * G + u);
-            load_row<T, CPL>(v + (s.row0 + (long)jj * a.H) * DV + col, vr[u]);
+            vr[u].load(v + (s.row0 + (long)jj * a.H) * DV + col);
         }
         float skr[R];
         load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
@@ -475,7 +501,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
 #pragma unroll
                 for (int u = 0; u < UB; ++u) {
                     const int jj = __shfl(j, sl * G + u0 + u);
-                    load_row<T, CPL>(v + (s.row0 + (long)jj * a.H) * DV + col, vr[u]);
+                    vr[u].load(v + (s.row0 + (long)jj * a.H) * DV + col);
                 }
             }
 #pragma unroll
@@ -484,7 +510,8 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
                 if (u0 + u < cnt) {
                     dp = dp + pu;
 #pragma unroll
-                    for (int c = 0; c < CPL; ++c) corr[c] = __builtin_fmaf(cfu, vr[u][c], corr[c]);
+                    for (int c = 0; c < CPL; ++c)
+                        corr[c] = __builtin_fmaf(cfu, vr[u].at(c), corr[c]);
                 }
             }
         }
