@@ -2,7 +2,8 @@
 // LDS-resident prepare cannot hold (N > PREP_N, packed layouts).
 //
 // sort_kernel gives one 1024-thread workgroup to each (row, role): a long single sequence has
-// few rows (B*H = 16 at configs[3]), so most CUs idle while the passes run one after another.
+// few rows (B*H = 16 for one 64K-token sequence of 16 heads), so most CUs idle while the passes
+// run one after another.
 // Here every row is split into S segments of one 256-thread workgroup each, and every LSD pass
 // is two launches:
 //   hist:    workgroup (row, s) counts the digits of its segment -> mcount[row][digit][s];

@@ -785,7 +785,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
 }
 
 // 4 waves per SIMD (128 VGPRs) where the spill stays small (bf16 rows, R <= 8: at most a
-// few dozen bytes per lane, 82 -> 73 us at configs[2]); no constraint otherwise
+// few dozen bytes per lane; 82 -> 73 us at B4 H16 T16384 d8 DV64); no constraint otherwise
 constexpr int rows_occupancy(int tsize, int R) { return tsize == 2 && R <= 8 ? 4 : 1; }
 template <typename T, int R, int DV>
 __global__ __launch_bounds__(64 * WAVES)
