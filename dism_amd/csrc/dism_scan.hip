@@ -110,11 +110,11 @@ __device__ __forceinline__ void for_runs(const int32_t* clab, int c0, int c1, F&
 //   cnt > 0 else 0;  rows with pairs get y and cnt in their record for the pair kernel.
 template <typename T, int R, int DV>
 __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
-    using G_ = Geo<T, DV>;
+    using G_ = Geo<T, DV, 3072>;
     constexpr int WIN = G_::WIN, RB = G_::RB, NI = G_::NI;
     constexpr int COLS = (DV + 63) / 64;
     constexpr int W = words_of(sizeof(T), R);
-    __shared__ __attribute__((aligned(16))) unsigned char s_v_all[WAVES][2][WBYTES];
+    __shared__ __attribute__((aligned(16))) unsigned char s_v_all[WAVES][2][G_::BYTES];
     auto& s_v = s_v_all[wave_id()];
     __shared__ __attribute__((aligned(16))) float s_r_all[WAVES][WIN][R];
     auto& s_r = s_r_all[wave_id()];
@@ -334,11 +334,11 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
 // Row-group layout: lane = r*G + g holds M[r][g*VPL .. g*VPL+VPL).
 template <typename T, int R, int DV>
 __global__ __launch_bounds__(64 * WAVES) void scan_rows_kernel(PathArgs a) {
-    using G_ = Geo<T, DV>;
+    using G_ = Geo<T, DV, 3072>;
     constexpr int WIN = G_::WIN, RB = G_::RB, NI = G_::NI;
     constexpr int W = words_of(sizeof(T), R);
     constexpr int G = 64 / R, VPL = DV / G;
-    __shared__ __attribute__((aligned(16))) unsigned char s_v_all[WAVES][2][WBYTES];
+    __shared__ __attribute__((aligned(16))) unsigned char s_v_all[WAVES][2][G_::BYTES];
     auto& s_v = s_v_all[wave_id()];
     __shared__ __attribute__((aligned(16))) float s_r_all[WAVES][WIN][R];
     auto& s_r = s_r_all[wave_id()];
