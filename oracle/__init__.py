@@ -73,6 +73,11 @@ def lib():
         L.orc_suffix_walk_from.argtypes = [P, P, i64, i64, i64]
         L.orc_backward_direct.argtypes = L.orc_backward.argtypes
         L.orc_tau_reduce.argtypes = [P, i32, i32, i64, i64, P]
+        L.orc_forward_flags.argtypes = L.orc_forward.argtypes + [P, P]
+        L.orc_backward_flags.argtypes = L.orc_backward.argtypes + [P]
+        L.orc_bucket_collisions.restype = ctypes.c_uint64
+        L.orc_bucket_collisions.argtypes = [P, P, i64]
+        L.orc_dense_rows.argtypes = [P, P, P, i32, i64, P]
         _lib = L
     return _lib
 
@@ -163,11 +168,37 @@ def reset_starts(reset):
     return np.ascontiguousarray(np.maximum.accumulate(pos, axis=-1).astype(np.int32))
 
 
-def forward(sq, sk, v, iq, ik, hard, lut, threads=0, direct=False, reset=None):
+def dense_rows(iq, ik, hard):
+    """Row classification of the HIP path: uint8 [B,H], 1 where a hard row's bucketed label
+    collisions M (bucket_collisions) exceed N^2/64 (and N <= 65536)."""
+    iq, ik = _i32(iq), _i32(ik)
+    B, H, N = iq.shape
+    out = np.empty(B * H, dtype=np.uint8)
+    lib().orc_dense_rows(_p(iq), _p(ik), _p(_flags(hard)), B * H, N, _p(out))
+    return out.reshape(B, H)
+
+
+def bucket_collisions(q, k):
+    """M of one row: sum over the 4096 label buckets (top 12 bits of label * 0x9E3779B1) of
+    (#queries in the bucket) x (#keys in the bucket)."""
+    q, k = _i32(q), _i32(k)
+    return int(lib().orc_bucket_collisions(_p(q), _p(k), q.shape[-1]))
+
+
+def _dense_arg(dense, B, H):
+    if dense is None:
+        return None
+    d = np.ascontiguousarray(np.broadcast_to(np.asarray(dense, dtype=np.uint8), (B, H)))
+    return d.reshape(-1)
+
+
+def forward(sq, sk, v, iq, ik, hard, lut, threads=0, direct=False, reset=None, dense=None):
     """CPU model forward.  Returns (O fp32 [B,N,H,DV], lse2 [B,H,N], Lmax, argmax).
 
-    direct=False: the decomposed fp32 sequence the HIP kernels reproduce bit for bit;
-    direct=True: the pairwise definition (same mathematics, other fp32 association).
+    direct=False: the sequence the HIP kernels reproduce bit for bit -- per row, the direct
+    (pairwise) definition for rows classified dense (dense_rows) and the decomposed one for
+    the others;  direct=True: the pairwise definition for every row.
+    dense: optional [B,H] (or scalar) override of the row classification.
     reset: optional [B,H,N] bool query resets (inference semantics: a reset query's match
     starts afresh at that query; keys stay)."""
     sq, sk, v, lut = _f32(sq), _f32(sk), _f32(v), _f32(lut)
@@ -180,19 +211,21 @@ def forward(sq, sk, v, iq, ik, hard, lut, threads=0, direct=False, reset=None):
     jarg = np.empty((B, H, N), dtype=np.int32)
     args = (_p(sq), _p(sk), _p(v), _p(iq), _p(ik), _p(_flags(hard)), _p(lut), lut.shape[1], B,
             N, H, R, DV, _p(out), _p(lse2), _p(lmax), _p(jarg), threads)
-    if reset is not None:
+    dflags = _dense_arg(dense, B, H)
+    if reset is not None or dflags is not None:
         assert not direct
-        wlo = reset_starts(reset)
-        lib().orc_forward_reset(*args, _p(wlo))
+        wlo = reset_starts(reset) if reset is not None else None
+        lib().orc_forward_flags(*args, None if wlo is None else _p(wlo),
+                                None if dflags is None else _p(dflags))
     else:
         (lib().orc_forward_direct if direct else lib().orc_forward)(*args)
     return out, lse2, lmax, jarg
 
 
 def backward(sq, sk, v, dout, iq, ik, hard, lut, dlut, lse2, threads=0, block=256,
-             direct=False):
+             direct=False, dense=None):
     """CPU model backward.  Returns (dSQ, dSK, dV fp32, dtau [H], rowtau [B,H,N]).
-    `direct` as in forward()."""
+    `direct` and `dense` as in forward()."""
     sq, sk, v, dout, lut, dlut, lse2 = map(_f32, (sq, sk, v, dout, lut, dlut, lse2))
     iq, ik = _i32(iq), _i32(ik)
     B, N, H, R = sq.shape
@@ -201,10 +234,15 @@ def backward(sq, sk, v, dout, iq, ik, hard, lut, dlut, lse2, threads=0, block=25
     dsk = np.empty_like(sk)
     dv = np.empty_like(v)
     rowtau = np.empty((B, H, N), dtype=np.float32)
-    fn = lib().orc_backward_direct if direct else lib().orc_backward
-    fn(_p(sq), _p(sk), _p(v), _p(dout), _p(iq), _p(ik), _p(_flags(hard)),
-                       _p(lut), _p(dlut), lut.shape[1], _p(lse2), B, N, H, R, DV, _p(dsq),
-                       _p(dsk), _p(dv), _p(rowtau), threads)
+    args = (_p(sq), _p(sk), _p(v), _p(dout), _p(iq), _p(ik), _p(_flags(hard)), _p(lut),
+            _p(dlut), lut.shape[1], _p(lse2), B, N, H, R, DV, _p(dsq), _p(dsk), _p(dv),
+            _p(rowtau), threads)
+    dflags = _dense_arg(dense, B, H)
+    if dflags is not None:
+        assert not direct
+        lib().orc_backward_flags(*args, _p(dflags))
+    else:
+        (lib().orc_backward_direct if direct else lib().orc_backward)(*args)
     dtau = np.empty(H, dtype=np.float32)
     lib().orc_tau_reduce(_p(rowtau), B, H, N, block, _p(dtau))
     return dsq, dsk, dv, dtau, rowtau

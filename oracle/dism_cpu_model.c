@@ -276,9 +276,11 @@ long orc_suffix_walk_from(const int32_t* q, const int32_t* k, long i, long j, lo
     return c;
 }
 
-/* ---------------- forward ----------------
+/* ---------------- direct (pairwise) definition ----------------
  * Vectors fp32 BNHD (bf16 inputs widened exactly by the caller), labels BHN, hard [B*H].
- * Per row i:
+ * Match lengths come from the two-row dynamic programme L[i,j] = (q[i]==k[j]) ?
+ * L[i-1,j-1]+1 : 0, with L[i-1,*] taken as 0 at a query reset (i == wlo[i]).
+ * Forward, per query row i:
  *   pass 1 (integer): L for every matching key; m = max(0, max_j LUT[L]); longest match with
  *                     ties -> largest j;
  *   pass 2, ascending j over matches:
@@ -286,7 +288,68 @@ long orc_suffix_walk_from(const int32_t* q, const int32_t* k, long i, long j, lo
  *     s = fma-chain(sq_i . sk_j); ps = p*s; acc = fma(ps, v_j, acc)
  *   out = acc/den, lse2 = m + log2(den).
  * This is the reference's online-max readout (readout.cuh:16-61) with the final maximum
- * applied from the start; the unit fallback contributes exp2(0 - m). */
+ * applied from the start; the unit fallback contributes exp2(0 - m).
+ * It is also the definition the HIP path uses for the rows it classifies as dense
+ * (orc_dense_row below). */
+static void direct_forward_row(const float* sq, const float* sk, const float* v,
+                               const int32_t* q, const int32_t* k, const float* tab, int b,
+                               int h, long N, int H, int R, int DV, float* out, float* lse2,
+                               int32_t* lmax, int32_t* jarg, const int32_t* wlo) {
+    /* lb[j+1] = L[i,j]; la[j] = L[i-1,j-1] */
+    int32_t* la = (int32_t*)calloc((size_t)N + 1, sizeof(int32_t));
+    int32_t* lb = (int32_t*)calloc((size_t)N + 1, sizeof(int32_t));
+    float* acc = (float*)malloc(sizeof(float) * (size_t)DV);
+    for (long i = 0; i < N; ++i) {
+        long row = ((long)b * N + i) * H + h;
+        float* o = out + row * DV;
+        const int reset = wlo && wlo[i] == i;
+        float m = 0.0f;
+        int32_t best = 0, bj = -1;
+        for (long j = 0; j <= i; ++j) {
+            if (q[i] != k[j]) { lb[j + 1] = 0; continue; }
+            int32_t L = reset ? 1 : la[j] + 1;
+            lb[j + 1] = L;
+            if (L >= best) { best = L; bj = (int32_t)j; }
+            if (tab[L] > m) m = tab[L];
+        }
+        float den = orc_exp2f(-m);
+        for (int d = 0; d < DV; ++d) acc[d] = 0.0f;
+        const float* sqi = sq + row * R;
+        for (long j = 0; j <= i; ++j) {
+            int32_t L = lb[j + 1];
+            if (!L) continue;
+            float p = orc_exp2f(tab[L] - m);
+            den = den + p;
+            long krow = ((long)b * N + j) * H + h;
+            const float* skj = sk + krow * R;
+            float s = 0.0f;
+            for (int r = 0; r < R; ++r) s = fmaf(sqi[r], skj[r], s);
+            float ps = p * s;
+            const float* vj = v + krow * DV;
+            for (int d = 0; d < DV; ++d) acc[d] = fmaf(ps, vj[d], acc[d]);
+        }
+        for (int d = 0; d < DV; ++d) o[d] = acc[d] / den;
+        lse2[i] = m + orc_log2f(den);
+        if (lmax) lmax[i] = best;
+        if (jarg) jarg[i] = bj;
+        int32_t* t = la; la = lb; lb = t;
+    }
+    free(la);
+    free(lb);
+    free(acc);
+}
+
+static void zero_forward_row(int b, int h, long N, int H, int DV, float* out, float* lse2,
+                             int32_t* lmax, int32_t* jarg) {
+    for (long i = 0; i < N; ++i) {
+        long row = ((long)b * N + i) * H + h;
+        for (int d = 0; d < DV; ++d) out[row * DV + d] = 0.0f;
+        lse2[i] = 0.0f;
+        if (lmax) lmax[i] = 0;
+        if (jarg) jarg[i] = -1;
+    }
+}
+
 void orc_forward_direct(const float* sq, const float* sk, const float* v, const int32_t* iq,
                  const int32_t* ik, const uint8_t* hard, const float* lut, long lut_stride,
                  int B, long N, int H, int R, int DV, float* out, float* lse2, int32_t* lmax,
@@ -297,61 +360,19 @@ void orc_forward_direct(const float* sq, const float* sk, const float* v, const 
 #endif
     for (int bh = 0; bh < B * H; ++bh) {
         int b = bh / H, h = bh % H;
-        const int32_t* q = iq + (long)bh * N;
-        const int32_t* k = ik + (long)bh * N;
-        const float* tab = lut + (long)h * lut_stride;
-        int32_t* la = (int32_t*)calloc((size_t)N + 1, sizeof(int32_t));
-        int32_t* lb = (int32_t*)calloc((size_t)N + 1, sizeof(int32_t));
-        float* acc = (float*)malloc(sizeof(float) * (size_t)DV);
-        for (long i = 0; i < N; ++i) {
-            long row = ((long)b * N + i) * H + h;
-            float* o = out + row * DV;
-            if (!hard[bh]) {
-                for (int d = 0; d < DV; ++d) o[d] = 0.0f;
-                lse2[(long)bh * N + i] = 0.0f;
-                if (lmax) lmax[(long)bh * N + i] = 0;
-                if (jarg) jarg[(long)bh * N + i] = -1;
-                continue;
-            }
-            /* lb[j+1] = L[i,j]; la[j] = L[i-1,j-1] */
-            float m = 0.0f;
-            int32_t best = 0, bj = -1;
-            for (long j = 0; j <= i; ++j) {
-                if (q[i] != k[j]) { lb[j + 1] = 0; continue; }
-                int32_t L = la[j] + 1;
-                lb[j + 1] = L;
-                if (L >= best) { best = L; bj = (int32_t)j; }
-                if (tab[L] > m) m = tab[L];
-            }
-            float den = orc_exp2f(-m);
-            for (int d = 0; d < DV; ++d) acc[d] = 0.0f;
-            const float* sqi = sq + row * R;
-            for (long j = 0; j <= i; ++j) {
-                int32_t L = lb[j + 1];
-                if (!L) continue;
-                float p = orc_exp2f(tab[L] - m);
-                den = den + p;
-                long krow = ((long)b * N + j) * H + h;
-                const float* skj = sk + krow * R;
-                float s = 0.0f;
-                for (int r = 0; r < R; ++r) s = fmaf(sqi[r], skj[r], s);
-                float ps = p * s;
-                const float* vj = v + krow * DV;
-                for (int d = 0; d < DV; ++d) acc[d] = fmaf(ps, vj[d], acc[d]);
-            }
-            for (int d = 0; d < DV; ++d) o[d] = acc[d] / den;
-            lse2[(long)bh * N + i] = m + orc_log2f(den);
-            if (lmax) lmax[(long)bh * N + i] = best;
-            if (jarg) jarg[(long)bh * N + i] = bj;
-            int32_t* t = la; la = lb; lb = t;
+        long so = (long)bh * N;
+        if (!hard[bh]) {
+            zero_forward_row(b, h, N, H, DV, out, lse2 + so, lmax ? lmax + so : NULL,
+                             jarg ? jarg + so : NULL);
+            continue;
         }
-        free(la);
-        free(lb);
-        free(acc);
+        direct_forward_row(sq, sk, v, iq + so, ik + so, lut + (long)h * lut_stride, b, h, N, H,
+                           R, DV, out, lse2 + so, lmax ? lmax + so : NULL,
+                           jarg ? jarg + so : NULL, NULL);
     }
 }
 
-/* ---------------- backward ----------------
+/* ---------------- direct backward ----------------
  * Row-major traversal (i ascending, j ascending) gives every per-key accumulator its
  * ascending-i order and every per-row accumulator its ascending-j order:
  *   p = exp2(LUT[L]-lse2_i); s = sq_i.sk_j; e = dO_i.v_j (fma chains)
@@ -359,7 +380,70 @@ void orc_forward_direct(const float* sq, const float* sk, const float* v, const 
  *   dsq_i += pe*sk_j; dsk_j += pe*sq_i; dv_j += ps*dO_i
  *   u += pse; vv = fma(p,g,vv); w = fma(pse,g,w); z += p
  *   rowtau_i = (w - u*((vv - f c)/(z+f)))/(z+f),  f = exp2(-lse2_i), c = G[i+1]
- * dtau_h = sum over (b,i) of rowtau in the fixed blocked order of orc_tau_reduce. */
+ * dtau_h = sum over (b,i) of rowtau in the fixed blocked order of orc_tau_reduce.
+ * The per-row outputs (dsq, dsk, dv of row (b,h), rowtau) must be zero on entry. */
+static void direct_backward_row(const float* sq, const float* sk, const float* v,
+                                const float* dout, const int32_t* q, const int32_t* k,
+                                const float* tab, const float* gt, const float* l2v, int b,
+                                int h, long N, int H, int R, int DV, float* dsq, float* dsk,
+                                float* dv, float* rowtau) {
+    int32_t* la = (int32_t*)calloc((size_t)N + 1, sizeof(int32_t));
+    int32_t* lb = (int32_t*)calloc((size_t)N + 1, sizeof(int32_t));
+    float* dq = (float*)malloc(sizeof(float) * (size_t)R);
+    for (long i = 0; i < N; ++i) {
+        long row = ((long)b * N + i) * H + h;
+        const float* sqi = sq + row * R;
+        const float* doi = dout + row * DV;
+        float l2 = l2v[i];
+        float c = gt[i + 1];
+        float u = 0.0f, vv = 0.0f, w = 0.0f, z = 0.0f;
+        for (int r = 0; r < R; ++r) dq[r] = 0.0f;
+        for (long j = 0; j <= i; ++j) {
+            if (q[i] != k[j]) { lb[j + 1] = 0; continue; }
+            int32_t L = la[j] + 1;
+            lb[j + 1] = L;
+            float p = orc_exp2f(tab[L] - l2);
+            long krow = ((long)b * N + j) * H + h;
+            const float* skj = sk + krow * R;
+            const float* vj = v + krow * DV;
+            float s = 0.0f;
+            for (int r = 0; r < R; ++r) s = fmaf(sqi[r], skj[r], s);
+            float e = 0.0f;
+            for (int d = 0; d < DV; ++d) e = fmaf(doi[d], vj[d], e);
+            float ps = p * s, pe = p * e, pse = ps * e;
+            float g = gt[L] - c;
+            for (int r = 0; r < R; ++r) dq[r] = fmaf(pe, skj[r], dq[r]);
+            float* dkj = dsk + krow * R;
+            for (int r = 0; r < R; ++r) dkj[r] = fmaf(pe, sqi[r], dkj[r]);
+            float* dvj = dv + krow * DV;
+            for (int d = 0; d < DV; ++d) dvj[d] = fmaf(ps, doi[d], dvj[d]);
+            u = u + pse;
+            vv = fmaf(p, g, vv);
+            w = fmaf(pse, g, w);
+            z = z + p;
+        }
+        for (int r = 0; r < R; ++r) dsq[row * R + r] = dq[r];
+        float f = orc_exp2f(-l2);
+        float mass = z + f;
+        float mean = fmaf(-f, c, vv) / mass;
+        rowtau[i] = fmaf(-u, mean, w) / mass;
+        int32_t* t = la; la = lb; lb = t;
+    }
+    free(la);
+    free(lb);
+    free(dq);
+}
+
+static void zero_backward_row(int b, int h, long N, int H, int R, int DV, float* dsq,
+                              float* dsk, float* dv, float* rowtau) {
+    for (long x = 0; x < N; ++x) {
+        long row = ((long)b * N + x) * H + h;
+        for (int r = 0; r < R; ++r) { dsq[row * R + r] = 0.0f; dsk[row * R + r] = 0.0f; }
+        for (int d = 0; d < DV; ++d) dv[row * DV + d] = 0.0f;
+        rowtau[x] = 0.0f;
+    }
+}
+
 void orc_backward_direct(const float* sq, const float* sk, const float* v, const float* dout,
                   const int32_t* iq, const int32_t* ik, const uint8_t* hard, const float* lut,
                   const float* dlut, long lut_stride, const float* lse2in, int B, long N, int H,
@@ -370,64 +454,56 @@ void orc_backward_direct(const float* sq, const float* sk, const float* v, const
 #endif
     for (int bh = 0; bh < B * H; ++bh) {
         int b = bh / H, h = bh % H;
-        const int32_t* q = iq + (long)bh * N;
-        const int32_t* k = ik + (long)bh * N;
-        const float* tab = lut + (long)h * lut_stride;
-        const float* gt = dlut + (long)h * lut_stride;
-        int32_t* la = (int32_t*)calloc((size_t)N + 1, sizeof(int32_t));
-        int32_t* lb = (int32_t*)calloc((size_t)N + 1, sizeof(int32_t));
-        float* dq = (float*)malloc(sizeof(float) * (size_t)R);
-        for (long x = 0; x < N; ++x) {
-            long row = ((long)b * N + x) * H + h;
-            for (int r = 0; r < R; ++r) { dsq[row * R + r] = 0.0f; dsk[row * R + r] = 0.0f; }
-            for (int d = 0; d < DV; ++d) dv[row * DV + d] = 0.0f;
-            rowtau[(long)bh * N + x] = 0.0f;
-        }
-        if (hard[bh]) {
-            for (long i = 0; i < N; ++i) {
-                long row = ((long)b * N + i) * H + h;
-                const float* sqi = sq + row * R;
-                const float* doi = dout + row * DV;
-                float l2 = lse2in[(long)bh * N + i];
-                float c = gt[i + 1];
-                float u = 0.0f, vv = 0.0f, w = 0.0f, z = 0.0f;
-                for (int r = 0; r < R; ++r) dq[r] = 0.0f;
-                for (long j = 0; j <= i; ++j) {
-                    if (q[i] != k[j]) { lb[j + 1] = 0; continue; }
-                    int32_t L = la[j] + 1;
-                    lb[j + 1] = L;
-                    float p = orc_exp2f(tab[L] - l2);
-                    long krow = ((long)b * N + j) * H + h;
-                    const float* skj = sk + krow * R;
-                    const float* vj = v + krow * DV;
-                    float s = 0.0f;
-                    for (int r = 0; r < R; ++r) s = fmaf(sqi[r], skj[r], s);
-                    float e = 0.0f;
-                    for (int d = 0; d < DV; ++d) e = fmaf(doi[d], vj[d], e);
-                    float ps = p * s, pe = p * e, pse = ps * e;
-                    float g = gt[L] - c;
-                    for (int r = 0; r < R; ++r) dq[r] = fmaf(pe, skj[r], dq[r]);
-                    float* dkj = dsk + krow * R;
-                    for (int r = 0; r < R; ++r) dkj[r] = fmaf(pe, sqi[r], dkj[r]);
-                    float* dvj = dv + krow * DV;
-                    for (int d = 0; d < DV; ++d) dvj[d] = fmaf(ps, doi[d], dvj[d]);
-                    u = u + pse;
-                    vv = fmaf(p, g, vv);
-                    w = fmaf(pse, g, w);
-                    z = z + p;
-                }
-                    for (int r = 0; r < R; ++r) dsq[row * R + r] = dq[r];
-                float f = orc_exp2f(-l2);
-                float mass = z + f;
-                float mean = fmaf(-f, c, vv) / mass;
-                rowtau[(long)bh * N + i] = fmaf(-u, mean, w) / mass;
-                int32_t* t = la; la = lb; lb = t;
-            }
-        }
-        free(la);
-        free(lb);
-        free(dq);
+        long so = (long)bh * N;
+        zero_backward_row(b, h, N, H, R, DV, dsq, dsk, dv, rowtau + so);
+        if (!hard[bh]) continue;
+        direct_backward_row(sq, sk, v, dout, iq + so, ik + so, lut + (long)h * lut_stride,
+                            dlut + (long)h * lut_stride, lse2in + so, b, h, N, H, R, DV, dsq,
+                            dsk, dv, rowtau + so);
     }
+}
+
+/* ---------------- dense-row classification ----------------
+ * The HIP path computes a hard row with the direct definition above ("dense" row) when its
+ * labels collide often:
+ *   M = sum over 4096 label buckets of (#queries in the bucket) * (#keys in the bucket),
+ *   bucket(label) = ((uint32)label * 0x9E3779B1) >> 20 (the top 12 bits of a multiplicative
+ *   hash), dense iff 64 * M > N^2 and N <= DENSE_MAX_N (its match-length boundaries are
+ *   16-bit).
+ * M is at least the exact collision count W = sum over labels of #queries * #keys (equal
+ * labels share a bucket) and exceeds it only by bucket sharing (~N^2/4096 for many distinct
+ * labels).  Dense rows have Theta(N^2) valid pairs; the decomposed definition's label scans
+ * and bigram walks would be serial in the largest label group, or cubic in N, there.  Random
+ * 256-symbol labels give M ~ N^2 / 256.  Soft rows are never dense. */
+#define DENSE_MAX_N 65536L
+#define DENSE_BUCKETS 4096
+
+static inline uint32_t label_bucket(int32_t label) {
+    return ((uint32_t)label * 0x9E3779B1u) >> 20;
+}
+
+uint64_t orc_bucket_collisions(const int32_t* q, const int32_t* k, long N) {
+    uint64_t cq[DENSE_BUCKETS], ck[DENSE_BUCKETS];
+    memset(cq, 0, sizeof(cq));
+    memset(ck, 0, sizeof(ck));
+    for (long x = 0; x < N; ++x) {
+        cq[label_bucket(q[x])]++;
+        ck[label_bucket(k[x])]++;
+    }
+    uint64_t m = 0;
+    for (int b = 0; b < DENSE_BUCKETS; ++b) m += cq[b] * ck[b];
+    return m;
+}
+
+int orc_dense_row(const int32_t* q, const int32_t* k, long N, int hard) {
+    if (!hard || N > DENSE_MAX_N) return 0;
+    return orc_bucket_collisions(q, k, N) * 64u > (uint64_t)N * (uint64_t)N;
+}
+
+void orc_dense_rows(const int32_t* iq, const int32_t* ik, const uint8_t* hard, int BH, long N,
+                    uint8_t* dense) {
+    for (int bh = 0; bh < BH; ++bh)
+        dense[bh] = (uint8_t)orc_dense_row(iq + (long)bh * N, ik + (long)bh * N, N, hard[bh]);
 }
 
 /* dtau_h: for each head, the B*N row terms in (b, i) order are cut into blocks of
@@ -557,14 +633,14 @@ static void forward_impl(const float* sq, const float* sk, const float* v, const
                          const int32_t* ik, const uint8_t* hard, const float* lut,
                          long lut_stride, int B, long N, int H, int R, int DV, float* out,
                          float* lse2, int32_t* lmax, int32_t* jarg, int threads,
-                         const int32_t* wlo);
+                         const int32_t* wlo, const uint8_t* dense);
 
 void orc_forward(const float* sq, const float* sk, const float* v, const int32_t* iq,
                  const int32_t* ik, const uint8_t* hard, const float* lut, long lut_stride,
                  int B, long N, int H, int R, int DV, float* out, float* lse2, int32_t* lmax,
                  int32_t* jarg, int threads) {
     forward_impl(sq, sk, v, iq, ik, hard, lut, lut_stride, B, N, H, R, DV, out, lse2, lmax,
-                 jarg, threads, NULL);
+                 jarg, threads, NULL, NULL);
 }
 
 /* orc_forward with query resets: wlo [B*H*N] holds, per query, the last reset position at or
@@ -576,14 +652,25 @@ void orc_forward_reset(const float* sq, const float* sk, const float* v, const i
                        float* lse2, int32_t* lmax, int32_t* jarg, int threads,
                        const int32_t* wlo) {
     forward_impl(sq, sk, v, iq, ik, hard, lut, lut_stride, B, N, H, R, DV, out, lse2, lmax,
-                 jarg, threads, wlo);
+                 jarg, threads, wlo, NULL);
+}
+
+/* The forward with an explicit row classification: dense [B*H] (1: the direct definition,
+ * 0: the decomposed one), or NULL for orc_dense_row's.  wlo may be NULL. */
+void orc_forward_flags(const float* sq, const float* sk, const float* v, const int32_t* iq,
+                       const int32_t* ik, const uint8_t* hard, const float* lut,
+                       long lut_stride, int B, long N, int H, int R, int DV, float* out,
+                       float* lse2, int32_t* lmax, int32_t* jarg, int threads,
+                       const int32_t* wlo, const uint8_t* dense) {
+    forward_impl(sq, sk, v, iq, ik, hard, lut, lut_stride, B, N, H, R, DV, out, lse2, lmax,
+                 jarg, threads, wlo, dense);
 }
 
 static void forward_impl(const float* sq, const float* sk, const float* v, const int32_t* iq,
                          const int32_t* ik, const uint8_t* hard, const float* lut,
                          long lut_stride, int B, long N, int H, int R, int DV, float* out,
                          float* lse2, int32_t* lmax, int32_t* jarg, int threads,
-                         const int32_t* wlo) {
+                         const int32_t* wlo, const uint8_t* dense) {
 #ifdef _OPENMP
     if (threads > 0) omp_set_num_threads(threads);
 #pragma omp parallel for schedule(dynamic, 1)
@@ -601,6 +688,13 @@ static void forward_impl(const float* sq, const float* sk, const float* v, const
                 if (lmax) lmax[(long)bh * N + i] = 0;
                 if (jarg) jarg[(long)bh * N + i] = -1;
             }
+            continue;
+        }
+        if (dense ? dense[bh] : orc_dense_row(q, k, N, 1)) {
+            const long so = (long)bh * N;
+            direct_forward_row(sq, sk, v, q, k, tab, b, h, N, H, R, DV, out, lse2 + so,
+                               lmax ? lmax + so : NULL, jarg ? jarg + so : NULL,
+                               wlo ? wlo + so : NULL);
             continue;
         }
         int32_t* qo = (int32_t*)malloc(sizeof(int32_t) * (size_t)N);
@@ -703,10 +797,28 @@ static void forward_impl(const float* sq, const float* sk, const float* v, const
  *       s = chain(sq_i.sk_j); e = tree(dO_i.v_j); cdk[r] = fma(dp*e, sq_i[r], cdk[r]);
  *       cdv[d] = fma(dp*s, dO_i[d], cdv[d])
  *   dsk[r] = dsk0[r] + cdk[r];  dv[d] = dv0[d] + cdv[d]  (only for keys with bigram pairs). */
+void orc_backward_flags(const float* sq, const float* sk, const float* v, const float* dout,
+                        const int32_t* iq, const int32_t* ik, const uint8_t* hard,
+                        const float* lut, const float* dlut, long lut_stride,
+                        const float* lse2in, int B, long N, int H, int R, int DV, float* dsq,
+                        float* dsk, float* dv, float* rowtau, int threads,
+                        const uint8_t* dense);
+
 void orc_backward(const float* sq, const float* sk, const float* v, const float* dout,
                   const int32_t* iq, const int32_t* ik, const uint8_t* hard, const float* lut,
                   const float* dlut, long lut_stride, const float* lse2in, int B, long N, int H,
                   int R, int DV, float* dsq, float* dsk, float* dv, float* rowtau, int threads) {
+    orc_backward_flags(sq, sk, v, dout, iq, ik, hard, lut, dlut, lut_stride, lse2in, B, N, H,
+                       R, DV, dsq, dsk, dv, rowtau, threads, NULL);
+}
+
+/* The backward with an explicit row classification (dense as in orc_forward_flags). */
+void orc_backward_flags(const float* sq, const float* sk, const float* v, const float* dout,
+                        const int32_t* iq, const int32_t* ik, const uint8_t* hard,
+                        const float* lut, const float* dlut, long lut_stride,
+                        const float* lse2in, int B, long N, int H, int R, int DV, float* dsq,
+                        float* dsk, float* dv, float* rowtau, int threads,
+                        const uint8_t* dense) {
 #ifdef _OPENMP
     if (threads > 0) omp_set_num_threads(threads);
 #pragma omp parallel for schedule(dynamic, 1)
@@ -725,6 +837,11 @@ void orc_backward(const float* sq, const float* sk, const float* v, const float*
             rowtau[(long)bh * N + x] = 0.0f;
         }
         if (!hard[bh]) continue;
+        if (dense ? dense[bh] : orc_dense_row(q, k, N, 1)) {
+            direct_backward_row(sq, sk, v, dout, q, k, tab, gt, l2v, b, h, N, H, R, DV, dsq,
+                                dsk, dv, rowtau + (long)bh * N);
+            continue;
+        }
         int32_t* qo = (int32_t*)malloc(sizeof(int32_t) * (size_t)N);
         int32_t* ko = (int32_t*)malloc(sizeof(int32_t) * (size_t)N);
         float* M = (float*)malloc(sizeof(float) * (size_t)R * DV);
