@@ -41,8 +41,8 @@ SIGNATURES = {
     "dism_hard_packed_backward": [_P, _P, _P, _P, _I32, _P, _I64, _P, _P, _I64, _I64, _P, _I64,
                                   _I64, _I32, _I32, _P, _I64, _P, _P, _P, _P, _P, _P],
     "dism_vocab_labels": [_P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P],
-    "dism_hard_prefill": [_P, _P, _P, _I32, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32,
-                          _P, _I64, _P, _P, _P],
+    "dism_hard_prefill": [_P, _P, _P, _I32, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32,
+                          _I32, _P, _I64, _P, _P, _P],
     "dism_decoder_init": [_P, _I64, _I64, _I32, _I32, _I64, _I32, _I32, _P],
     "dism_decoder_prime": [_P, _I64, _I64, _I64, _I32, _I32, _I64, _I32, _I32, _I64, _P, _P,
                            _P, _P, _P, _P, _I64, _P],

@@ -52,7 +52,7 @@ hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 struct Layout {
     int64_t corder, clab, ctab, bpos[2], blab[2], bplab[2], btab[2], shift, tmp[3];
     int64_t stage[2][2], bhcount[2], own[2], ocount, mode, onebyte;
-    int64_t pnb, prow, mcount, mdig, total;
+    int64_t pnb, prow, mcount, mdig, dflag, dlist, dcount, dbound, total;
     int prow_stride;
 };
 
@@ -123,6 +123,10 @@ Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     L.tmp[2] = take(BH * N * 4);
     L.pnb = take(BH * N * 4);
     L.prow = take(BH * N * L.prow_stride * 4);
+    L.dflag = take(BH * 4);
+    L.dlist = take(BH * 4);
+    L.dcount = take(4 * 4);
+    L.dbound = take(N <= dism::DENSE_MAX_N ? BH * dism::dense_row_entries((int)N) * 2 : 0);
     L.total = o;
     return L;
 }
@@ -155,6 +159,10 @@ dism::Orders orders(const Layout& L, void* ws) {
     o.onebyte = at<int32_t>(ws, L.onebyte);
     o.mcount = at<int32_t>(ws, L.mcount);
     o.mdig = at<int32_t>(ws, L.mdig);
+    o.dflag = at<int32_t>(ws, L.dflag);
+    o.dlist = at<int32_t>(ws, L.dlist);
+    o.dcount = at<int32_t>(ws, L.dcount);
+    o.dbound = at<uint16_t>(ws, L.dbound);
     return o;
 }
 
@@ -199,12 +207,37 @@ int32_t check_common(const void* sq, const void* sk, const void* v, int32_t dtyp
     return DISM_OK;
 }
 
+// Orders, plans and dense-row data of one call (dism_hard_prepare).  cls_n > 0: the
+// dense-row classification counts only each row's first cls_n positions (a prefill's rows are
+// padded after the real tokens); wlo: the query resets the dense rows' boundaries follow.
+int32_t prepare_impl(const void* sq, const void* sk, const void* v, int32_t dtype,
+                     const int32_t* iq, const int32_t* ik, int64_t B, int64_t N, int64_t H,
+                     int32_t R, int32_t DV, void* workspace, int64_t workspace_bytes,
+                     int64_t cls_n, const int32_t* wlo, void* stream) {
+    int32_t st = check_common(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
+                              workspace_bytes, "hard prepare");
+    if (st) return st;
+    const Layout L = layout(B, N, H, R, DV);
+    dism::SortArgs sa{};
+    sa.lab[0] = iq;
+    sa.lab[1] = ik;
+    sa.BH = B * H;
+    sa.n = (int)N;
+    sa.cls_n = (int)cls_n;
+    for (int t = 0; t < 3; ++t) sa.tmp[t] = at<int32_t>(workspace, L.tmp[t]);
+    sa.o = orders(L, workspace);
+    sa.pnb = at<int32_t>(workspace, L.pnb);
+    dism::PathArgs pa = path(L, workspace, B, N, H, iq, ik, nullptr, nullptr, 0, nullptr, 0);
+    pa.wlo = wlo;
+    return hip_status(dism::launch_prepare(sa, pa, S(stream)), "hard prepare");
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* dism_last_error(void) { return g_error.c_str(); }
-int32_t dism_abi_version(void) { return 5; }
+int32_t dism_abi_version(void) { return 6; }
 
 int32_t dism_sign_labels(const void* x, int32_t dtype, int64_t B, int64_t N, int64_t H, int32_t d,
                          int32_t* labels, void* stream) {
@@ -280,20 +313,8 @@ int32_t dism_hard_prepare(const void* sq, const void* sk, const void* v, int32_t
                           const int32_t* iq, const int32_t* ik, int64_t B, int64_t N, int64_t H,
                           int32_t R, int32_t DV, void* workspace, int64_t workspace_bytes,
                           void* stream) {
-    int32_t st = check_common(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
-                              workspace_bytes, "hard prepare");
-    if (st) return st;
-    const Layout L = layout(B, N, H, R, DV);
-    dism::SortArgs sa{};
-    sa.lab[0] = iq;
-    sa.lab[1] = ik;
-    sa.BH = B * H;
-    sa.n = (int)N;
-    for (int t = 0; t < 3; ++t) sa.tmp[t] = at<int32_t>(workspace, L.tmp[t]);
-    sa.o = orders(L, workspace);
-    sa.pnb = at<int32_t>(workspace, L.pnb);
-    dism::PathArgs pa = path(L, workspace, B, N, H, iq, ik, nullptr, nullptr, 0, nullptr, 0);
-    return hip_status(dism::launch_prepare(sa, pa, S(stream)), "hard prepare");
+    return prepare_impl(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace, workspace_bytes,
+                        0, nullptr, stream);
 }
 
 int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t dtype,
@@ -325,8 +346,11 @@ int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t
     int32_t st2;
     if ((st2 = hip_status(dism::launch_scan_forward(a, R, DV, dtype, S(stream)), "hard readout")))
         return st2;
-    return hip_status(dism::launch_pairs_finish(a, R, DV, dtype, S(stream)),
-                      "hard readout pairs");
+    if ((st2 = hip_status(dism::launch_pairs_finish(a, R, DV, dtype, S(stream)),
+                          "hard readout pairs")))
+        return st2;
+    return hip_status(dism::launch_dense_forward(a, R, DV, dtype, S(stream)),
+                      "hard readout dense rows");
 }
 
 int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t dtype,
@@ -393,7 +417,9 @@ int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t
     a.fwd_phase = 2;
     if ((st = hip_status(dism::launch_scan_forward(a, R, DV, dtype, s), "hard forward")))
         return st;
-    return hip_status(dism::launch_pairs_finish(a, R, DV, dtype, s), "hard forward pairs");
+    if ((st = hip_status(dism::launch_pairs_finish(a, R, DV, dtype, s), "hard forward pairs")))
+        return st;
+    return hip_status(dism::launch_dense_forward(a, R, DV, dtype, s), "hard forward dense rows");
 }
 
 }  // extern "C"
@@ -459,7 +485,11 @@ int32_t dism_hard_backward_queries(const void* sq, const void* sk, const void* v
     a.dlut = dlut;
     a.dsq = dsq;
     a.rowtau = rowtau;
-    return hip_status(dism::launch_scan_rows(a, R, DV, dtype, S(stream)), "hard backward rows");
+    if ((st = hip_status(dism::launch_scan_rows(a, R, DV, dtype, S(stream)),
+                         "hard backward rows")))
+        return st;
+    return hip_status(dism::launch_dense_rows(a, R, DV, dtype, S(stream)),
+                      "hard backward dense rows");
 }
 
 int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, const void* dout,
@@ -477,7 +507,11 @@ int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, c
     if (!dsk || !dv) return fail(DISM_ERR_INVALID, "hard backward: null pointer");
     a.dsk = dsk;
     a.dv = dv;
-    return hip_status(dism::launch_scan_keys(a, R, DV, dtype, S(stream)), "hard backward keys");
+    if ((st = hip_status(dism::launch_scan_keys(a, R, DV, dtype, S(stream)),
+                         "hard backward keys")))
+        return st;
+    return hip_status(dism::launch_dense_keys(a, R, DV, dtype, S(stream)),
+                      "hard backward dense keys");
 }
 
 int32_t dism_hard_backward_key_pairs(const void* sq, const void* sk, const void* v,
@@ -717,6 +751,7 @@ int32_t dism_hard_packed_readout(const void* sq, const void* sk, const void* v, 
     a.jarg = jarg;
     if ((st = hip_status(dism::launch_scan_forward(a, R, DV, dtype, S(stream)), what))) return st;
     if ((st = hip_status(dism::launch_pairs_finish(a, R, DV, dtype, S(stream)), what))) return st;
+    if ((st = hip_status(dism::launch_dense_forward(a, R, DV, dtype, S(stream)), what))) return st;
     dism::PackedZero z = packed_zero(hard, rows, N, H, R, DV);
     z.out = out;
     z.out_dtype = out_dtype;
@@ -757,6 +792,8 @@ int32_t dism_hard_packed_backward(const void* sq, const void* sk, const void* v,
     if ((st = hip_status(dism::launch_scan_rows(a, R, DV, dtype, s), what))) return st;
     if ((st = hip_status(dism::launch_scan_keys(a, R, DV, dtype, s), what))) return st;
     if ((st = hip_status(dism::launch_pairs_keys(a, R, DV, dtype, s), what))) return st;
+    if ((st = hip_status(dism::launch_dense_rows(a, R, DV, dtype, s), what))) return st;
+    if ((st = hip_status(dism::launch_dense_keys(a, R, DV, dtype, s), what))) return st;
     dism::PackedZero z = packed_zero(hard, rows, N, H, R, DV);
     z.dsq = dsq;
     z.dsk = dsk;
@@ -855,13 +892,15 @@ int64_t dism_hard_prefill_workspace_bytes(int64_t B, int64_t N, int64_t H, int32
 
 int32_t dism_hard_prefill(const void* sq, const void* sk, const void* v, int32_t dtype,
                           const int32_t* iq, const int32_t* ik, const uint8_t* reset,
-                          const float* lut, int64_t lut_stride, int64_t B, int64_t N, int64_t H,
-                          int32_t R, int32_t DV, void* workspace, int64_t workspace_bytes,
-                          float* out, float* lse2, void* stream) {
+                          const float* lut, int64_t lut_stride, int64_t B, int64_t N,
+                          int64_t n_valid, int64_t H, int32_t R, int32_t DV, void* workspace,
+                          int64_t workspace_bytes, float* out, float* lse2, void* stream) {
     const char* what = "hard prefill";
     int32_t st = check_common(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
                               workspace_bytes, what);
     if (st) return st;
+    if (n_valid <= 0 || n_valid > N)
+        return fail(DISM_ERR_INVALID, "%s: valid length must be in [1, N]", what);
     if (!lut || !out || !lse2) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
     if (lut_stride < N + 1) return fail(DISM_ERR_INVALID, "hard log-weight table is too short");
     if (!aligned16(out)) return fail(DISM_ERR_INVALID, "%s: output must be 16-byte aligned", what);
@@ -877,8 +916,8 @@ int32_t dism_hard_prefill(const void* sq, const void* sk, const void* v, int32_t
         return st;
     if (reset && (st = hip_status(dism::launch_reset_starts(reset, B * H, N, wlo, s), what)))
         return st;
-    if ((st = dism_hard_prepare(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
-                                workspace_bytes, stream)))
+    if ((st = prepare_impl(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
+                           workspace_bytes, n_valid, reset ? wlo : nullptr, stream)))
         return st;
     dism::PathArgs a = path(L, workspace, B, N, H, iq, ik, ones, nullptr, 0, lut, lut_stride);
     a.wlo = reset ? wlo : nullptr;
@@ -889,7 +928,8 @@ int32_t dism_hard_prefill(const void* sq, const void* sk, const void* v, int32_t
     a.out_dtype = DISM_F32;
     a.lse2 = lse2;
     if ((st = hip_status(dism::launch_scan_forward(a, R, DV, dtype, s), what))) return st;
-    return hip_status(dism::launch_pairs_finish(a, R, DV, dtype, s), what);
+    if ((st = hip_status(dism::launch_pairs_finish(a, R, DV, dtype, s), what))) return st;
+    return hip_status(dism::launch_dense_forward(a, R, DV, dtype, s), what);
 }
 
 int64_t dism_decoder_state_bytes(int64_t rows, int32_t R, int32_t DV, int64_t capacity,

@@ -49,7 +49,23 @@ struct Orders {
     // [B*H][32], then per-row digit lists [B*H][8]
     int32_t* mcount;
     int32_t* mdig;
+    // dense rows (dism_dense.hip): per-row flag [B*H] (1: the row's bucketed label
+    // collisions exceed N^2/64), the flagged rows ascending [B*H] and their count [1], and the
+    // 16-bit boundary rows L[64s - 1, j], j < 64s, of every 64-row query strip s >= 1
+    // ([B*H][dense_row_entries(N)], only when N <= DENSE_MAX_N)
+    int32_t* dflag;
+    int32_t* dlist;
+    int32_t* dcount;
+    uint16_t* dbound;
 };
+
+constexpr int DENSE_MAX_N = 65536;   // longest row of the dense path (16-bit lengths)
+constexpr int DENSE_BUCKETS = 4096;  // label buckets of the classification
+__host__ __device__ inline long dense_strip_offset(int s) { return 32L * s * (s - 1); }
+__host__ __device__ inline long dense_row_entries(int n) {
+    const int q = (n + 63) / 64;
+    return dense_strip_offset(q);
+}
 
 constexpr int PREP_N = 16384;     // longest row of the LDS-resident prepare kernel
 constexpr int MSORT_SEGMENTS = 32;  // most workgroups per row of the multi-block sort
@@ -65,6 +81,7 @@ struct SortArgs {
     Orders o;
     int role_base;          // first role of a launch (blockIdx.y + role_base)
     int lds_rows;           // rows with one label byte go to prepare_lds_kernel (sort skips them)
+    int cls_n;              // positions the dense-row classification counts (0: all n)
 };
 
 // Per query row record (prow, valid when the row's bigram pair count pnb > 0):
@@ -219,6 +236,14 @@ hipError_t launch_scan_forward(const PathArgs& a, int R, int DV, int dtype, hipS
 hipError_t launch_pairs_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_scan_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_pairs_keys(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
+// dense rows (dism_dense.hip): classification (before the label scans), the row list and the
+// boundary rows (before the dense kernels), then the tile kernels for the flagged hard rows
+hipError_t launch_dense_classify(const int32_t* iq, const int32_t* ik, long BH, int n,
+                                 int cls_n, int32_t* dflag, hipStream_t s);
+hipError_t launch_dense_prepare(const PathArgs& a, hipStream_t s);
+hipError_t launch_dense_forward(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
+hipError_t launch_dense_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
+hipError_t launch_dense_keys(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_scan_keys(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 
 }  // namespace dism

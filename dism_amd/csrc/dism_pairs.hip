@@ -198,11 +198,13 @@ __global__ __launch_bounds__(LIST_THREADS) void owner_lists_kernel(PathArgs a) {
     const int bh = blockIdx.x, side = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int BH = a.B * a.H, n = a.n;
     const int32_t* cnt = a.o.bhcount[side];
+    const int32_t* dense = a.o.dflag;  // dense rows' pairs belong to dism_dense.hip
     int before[3] = {0, 0, 0}, total[3] = {0, 0, 0};
     for (int r = tid; r < BH; r += LIST_THREADS) {
+        const bool drop = dense[r] != 0;
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
-            const int v = cnt[(long)r * 4 + c];
+            const int v = drop ? 0 : cnt[(long)r * 4 + c];
             total[c] += v;
             if (r < bh) before[c] += v;
         }
@@ -237,7 +239,7 @@ __global__ __launch_bounds__(LIST_THREADS) void owner_lists_kernel(PathArgs a) {
     int4* own = a.o.own[side];
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
-        const int m = cnt[(long)bh * 4 + c];
+        const int m = dense[bh] ? 0 : cnt[(long)bh * 4 + c];
         const int4* src = a.o.stage[side][c == 1 ? 1 : 0] + so;
         for (int k = tid; k < m; k += LIST_THREADS) {
             const int4 rec = src[c == 2 ? n - 1 - k : k];
@@ -270,6 +272,9 @@ static SortArgs sort_args(const SortArgs& sa, const PathArgs& pa) {
 
 hipError_t launch_prepare_labels(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
     const SortArgs b = sort_args(sa, pa);
+    // the dense-row flags first: the label scans skip dense rows, the owner lists drop them
+    hipError_t e = launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n, sa.o.dflag, s);
+    if (e != hipSuccess) return e;
     // prepare_lds_kernel role 0 orders every row: in LDS, or in global memory for rows whose
     // labels differ in more than one byte
     if (!b.lds_rows) return launch_msort_labels(b, s);
@@ -287,7 +292,8 @@ hipError_t launch_prepare_pairs(const SortArgs& sa, const PathArgs& pa, hipStrea
         if (e == hipSuccess) e = launch_pair_plan(pa, s);
         if (e == hipSuccess) e = launch_prepare_lds(b, 1, 1, s);
     }
-    return e != hipSuccess ? e : launch_owner_lists(pa, s);
+    if (e == hipSuccess) e = launch_owner_lists(pa, s);
+    return e != hipSuccess ? e : launch_dense_prepare(pa, s);
 }
 
 hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
@@ -296,12 +302,15 @@ hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s)
         const hipError_t e = launch_prepare_labels(sa, pa, s);
         return e != hipSuccess ? e : launch_prepare_pairs(sa, pa, s);
     }
-    // one stream: both LDS roles in one grid (64-block roles side by side), then the bigram
-    // sorts of the other rows, the plan and the owner lists
-    hipError_t e = launch_prepare_lds(b, 0, 2, s);
+    // one stream: the dense-row flags, both LDS roles in one grid (64-block roles side by
+    // side), then the bigram sorts of the other rows, the plan, the owner lists and the dense
+    // rows' list and boundaries
+    hipError_t e = launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n, sa.o.dflag, s);
+    if (e == hipSuccess) e = launch_prepare_lds(b, 0, 2, s);
     if (e == hipSuccess) e = launch_sort(b, 1, 2, s);
     if (e == hipSuccess) e = launch_pair_plan(pa, s);
-    return e != hipSuccess ? e : launch_owner_lists(pa, s);
+    if (e == hipSuccess) e = launch_owner_lists(pa, s);
+    return e != hipSuccess ? e : launch_dense_prepare(pa, s);
 }
 
 // Work of the persistent pair kernels of one side: items [0, i0) small class (16 owners

@@ -82,6 +82,8 @@ __device__ __forceinline__ bool scan_item(const PathArgs& a, Item& it) {
     const int item = xcd_work_item();
     it.bh = item >> 8;
     if (it.bh >= a.B * a.H) return false;
+    // dense hard rows are computed whole by the tile kernels (dism_dense.hip)
+    if (a.o.dflag[it.bh] && a.hard[it.bh]) return false;
     it.bucket = item & 255;
     it.b = it.bh / a.H;
     it.h = it.bh - it.b * a.H;
@@ -128,7 +130,9 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
     if (!scan_item(a, it)) return;
     // fwd_phase 1: rows whose labels differ in one byte, pair counts from the histogram;
     // 2: the other rows, pair counts from the plan (pnb); 0: every row from pnb
-    const int onebyte = a.fwd_phase ? a.o.onebyte[it.bh] : 0;
+    // (phase 1's per-wave histogram holds 16-bit counts: rows of 65536 and more keys take
+    // their pair counts from the plan, in phase 2)
+    const int onebyte = a.fwd_phase ? (a.o.onebyte[it.bh] && a.n < 65536) : 0;
     if ((a.fwd_phase == 1 && !onebyte) || (a.fwd_phase == 2 && onebyte)) return;
     const bool hist_nb = a.fwd_phase == 1;
     const int lshift = hist_nb ? a.o.shift[it.bh] : 0;

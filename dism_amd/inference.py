@@ -105,7 +105,7 @@ class PreparedHardPrefill:
         with torch.cuda.device(self.device):
             _lib.call("dism_hard_prefill", a.data_ptr(), c.data_ptr(), d.data_ptr(), code,
                       self.iq.data_ptr(), self.ik.data_ptr(), reset, self.lut.data_ptr(),
-                      self.lut.shape[1], b, self.n_pad, h, r, dv, ws.data_ptr(), nbytes,
+                      self.lut.shape[1], b, self.n_pad, self.n, h, r, dv, ws.data_ptr(), nbytes,
                       out.data_ptr(), lse2.data_ptr(), _stream(self.device))
         self.last_lse2 = lse2[..., :self.n]
         return out[:, :self.n] if self.n_pad != self.n else out

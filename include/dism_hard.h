@@ -254,14 +254,16 @@ int64_t dism_hard_prefill_workspace_bytes(int64_t B, int64_t N, int64_t H, int32
 
 /* Hard prefill: out [B,N,H,DV] fp32 and lse2 [B,H,N] for labels iq, ik [B,H,N] with optional
  * query resets [B,H,N] (uint8, NULL = none): prepare + readout of the training forward, every
- * row hard.  lut_stride >= N + 1.  Replaces HardDismPrefill's plan + execute
+ * row hard.  lut_stride >= N + 1.  The first n_valid positions of each row are the real tokens
+ * (1 <= n_valid <= N; positions past it are padding that the dense-row classification does
+ * not count).  Replaces HardDismPrefill's plan + execute
  * (dism_v3/python/flash_dism/inference/prefill_batch.py:67-118, README.md:229-292); equal
- * bit for bit to dism_hard_readout's fp32 output when there are no resets. */
+ * bit for bit to dism_hard_readout's fp32 output when there are no resets and no padding. */
 int32_t dism_hard_prefill(const void* sq, const void* sk, const void* v, int32_t dtype,
                           const int32_t* iq, const int32_t* ik, const uint8_t* reset,
-                          const float* lut, int64_t lut_stride, int64_t B, int64_t N, int64_t H,
-                          int32_t R, int32_t DV, void* workspace, int64_t workspace_bytes,
-                          float* out, float* lse2, void* stream);
+                          const float* lut, int64_t lut_stride, int64_t B, int64_t N,
+                          int64_t n_valid, int64_t H, int32_t R, int32_t DV, void* workspace,
+                          int64_t workspace_bytes, float* out, float* lse2, void* stream);
 
 /* Incremental decoder state bytes for rows = B*H, capacity positions and `slots` label-table
  * entries per row (a power of two >= 64; at least twice the distinct key labels a row will

@@ -178,6 +178,30 @@ def dense_rows(iq, ik, hard):
     return out.reshape(B, H)
 
 
+def packed_dense_flags(iq, ik, offsets):
+    """Row classification of a packed call (B = 1): the HIP path classifies each head row of
+    its document-tagged labels tag = rank * docs + d (rank: dense rank of the raw label among
+    the row's distinct labels in unsigned order; d: index among the non-empty documents).
+    Returns uint8 [1, H]."""
+    iq, ik = _i32(iq), _i32(ik)
+    _, H, N = iq.shape
+    offs = [int(x) for x in offsets]
+    docs = [(a, z) for a, z in zip(offs, offs[1:]) if z > a]
+    dindex = np.empty(N, np.uint64)
+    for d, (a, z) in enumerate(docs):
+        dindex[a:z] = d
+    tq = np.empty_like(iq)
+    tk = np.empty_like(ik)
+    for h in range(H):
+        uq, uk = iq[0, h].view(np.uint32), ik[0, h].view(np.uint32)
+        uniq = np.unique(np.concatenate([uq, uk]))
+        for src, dst in ((uq, tq), (uk, tk)):
+            rank = np.searchsorted(uniq, src).astype(np.uint64)
+            tag = (rank * np.uint64(len(docs)) + dindex) & np.uint64(0xFFFFFFFF)
+            dst[0, h] = tag.astype(np.uint32).view(np.int32)
+    return dense_rows(tq, tk, np.ones((1, H), bool))
+
+
 def bucket_collisions(q, k):
     """M of one row: sum over the 4096 label buckets (top 12 bits of label * 0x9E3779B1) of
     (#queries in the bucket) x (#keys in the bucket)."""

@@ -41,7 +41,7 @@ def test_python_signatures_cover_header(lib):
 
 
 def test_version_and_workspace(lib):
-    assert lib.dism_abi_version() == 5
+    assert lib.dism_abi_version() == 6
     ws = lib.dism_hard_workspace_bytes(4, 16384, 16, 8, 64, 0)
     assert ws > 4 * 16384 * 16 * 64 * 4  # holds one fp32 readout row per query
     assert ws % 256 == 0

@@ -51,16 +51,20 @@ def _expected(x, offsets, hard):
     g = [np.zeros(sq.shape, np.float32), np.zeros(sk.shape, np.float32),
          np.zeros(v.shape, np.float32)]
     rowtau = np.zeros((1, h, n), np.float32)
+    # each head row of the packed call is computed with its own classification (dense rows:
+    # the direct definition) for all of its documents
+    dense = oracle.packed_dense_flags(q, k, offsets)
     for a, z in _docs(offsets):
         flags = hard[a // row_n:a // row_n + 1]
         lut = oracle.log_weights(tau, z - a)
         dlut = oracle.dlog_weights(tau, z - a)
         args = (sq[:, a:z], sk[:, a:z], v[:, a:z])
         labs = (q[:, :, a:z], k[:, :, a:z])
-        od, l2d, lmd, jad = oracle.forward(*args, *labs, flags, lut)
+        od, l2d, lmd, jad = oracle.forward(*args, *labs, flags, lut, dense=dense)
         o[:, a:z], l2[:, :, a:z], lm[:, :, a:z] = od, l2d, lmd
         ja[:, :, a:z] = np.where(jad >= 0, jad + a, -1)
-        dsq, dsk, dv, _, rt = oracle.backward(*args, do[:, a:z], *labs, flags, lut, dlut, l2d)
+        dsq, dsk, dv, _, rt = oracle.backward(*args, do[:, a:z], *labs, flags, lut, dlut, l2d,
+                                              dense=dense)
         g[0][:, a:z], g[1][:, a:z], g[2][:, a:z] = dsq, dsk, dv
         rowtau[:, :, a:z] = rt
     dtau = np.empty(h, dtype=np.float32)
