@@ -19,6 +19,7 @@ SIGNATURES = {
     "dism_hard_chunk": [_P, _P, _I64, _I64, _P],
     "dism_hard_boundary": [_P, _P, _P, _I64, _I64, _I64, _I32, _I32, _P, _P],
     "dism_hard_prepare": [_P, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _I32, _I32, _P, _I64, _P],
+    "dism_hard_row_modes": [_P, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P],
     "dism_hard_readout": [_P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _I64, _I64, _I64, _I64,
                           _I32, _I32, _P, _I64, _P, _I32, _P, _P, _P, _P],
     "dism_hard_forward": [_P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _I64, _I64, _I64, _I64,

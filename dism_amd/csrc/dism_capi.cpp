@@ -52,7 +52,7 @@ hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 struct Layout {
     int64_t corder, clab, ctab, bpos[2], blab[2], bplab[2], btab[2], shift, tmp[3];
     int64_t stage[2][2], bhcount[2], own[2], ocount, mode, onebyte;
-    int64_t pnb, prow, mcount, mdig, dflag, dlist, dcount, dbound, total;
+    int64_t pnb, prow, mcount, mdig, dflag, dlist, dcount, dbound, dcost, total;
     int prow_stride;
 };
 
@@ -124,9 +124,10 @@ Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     L.pnb = take(BH * N * 4);
     L.prow = take(BH * N * L.prow_stride * 4);
     L.dflag = take(BH * 4);
-    L.dlist = take(BH * 4);
+    L.dlist = take(2 * BH * 4);
     L.dcount = take(4 * 4);
     L.dbound = take(N <= dism::DENSE_MAX_N ? BH * dism::dense_row_entries((int)N) * 2 : 0);
+    L.dcost = take(BH * 8);
     L.total = o;
     return L;
 }
@@ -163,6 +164,7 @@ dism::Orders orders(const Layout& L, void* ws) {
     o.dlist = at<int32_t>(ws, L.dlist);
     o.dcount = at<int32_t>(ws, L.dcount);
     o.dbound = at<uint16_t>(ws, L.dbound);
+    o.dcost = at<unsigned long long>(ws, L.dcost);
     return o;
 }
 
@@ -315,6 +317,19 @@ int32_t dism_hard_prepare(const void* sq, const void* sk, const void* v, int32_t
                           void* stream) {
     return prepare_impl(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace, workspace_bytes,
                         0, nullptr, stream);
+}
+
+int32_t dism_hard_row_modes(const void* workspace, int64_t workspace_bytes, int64_t B,
+                            int64_t N, int64_t H, int32_t R, int32_t DV, int32_t* modes,
+                            void* stream) {
+    if (!workspace || !modes) return fail(DISM_ERR_INVALID, "row modes: null pointer");
+    if (!dims_ok(B, N, H) || B * H * N > INT_MAX || !rdv_ok(R, DV))
+        return fail(DISM_ERR_INVALID, "row modes: invalid dimensions");
+    const Layout L = layout(B, N, H, R, DV);
+    if (workspace_bytes < L.total) return fail(DISM_ERR_INVALID, "row modes: workspace too small");
+    return hip_status(hipMemcpyAsync(modes, static_cast<const char*>(workspace) + L.dflag,
+                                     B * H * 4, hipMemcpyDeviceToDevice, S(stream)),
+                      "row modes");
 }
 
 int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t dtype,

@@ -54,10 +54,9 @@ __device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long x,
 // Classification: one workgroup per (b,h) row of n positions, counting the first cn of them
 // (a prefill's rows are padded after the real tokens); bucket counts in LDS (runs of equal
 // buckets in a thread's 16 consecutive labels are added with one atomic).
-__global__ __launch_bounds__(256) void dense_classify_kernel(const int32_t* __restrict__ iq,
-                                                             const int32_t* __restrict__ ik,
-                                                             int n, int cn,
-                                                             int32_t* __restrict__ dflag) {
+__global__ __launch_bounds__(256) void dense_classify_kernel(
+    const int32_t* __restrict__ iq, const int32_t* __restrict__ ik, int n, int cn,
+    int32_t* __restrict__ dflag, unsigned long long* __restrict__ dcost) {
     __shared__ uint32_t s_cnt[2][DENSE_BUCKETS];
     __shared__ unsigned long long s_red[4];
     const int tid = threadIdx.x;
@@ -92,6 +91,7 @@ __global__ __launch_bounds__(256) void dense_classify_kernel(const int32_t* __re
     if ((tid & 63) == 0) s_red[tid >> 6] = m;
     __syncthreads();
     if (tid == 0) {
+        dcost[bh] = 0ull;  // the walk probe adds to it
         const unsigned long long t = s_red[0] + s_red[1] + s_red[2] + s_red[3];
         dflag[bh] =
             (n <= DENSE_MAX_N && t * 64ull > (unsigned long long)cn * (unsigned long long)cn)
@@ -99,33 +99,50 @@ __global__ __launch_bounds__(256) void dense_classify_kernel(const int32_t* __re
     }
 }
 
-// The dense rows in ascending order and their count (one workgroup).
-__global__ __launch_bounds__(1024) void dense_list_kernel(const int32_t* __restrict__ dflag,
-                                                          int BH, int32_t* __restrict__ dlist,
+// Row modes and lists (one workgroup, after the walk probe): mode 2 for the sparse rows
+// whose walk-cost estimate exceeds N^2; the mode-1 rows ascending in dlist[0..), the rows of
+// modes 1 and 2 ascending in dlist[BH..), their counts in dcount[0], dcount[1].
+__global__ __launch_bounds__(1024) void dense_mode_kernel(int32_t* __restrict__ dflag,
+                                                          const unsigned long long* __restrict__ dcost,
+                                                          int BH, int n,
+                                                          int32_t* __restrict__ dlist,
                                                           int32_t* __restrict__ dcount) {
-    __shared__ int s_w[16];
-    __shared__ int s_base;
+    __shared__ int s_w[2][16];
+    __shared__ int s_base[2];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    if (tid == 0) s_base = 0;
+    const unsigned long long nn = (unsigned long long)n * (unsigned long long)n;
+    if (tid < 2) s_base[tid] = 0;
     __syncthreads();
     for (int c0 = 0; c0 < BH; c0 += 1024) {
         const int x = c0 + tid;
-        const bool f = x < BH && dflag[x] != 0;
-        const unsigned long long m = __ballot(f);
-        if (lane == 0) s_w[w] = __popcll(m);
+        int mode = x < BH ? dflag[x] : 0;
+        if (x < BH && mode == 0 && n <= DENSE_MAX_N && n > 64 && dcost[x] > nn) {
+            mode = 2;
+            dflag[x] = 2;
+        }
+        const unsigned long long m1 = __ballot(mode == 1), m2 = __ballot(mode != 0);
+        if (lane == 0) {
+            s_w[0][w] = __popcll(m1);
+            s_w[1][w] = __popcll(m2);
+        }
         __syncthreads();
-        int before = s_base;
-        for (int v = 0; v < w; ++v) before += s_w[v];
-        if (f) dlist[before + __popcll(m & ((1ull << lane) - 1ull))] = x;
+        int b1 = s_base[0], b2 = s_base[1];
+        for (int v = 0; v < w; ++v) {
+            b1 += s_w[0][v];
+            b2 += s_w[1][v];
+        }
+        const unsigned long long below = (1ull << lane) - 1ull;
+        if (mode == 1) dlist[b1 + __popcll(m1 & below)] = x;
+        if (mode != 0) dlist[BH + b2 + __popcll(m2 & below)] = x;
         __syncthreads();
-        if (tid == 0) {
+        if (tid < 2) {
             int t = 0;
-            for (int v = 0; v < 16; ++v) t += s_w[v];
-            s_base += t;
+            for (int v = 0; v < 16; ++v) t += s_w[tid][v];
+            s_base[tid] += t;
         }
         __syncthreads();
     }
-    if (tid == 0) *dcount = s_base;
+    if (tid < 2) dcount[tid] = s_base[tid];
 }
 
 // query i starts its match afresh (query reset or document start)
@@ -140,18 +157,19 @@ __device__ __forceinline__ const uint16_t* dense_strip(const PathArgs& a, int bh
 }
 
 // ---------------------------------------------------------------------------------------
-// Boundary rows: wave per (dense row, band of 64 diagonals), persistent.  Lane l follows
+// Boundary rows: wave per (row of mode 1 or 2, band of 64 diagonals), persistent.  Lane l follows
 // diagonal d = 64 band + l (cells (t, t - d)); labels are staged 64 steps at a time.
 __global__ __launch_bounds__(256) void dense_bound_kernel(PathArgs a) {
     __shared__ int s_q[4][64], s_r[4][64], s_k[4][128];
     const int w = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
     const int n = a.n, Q = (n + 63) >> 6;
-    const int cnt = __builtin_amdgcn_readfirstlane(*a.o.dcount);
+    const int cnt = __builtin_amdgcn_readfirstlane(a.o.dcount[1]);
     const long items = (long)cnt * Q;
     const int tend = 64 * (Q - 1) - 1;  // last boundary row
+    const int32_t* rows = a.o.dlist + (long)a.B * a.H;
     for (long x = (long)blockIdx.x * 4 + w; x < items; x += (long)gridDim.x * 4) {
         const int band = (int)(x / cnt);
-        const int bh = a.o.dlist[x % cnt];
+        const int bh = rows[x % cnt];
         const int d0 = 64 * band;
         if (d0 > tend) continue;  // (soft rows too: a prepare call has no row flags)
         const long so = (long)bh * n;
@@ -720,16 +738,17 @@ __global__ __launch_bounds__(DENSE_THREADS) void dense_keys_kernel(PathArgs a) {
 
 // ---------------------------------------------------------------------------------------
 hipError_t launch_dense_classify(const int32_t* iq, const int32_t* ik, long BH, int n,
-                                 int cls_n, int32_t* dflag, hipStream_t s) {
+                                 int cls_n, int32_t* dflag, unsigned long long* dcost,
+                                 hipStream_t s) {
     const int cn = cls_n > 0 && cls_n < n ? cls_n : n;
     hipLaunchKernelGGL(dense_classify_kernel, dim3((unsigned)BH), dim3(256), 0, s, iq, ik, n, cn,
-                       dflag);
+                       dflag, dcost);
     return hipGetLastError();
 }
 
 hipError_t launch_dense_prepare(const PathArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(dense_list_kernel, dim3(1), dim3(1024), 0, s, a.o.dflag, a.B * a.H,
-                       a.o.dlist, a.o.dcount);
+    hipLaunchKernelGGL(dense_mode_kernel, dim3(1), dim3(1024), 0, s, a.o.dflag, a.o.dcost,
+                       a.B * a.H, a.n, a.o.dlist, a.o.dcount);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.n > DENSE_MAX_N || a.n <= 64) return e;
     hipLaunchKernelGGL(dense_bound_kernel, dim3(DENSE_GRID), dim3(256), 0, s, a);

@@ -49,14 +49,16 @@ struct Orders {
     // [B*H][32], then per-row digit lists [B*H][8]
     int32_t* mcount;
     int32_t* mdig;
-    // dense rows (dism_dense.hip): per-row flag [B*H] (1: the row's bucketed label
-    // collisions exceed N^2/64), the flagged rows ascending [B*H] and their count [1], and the
-    // 16-bit boundary rows L[64s - 1, j], j < 64s, of every 64-row query strip s >= 1
+    // dense rows (dism_dense.hip): per-row mode [B*H] (1: the row's bucketed label
+    // collisions exceed N^2/64; 2: not dense, but its bigram walks would be long), the rows
+    // of each kind ascending and their counts, and the 16-bit boundary rows L[64s - 1, j],
+    // j < 64s, of every 64-row query strip s >= 1 of the rows of modes 1 and 2
     // ([B*H][dense_row_entries(N)], only when N <= DENSE_MAX_N)
-    int32_t* dflag;
-    int32_t* dlist;
-    int32_t* dcount;
+    int32_t* dflag;       // row mode: 0 sparse, 1 dense, 2 sparse with strip-bounded walks
+    int32_t* dlist;       // mode-1 rows, then (at dlist + B*H) the rows of modes 1 and 2
+    int32_t* dcount;      // [0]: mode-1 rows, [1]: rows of modes 1 and 2
     uint16_t* dbound;
+    unsigned long long* dcost;  // [B*H] walk-cost estimate of the probe (dism_pairs.hip)
 };
 
 constexpr int DENSE_MAX_N = 65536;   // longest row of the dense path (16-bit lengths)
@@ -239,7 +241,9 @@ hipError_t launch_pairs_keys(const PathArgs& a, int R, int DV, int dtype, hipStr
 // dense rows (dism_dense.hip): classification (before the label scans), the row list and the
 // boundary rows (before the dense kernels), then the tile kernels for the flagged hard rows
 hipError_t launch_dense_classify(const int32_t* iq, const int32_t* ik, long BH, int n,
-                                 int cls_n, int32_t* dflag, hipStream_t s);
+                                 int cls_n, int32_t* dflag, unsigned long long* dcost,
+                                 hipStream_t s);
+hipError_t launch_walk_probe(const PathArgs& a, hipStream_t s);
 hipError_t launch_dense_prepare(const PathArgs& a, hipStream_t s);
 hipError_t launch_dense_forward(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_dense_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);

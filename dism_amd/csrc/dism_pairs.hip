@@ -102,11 +102,15 @@ __device__ __forceinline__ void partner_range(const PathArgs& a, int bh, long so
 // walk without its first comparison.
 // dlo: the lowest query position the walk may reach (walk_lo: document start, last reset;
 // calls with either have no carry boundary).
+// wb: the row's 16-bit strip boundaries (rows whose walks the probe found long, mode 2): the
+// walk stops at its 64-row strip's first row i0 and adds L[i0 - 1, j - c] from the boundary
+// row (unless a reset or document start at or above i0 ends the walk first).
 __device__ __forceinline__ int pair_length(const int32_t* __restrict__ q,
                                            const int32_t* __restrict__ k, int i, int j,
                                            const int32_t* __restrict__ bound, int strip, int n,
-                                           int dlo) {
-    const int lo = bound ? (i / strip) * strip : dlo;
+                                           int dlo, const uint16_t* __restrict__ wb = nullptr) {
+    const int s0 = wb ? (i & ~63) : 0;
+    const int lo = bound ? (i / strip) * strip : (s0 > dlo ? s0 : dlo);
     int c = i - 1 >= lo ? 2 : 1;
     if (c == 2) {
         // the walk compares WALK_PF label pairs per step, all loads in flight together
@@ -132,8 +136,15 @@ __device__ __forceinline__ int pair_length(const int32_t* __restrict__ q,
     if (bound && lo > 0 && i - c < lo && j - c >= 0) {
         const int jj = j - c;
         c += jj - bound[(long)(lo / strip - 1) * n + jj];
+    } else if (wb && s0 > dlo && i - c < s0 && j - c >= 0) {
+        c += (int)wb[dense_strip_offset(s0 >> 6) + (j - c)];
     }
     return c;
+}
+
+// strip boundaries of row bh when its pair walks use them (mode 2), else null
+__device__ __forceinline__ const uint16_t* walk_bound_of(const PathArgs& a, int bh) {
+    return a.o.dflag[bh] == 2 ? a.o.dbound + (long)bh * dense_row_entries(a.n) : nullptr;
 }
 
 __device__ __forceinline__ int owner_class(int cnt) {
@@ -201,7 +212,7 @@ __global__ __launch_bounds__(LIST_THREADS) void owner_lists_kernel(PathArgs a) {
     const int32_t* dense = a.o.dflag;  // dense rows' pairs belong to dism_dense.hip
     int before[3] = {0, 0, 0}, total[3] = {0, 0, 0};
     for (int r = tid; r < BH; r += LIST_THREADS) {
-        const bool drop = dense[r] != 0;
+        const bool drop = dense[r] == 1;
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             const int v = drop ? 0 : cnt[(long)r * 4 + c];
@@ -239,7 +250,7 @@ __global__ __launch_bounds__(LIST_THREADS) void owner_lists_kernel(PathArgs a) {
     int4* own = a.o.own[side];
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
-        const int m = dense[bh] ? 0 : cnt[(long)bh * 4 + c];
+        const int m = dense[bh] == 1 ? 0 : cnt[(long)bh * 4 + c];
         const int4* src = a.o.stage[side][c == 1 ? 1 : 0] + so;
         for (int k = tid; k < m; k += LIST_THREADS) {
             const int4 rec = src[c == 2 ? n - 1 - k : k];
@@ -273,7 +284,7 @@ static SortArgs sort_args(const SortArgs& sa, const PathArgs& pa) {
 hipError_t launch_prepare_labels(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
     const SortArgs b = sort_args(sa, pa);
     // the dense-row flags first: the label scans skip dense rows, the owner lists drop them
-    hipError_t e = launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n, sa.o.dflag, s);
+    hipError_t e = launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n, sa.o.dflag, sa.o.dcost, s);
     if (e != hipSuccess) return e;
     // prepare_lds_kernel role 0 orders every row: in LDS, or in global memory for rows whose
     // labels differ in more than one byte
@@ -293,6 +304,7 @@ hipError_t launch_prepare_pairs(const SortArgs& sa, const PathArgs& pa, hipStrea
         if (e == hipSuccess) e = launch_prepare_lds(b, 1, 1, s);
     }
     if (e == hipSuccess) e = launch_owner_lists(pa, s);
+    if (e == hipSuccess && pa.n <= DENSE_MAX_N) e = launch_walk_probe(pa, s);
     return e != hipSuccess ? e : launch_dense_prepare(pa, s);
 }
 
@@ -305,11 +317,12 @@ hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s)
     // one stream: the dense-row flags, both LDS roles in one grid (64-block roles side by
     // side), then the bigram sorts of the other rows, the plan, the owner lists and the dense
     // rows' list and boundaries
-    hipError_t e = launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n, sa.o.dflag, s);
+    hipError_t e = launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n, sa.o.dflag, sa.o.dcost, s);
     if (e == hipSuccess) e = launch_prepare_lds(b, 0, 2, s);
     if (e == hipSuccess) e = launch_sort(b, 1, 2, s);
     if (e == hipSuccess) e = launch_pair_plan(pa, s);
     if (e == hipSuccess) e = launch_owner_lists(pa, s);
+    if (e == hipSuccess && pa.n <= DENSE_MAX_N) e = launch_walk_probe(pa, s);
     return e != hipSuccess ? e : launch_dense_prepare(pa, s);
 }
 
@@ -434,6 +447,86 @@ __device__ __forceinline__ unsigned long long shfl_xor64(unsigned long long x, i
     return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
 }
 
+// ---------------------------------------------------------------------------------------
+// Walk-cost probe (after the owner lists).  For every bigram pair that ends a diagonal run of
+// matches ((i+1, j+1) does not continue it), the run's length l: exact up to WALK_EXACT
+// labels, beyond that the largest offset 2^m at which the labels still match (within a factor
+// 2 of a true run's length).  Per row, S += l^2 / 2, about the label comparisons that the
+// run's pairs' walks would cost.  Rows with S > N^2 get strip boundaries (mode 2,
+// dense_mode_kernel): their walks then stop within 64 rows (pair_length), so no row's walks
+// cost more than O(N^2) in all.  The estimate only picks the method; lengths stay exact.
+constexpr int WALK_EXACT = 64;
+
+__device__ __forceinline__ int probe_run(const int32_t* __restrict__ q,
+                                         const int32_t* __restrict__ k, int i, int j, int dlo) {
+    int c = i - 1 >= dlo ? 2 : 1;
+    if (c == 2) {
+        constexpr int PF = 4;
+        while (c < WALK_EXACT) {
+            int qv[PF], kv[PF];
+#pragma unroll
+            for (int u = 0; u < PF; ++u) {
+                const int iq = i - c - u, jk = j - c - u;
+                qv[u] = q[iq > 0 ? iq : 0];
+                kv[u] = k[jk > 0 ? jk : 0];
+            }
+            int run = 0;
+#pragma unroll
+            for (int u = 0; u < PF; ++u)
+                if (run == u && i - c - u >= dlo && j - c - u >= 0 && qv[u] == kv[u]) ++run;
+            c += run;
+            if (run < PF) return c;
+        }
+    }
+    if (c < WALK_EXACT) return c;
+    int est = c;
+    for (int o = 2 * WALK_EXACT;; o *= 2) {
+        const int ii = i - (o - 1), jj = j - (o - 1);
+        if (ii < dlo || jj < 0 || q[ii] != k[jj]) break;
+        est = o;
+    }
+    return est;
+}
+
+template <int G>
+__device__ __forceinline__ void probe_item(const PathArgs& a, int base, int k0, int ncls) {
+    Slot s;
+    if (!load_slot<0, G>(a, base, k0, ncls, s)) return;
+    const int n = a.n, sub = lane_id() % G;
+    const int i = s.p;
+    const int32_t* kb = a.o.bpos[1] + s.so;
+    const int32_t* q = a.iq + s.so;
+    const int32_t* k = a.ik + s.so;
+    const int dlo = walk_lo(a, s.so, i);
+    const bool next_reset = i + 1 < n && walk_lo(a, s.so, i + 1) == i + 1;
+    unsigned long long cost = 0;
+    for (int c0 = 0; c0 < s.maxcnt; c0 += G) {
+        const int kq = c0 + sub;
+        if (kq < s.cnt) {
+            const int j = kb[s.lo + kq];
+            const bool ends = i + 1 >= n || j + 1 >= n || next_reset || q[i + 1] != k[j + 1];
+            if (ends) {
+                const unsigned long long l = (unsigned long long)probe_run(q, k, i, j, dlo);
+                cost += l * l / 2;
+            }
+        }
+    }
+#pragma unroll
+    for (int o = G / 2; o >= 1; o >>= 1) cost += shfl_xor64(cost, o);
+    if (sub == 0 && cost) atomicAdd(&a.o.dcost[s.bh], cost);
+}
+
+__global__ __launch_bounds__(64 * WAVES) void walk_probe_kernel(PathArgs a) {
+    for_owner_items<0, OWNER_SMALL, OWNER_MEDIUM>(a, [&](auto g, int base, int k0, int ncls) {
+        probe_item<decltype(g)::value>(a, base, k0, ncls);
+    });
+}
+
+hipError_t launch_walk_probe(const PathArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(walk_probe_kernel, dim3(PAIR_GRID), dim3(64 * WAVES), 0, s, a);
+    return hipGetLastError();
+}
+
 template <typename T, int R, int DV, int G>
 __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0, int ncls,
                                             FinishLds& S) {
@@ -447,6 +540,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
     const int32_t* q = a.iq + s.so;
     const int32_t* k = a.ik + s.so;
     const int32_t* bnd = s.hard ? bound_of(a, s.bh) : nullptr;
+    const uint16_t* wb = bnd ? nullptr : walk_bound_of(a, s.bh);
     const float* lut = a.lut + (long)s.h * a.lut_stride;
     const T* sq = reinterpret_cast<const T*>(a.sq);
     const T* sk = reinterpret_cast<const T*>(a.sk);
@@ -487,7 +581,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
         }
         float skr[R];
         load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
-        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i)) : 1;
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb) : 1;
         const float lw = lut[L];
         float mm = has && lw > m0 ? lw : m0;
         key = has ? (((unsigned long long)(unsigned)L << 32) | (unsigned)j) : 0ull;
@@ -534,7 +628,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
             const int kq = c0 + sub;
             if (kq < cnt) {
                 const int j = kb[lo + kq];
-                const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i));
+                const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb);
                 const float lw = lut[L];
                 if (lw > m0) atomicMax(&S.m[sl], __float_as_uint(lw));
                 atomicMax(&S.key[sl], ((unsigned long long)(unsigned)L << 32) | (unsigned)j);
@@ -551,7 +645,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
             const int kq = c0 + sub;
             if (kq < cnt) {
                 const int j = kb[lo + kq];
-                const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i));
+                const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb);
                 const float p = exp2_fp32(lut[L] - m);
                 float skr[R];
                 load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
@@ -656,6 +750,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
     const int32_t* q = a.iq + s.so;
     const int32_t* k = a.ik + s.so;
     const int32_t* bnd = s.hard ? bound_of(a, s.bh) : nullptr;
+    const uint16_t* wb = bnd ? nullptr : walk_bound_of(a, s.bh);
     const float* lut = a.lut + (long)s.h * a.lut_stride;
     const float* glut = a.dlut + (long)s.h * a.lut_stride;
     const T* sq = reinterpret_cast<const T*>(a.sq);
@@ -690,7 +785,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
         }
         float skr[R];
         load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
-        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i)) : 1;
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb) : 1;
         float sdot = 0.0f;
 #pragma unroll
         for (int r = 0; r < R; ++r) sdot = __builtin_fmaf(sqr[r], skr[r], sdot);
@@ -731,7 +826,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
         const int kq = c0 + sub;
         if (kq < cnt) {
             const int j = kb[lo + kq];
-            const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i));
+            const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb);
             float skr[R];
             load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
             float sdot = 0.0f;
@@ -831,6 +926,7 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
     const int32_t* q = a.iq + s.so;
     const int32_t* k = a.ik + s.so;
     const int32_t* bnd = s.hard ? bound_of(a, s.bh) : nullptr;
+    const uint16_t* wb = bnd ? nullptr : walk_bound_of(a, s.bh);
     const float* lut = a.lut + (long)s.h * a.lut_stride;
     const float lut1 = lut[1];
     const T* sq = reinterpret_cast<const T*>(a.sq);
@@ -874,7 +970,7 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
         const float l2 = a.lse2[s.so + i];
         float sqr[R];
         load_row<T, R>(sq + (s.row0 + (long)i * a.H) * R, sqr);
-        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i)) : 1;
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb) : 1;
         const float p = exp2_fp32(lut[L] - l2);
         float sdot = 0.0f;
 #pragma unroll
@@ -912,7 +1008,7 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
         const int kq = c0 + sub;
         if (kq < cnt) {
             const int i = qb[lo + kq];
-            const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i));
+            const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb);
             const float l2 = a.lse2[s.so + i];
             const float p = exp2_fp32(lut[L] - l2);
             float sqr[R];

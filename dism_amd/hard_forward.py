@@ -75,6 +75,18 @@ def prepare_workspace(sq, sk, v, idx_q, idx_k):
     return ws
 
 
+def row_modes(workspace, sq, v):
+    """Row modes [B,H] int32 of a workspace prepared for vectors shaped like sq/v: 0 sparse,
+    1 dense (direct tile kernels), 2 sparse with strip-bounded walks."""
+    b, n, h, r = sq.shape
+    dv = v.shape[3]
+    out = torch.empty((b, h), dtype=torch.int32, device=workspace.device)
+    with torch.cuda.device(workspace.device):
+        _lib.call("dism_hard_row_modes", workspace.data_ptr(), workspace.numel(), b, n, h, r,
+                  dv, out.data_ptr(), _stream(workspace))
+    return out
+
+
 def _readout(sq, sk, v, idx_q, idx_k, hard, boundary, strip, log_weights, out_dtype,
              matches, workspace=None):
     b, n, h, r, dv, dt = check_vectors(sq, sk, v)

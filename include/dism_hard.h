@@ -109,6 +109,15 @@ int32_t dism_hard_prepare(const void* sq, const void* sk, const void* v, int32_t
                           int32_t R, int32_t DV, void* workspace, int64_t workspace_bytes,
                           void* stream);
 
+/* Row modes of a prepared workspace, [B*H] int32 to `modes` (device memory): 0 = sparse row
+ * (label scans + bigram walks), 1 = dense row (the bucketed label collisions exceed N^2/64:
+ * direct tile kernels), 2 = sparse row whose walks stop at 64-row strip boundaries (the walk
+ * probe estimated their cost above N^2).  An introspection aid for tests and tuning; no
+ * reference counterpart. */
+int32_t dism_hard_row_modes(const void* workspace, int64_t workspace_bytes, int64_t B,
+                            int64_t N, int64_t H, int32_t R, int32_t DV, int32_t* modes,
+                            void* stream);
+
 /* Hard readout on a prepared workspace: O [B,N,H,DV] (out_dtype bf16|f32) and lse2 [B,H,N]
  * fp32; optional lmax/jarg [B,H,N] int32 receive the longest match length per query and its
  * key (ties -> most recent key, -1 if none).  boundary may be NULL (lengths recomputed from

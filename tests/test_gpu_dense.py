@@ -163,3 +163,39 @@ def test_phase1_counts_rows_past_65535():
     assert_bits(host(m["length"]), lm, "lmax")
     assert_bits(host(m["index"]), ja, "argmax")
     assert lm[0, 0, -1] == 2 and ja[0, 0, -1] == n - 1
+
+
+def _periodic_row(n, period, rng):
+    base = rng.integers(0, 256, period).astype(np.int32)
+    return base[np.arange(n) % period]
+
+
+def test_long_repeats_take_strip_bounded_walks():
+    """Rows with few label collisions but long repeats (a random 256-symbol pattern of period
+    200, and the same with one mutated position per period) are not dense; the walk probe
+    gives them strip boundaries (mode 2) so their bigram walks stop within 64 rows.  Lengths
+    stay exact: bit for bit against the CPU model's unbounded walks."""
+    import dism_amd
+    from dism_amd.hard_forward import row_modes
+    n, b, h = 4096, 1, 4
+    rng = np.random.default_rng(23)
+    q = rng.integers(0, 256, (b, h, n)).astype(np.int32)
+    k = rng.integers(0, 256, (b, h, n)).astype(np.int32)
+    q[0, 1] = _periodic_row(n, 200, rng)
+    k[0, 1] = q[0, 1]
+    q[0, 2] = _periodic_row(n, 233, rng)
+    k[0, 2] = np.roll(q[0, 2], 5)
+    k[0, 2, ::233] = 999                       # runs broken once per period
+    sq, sk, v = vectors(n, b=b, h=h, r=8, dv=64, seed=9)
+    hard = np.ones((b, h), bool)
+    do = oracle.bf16_round(rng.standard_normal(v.shape))
+    tau = np.array([0.5, 0.1, -0.2, 1.0], np.float32)
+    assert not oracle.dense_rows(q, k, hard).any()
+    x = (sq, sk, v, q, k, hard, tau)
+    print("long repeats n=4096", flush=True)
+    _check(x, do, threads=4, what="long repeats")
+    t = [dev(a, torch.bfloat16) for a in (sq, sk, v)]
+    _, _, state = dism_amd.forward_hard(*t, dev(q), dev(k), dev(hard), dev(tau),
+                                        save_state=True)
+    modes = host(row_modes(state["workspace"], t[0], t[2]))
+    assert modes.tolist() == [[0, 2, 2, 0]], modes
