@@ -58,9 +58,12 @@ def main():
     ap.add_argument("--carry-strip", type=int, default=0,
                     help="composed carry boundary strip height (0 = off)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--workload", default="train", choices=("train", "decode", "vocab"),
+    ap.add_argument("--workload", default="train",
+                    choices=("train", "decode", "vocab", "refshape"),
                     help="train: the BASELINE metric (default); decode: prefill + token-by-token "
-                         "decoding at the nanochat layer shape; vocab: codebook argmax labels")
+                         "decoding at the nanochat layer shape; vocab: codebook argmax labels; "
+                         "refshape: the reference's own benchmark shape (B16 H6 N2048 R32 DV64, "
+                         "random-512 and identical labels, forward and backward timed apart)")
     ap.add_argument("--streams", type=int, default=2, choices=(1, 2),
                     help="2: the backward's key chain runs concurrently on a side stream")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
@@ -88,6 +91,8 @@ def main():
         return bench_decode(args)
     if args.workload == "vocab":
         return bench_vocab(args)
+    if args.workload == "refshape":
+        return bench_refshape(args)
 
     dev = torch.device("cuda:0")
     B, T, H, D, DV = args.B, args.T, args.H, args.dqk, args.dv
@@ -297,6 +302,114 @@ def _time(fn, steps, warmup):
     e.record()
     torch.cuda.synchronize()
     return s.elapsed_time(e) / steps
+
+
+def _median_ms(fn, calls=20, samples=7, warmup=10):
+    """The reference's measure (dism_v3/tools/bench_training.py:39-61): warmup calls, then
+    `samples` samples of `calls` calls each between CUDA events; the median sample over
+    `calls`, in ms."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(samples):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(calls):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        out.append(s.elapsed_time(e) / calls)
+    return float(np.median(out))
+
+
+# published RTX 5090 numbers for this shape (BASELINE.md section 1; dism_v3/docs/
+# HARD_FORWARD_PLAN.md:245-246, HARD_BACKWARD_QUADRATIC.md:134-135), ms
+REF_5090 = {"random": {"forward": 0.4780, "backward": 2.271, "backward_recompute": 2.458},
+            "identical": {"forward": 0.4813, "backward": 3.062, "backward_recompute": 3.169}}
+
+
+def bench_refshape(args):
+    """The reference's benchmark shape: B16 H6 N2048 R32 DV64 bf16, tau 0.5, every row hard,
+    labels random over 512 symbols or all identical.  Forward = LUT + the one-call forward
+    (dism_hard_forward: prepare, label scans, bigram corrections, dense rows); backward = dlog
+    table + dism_hard_backward on the forward's workspace and normalizer; backward_recompute =
+    forward + backward (the reference's default training route recomputes its boundaries).
+    Timed like the reference (10 warmups, median of 7 samples of 20 calls).  Prints one JSON
+    line."""
+    import torch
+    import dism_amd
+    from dism_amd import _lib
+    from dism_amd._checks import DTYPE_CODE
+    from dism_amd.hard_forward import row_modes
+    B, H, N, R, DV = 16, 6, 2048, 32, 64
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(20261207)
+    x = lambda *sh: torch.randn(*sh, generator=g).to(dev, torch.bfloat16)  # noqa: E731
+    sq, sk, v, do = x(B, N, H, R), x(B, N, H, R), x(B, N, H, DV), x(B, N, H, DV)
+    tau = torch.full((H,), 0.5, dtype=torch.float32, device=dev)
+    hard = torch.ones((B, H), dtype=torch.bool, device=dev)
+    code = DTYPE_CODE[torch.bfloat16]
+    nbytes = _lib.workspace_bytes(B, N, H, R, DV, code)
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+    out = torch.empty((B, N, H, DV), dtype=torch.bfloat16, device=dev)
+    lse2 = torch.empty((B, H, N), dtype=torch.float32, device=dev)
+    dsq = torch.empty((B, N, H, R), dtype=torch.float32, device=dev)
+    dsk = torch.empty_like(dsq)
+    dvv = torch.empty((B, N, H, DV), dtype=torch.float32, device=dev)
+    rowtau = torch.empty((B, H, N), dtype=torch.float32, device=dev)
+    dtau = torch.empty((H,), dtype=torch.float32, device=dev)
+    S = torch.cuda.current_stream(dev).cuda_stream
+    result = {"metric": "hard DISM forward / backward time at the reference's benchmark shape",
+              "unit": "ms", "higher_is_better": False,
+              "config": {"workload": "reference benchmark shape (HARD_FORWARD_PLAN.md:245)",
+                         "B": B, "H": H, "N": N, "R": R, "DV": DV, "tau": 0.5,
+                         "labels": "random over 512 symbols | all identical"},
+              "data": "synthetic N(0,1) bf16 vectors (seed 20261207)",
+              "timing": "10 warmups, median of 7 samples of 20 calls (CUDA events)"}
+    for kind in ("random", "identical"):
+        if kind == "random":
+            lab = torch.randint(0, 512, (B, H, N), generator=g, dtype=torch.int32).to(dev)
+        else:
+            lab = torch.zeros((B, H, N), dtype=torch.int32, device=dev)
+        iq = lab
+        ik = lab if kind == "identical" else \
+            torch.randint(0, 512, (B, H, N), generator=g, dtype=torch.int32).to(dev)
+        state = {}
+
+        def forward():
+            lut = dism_amd.hard_log_weights(tau, N)
+            state["lut"] = lut
+            _lib.call("dism_hard_forward", sq.data_ptr(), sk.data_ptr(), v.data_ptr(), code,
+                      iq.data_ptr(), ik.data_ptr(), hard.data_ptr(), 0, 0, lut.data_ptr(),
+                      N + 1, B, N, H, R, DV, ws.data_ptr(), nbytes, out.data_ptr(), code,
+                      lse2.data_ptr(), 0, 0, S)
+
+        def backward():
+            dl = dism_amd.hard_dlog_weights(tau, N + 1)
+            _lib.call("dism_hard_backward", sq.data_ptr(), sk.data_ptr(), v.data_ptr(),
+                      do.data_ptr(), code, iq.data_ptr(), ik.data_ptr(), hard.data_ptr(), 0, 0,
+                      state["lut"].data_ptr(), dl.data_ptr(), N + 1, lse2.data_ptr(), B, N, H,
+                      R, DV, ws.data_ptr(), nbytes, dsq.data_ptr(), dsk.data_ptr(),
+                      dvv.data_ptr(), rowtau.data_ptr(), dtau.data_ptr(), S)
+
+        def both():
+            forward()
+            backward()
+        f_ms = _median_ms(forward)
+        b_ms = _median_ms(backward)
+        fb_ms = _median_ms(both)
+        modes = row_modes(ws, sq, v).cpu()
+        ref = REF_5090[kind]
+        result[kind] = {"forward_ms": f_ms, "backward_ms": b_ms, "fwd_bwd_ms": fb_ms,
+                        "row_modes": {str(m): int((modes == m).sum()) for m in (0, 1, 2)},
+                        "bht_per_s_fwd_bwd": B * H * N / (fb_ms / 1e3),
+                        "rtx5090_ms": ref,
+                        "speedup_vs_rtx5090": {"forward": ref["forward"] / f_ms,
+                                               "backward": ref["backward"] / b_ms,
+                                               "fwd_bwd": ref["backward_recompute"] / fb_ms}}
+    print(json.dumps(result), flush=True)
 
 
 def bench_decode(args):

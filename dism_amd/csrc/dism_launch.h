@@ -230,6 +230,9 @@ hipError_t launch_msort_pairs(const SortArgs& a, hipStream_t s);
 // rows' mode must be 0)
 hipError_t launch_sort_labels(const SortArgs& a, hipStream_t s);
 hipError_t launch_prepare_lds(const SortArgs& a, int role0, int roles, hipStream_t s);
+// label-scan buckets of about 2N/256 entries for rows with multi-byte labels (after the
+// combined label order)
+hipError_t launch_ctab_balance(const SortArgs& a, hipStream_t s);
 // The following return hipErrorInvalidValue for an unsupported (R, DV, dtype).
 hipError_t launch_pair_plan(const PathArgs& a, hipStream_t s);
 hipError_t launch_owner_lists(const PathArgs& a, hipStream_t s);

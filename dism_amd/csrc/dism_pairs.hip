@@ -288,8 +288,8 @@ hipError_t launch_prepare_labels(const SortArgs& sa, const PathArgs& pa, hipStre
     if (e != hipSuccess) return e;
     // prepare_lds_kernel role 0 orders every row: in LDS, or in global memory for rows whose
     // labels differ in more than one byte
-    if (!b.lds_rows) return launch_msort_labels(b, s);
-    return launch_prepare_lds(b, 0, 1, s);
+    e = b.lds_rows ? launch_prepare_lds(b, 0, 1, s) : launch_msort_labels(b, s);
+    return e != hipSuccess ? e : launch_ctab_balance(b, s);
 }
 
 hipError_t launch_prepare_pairs(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
@@ -319,6 +319,7 @@ hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s)
     // rows' list and boundaries
     hipError_t e = launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n, sa.o.dflag, sa.o.dcost, s);
     if (e == hipSuccess) e = launch_prepare_lds(b, 0, 2, s);
+    if (e == hipSuccess) e = launch_ctab_balance(b, s);
     if (e == hipSuccess) e = launch_sort(b, 1, 2, s);
     if (e == hipSuccess) e = launch_pair_plan(pa, s);
     if (e == hipSuccess) e = launch_owner_lists(pa, s);

@@ -726,4 +726,41 @@ hipError_t launch_sort(const SortArgs& a, int role0, int roles, hipStream_t s) {
 
 hipError_t launch_sort_labels(const SortArgs& a, hipStream_t s) { return launch_msort_labels(a, s); }
 
+// Work buckets of the label scans for rows whose labels differ in more than one byte: the top
+// sorted digit can then hold a handful of values (labels 0..511: two), which left one scan
+// wave walking hundreds of label groups in series.  Here the 2N entries of the combined order
+// are cut into 256 ranges of about 2N/256 entries, each boundary moved forward to the next
+// label change (upper bound of the label before it), so every label group stays whole.
+// One workgroup per row, thread b computes boundary b.
+__global__ __launch_bounds__(256) void ctab_balance_kernel(const int32_t* __restrict__ clab_all,
+                                                           const int32_t* __restrict__ onebyte,
+                                                           int32_t* __restrict__ ctab_all,
+                                                           int n) {
+    const long bh = blockIdx.x;
+    if (onebyte[bh]) return;
+    const int tid = (int)threadIdx.x, n2 = 2 * n;
+    const int32_t* clab = clab_all + bh * n2;
+    int32_t* ctab = ctab_all + bh * (RADIX + 1);
+    int x = 0;
+    if (tid > 0) {
+        const int t = (int)((long)tid * n2 / RADIX);
+        // first index in [t, n2) whose (unsigned) label exceeds the one before t
+        const uint32_t prev = (uint32_t)clab[t - 1];
+        int lo = t, hi = n2;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if ((uint32_t)clab[mid] <= prev) lo = mid + 1; else hi = mid;
+        }
+        x = lo;
+    }
+    ctab[tid] = x;
+    if (tid == 0) ctab[RADIX] = n2;
+}
+
+hipError_t launch_ctab_balance(const SortArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(ctab_balance_kernel, dim3((unsigned)a.BH), dim3(RADIX), 0, s, a.o.clab,
+                       a.o.onebyte, a.o.ctab, a.n);
+    return hipGetLastError();
+}
+
 }  // namespace dism
