@@ -1,5 +1,5 @@
 // dism_dense.hip -- dense rows: hard rows whose labels collide often, computed with the
-// direct (pairwise) definition over 64 x 32 query-key tiles.
+// direct (pairwise) definition, one wave per 64-row strip.
 //
 // A row is dense when its bucketed label collisions M = sum over 4096 label buckets of
 // #queries x #keys exceed N^2/64 (dense_classify_kernel; N <= DENSE_MAX_N).  Such rows have
@@ -12,9 +12,8 @@
 // Match lengths: the diagonal recurrence L[i,j] = (q[i] == k[j]) ? L[i-1,j-1] + 1 : 0
 // (reset to 1 at a query reset / document start).  dense_bound_kernel sweeps each band of 64
 // diagonals once (lane = diagonal, one query row per step) and stores the boundary rows
-// L[64s - 1, j] (16-bit) of every 64-row query strip s.  A tile then rebuilds its lengths from
-// its strip's boundary row: one thread per diagonal crossing the tile walks the strip's 64
-// rows (dense_lengths).
+// L[64s - 1, j] (16-bit) of every 64-row query strip s.  A strip's lengths then come from
+// 64-bit diagonal masks and its boundary row (diag_length).
 //
 // fp32 sequences (oracle/dism_cpu_model.c direct_forward_row / direct_backward_row):
 //   forward, per query i, keys j ascending over valid pairs:
@@ -29,16 +28,14 @@
 //       rowtau = fma(-u, mean, w) / mass, f = exp2(-l2), mass = z + f,
 //       mean = fma(-f, c, vv) / mass;
 //     per key (i ascending): dk[r] = fma(pe, sq[r], dk[r]); dv[d] = fma(ps, dO[d], dv[d]).
-// A tile computes the per-pair scalars lane-parallel (phase A) into LDS, then folds them in
-// order (phase B, lanes = accumulator elements).  Invalid cells contribute exact zeros
-// (accumulators start at +0 and are never -0, so +0 terms are exact no-ops) unless a staged
-// row holds a non-finite value; then phase B skips invalid cells explicitly.
+// Invalid cells (no match, or j > i) contribute exact zeros: accumulators start at +0 and
+// are never -0, so +0 terms are exact no-ops -- unless the walked side's row holds a
+// non-finite value, for which such cells are skipped explicitly.
 #include "dism_path.h"
 
 namespace dism {
 
 constexpr int DENSE_THREADS = 256;
-constexpr int DK = 32;              // keys per tile
 constexpr unsigned DENSE_GRID = 512;   // persistent workgroups of the tile kernels
 
 __device__ __forceinline__ uint32_t label_bucket(int32_t x) {
@@ -207,79 +204,118 @@ __global__ __launch_bounds__(256) void dense_bound_kernel(PathArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Tile lengths: the 64 x KT tile (rows i0 + il, keys j0 + jl) into sL[il * (KT + 1) + jl]
-// (0 for non-causal cells and rows past n).  Thread t < 63 + KT walks the diagonal
-// il - jl = t - (KT - 1) down the strip's 64 rows from the boundary row i0 - 1.
-// sk holds the labels of keys j0 - 64 .. j0 + KT - 1 (sk[jl + 64]).
-template <int KT>
-__device__ __forceinline__ void dense_lengths(const int* sq, const int* sr, const int* sk,
-                                              int* sL, int i0, int j0, int nq, int n,
-                                              const uint16_t* bstrip, int tid) {
-    if (tid >= 63 + KT) return;
-    const int dl = tid - (KT - 1);
-    const int jc = j0 - 1 - dl;
-    int L = (bstrip && jc >= 0 && jc < i0) ? (int)bstrip[jc] : 0;
-    for (int il = 0; il < 64; ++il) {
-        const int jl = il - dl, j = j0 + jl;
-        const bool in = jl < KT;
-        const int kv = in ? sk[jl + 64] : 0;
-        const bool eq = in && il < nq && j >= 0 && j < n && sq[il] == kv;
-        L = eq ? (sr[il] ? 1 : L + 1) : 0;
-        if (jl >= 0 && in) sL[il * (KT + 1) + jl] = (j <= i0 + il) ? L : 0;
-    }
-}
+// Wave-level tiles.  One 64-lane wave owns one work item -- a 64-row query strip (forward,
+// dSQ / rowtau: lane = query row) or a 64-key strip (dSK / dV: lane = key) -- and walks the
+// other side in ascending order; waves never synchronise with each other.  The walked side's
+// row is the same for every lane at each step, so it is read with scalar loads: the FMAs take
+// it as an SGPR operand and the scalar unit unpacks bf16.
+//
+// Match lengths from diagonal masks: for a diagonal d = i - j crossing a 64-row query strip
+// i0 .. i0+63, bit r of its mask is (q[i0+r] == k[i0+r-d]) (one ballot, lanes = rows).  The
+// length at strip row r is the run of set bits ending at r: it stops at the last clear bit,
+// or at the last query reset at or above r (where the match starts afresh), or else runs into
+// the strip's boundary row i0 - 1, whose length dense_bound_kernel stored (the carry).
 
-// Stage `rows` rows of width W (elements of T) as fp32 into dst[row][W]; source row x at
-// src + (row0 + pos(x) * H) * W; rows with pos(x) outside [0, n) are zero.  Returns (via the
-// workgroup) whether every staged value is finite.
-template <typename T, int W, typename Pos>
-__device__ __forceinline__ bool stage_rows(float* dst, const T* src, long row0, long H,
-                                           int rows, int n, Pos pos, int tid) {
-    constexpr int E = (int)(16 / sizeof(T)) < W ? (int)(16 / sizeof(T)) : W;
-    constexpr int CH = W / E;  // chunks per row
-    bool fin = true;
-    for (int c = tid; c < rows * CH; c += DENSE_THREADS) {
-        const int x = c / CH, col = (c - x * CH) * E;
-        const int p = pos(x);
-        float f[E];
-        if (p >= 0 && p < n) {
-            load_row<T, E>(src + (row0 + (long)p * H) * W + col, f);
-        } else {
-#pragma unroll
-            for (int e = 0; e < E; ++e) f[e] = 0.0f;
-        }
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            fin = fin && (__builtin_fabsf(f[e]) <= 3.402823466e38f);
-            dst[x * W + col + e] = f[e];
-        }
-    }
-    return __syncthreads_and(fin ? 1 : 0) != 0;
-}
+typedef __attribute__((address_space(4))) const uint32_t cu32_t;
 
-template <int N>
-__device__ __forceinline__ void lds_vec(const float* p, float (&out)[N]) {
-    if constexpr (N % 4 == 0) {
-#pragma unroll
-        for (int c = 0; c < N / 4; ++c) {
-            const float4 x = reinterpret_cast<const float4*>(p)[c];
-            out[4 * c] = x.x; out[4 * c + 1] = x.y; out[4 * c + 2] = x.z; out[4 * c + 3] = x.w;
-        }
-    } else if constexpr (N % 2 == 0) {
+// N consecutive elements of a wave-uniform row as fp32 (scalar loads)
+template <typename T, int N>
+__device__ __forceinline__ void uniform_row(const T* p, float (&out)[N]) {
+    cu32_t* w = (cu32_t*)(const void*)p;
+    if constexpr (sizeof(T) == 2) {
+        static_assert(N % 2 == 0, "bf16 rows hold an even element count");
 #pragma unroll
         for (int c = 0; c < N / 2; ++c) {
-            const float2 x = reinterpret_cast<const float2*>(p)[c];
-            out[2 * c] = x.x; out[2 * c + 1] = x.y;
+            const uint32_t x = w[c];
+            out[2 * c] = bf16_lo(x);
+            out[2 * c + 1] = bf16_hi(x);
         }
     } else {
 #pragma unroll
-        for (int c = 0; c < N; ++c) out[c] = p[c];
+        for (int c = 0; c < N; ++c) out[c] = __uint_as_float(w[c]);
     }
 }
 
-__device__ __forceinline__ void lds4(const float* p, float (&o)[4]) {
-    const float4 x = *reinterpret_cast<const float4*>(p);
-    o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w;
+// acc[e] = fma(c, row[e], acc[e]) over a wave-uniform row (scalar loads), 32 elements per
+// chunk so the unpacked chunk fits the scalar registers; SAFE: only where `valid`
+template <typename T, int N, bool SAFE>
+__device__ __forceinline__ void fma_uniform_row(const T* p, float c, bool valid, float (&acc)[N]) {
+    constexpr int CH = N < 32 ? N : 32;
+#pragma unroll
+    for (int c0 = 0; c0 < N; c0 += CH) {
+        float x[CH];
+        uniform_row<T, CH>(p + c0, x);
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+            if constexpr (SAFE) acc[c0 + e] = valid ? __builtin_fmaf(c, x[e], acc[c0 + e]) : acc[c0 + e];
+            else acc[c0 + e] = __builtin_fmaf(c, x[e], acc[c0 + e]);
+        }
+    }
+}
+
+// s = chain over e of fma(a[e], row[e], s) for a wave-uniform row (scalar loads, chunked)
+template <typename T, int N>
+__device__ __forceinline__ float dot_uniform_row(const T* p, const float (&a)[N]) {
+    constexpr int CH = N < 32 ? N : 32;
+    float s = 0.0f;
+#pragma unroll
+    for (int c0 = 0; c0 < N; c0 += CH) {
+        float x[CH];
+        uniform_row<T, CH>(p + c0, x);
+#pragma unroll
+        for (int e = 0; e < CH; ++e) s = __builtin_fmaf(a[c0 + e], x[e], s);
+    }
+    return s;
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// masks and carries of diagonals, addressed by slot (the caller's diagonal numbering)
+struct DiagMasks {
+    unsigned long long m[128];
+    int c[128];
+};
+
+// length at strip row r of a diagonal (mask m, carry c); rm: the strip's reset rows
+__device__ __forceinline__ int diag_length(unsigned long long m, int c, int r,
+                                           unsigned long long rm) {
+    const unsigned long long upto = (2ull << r) - 1ull;  // rows 0 .. r (r = 63: all)
+    const unsigned long long z = ~m & upto, rz = rm & upto;
+    const int p0 = 63 - __clzll((long long)z);   // last mismatch at or above r, -1 if none
+    const int pr = 63 - __clzll((long long)rz);  // last reset at or above r, -1 if none
+    const int L = pr > p0 ? r - pr + 1 : (p0 >= 0 ? r - p0 : r + 1 + c);
+    return ((m >> r) & 1ull) ? L : 0;
+}
+
+// length at (strip row r, diagonal d = i - j) from the ring slot d & 127; 0 for d < 0
+__device__ __forceinline__ int strip_length(const DiagMasks& D, int d, int r,
+                                            unsigned long long rm) {
+    const int slot = d & 127;
+    const int L = diag_length(D.m[slot], D.c[slot], r, rm);
+    return d >= 0 ? L : 0;
+}
+
+// Fill slot (d & 127) for diagonals d in [d_lo, d_hi] (d >= 0) of the strip at i0: lanes are
+// the strip's rows (qlab: the lane's query label, qv: the row exists).
+__device__ __forceinline__ void fill_diags(DiagMasks& D, const int32_t* __restrict__ k, int n,
+                                           int i0, int qlab, bool qv,
+                                           const uint16_t* __restrict__ bstrip, int d_lo,
+                                           int d_hi, int lane) {
+    for (int d = d_lo; d <= d_hi; ++d) {
+        const int j = i0 + lane - d;
+        const bool in = qv && j >= 0 && j < n;
+        const int kv = k[in ? j : 0];
+        const unsigned long long m = __ballot(in && kv == qlab);
+        const int jc = i0 - 1 - d;
+        if (lane == 0) {
+            D.m[d & 127] = m;
+            D.c[d & 127] = (bstrip && jc >= 0) ? (int)bstrip[jc] : 0;
+        }
+    }
 }
 
 // persistent item order: the longest strips first
@@ -295,443 +331,328 @@ __device__ __forceinline__ DenseItem dense_item(const PathArgs& a, long x, int c
     return it;
 }
 
-template <typename T>
-__device__ __forceinline__ void store_out(void* out, int out_dtype, long idx, const float* x,
-                                          int cnt) {
-    if (out_dtype == DTYPE_F32) {
-        float* o = reinterpret_cast<float*>(out) + idx;
-        for (int c = 0; c < cnt; ++c) o[c] = x[c];
+// 1 when every element of row p (N elements of T) is finite
+template <typename T, int N>
+__device__ __forceinline__ bool row_finite(const T* p) {
+    float f[N];
+    load_row<T, N>(p, f);
+    bool ok = true;
+#pragma unroll
+    for (int c = 0; c < N; ++c) ok = ok && (__builtin_fabsf(f[c]) <= 3.402823466e38f);
+    return ok;
+}
+
+template <int N>
+__device__ __forceinline__ void store_f32_row(float* o, const float (&x)[N]) {
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (int c = 0; c < N / 4; ++c)
+            reinterpret_cast<float4*>(o)[c] = make_float4(x[4 * c], x[4 * c + 1], x[4 * c + 2],
+                                                          x[4 * c + 3]);
     } else {
-        uint16_t* o = reinterpret_cast<uint16_t*>(out) + idx;
-        for (int c = 0; c < cnt; ++c) o[c] = (uint16_t)f32_to_bf16_bits(x[c]);
+#pragma unroll
+        for (int c = 0; c < N; ++c) o[c] = x[c];
     }
 }
 
+template <int N>
+__device__ __forceinline__ void store_row(void* out, int out_dtype, long idx,
+                                          const float (&x)[N]) {
+    if (out_dtype == DTYPE_F32) {
+        store_f32_row<N>(reinterpret_cast<float*>(out) + idx, x);
+    } else {
+        uint32_t* o = reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(out) + idx);
+#pragma unroll
+        for (int c = 0; c < N; c += 2)
+            o[c / 2] = f32_to_bf16_bits(x[c]) | (f32_to_bf16_bits(x[c + 1]) << 16);
+    }
+}
+
+constexpr int DKT = 32;  // keys per diagonal refill of the query-strip kernels
+
 // ---------------------------------------------------------------------------------------
-// forward: workgroup per (dense row, 64-query strip), key tiles of DK ascending; pass 1 the
-// row shift m and the longest match, pass 2 the readout.
+// forward: wave per (dense row, 64-query strip); pass 1 the row shift m and the longest
+// match, pass 2 the readout, keys ascending.
 template <typename T, int R, int DV>
 __global__ __launch_bounds__(DENSE_THREADS) void dense_forward_kernel(PathArgs a) {
-    constexpr int KT = DK, KS = KT + 1, CPT = DV / 16, KG = KT / 4;
-    __shared__ int s_qlab[64], s_rst[64], s_klab[KT + 64];
-    __shared__ int s_L[64 * KS];
-    __shared__ __attribute__((aligned(16))) float s_sk[KT * R];
-    __shared__ __attribute__((aligned(16))) float s_v[KT * DV];
-    __shared__ __attribute__((aligned(16))) float s_c[KT * 64];
-    __shared__ __attribute__((aligned(16))) float s_p[KT * 64];
-    __shared__ float s_m[64], s_den[64];
-    __shared__ float s_pm[4][64];
-    __shared__ unsigned long long s_key[4][64];
-    const int tid = (int)threadIdx.x, l = tid & 63, g = tid >> 6;
-    const int qq = tid & 15, cg = tid >> 4;
+    __shared__ DiagMasks s_d[DENSE_THREADS / 64];
+    const int lane = lane_id(), w = wave_id();
+    DiagMasks& D = s_d[w];
     const int n = a.n, Q = (n + 63) >> 6;
-    const int cnt = __builtin_amdgcn_readfirstlane(*a.o.dcount);
+    const int cnt = __builtin_amdgcn_readfirstlane(a.o.dcount[0]);
     const long items = (long)cnt * Q;
     const T* sq = reinterpret_cast<const T*>(a.sq);
     const T* sk = reinterpret_cast<const T*>(a.sk);
     const T* v = reinterpret_cast<const T*>(a.v);
-    for (long x = blockIdx.x; x < items; x += gridDim.x) {
+    for (long x = (long)blockIdx.x * (DENSE_THREADS / 64) + w; x < items;
+         x += (long)gridDim.x * (DENSE_THREADS / 64)) {
         const DenseItem it = dense_item(a, x, cnt, Q, true);
-        const int bh = it.bh, qs = it.strip;
+        const int bh = __builtin_amdgcn_readfirstlane(it.bh);
+        const int qs = __builtin_amdgcn_readfirstlane(it.strip);
         if (!a.hard[bh]) continue;
         const int b = bh / a.H, h = bh - b * a.H;
         const long so = (long)bh * n, row0 = (long)b * n * a.H + h;
         const int i0 = qs * 64, nq = n - i0 < 64 ? n - i0 : 64;
+        const int i = i0 + lane;
+        const bool qv = lane < nq;
+        const int32_t* k = a.ik + so;
+        const int qlab = qv ? a.iq[so + i] : 0;
+        const unsigned long long rm = __ballot(qv && dense_reset(a, so, i));
         const uint16_t* bstrip = dense_strip(a, bh, qs);
         const float* lut = a.lut + (long)h * a.lut_stride;
-        const int nkt = (i0 + nq + KT - 1) / KT;
-        __syncthreads();
-        if (tid < 64) {
-            s_qlab[tid] = tid < nq ? a.iq[so + i0 + tid] : 0;
-            s_rst[tid] = tid < nq ? dense_reset(a, so, i0 + tid) : 0;
-        }
+        const int nk = i0 + nq;  // keys 0 .. nk-1 can pair with the strip
         float sqr[R];
-        load_row<T, R>(sq + (row0 + (long)(l < nq ? i0 + l : i0) * a.H) * R, sqr);
-        auto stage_keys = [&](int j0) {
-            if (tid < KT + 64) {
-                const int j = j0 - 64 + tid;
-                s_klab[tid] = (j >= 0 && j < n) ? a.ik[so + j] : 0;
-            }
-        };
+        load_row<T, R>(sq + (row0 + (long)(qv ? i : i0) * a.H) * R, sqr);
         // ---- pass 1: m = max(0, LUT[L]), longest match (ties -> largest key)
         float m = 0.0f;
         int best = 0, bj = -1;
-        for (int kt = 0; kt < nkt; ++kt) {
-            const int j0 = kt * KT;
-            __syncthreads();
-            stage_keys(j0);
-            __syncthreads();
-            dense_lengths<KT>(s_qlab, s_rst, s_klab, s_L, i0, j0, nq, n, bstrip, tid);
-            __syncthreads();
-#pragma unroll
-            for (int u = 0; u < KG; ++u) {
-                const int jl = g * KG + u;
-                const int L = s_L[l * KS + jl];
+        int filled = i0 + 64;  // lowest diagonal filled so far
+        for (int j0 = 0; j0 < nk; j0 += DKT) {
+            const int lo = i0 - (j0 + DKT - 1) > 0 ? i0 - (j0 + DKT - 1) : 0;
+            const int hi = i0 + 63 - j0 < filled - 1 ? i0 + 63 - j0 : filled - 1;
+            fill_diags(D, k, n, i0, qlab, qv, bstrip, lo, hi, lane);
+            filled = lo;
+            wave_sync_lds();
+            const int je = j0 + DKT < nk ? j0 + DKT : nk;
+            for (int j = j0; j < je; ++j) {
+                const int L = strip_length(D, i - j, lane, rm);
                 if (L > 0) {
                     const float lw = lut[L];
                     if (lw > m) m = lw;
                     if (L >= best) {
                         best = L;
-                        bj = j0 + jl;
+                        bj = j;
                     }
                 }
             }
+            wave_sync_lds();
         }
-        s_pm[g][l] = m;
-        s_key[g][l] = ((unsigned long long)(uint32_t)best << 32) | (uint32_t)(bj + 1);
-        __syncthreads();
-        if (g == 0) {
-            float mm = s_pm[0][l];
-            unsigned long long key = s_key[0][l];
+        // ---- pass 2: den = exp2(-m) + sum p; acc = sum (p s) v, keys ascending
+        float den = exp2_fp32(-m), acc[DV];
 #pragma unroll
-            for (int u = 1; u < 4; ++u) {
-                mm = s_pm[u][l] > mm ? s_pm[u][l] : mm;
-                key = s_key[u][l] > key ? s_key[u][l] : key;
-            }
-            s_m[l] = mm;
-            s_key[0][l] = key;
-        }
-        __syncthreads();
-        const float mq = s_m[l];
-        // ---- pass 2
-        float acc[4][CPT], den[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            den[q] = exp2_fp32(-s_m[4 * qq + q]);
-#pragma unroll
-            for (int c = 0; c < CPT; ++c) acc[q][c] = 0.0f;
-        }
-        for (int kt = 0; kt < nkt; ++kt) {
-            const int j0 = kt * KT;
-            __syncthreads();
-            stage_keys(j0);
-            stage_rows<T, R>(s_sk, sk, row0, a.H, KT, n, [&](int y) { return j0 + y; }, tid);
-            const bool fin =
-                stage_rows<T, DV>(s_v, v, row0, a.H, KT, n, [&](int y) { return j0 + y; }, tid);
-            dense_lengths<KT>(s_qlab, s_rst, s_klab, s_L, i0, j0, nq, n, bstrip, tid);
-            __syncthreads();
-            // phase A: lane = query l, keys g*KG .. g*KG + KG - 1
-#pragma unroll 2
-            for (int u = 0; u < KG; ++u) {
-                const int jl = g * KG + u;
-                const int L = s_L[l * KS + jl];
-                const bool valid = L > 0;
-                const float p = valid ? exp2_fp32(lut[L] - mq) : 0.0f;
-                float skr[R];
-                lds_vec<R>(&s_sk[jl * R], skr);
-                float s = 0.0f;
-#pragma unroll
-                for (int r = 0; r < R; ++r) s = __builtin_fmaf(sqr[r], skr[r], s);
-                s_c[jl * 64 + l] = valid ? p * s : 0.0f;
-                s_p[jl * 64 + l] = p;
-            }
-            __syncthreads();
-            // phase B: lanes = 4 queries x CPT columns, keys ascending
-            auto fold = [&](auto safe) {
-                for (int jl = 0; jl < KT; ++jl) {
-                    float c4[4], vv[CPT];
-                    lds4(&s_c[jl * 64 + 4 * qq], c4);
-                    lds_vec<CPT>(&s_v[jl * DV + cg * CPT], vv);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        if (decltype(safe)::value && s_L[(4 * qq + q) * KS + jl] == 0) continue;
-#pragma unroll
-                        for (int c = 0; c < CPT; ++c)
-                            acc[q][c] = __builtin_fmaf(c4[q], vv[c], acc[q][c]);
-                    }
-                    if (cg == 0) {
-                        float p4[4];
-                        lds4(&s_p[jl * 64 + 4 * qq], p4);
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) den[q] = den[q] + p4[q];
-                    }
+        for (int d = 0; d < DV; ++d) acc[d] = 0.0f;
+        filled = i0 + 64;
+        for (int j0 = 0; j0 < nk; j0 += DKT) {
+            const int lo = i0 - (j0 + DKT - 1) > 0 ? i0 - (j0 + DKT - 1) : 0;
+            const int hi = i0 + 63 - j0 < filled - 1 ? i0 + 63 - j0 : filled - 1;
+            fill_diags(D, k, n, i0, qlab, qv, bstrip, lo, hi, lane);
+            filled = lo;
+            const int je = j0 + DKT < nk ? j0 + DKT : nk;
+            // keys of this refill whose value rows are all finite (the common case): invalid
+            // cells then add exact zeros; otherwise they are skipped explicitly
+            const int jf = j0 + (lane < DKT ? lane : 0);
+            const unsigned long long fin =
+                __ballot(lane < je - j0 && row_finite<T, DV>(v + (row0 + (long)jf * a.H) * DV));
+            wave_sync_lds();
+            auto keys = [&](auto safe) {
+                for (int j = j0; j < je; ++j) {
+                    const int L = strip_length(D, i - j, lane, rm);
+                    const bool valid = L > 0;
+                    const long krow = row0 + (long)__builtin_amdgcn_readfirstlane(j) * a.H;
+                    const float s = dot_uniform_row<T, R>(sk + krow * R, sqr);
+                    const float p = valid ? exp2_fp32(lut[L] - m) : 0.0f;
+                    const float c = valid ? p * s : 0.0f;
+                    den = den + p;
+                    fma_uniform_row<T, DV, decltype(safe)::value>(v + krow * DV, c, valid, acc);
                 }
             };
-            if (fin) fold(std::integral_constant<bool, false>{});
-            else fold(std::integral_constant<bool, true>{});
+            // (a tile whose value rows are all finite lets invalid cells add exact zeros)
+            if (fin == (je - j0 == 64 ? ~0ull : ((1ull << (je - j0)) - 1ull)))
+                keys(std::integral_constant<bool, false>{});
+            else
+                keys(std::integral_constant<bool, true>{});
+            wave_sync_lds();
         }
-        if (cg == 0) {
+        if (qv) {
+            float o[DV];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) s_den[4 * qq + q] = den[q];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int il = 4 * qq + q;
-            if (il >= nq) continue;
-            const float dd = s_den[il];
-            float o[CPT];
-#pragma unroll
-            for (int c = 0; c < CPT; ++c) o[c] = acc[q][c] / dd;
-            store_out<T>(a.out, a.out_dtype, (row0 + (long)(i0 + il) * a.H) * DV + cg * CPT, o,
-                         CPT);
-        }
-        if (tid < nq) {
-            const float dd = s_den[tid];
-            a.lse2[so + i0 + tid] = s_m[tid] + log2_fp32(dd);
-            const unsigned long long key = s_key[0][tid];
-            if (a.lmax) a.lmax[so + i0 + tid] = (int)(key >> 32);
-            if (a.jarg) a.jarg[so + i0 + tid] = (int)(uint32_t)(key & 0xffffffffu) - 1;
+            for (int e = 0; e < DV; ++e) o[e] = acc[e] / den;
+            store_row<DV>(a.out, a.out_dtype, (row0 + (long)i * a.H) * DV, o);
+            a.lse2[so + i] = m + log2_fp32(den);
+            if (a.lmax) a.lmax[so + i] = best;
+            if (a.jarg) a.jarg[so + i] = bj;
         }
     }
 }
 
 // ---------------------------------------------------------------------------------------
-// backward, query rows (dSQ, rowtau): workgroup per (dense row, 64-query strip).
+// backward, query rows (dSQ, rowtau): wave per (dense row, 64-query strip), keys ascending.
 template <typename T, int R, int DV>
 __global__ __launch_bounds__(DENSE_THREADS) void dense_rows_kernel(PathArgs a) {
-    constexpr int KT = DK, KS = KT + 1, KG = KT / 4;
-    constexpr int RPT = R >= 4 ? R / 4 : 1;  // readout rows per thread in phase B
-    __shared__ int s_qlab[64], s_rst[64], s_klab[KT + 64];
-    __shared__ int s_L[64 * KS];
-    __shared__ __attribute__((aligned(16))) float s_sk[KT * R];
-    __shared__ __attribute__((aligned(16))) float s_v[KT * DV];
-    __shared__ __attribute__((aligned(16))) float s_pe[KT * 64];
-    __shared__ __attribute__((aligned(16))) float s_pse[KT * 64];
-    __shared__ __attribute__((aligned(16))) float s_pp[KT * 64];
-    __shared__ __attribute__((aligned(16))) float s_gg[KT * 64];
-    __shared__ float s_red[4][64];
-    const int tid = (int)threadIdx.x, l = tid & 63, g = tid >> 6;
+    __shared__ DiagMasks s_d[DENSE_THREADS / 64];
+    const int lane = lane_id(), w = wave_id();
+    DiagMasks& D = s_d[w];
     const int n = a.n, Q = (n + 63) >> 6;
-    const int cnt = __builtin_amdgcn_readfirstlane(*a.o.dcount);
+    const int cnt = __builtin_amdgcn_readfirstlane(a.o.dcount[0]);
     const long items = (long)cnt * Q;
     const T* sq = reinterpret_cast<const T*>(a.sq);
     const T* sk = reinterpret_cast<const T*>(a.sk);
     const T* v = reinterpret_cast<const T*>(a.v);
     const T* dout = reinterpret_cast<const T*>(a.dout);
-    for (long x = blockIdx.x; x < items; x += gridDim.x) {
+    for (long x = (long)blockIdx.x * (DENSE_THREADS / 64) + w; x < items;
+         x += (long)gridDim.x * (DENSE_THREADS / 64)) {
         const DenseItem it = dense_item(a, x, cnt, Q, true);
-        const int bh = it.bh, qs = it.strip;
+        const int bh = __builtin_amdgcn_readfirstlane(it.bh);
+        const int qs = __builtin_amdgcn_readfirstlane(it.strip);
         if (!a.hard[bh]) continue;
         const int b = bh / a.H, h = bh - b * a.H;
         const long so = (long)bh * n, row0 = (long)b * n * a.H + h;
         const int i0 = qs * 64, nq = n - i0 < 64 ? n - i0 : 64;
+        const int i = i0 + lane;
+        const bool qv = lane < nq;
+        const int ic = qv ? i : i0;
+        const int32_t* k = a.ik + so;
+        const int qlab = qv ? a.iq[so + i] : 0;
+        const unsigned long long rm = __ballot(qv && dense_reset(a, so, i));
         const uint16_t* bstrip = dense_strip(a, bh, qs);
         const float* lut = a.lut + (long)h * a.lut_stride;
         const float* glut = a.dlut + (long)h * a.lut_stride;
-        const int nkt = (i0 + nq + KT - 1) / KT;
-        __syncthreads();
-        if (tid < 64) {
-            s_qlab[tid] = tid < nq ? a.iq[so + i0 + tid] : 0;
-            s_rst[tid] = tid < nq ? dense_reset(a, so, i0 + tid) : 0;
-        }
-        const int il_me = l < nq ? l : 0;
-        const int i = i0 + il_me;
+        const int nk = i0 + nq;
         float sqr[R], dor[DV];
-        load_row<T, R>(sq + (row0 + (long)i * a.H) * R, sqr);
-        load_row<T, DV>(dout + (row0 + (long)i * a.H) * DV, dor);
-        const float l2 = a.lse2[so + i];
-        const float cc = glut[i - doc_start(a, i) + 1];
-        float dq[RPT], chain = 0.0f;  // chain: u (g 0), vv (1), w (2), z (3)
+        load_row<T, R>(sq + (row0 + (long)ic * a.H) * R, sqr);
+        load_row<T, DV>(dout + (row0 + (long)ic * a.H) * DV, dor);
+        const float l2 = a.lse2[so + ic];
+        const float cc = glut[ic - doc_start(a, ic) + 1];
+        float dq[R], u = 0.0f, vv = 0.0f, ww = 0.0f, z = 0.0f;
 #pragma unroll
-        for (int x2 = 0; x2 < RPT; ++x2) dq[x2] = 0.0f;
-        const int r0 = g * RPT;
-        for (int kt = 0; kt < nkt; ++kt) {
-            const int j0 = kt * KT;
-            __syncthreads();
-            if (tid < KT + 64) {
-                const int j = j0 - 64 + tid;
-                s_klab[tid] = (j >= 0 && j < n) ? a.ik[so + j] : 0;
-            }
-            const bool fin = stage_rows<T, R>(s_sk, sk, row0, a.H, KT, n,
-                                              [&](int y) { return j0 + y; }, tid);
-            stage_rows<T, DV>(s_v, v, row0, a.H, KT, n, [&](int y) { return j0 + y; }, tid);
-            dense_lengths<KT>(s_qlab, s_rst, s_klab, s_L, i0, j0, nq, n, bstrip, tid);
-            __syncthreads();
-            // phase A: lane = query l, keys g*KG ..
-#pragma unroll 1
-            for (int u = 0; u < KG; ++u) {
-                const int jl = g * KG + u;
-                const int L = s_L[l * KS + jl];
-                const bool valid = L > 0;
-                const float p = valid ? exp2_fp32(lut[L] - l2) : 0.0f;
-                float s = 0.0f, e = 0.0f;
-                {
-                    float skr[R];
-                    lds_vec<R>(&s_sk[jl * R], skr);
-#pragma unroll
-                    for (int r = 0; r < R; ++r) s = __builtin_fmaf(sqr[r], skr[r], s);
-                }
-#pragma unroll
-                for (int d0 = 0; d0 < DV; d0 += 16) {
-                    float vr[16];
-                    lds_vec<16>(&s_v[jl * DV + d0], vr);
-#pragma unroll
-                    for (int d = 0; d < 16; ++d) e = __builtin_fmaf(dor[d0 + d], vr[d], e);
-                }
-                const float ps = p * s, pe = p * e, pse = ps * e;
-                const float gg = valid ? glut[L] - cc : 0.0f;
-                s_pe[jl * 64 + l] = valid ? pe : 0.0f;
-                s_pse[jl * 64 + l] = valid ? pse : 0.0f;
-                s_pp[jl * 64 + l] = p;
-                s_gg[jl * 64 + l] = gg;
-            }
-            __syncthreads();
-            // phase B: lane = query l; g: readout rows r0.., and one of the four chains
-            auto fold = [&](auto safe) {
-                for (int jl = 0; jl < KT; ++jl) {
-                    if (decltype(safe)::value && s_L[l * KS + jl] == 0) continue;
-                    const float pe = s_pe[jl * 64 + l];
-                    if (r0 < R) {
-                        float skr[RPT];
-                        lds_vec<RPT>(&s_sk[jl * R + r0], skr);
-#pragma unroll
-                        for (int x2 = 0; x2 < RPT; ++x2) dq[x2] = __builtin_fmaf(pe, skr[x2], dq[x2]);
-                    }
-                    if (g == 0) chain = chain + s_pse[jl * 64 + l];
-                    else if (g == 1) chain = __builtin_fmaf(s_pp[jl * 64 + l], s_gg[jl * 64 + l], chain);
-                    else if (g == 2) chain = __builtin_fmaf(s_pse[jl * 64 + l], s_gg[jl * 64 + l], chain);
-                    else chain = chain + s_pp[jl * 64 + l];
+        for (int r = 0; r < R; ++r) dq[r] = 0.0f;
+        int filled = i0 + 64;
+        for (int j0 = 0; j0 < nk; j0 += DKT) {
+            const int lo = i0 - (j0 + DKT - 1) > 0 ? i0 - (j0 + DKT - 1) : 0;
+            const int hi = i0 + 63 - j0 < filled - 1 ? i0 + 63 - j0 : filled - 1;
+            fill_diags(D, k, n, i0, qlab, qv, bstrip, lo, hi, lane);
+            filled = lo;
+            const int je = j0 + DKT < nk ? j0 + DKT : nk;
+            const int jf = j0 + (lane < DKT ? lane : 0);
+            const unsigned long long fin =
+                __ballot(lane < je - j0 && row_finite<T, R>(sk + (row0 + (long)jf * a.H) * R));
+            wave_sync_lds();
+            auto keys = [&](auto safe) {
+                for (int j = j0; j < je; ++j) {
+                    const int L = strip_length(D, i - j, lane, rm);
+                    const bool valid = L > 0;
+                    const long krow = row0 + (long)__builtin_amdgcn_readfirstlane(j) * a.H;
+                    const float s = dot_uniform_row<T, R>(sk + krow * R, sqr);
+                    const float e = dot_uniform_row<T, DV>(v + krow * DV, dor);
+                    const float p = valid ? exp2_fp32(lut[L] - l2) : 0.0f;
+                    const float ps = p * s, pe = valid ? p * e : 0.0f;
+                    const float pse = valid ? ps * e : 0.0f;
+                    const float g = valid ? glut[L] - cc : 0.0f;
+                    fma_uniform_row<T, R, decltype(safe)::value>(sk + krow * R, pe, valid, dq);
+                    u = u + pse;
+                    vv = __builtin_fmaf(p, g, vv);
+                    ww = __builtin_fmaf(pse, g, ww);
+                    z = z + p;
                 }
             };
-            if (fin) fold(std::integral_constant<bool, false>{});
-            else fold(std::integral_constant<bool, true>{});
+            if (fin == (je - j0 == 64 ? ~0ull : ((1ull << (je - j0)) - 1ull)))
+                keys(std::integral_constant<bool, false>{});
+            else
+                keys(std::integral_constant<bool, true>{});
+            wave_sync_lds();
         }
-        if (l < nq && r0 < R) {
-            float* o = a.dsq + (row0 + (long)(i0 + l) * a.H) * R + r0;
-#pragma unroll
-            for (int x2 = 0; x2 < RPT; ++x2) o[x2] = dq[x2];
-        }
-        s_red[g][l] = chain;
-        __syncthreads();
-        if (g == 0 && l < nq) {
-            const float u = s_red[0][l], vv = s_red[1][l], w = s_red[2][l], z = s_red[3][l];
+        if (qv) {
+            store_f32_row<R>(a.dsq + (row0 + (long)i * a.H) * R, dq);
             const float f = exp2_fp32(-l2);
             const float mass = z + f;
             const float mean = __builtin_fmaf(-f, cc, vv) / mass;
-            a.rowtau[so + i0 + l] = __builtin_fmaf(-u, mean, w) / mass;
+            a.rowtau[so + i] = __builtin_fmaf(-u, mean, ww) / mass;
         }
     }
 }
 
 // ---------------------------------------------------------------------------------------
-// backward, keys (dSK, dV): workgroup per (dense row, strip of DK keys), 64-query tiles
-// ascending from the tile holding the strip's first key.
+// backward, keys (dSK, dV): wave per (dense row, 64-key strip), lane = key, queries ascending
+// from the strip's first key; the masks of each 64-row query strip are rebuilt (lanes =
+// rows for the ballots).
 template <typename T, int R, int DV>
 __global__ __launch_bounds__(DENSE_THREADS) void dense_keys_kernel(PathArgs a) {
-    constexpr int KT = DK, KS = KT + 1, QG = 64 / 8;
-    constexpr int RB = R >= 8 ? R / 8 : 1;   // dSK rows per thread (8 row groups)
-    constexpr int C2 = DV / 32;              // dV columns per thread (32 column groups)
-    __shared__ int s_qlab[64], s_rst[64], s_klab[KT + 64];
-    __shared__ int s_L[64 * KS];
-    __shared__ __attribute__((aligned(16))) float s_sq[64 * R];
-    __shared__ __attribute__((aligned(16))) float s_do[64 * DV];
-    __shared__ __attribute__((aligned(16))) float s_pe[64 * KT];
-    __shared__ __attribute__((aligned(16))) float s_ps[64 * KT];
-    __shared__ float s_l2[64];
-    const int tid = (int)threadIdx.x;
-    const int kl = tid & 31, g8 = tid >> 5;     // phase A: key kl, queries g8*QG ..
-    const int kq = tid & 7, cgv = tid >> 3;     // phase B dV: keys 4kq.., columns cgv*C2 ..
-    const int n = a.n, S = (n + KT - 1) / KT;
-    const int cnt = __builtin_amdgcn_readfirstlane(*a.o.dcount);
+    __shared__ DiagMasks s_d[DENSE_THREADS / 64];
+    const int lane = lane_id(), w = wave_id();
+    DiagMasks& D = s_d[w];
+    const int n = a.n, S = (n + 63) >> 6;
+    const int cnt = __builtin_amdgcn_readfirstlane(a.o.dcount[0]);
     const long items = (long)cnt * S;
     const T* sq = reinterpret_cast<const T*>(a.sq);
     const T* sk = reinterpret_cast<const T*>(a.sk);
     const T* v = reinterpret_cast<const T*>(a.v);
     const T* dout = reinterpret_cast<const T*>(a.dout);
-    for (long x = blockIdx.x; x < items; x += gridDim.x) {
+    for (long x = (long)blockIdx.x * (DENSE_THREADS / 64) + w; x < items;
+         x += (long)gridDim.x * (DENSE_THREADS / 64)) {
         const DenseItem it = dense_item(a, x, cnt, S, false);
-        const int bh = it.bh, ks = it.strip;
+        const int bh = __builtin_amdgcn_readfirstlane(it.bh);
+        const int ks = __builtin_amdgcn_readfirstlane(it.strip);
         if (!a.hard[bh]) continue;
         const int b = bh / a.H, h = bh - b * a.H;
         const long so = (long)bh * n, row0 = (long)b * n * a.H + h;
-        const int j0 = ks * KT, nk = n - j0 < KT ? n - j0 : KT;
+        const int j0 = ks * 64, nk = n - j0 < 64 ? n - j0 : 64;
+        const int j = j0 + lane;
+        const bool kv = lane < nk;
+        const int jc = kv ? j : j0;
+        const int32_t* k = a.ik + so;
         const float* lut = a.lut + (long)h * a.lut_stride;
-        const int jme = j0 + (kl < nk ? kl : 0);
         float skr[R], vr[DV];
-        load_row<T, R>(sk + (row0 + (long)jme * a.H) * R, skr);
-        load_row<T, DV>(v + (row0 + (long)jme * a.H) * DV, vr);
-        float dk[RB], dv[4][C2];
+        load_row<T, R>(sk + (row0 + (long)jc * a.H) * R, skr);
+        load_row<T, DV>(v + (row0 + (long)jc * a.H) * DV, vr);
+        float dk[R], dvv[DV];
 #pragma unroll
-        for (int x2 = 0; x2 < RB; ++x2) dk[x2] = 0.0f;
+        for (int r = 0; r < R; ++r) dk[r] = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int c = 0; c < C2; ++c) dv[q][c] = 0.0f;
-        const int rk0 = g8 * RB;
-        __syncthreads();
-        if (tid < KT + 64) {
-            const int j = j0 - 64 + tid;
-            s_klab[tid] = (j >= 0 && j < n) ? a.ik[so + j] : 0;
-        }
-        for (int qt = j0 / 64; qt * 64 < n; ++qt) {
+        for (int e = 0; e < DV; ++e) dvv[e] = 0.0f;
+        for (int qt = ks; qt < S; ++qt) {
             const int i0 = qt * 64, nq = n - i0 < 64 ? n - i0 : 64;
-            __syncthreads();
-            if (tid < 64) {
-                s_qlab[tid] = tid < nq ? a.iq[so + i0 + tid] : 0;
-                s_rst[tid] = tid < nq ? dense_reset(a, so, i0 + tid) : 0;
-                s_l2[tid] = tid < nq ? a.lse2[so + i0 + tid] : 0.0f;
+            // masks of the diagonals d = i - j in [i0 - j0 - 63, i0 - j0 + 63] at slot
+            // d - (i0 - j0 - 63); ballots with lanes = the query strip's rows
+            const bool rv = lane < nq;
+            const int qlab = rv ? a.iq[so + i0 + lane] : 0;
+            const unsigned long long rm = __ballot(rv && dense_reset(a, so, i0 + lane));
+            const uint16_t* bstrip = dense_strip(a, bh, qt);
+            const int dbase = i0 - j0 - 63;
+            for (int t = 0; t < 127; ++t) {
+                const int d = dbase + t;
+                const int jj = i0 + lane - d;
+                const bool in = rv && d >= 0 && jj >= 0 && jj < n;
+                const int kk = k[in ? jj : 0];
+                const unsigned long long mm = __ballot(in && kk == qlab);
+                const int jcar = i0 - 1 - d;
+                if (lane == 0) {
+                    D.m[t] = mm;
+                    D.c[t] = (bstrip && d >= 0 && jcar >= 0) ? (int)bstrip[jcar] : 0;
+                }
             }
-            const bool f1 = stage_rows<T, R>(s_sq, sq, row0, a.H, 64, n,
-                                             [&](int y) { return i0 + y; }, tid);
-            const bool f2 = stage_rows<T, DV>(s_do, dout, row0, a.H, 64, n,
-                                              [&](int y) { return i0 + y; }, tid);
-            dense_lengths<KT>(s_qlab, s_rst, s_klab, s_L, i0, j0, nq, n, dense_strip(a, bh, qt),
-                              tid);
-            __syncthreads();
-            // phase A: lane = key kl, queries g8*QG ..
-#pragma unroll 1
-            for (int u = 0; u < QG; ++u) {
-                const int il = g8 * QG + u;
-                const int L = s_L[il * KS + kl];
+            // are the strip's sq and dO rows all finite
+            const long qrow_l = row0 + (long)(rv ? i0 + lane : i0) * a.H;
+            const bool fin_all =
+                __ballot(!rv || (row_finite<T, R>(sq + qrow_l * R) &&
+                                 row_finite<T, DV>(dout + qrow_l * DV))) == ~0ull;
+            wave_sync_lds();
+            auto rows = [&](auto safe) {
+            constexpr bool SAFE = decltype(safe)::value;
+            for (int il = 0; il < nq; ++il) {
+                const int i = i0 + il;
+                const int t = il - lane + 63;  // slot of d = i - j
+                const int L0 = diag_length(D.m[t], D.c[t], il, rm);
+                const int L = (i >= j && kv) ? L0 : 0;
                 const bool valid = L > 0;
-                const float p = valid ? exp2_fp32(lut[L] - s_l2[il]) : 0.0f;
-                float s = 0.0f, e = 0.0f;
-                {
-                    float sqv[R];
-                    lds_vec<R>(&s_sq[il * R], sqv);
-#pragma unroll
-                    for (int r = 0; r < R; ++r) s = __builtin_fmaf(sqv[r], skr[r], s);
-                }
-#pragma unroll
-                for (int d0 = 0; d0 < DV; d0 += 16) {
-                    float dd[16];
-                    lds_vec<16>(&s_do[il * DV + d0], dd);
-#pragma unroll
-                    for (int d = 0; d < 16; ++d) e = __builtin_fmaf(dd[d], vr[d0 + d], e);
-                }
-                s_pe[il * KT + kl] = valid ? p * e : 0.0f;
-                s_ps[il * KT + kl] = valid ? p * s : 0.0f;
+                const long qrow = row0 + (long)__builtin_amdgcn_readfirstlane(i) * a.H;
+                const float l2 = a.lse2[so + __builtin_amdgcn_readfirstlane(i)];
+                // (fma(a, b, s) = fma(b, a, s): the chains s = sum sq[r] sk[r] and
+                // e = sum dO[q] v[q] in the documented order)
+                const float s = dot_uniform_row<T, R>(sq + qrow * R, skr);
+                const float e = dot_uniform_row<T, DV>(dout + qrow * DV, vr);
+                const float p = valid ? exp2_fp32(lut[L] - l2) : 0.0f;
+                const float pe = valid ? p * e : 0.0f, ps = valid ? p * s : 0.0f;
+                fma_uniform_row<T, R, SAFE>(sq + qrow * R, pe, valid, dk);
+                fma_uniform_row<T, DV, SAFE>(dout + qrow * DV, ps, valid, dvv);
             }
-            __syncthreads();
-            // phase B: queries ascending
-            auto fold = [&](auto safe) {
-                for (int il = 0; il < 64; ++il) {
-                    // dSK: key kl, rows rk0 ..
-                    if (rk0 < R && !(decltype(safe)::value && s_L[il * KS + kl] == 0)) {
-                        const float pe = s_pe[il * KT + kl];
-                        float sqv[RB];
-                        lds_vec<RB>(&s_sq[il * R + rk0], sqv);
-#pragma unroll
-                        for (int x2 = 0; x2 < RB; ++x2) dk[x2] = __builtin_fmaf(pe, sqv[x2], dk[x2]);
-                    }
-                    // dV: keys 4kq .. 4kq+3, columns cgv*C2 ..
-                    float ps4[4], dd[C2];
-                    lds4(&s_ps[il * KT + 4 * kq], ps4);
-                    lds_vec<C2>(&s_do[il * DV + cgv * C2], dd);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        if (decltype(safe)::value && s_L[il * KS + 4 * kq + q] == 0) continue;
-#pragma unroll
-                        for (int c = 0; c < C2; ++c) dv[q][c] = __builtin_fmaf(ps4[q], dd[c], dv[q][c]);
-                    }
-                }
             };
-            if (f1 && f2) fold(std::integral_constant<bool, false>{});
-            else fold(std::integral_constant<bool, true>{});
+            if (fin_all) rows(std::integral_constant<bool, false>{});
+            else rows(std::integral_constant<bool, true>{});
+            wave_sync_lds();
         }
-        if (kl < nk && rk0 < R) {
-            float* o = a.dsk + (row0 + (long)(j0 + kl) * a.H) * R + rk0;
-#pragma unroll
-            for (int x2 = 0; x2 < RB; ++x2) o[x2] = dk[x2];
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int jl = 4 * kq + q;
-            if (jl >= nk) continue;
-            float* o = a.dv + (row0 + (long)(j0 + jl) * a.H) * DV + cgv * C2;
-#pragma unroll
-            for (int c = 0; c < C2; ++c) o[c] = dv[q][c];
+        if (kv) {
+            store_f32_row<R>(a.dsk + (row0 + (long)j * a.H) * R, dk);
+            store_f32_row<DV>(a.dv + (row0 + (long)j * a.H) * DV, dvv);
         }
     }
 }
