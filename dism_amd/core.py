@@ -118,13 +118,18 @@ def dism_core_hard(sq, sk, v, idx_q, idx_k, hard, tau, *, layout=None):
 
 
 def dism_core(q, k, sq, sk, v, q_lse, k_lse, idx_q, idx_k, direction, hard, rtau, *,
-              cu_seqlens=None, layout=None, ctas=0, hard_planner=None, _lse_preabsorbed=False):
+              cu_seqlens=None, layout=None, ctas=0, hard_planner=None, _lse_preabsorbed=False,
+              all_hard=None):
     """Differentiable core with the reference's signature (flash_dism/__init__.py:20-40,
     backward.py:41-54) for sequences that are all hard: O = hard output (the soft core skips
     hard rows), gradients for sq, sk, v and rtau; q, k, q_lse, k_lse receive zero gradients.
     Soft rows raise NotImplementedError (they need the soft core).  ``rtau`` is the natural-log
     coefficient, used as is (no softplus), as in the reference's hard path.  ``cu_seqlens`` or
-    ``layout`` selects packed batch-1 execution (hard [training_rows, H])."""
+    ``layout`` selects packed batch-1 execution (hard [training_rows, H]).
+
+    The soft-row check reads ``hard`` on the host.  Inside torch.compile that read is not
+    possible, so a compiled caller must assert ``all_hard=True`` (otherwise tracing raises);
+    ``all_hard=True`` also skips the host read in eager mode."""
     if hard_planner is not None:
         raise NotImplementedError("the asynchronous hard planner is not part of the MI355X "
                                   "hard core")
@@ -153,8 +158,13 @@ def dism_core(q, k, sq, sk, v, q_lse, k_lse, idx_q, idx_k, direction, hard, rtau
         require(tuple(direction.shape) == (b, h), "direction must be [B,H]")
         require(isinstance(hard, torch.Tensor) and tuple(hard.shape) == (b, h),
                 "fixed hard must be [B,H]")
-    # (a host read of the flags; skipped inside a compiled graph, where soft rows give zeros)
-    if not torch.compiler.is_compiling() and not bool(hard.all()):
+    if torch.compiler.is_compiling():
+        if all_hard is not True:
+            raise NotImplementedError(
+                "dism_core under torch.compile cannot check the hard flags on the host: pass "
+                "all_hard=True to assert that every row is hard (soft rows need the soft DISM "
+                "core, which the MI355X hard core does not provide)")
+    elif all_hard is not True and not bool(hard.all()):
         raise NotImplementedError(
             "soft rows need the soft DISM core, which the MI355X hard core does not provide")
     out = dism_core_hard(sq, sk, v, idx_q, idx_k, hard, rtau, layout=layout)

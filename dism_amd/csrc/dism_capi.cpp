@@ -5,7 +5,9 @@
 #include <climits>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/dism_hard.h"
 #include "dism_launch.h"
@@ -58,34 +60,59 @@ struct Layout {
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
-// Side stream of the calling thread on the current device (default priority, non-blocking)
-// with its fork/join events, created on first use and kept for the thread's lifetime: the
-// only state the library keeps.  Null if HIP cannot create them (callers then run serially).
+// Side streams (default priority, non-blocking) with their fork/join events, one set per
+// concurrent call: a per-device pool that a call borrows from and returns to, so the number of
+// streams and events is bounded by the largest number of simultaneous calls on a device,
+// however many threads call over the process's lifetime.  The pool lives until the process
+// ends.  A call without a set (HIP could not create one) runs its launches serially.
 struct SideStream {
     hipStream_t stream = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
 };
 
-SideStream* side_stream() {
-    constexpr int MAX_DEVICES = 64;
-    thread_local SideStream cache[MAX_DEVICES];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
-    SideStream& c = cache[dev];
-    if (!c.stream) {
-        if (hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking) != hipSuccess) {
-            c.stream = nullptr;
-            return nullptr;
+constexpr int MAX_DEVICES = 64;
+std::mutex g_side_mutex;
+std::vector<SideStream*> g_side_free[MAX_DEVICES];
+
+class SideLease {
+  public:
+    SideLease() {
+        if (hipGetDevice(&dev_) != hipSuccess || dev_ < 0 || dev_ >= MAX_DEVICES) return;
+        {
+            std::lock_guard<std::mutex> lock(g_side_mutex);
+            if (!g_side_free[dev_].empty()) {
+                s_ = g_side_free[dev_].back();
+                g_side_free[dev_].pop_back();
+                return;
+            }
         }
-        if (hipEventCreateWithFlags(&c.fork, hipEventDisableTiming) != hipSuccess ||
-            hipEventCreateWithFlags(&c.join, hipEventDisableTiming) != hipSuccess) {
-            hipStreamDestroy(c.stream);
-            c.stream = nullptr;
-            return nullptr;
+        SideStream* c = new SideStream;
+        if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+            delete c;
+            return;
         }
+        if (hipEventCreateWithFlags(&c->fork, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&c->join, hipEventDisableTiming) != hipSuccess) {
+            if (c->fork) hipEventDestroy(c->fork);
+            hipStreamDestroy(c->stream);
+            delete c;
+            return;
+        }
+        s_ = c;
     }
-    return &c;
-}
+    ~SideLease() {
+        if (!s_) return;
+        std::lock_guard<std::mutex> lock(g_side_mutex);
+        g_side_free[dev_].push_back(s_);
+    }
+    SideLease(const SideLease&) = delete;
+    SideLease& operator=(const SideLease&) = delete;
+    SideStream* get() const { return s_; }
+
+  private:
+    int dev_ = -1;
+    SideStream* s_ = nullptr;
+};
 
 Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     Layout L;
@@ -407,7 +434,8 @@ int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t
     // the scan takes the rows prepared in LDS, counting their bigram partners itself (phase
     // 1); after the join the scan takes the remaining rows from the plan's counts (phase 2),
     // then the pair kernels run.  Without a side stream the same launches run in order.
-    SideStream* side = side_stream();
+    SideLease lease;
+    SideStream* side = lease.get();
     const hipStream_t s = S(stream);
     hipStream_t ps = s;
     if (side) {
@@ -570,7 +598,8 @@ int32_t dism_hard_backward(const void* sq, const void* sk, const void* v, const 
     // are independent: the key chain runs on a side stream, forked from and joined back into
     // the caller's stream (the row pairs are enqueued first so their persistent grid starts
     // first)
-    SideStream* side = side_stream();
+    SideLease lease;
+    SideStream* side = lease.get();
     const hipStream_t s = S(stream);
     void* ks = stream;
     if (side) {

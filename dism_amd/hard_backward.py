@@ -51,7 +51,9 @@ def backward_hard(sq, sk, v, dout, idx_q, idx_k, hard, normalizer, state, *, lay
         carry, strip = state["carry"], int(state["carry_strip"])
         check_tensor(carry, torch.int32, (b, h, (n - 1) // strip, n), "integer boundary",
                      sq.device)
-    elif state.get("boundary") is not None:
+    elif _given(state, "boundary"):
+        # a boundary handed in by the caller (e.g. a reference-format state) bounds the walks;
+        # a lazily offered one is not computed for this
         carry, strip = state["boundary"], 32
         check_tensor(carry, torch.int32, (b, h, (n - 1) // 32, n), "integer boundary", sq.device)
     else:
@@ -74,6 +76,13 @@ def backward_hard(sq, sk, v, dout, idx_q, idx_k, hard, normalizer, state, *, lay
                   dv, ws.data_ptr(), ws.numel(), dsq.data_ptr(), dsk.data_ptr(),
                   dvv.data_ptr(), rowtau.data_ptr(), dtau.data_ptr(), _stream(sq))
     return dsq, dsk, dvv, dtau
+
+
+def _given(state, key):
+    materialized = getattr(state, "materialized", None)
+    if materialized is not None:
+        return materialized(key) and state.get(key) is not None
+    return state.get(key) is not None
 
 
 def _state_tau(state, lut):

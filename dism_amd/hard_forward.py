@@ -9,8 +9,9 @@ O(B*H*N^2/32) int32 boundary in between):
     (rare) pairs with L >= 2 are recomputed from the labels by a suffix walk inside the
     readout.  ``carry_strip`` S > 0 (default 0 = off, env DISM_HARD_CARRY_STRIP) adds a
     composed boundary of strip height S (B*H*N^2/S int32) that bounds each walk by S steps,
-    for inputs with very long repeats.  With save_state=True the reference's strip-32
-    summary/boundary are produced too, so callers that inspect them still work;
+    for inputs with very long repeats.  With save_state=True the state also offers the
+    reference's strip-32 summary/boundary, computed when first read (callers that inspect
+    them still work; the backward does not read them);
   * fp32 vectors are accepted besides bf16 (all vectors share one dtype);
   * ``return_matches=True`` additionally returns, per query, the longest match length and
     its key index (ties -> most recent key, -1 if none).
@@ -177,6 +178,42 @@ def _forward_core(sq, sk, v, idx_q, idx_k, hard, tau, carry_strip, out_dtype, ma
     return out, lse2, lut, carry, strip, lmax, jarg, ws
 
 
+class _LazyState(dict):
+    """forward_hard's state: the reference-format strip-32 summary and boundary
+    (O(B*H*N^2/32) int32 each) are computed on first access only; the backward here does not
+    need them."""
+
+    def __init__(self, lazy, **items):
+        super().__init__(**items)
+        self._lazy = dict(lazy)
+
+    def _fill(self, key):
+        if key in self._lazy and not dict.__contains__(self, key):
+            dict.__setitem__(self, key, self._lazy.pop(key)())
+
+    def __getitem__(self, key):
+        self._fill(key)
+        return dict.__getitem__(self, key)
+
+    def get(self, key, default=None):
+        self._fill(key)
+        return dict.get(self, key, default)
+
+    def __contains__(self, key):
+        return key in self._lazy or dict.__contains__(self, key)
+
+    def keys(self):
+        return list(dict.keys(self)) + [k for k in self._lazy if not dict.__contains__(self, k)]
+
+    def items(self):
+        for k in self._lazy.copy():
+            self._fill(k)
+        return dict.items(self)
+
+    def materialized(self, key):
+        return dict.__contains__(self, key)
+
+
 @torch.no_grad()
 def forward_hard(sq, sk, v, idx_q, idx_k, hard, tau, *, layout=None, ctas=0, save_state=False,
                  _graph_choice=None, carry_strip=None, return_matches=False, out_dtype=None):
@@ -198,11 +235,13 @@ def forward_hard(sq, sk, v, idx_q, idx_k, hard, tau, *, layout=None, ctas=0, sav
             sq, sk, v, idx_q, idx_k, hard, tau, layout, out_dtype, return_matches)
         result = [out, lse2]
         if save_state:
-            summary = summarize_hard(idx_q, idx_k, hard, layout=layout)
-            boundary = hard_chunk_scan(summary, layout=layout, heads=sq.shape[2])
-            result.append(dict(summary=summary, boundary=boundary, log_weights=lut, tau=tau,
-                               strip=32, carry=None, carry_strip=0, workspace=ws,
-                               layout=layout))
+            result.append(_LazyState(
+                {"summary": lambda: summarize_hard(idx_q, idx_k, hard, layout=layout),
+                 "boundary": lambda: hard_chunk_scan(
+                     summarize_hard(idx_q, idx_k, hard, layout=layout), layout=layout,
+                     heads=sq.shape[2])},
+                log_weights=lut, tau=tau, strip=32, carry=None, carry_strip=0, workspace=ws,
+                layout=layout))
         if return_matches:
             result.append(dict(length=lmax, index=jarg))
         return tuple(result)
@@ -210,10 +249,10 @@ def forward_hard(sq, sk, v, idx_q, idx_k, hard, tau, *, layout=None, ctas=0, sav
         sq, sk, v, idx_q, idx_k, hard, tau, carry_strip, out_dtype, return_matches)
     result = [out, lse2]
     if save_state:
-        summary = summarize_hard(idx_q, idx_k, hard)
-        boundary = hard_chunk_scan(summary)
-        result.append(dict(summary=summary, boundary=boundary, log_weights=lut, tau=tau,
-                           strip=32, carry=carry, carry_strip=strip, workspace=ws))
+        result.append(_LazyState(
+            {"summary": lambda: summarize_hard(idx_q, idx_k, hard),
+             "boundary": lambda: hard_chunk_scan(summarize_hard(idx_q, idx_k, hard))},
+            log_weights=lut, tau=tau, strip=32, carry=carry, carry_strip=strip, workspace=ws))
     if return_matches:
         result.append(dict(length=lmax, index=jarg))
     return tuple(result)

@@ -983,9 +983,12 @@ void orc_backward_flags(const float* sq, const float* sk, const float* v, const 
 
 /* ---------------- vocabulary labels ----------------
  * labels[b,h,n] = argmax_v sum_d x[b,n,h,d] * vocab[h*vhs + v*D + d], summed in d order in
- * double (products of bf16 values are exact; for ordinary inputs so is the sum), first index
- * on ties -- the argmax of dism_v3/python/flash_dism/reference/dism_v3_ref.py:159-162 (torch
- * argmax returns the first maximal index) evaluated exactly. */
+ * double, first index on ties -- the argmax of
+ * dism_v3/python/flash_dism/reference/dism_v3_ref.py:159-162 (torch argmax returns the first
+ * maximal index).  The products of bf16 values are exact in double; the sum is exact while the
+ * products' exponents span less than about 53 - 16 - log2(D) bits (not for arbitrarily spread
+ * inputs, e.g. mixing subnormals with large values).  tests/test_oracle.py checks it against
+ * exact rational arithmetic on random rows, exact ties and one-ulp near ties. */
 void orc_vocab_labels(const float* x, const float* vocab, long vhs, int B, long N, int H, long V,
                       int D, int32_t* labels) {
     for (int b = 0; b < B; ++b)

@@ -1,5 +1,7 @@
 """torch.library registration of the hard core (CPU: fake/meta shapes and argument checks;
 GPU: eager vs torch.compile, reference-signature core)."""
+import functools
+
 import numpy as np
 import pytest
 import torch
@@ -67,7 +69,11 @@ def test_compiled_matches_eager():
         return out.detach(), [t.grad for t in leaves] + [tau.grad, qs.grad, lse.grad]
 
     eager = run(dism_amd.dism_core)
-    compiled = run(torch.compile(dism_amd.dism_core, backend="aot_eager", fullgraph=True))
+    compiled = run(torch.compile(functools.partial(dism_amd.dism_core, all_hard=True),
+                                 backend="aot_eager", fullgraph=True))
+    # without the assertion a compiled caller is refused (the flags cannot be read there)
+    with pytest.raises(Exception, match="all_hard=True"):
+        run(torch.compile(dism_amd.dism_core, backend="aot_eager", fullgraph=True))
     assert torch.equal(eager[0], compiled[0])
     for a, c in zip(eager[1], compiled[1]):
         assert torch.equal(a, c)

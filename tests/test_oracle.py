@@ -335,3 +335,58 @@ def test_forward_with_query_resets_pinned_by_fp64():
         assert np.abs(plain - got).max() > 1e-3
     starts = oracle.reset_starts(np.array([[[0, 1, 0, 0, 1, 0]]], bool))
     assert starts.tolist() == [[[0, 1, 1, 1, 4, 4]]]
+
+
+# ---------------------------------------------------------------- codebook argmax labels
+def _exact_vocab_labels(x, vocab):
+    """Argmax over v of sum_d x[d] * e[v, d] in exact rational arithmetic (every bf16 value is
+    a dyadic rational, so the scaled products are Python integers), first index on ties."""
+    from fractions import Fraction
+    B, N, H, D = x.shape
+    shared = vocab.ndim == 2
+    V = vocab.shape[-2]
+    xs = [[[[Fraction(float(t)) for t in x[b_, n_, h_]] for h_ in range(H)] for n_ in range(N)]
+          for b_ in range(B)]
+    es = [[[Fraction(float(t)) for t in (vocab[v_] if shared else vocab[h_, v_])]
+           for v_ in range(V)] for h_ in range(1 if shared else H)]
+    out = np.empty((B, H, N), np.int32)
+    for b_ in range(B):
+        for n_ in range(N):
+            for h_ in range(H):
+                tok = xs[b_][n_][h_]
+                table = es[0 if shared else h_]
+                best, bi = None, 0
+                for v_ in range(V):
+                    sc = sum(a * e for a, e in zip(tok, table[v_]))
+                    if best is None or sc > best:
+                        best, bi = sc, v_
+                out[b_, h_, n_] = bi
+    return out
+
+
+def test_vocab_labels_exact_argmax():
+    """orc_vocab_labels (fp64 sums in d order, first index on ties) against exact rational
+    arithmetic: random rows, duplicated codebook rows (exact ties: the first index wins) and
+    rows one bf16 ulp apart (near ties: the larger exact score wins, asserted explicitly).
+    The fp64 sum of D bf16 products is exact while the products' exponents span less than
+    about 53 - 16 - log2(D) bits, which holds for these inputs."""
+    rng = np.random.default_rng(29)
+    B, N, H, D, V = 1, 24, 2, 32, 40
+    vocab = oracle.bf16_round(rng.standard_normal((H, V, D)))
+    vocab[:, 5] = oracle.bf16_round(vocab[:, 5] * 3.0)   # long rows: tokens along them
+    vocab[:, 8] = oracle.bf16_round(vocab[:, 8] * 3.0)   # pick them over every other row
+    vocab[:, 17] = vocab[:, 5]                      # exact duplicate of row 5
+    vocab[:, 30] = vocab[:, 8]
+    bits = vocab.view(np.uint32)
+    bits[:, 30, 3] += 1 << 16                       # row 30 = row 8 with one coordinate +1 ulp
+    x = oracle.bf16_round(rng.standard_normal((B, N, H, D)))
+    x[0, :6] = vocab[:, 5][None] * 2.0              # tokens aimed at the duplicated rows
+    x[0, 6:12] = vocab[:, 8][None]                  # near tie between rows 8 and 30: the
+    # bump raised |e[30,3]|, and x[3] has e[8,3]'s sign, so row 30 is larger by one ulp term
+    got = oracle.vocab_labels(x, vocab)
+    want = _exact_vocab_labels(x, vocab)
+    np.testing.assert_array_equal(got, want)
+    assert (got[0, :, :6] == 5).all()               # first index of the exact tie
+    assert (got[0, :, 6:12] == 30).all()            # the one-ulp larger row
+    shared = oracle.bf16_round(rng.standard_normal((V, D)))
+    np.testing.assert_array_equal(oracle.vocab_labels(x, shared), _exact_vocab_labels(x, shared))
