@@ -19,6 +19,8 @@ SIGNATURES = {
     "dism_hard_chunk": [_P, _P, _I64, _I64, _P],
     "dism_hard_boundary": [_P, _P, _P, _I64, _I64, _I64, _I32, _I32, _P, _P],
     "dism_hard_prepare": [_P, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _I32, _I32, _P, _I64, _P],
+    "dism_hard_forward_noalloc": [_P, _P, _P, _I32, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                  _I32, _I32, _P, _I32, _P, _P, _P, _P],
     "dism_hard_row_modes": [_P, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P],
     "dism_hard_readout": [_P, _P, _P, _I32, _P, _P, _P, _P, _I32, _P, _I64, _I64, _I64, _I64,
                           _I32, _I32, _P, _I64, _P, _I32, _P, _P, _P, _P],
@@ -58,6 +60,7 @@ SIZE_SIGNATURES = {
     "dism_hard_prefill_workspace_bytes": [_I64, _I64, _I64, _I32, _I32, _I32],
     "dism_decoder_state_bytes": [_I64, _I32, _I32, _I64, _I32, _I32],
     "dism_decoder_prime_workspace_bytes": [_I64, _I64, _I64, _I32, _I32, _I32],
+    "dism_hard_forward_noalloc_max_bytes": [],
 }
 
 _lib = None

@@ -467,6 +467,72 @@ int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t
 
 }  // extern "C"
 
+// ---------------------------------------------------------------------------------------
+// Allocation-free forward: the workspace is this file-scope device array instead of a caller
+// buffer.  Each device the library runs on holds its own copy until the process ends.  In
+// host code `scratch` only names the symbol: its device address comes from
+// hipGetSymbolAddress, once per device (with that device current), and only that address is
+// passed to kernels.
+constexpr int64_t NOALLOC_SCRATCH_BYTES = int64_t(128) << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// device address of `scratch` on the current device (null after an error, with its text set)
+void* scratch_address() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+        fail(DISM_ERR_HIP, "forward (no allocation): no current HIP device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            fail(DISM_ERR_HIP, "forward (no allocation): hipGetSymbolAddress failed: %d (%s)",
+                 (int)e, hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" {
+
+int64_t dism_hard_forward_noalloc_max_bytes(void) { return NOALLOC_SCRATCH_BYTES; }
+
+int32_t dism_hard_forward_noalloc(const void* sq, const void* sk, const void* v, int32_t dtype,
+                                  const int32_t* iq, const int32_t* ik, const uint8_t* hard,
+                                  const float* lut, int64_t lut_stride, int64_t B, int64_t N,
+                                  int64_t H, int32_t R, int32_t DV, void* out, int32_t out_dtype,
+                                  float* lse2, int32_t* lmax, int32_t* jarg, void* stream) {
+    const char* what = "hard forward (no allocation)";
+    if (!dims_ok(B, N, H) || B * H * N > INT_MAX || !rdv_ok(R, DV) || !dtype_ok(dtype))
+        return fail(DISM_ERR_INVALID, "%s: unsupported dimensions or dtype", what);
+    const int64_t need = layout(B, N, H, R, DV).total;
+    if (need > NOALLOC_SCRATCH_BYTES)
+        return fail(DISM_ERR_INVALID,
+                    "%s: this shape needs %lld workspace bytes, above the %lld of the library's "
+                    "device scratch; use dism_hard_forward with a caller workspace",
+                    what, (long long)need, (long long)NOALLOC_SCRATCH_BYTES);
+    void* ws = scratch_address();
+    if (!ws) return DISM_ERR_HIP;
+    // the staged forward on the caller's stream only: prepare, then the readout (label scans,
+    // bigram corrections, dense rows); no side stream, no allocation
+    int32_t st = prepare_impl(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, ws, need, 0, nullptr,
+                              stream);
+    if (st) return st;
+    return dism_hard_readout(sq, sk, v, dtype, iq, ik, hard, nullptr, 0, lut, lut_stride, B, N,
+                             H, R, DV, ws, need, out, out_dtype, lse2, lmax, jarg, stream);
+}
+
+}  // extern "C"
+
 static int32_t backward_common(const void* sq, const void* sk, const void* v, const void* dout,
                                int32_t dtype, const int32_t* iq, const int32_t* ik,
                                const uint8_t* hard, const int32_t* boundary, int32_t strip,

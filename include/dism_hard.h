@@ -109,6 +109,22 @@ int32_t dism_hard_prepare(const void* sq, const void* sk, const void* v, int32_t
                           int32_t R, int32_t DV, void* workspace, int64_t workspace_bytes,
                           void* stream);
 
+/* Allocation-free one-call forward: dism_hard_forward's outputs for the same inputs (bit for
+ * bit), with its workspace in a device array inside the library instead of a caller buffer,
+ * and every launch on `stream` (no side stream).  No reference counterpart: for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The array holds dism_hard_forward_noalloc_max_bytes() bytes (128 MiB) on every
+ * device the library runs on, until the process ends; shapes whose
+ * dism_hard_workspace_bytes exceeds it fail with DISM_ERR_INVALID.  All calls on one device
+ * share the array: calls that overlap in time on one device (other streams, other threads)
+ * race and must be serialized by the caller.  Calls no hipMalloc/hipFree. */
+int64_t dism_hard_forward_noalloc_max_bytes(void);
+int32_t dism_hard_forward_noalloc(const void* sq, const void* sk, const void* v, int32_t dtype,
+                                  const int32_t* iq, const int32_t* ik, const uint8_t* hard,
+                                  const float* lut, int64_t lut_stride, int64_t B, int64_t N,
+                                  int64_t H, int32_t R, int32_t DV, void* out, int32_t out_dtype,
+                                  float* lse2, int32_t* lmax, int32_t* jarg, void* stream);
+
 /* Row modes of a prepared workspace, [B*H] int32 to `modes` (device memory): 0 = sparse row
  * (label scans + bigram walks), 1 = dense row (the bucketed label collisions exceed N^2/64:
  * direct tile kernels), 2 = sparse row whose walks stop at 64-row strip boundaries (the walk
