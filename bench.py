@@ -1,17 +1,21 @@
-"""Benchmark: flash_dism hard core fwd+bwd on one MI355X (BASELINE.json metric).
+"""Benchmark: flash_dism hard core on one MI355X (BASELINE.json metric).
 
-A step is one training pass of the hard DISM op over one synthetic batch of the headline
-configuration (B=4, H=16, T=16384, d_qk=8, d_v=64, bf16, periodic
-component on 25% of the heads):
-    labels (sign binarizer, q and k) -> log2 weight table -> [carry boundary, off by default]
-    -> forward (position orders and bigram-pair plans, the bigram half on a side stream
-    overlapping the length-1 label scan; then the pair corrections) -> dlog table
-    -> row pairs -> query-row scan (dSQ, tau terms) -> tau reduction, with the key scan (dV,
-    dSK) -> key pairs chain on a side stream (--streams 2, the default; joined each step).
-Inputs are resident in HBM before timing.  Prints ONE JSON line.  The timed region records
-events only around the two label scans (`roofline` uses the dominant one's live duration);
-`kernel_ms` comes from a separate instrumented pass with events around every stage (under
---streams 2 the overlapping stages' times include their contention).
+Default (the line the driver records): BASELINE.json configs[2] -- B=4, H=16, T=16384,
+d_qk=8, d_v=64, bf16, periodic component on 25% of the heads, forward + backward.  A step is
+one training pass of the hard DISM op over one synthetic batch:
+    labels (sign binarizer, q and k) -> log2 weight table -> forward (dism_hard_forward:
+    dense-row classification and position orders, the bigram half of the prepare on a side
+    stream overlapping the length-1 label scan, the pair corrections, the dense rows) -> dlog
+    table -> row pairs -> query-row scan / dense rows (dSQ, tau terms) -> tau reduction, with
+    the key scan / dense keys (dV, dSK) -> key pairs chain on a side stream (--streams 2, the
+    default; joined each step).
+`--config K` measures BASELINE.json configs[K] instead (0: forward only, fp32, B1 H4 T256;
+1: low-entropy d_qk=2 fwd+bwd; 3: one T=65536 sequence with copied spans, forward only;
+4: the nanochat-shaped layer, projections + op forward and backward).  Inputs are resident in
+HBM before timing.  Prints ONE JSON line.  The timed region records events only around the
+roofline candidates' stages (`roofline` uses the dominant one's live duration); `kernel_ms`
+comes from a separate instrumented pass with events around every stage (under --streams 2 the
+overlapping stages' times include their contention).
 """
 import argparse
 import json
@@ -25,6 +29,23 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK = 8.0e12             # bytes/s
+FP32_PEAK = 157.3e12          # flop/s, MI355X fp32 (vector)
+METRIC = "DISM fwd+bwd tokens/sec (B*H*T/s) at T=16k, 1 GPU"
+
+# BASELINE.json configs (generators as BASELINE.md section 2: seeds 20261201 + index, labels
+# by the sign binarizer, sq = q, sk = k, every row hard)
+CONFIGS = {
+    0: dict(B=1, H=4, T=256, dqk=8, dv=64, dtype="f32", fwd_only=True, gen="plain",
+            workload="BASELINE configs[0]: CPU reference path case, forward only, fp32"),
+    1: dict(B=2, H=8, T=2048, dqk=2, dv=64, dtype="bf16", fwd_only=False, gen="plain",
+            workload="BASELINE configs[1]: low-entropy (d_qk=2, alphabet 4) fwd+bwd"),
+    2: dict(B=4, H=16, T=16384, dqk=8, dv=64, dtype="bf16", fwd_only=False, gen="periodic",
+            workload="BASELINE configs[2]: hard DISM fwd+bwd, periodic heads"),
+    3: dict(B=1, H=16, T=65536, dqk=8, dv=128, dtype="bf16", fwd_only=True, gen="copied",
+            workload="BASELINE configs[3]: long single sequence, copied spans, forward only"),
+    4: dict(B=8, H=10, T=2048, dqk=8, dv=128, dtype="bf16", fwd_only=False, gen="layer",
+            workload="BASELINE configs[4]: nanochat-shaped DISM layer fwd+bwd (d_model 1280)"),
+}
 
 
 def make_inputs(B, T, H, dqk, dv, seed, periodic=True):
@@ -44,16 +65,57 @@ def make_inputs(B, T, H, dqk, dv, seed, periodic=True):
     return q, k, v, do
 
 
+def config_inputs(idx):
+    """q, k, v, dO float32 arrays of configs[idx] (not rounded)."""
+    c = CONFIGS[idx]
+    B, T, H, D, DV = c["B"], c["T"], c["H"], c["dqk"], c["dv"]
+    seed = 20261201 + idx
+    if c["gen"] == "periodic":
+        return make_inputs(B, T, H, D, DV, seed)
+    if c["gen"] == "layer":  # the core's inputs inside the layer: bf16 projections of x
+        import torch
+        rnd = lambda a: torch.from_numpy(a).bfloat16().float().numpy()  # noqa: E731
+        x, wq, wk, wv, _, do, _ = layer_arrays()
+        xb = rnd(x)
+        proj = lambda w, d: (xb @ rnd(w)).reshape(B, T, H, d)  # noqa: E731
+        return proj(wq, D), proj(wk, D), proj(wv, DV), do
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, T, H, D), dtype=np.float32)
+    k = rng.standard_normal((B, T, H, D), dtype=np.float32)
+    if c["gen"] == "copied":
+        from tests._data import copied_spans
+        copied_spans(q, k)
+    v = rng.standard_normal((B, T, H, DV), dtype=np.float32)
+    do = rng.standard_normal((B, T, H, DV), dtype=np.float32)
+    return q, k, v, do
+
+
+def valid_pairs(iq, ik):
+    """Causal equal-label pairs (j <= i, iq[i] == ik[j]) per (b,h) row, int64 [B*H]."""
+    B, H, N = iq.shape
+    out = np.zeros(B * H, np.int64)
+    for r in range(B * H):
+        q, k = iq.reshape(-1, N)[r], ik.reshape(-1, N)[r]
+        # per label: for each query, #keys with the label at positions <= i
+        order = np.lexsort((np.r_[np.zeros(N, np.int8), np.ones(N, np.int8)],
+                            np.r_[np.arange(N), np.arange(N)], np.r_[k, q]))
+        lab = np.r_[k, q][order]
+        isq = np.r_[np.zeros(N, bool), np.ones(N, bool)][order]
+        starts = np.r_[True, lab[1:] != lab[:-1]]
+        keys_before = np.cumsum(~isq)
+        grp_base = np.maximum.accumulate(np.where(starts, np.arange(2 * N), 0))
+        base_keys = np.where(grp_base > 0, keys_before[grp_base - 1], 0)
+        out[r] = int((keys_before - base_keys)[isq].sum())
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--B", type=int, default=4)
-    ap.add_argument("--H", type=int, default=16)
-    ap.add_argument("--T", type=int, default=16384)
-    ap.add_argument("--dqk", type=int, default=8)
-    ap.add_argument("--dv", type=int, default=64)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS),
+                    help="BASELINE.json configs[K] (default 2, the headline metric)")
     ap.add_argument("--tau", type=float, default=0.5)
     ap.add_argument("--carry-strip", type=int, default=0,
                     help="composed carry boundary strip height (0 = off)")
@@ -84,50 +146,56 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": args.calibrate_copy}), flush=True)
         return
-    import dism_amd
-    from dism_amd import _lib
-    from dism_amd._checks import DTYPE_CODE
     if args.workload == "decode":
         return bench_decode(args)
     if args.workload == "vocab":
         return bench_vocab(args)
     if args.workload == "refshape":
         return bench_refshape(args)
+    return bench_train(args)
 
+
+def bench_train(args):
+    import torch
+    import dism_amd
+    from dism_amd import _lib
+    from dism_amd._checks import DTYPE_CODE
+    from dism_amd.hard_forward import row_modes
+    cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
-    B, T, H, D, DV = args.B, args.T, args.H, args.dqk, args.dv
-    q, k, v, do = make_inputs(B, T, H, D, DV, seed=20261203)
-    bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16).contiguous()  # noqa: E731
-    tq, tk, tv, tdo = bf(q), bf(k), bf(v), bf(do)
+    B, T, H, D, DV = cfg["B"], cfg["T"], cfg["H"], cfg["dqk"], cfg["dv"]
+    fwd_only = cfg["fwd_only"]
+    vdt = torch.float32 if cfg["dtype"] == "f32" else torch.bfloat16
+    q, k, v, do = config_inputs(args.config)
+    put = lambda a: torch.from_numpy(a).to(dev).to(vdt).contiguous()  # noqa: E731
+    tq, tk, tv, tdo = put(q), put(k), put(v), put(do)
     tau = torch.full((H,), args.tau, dtype=torch.float32, device=dev)
     hard = torch.ones((B, H), dtype=torch.bool, device=dev)
     stream = torch.cuda.current_stream(dev)
     S = stream.cuda_stream
     strip = args.carry_strip
     n = T
-    # persistent outputs / scratch (allocated once, outside the timed region)
     dsq = torch.empty((B, T, H, D), dtype=torch.float32, device=dev)
     dsk = torch.empty_like(dsq)
     dvv = torch.empty((B, T, H, DV), dtype=torch.float32, device=dev)
     rowtau = torch.empty((B, H, T), dtype=torch.float32, device=dev)
     dtau = torch.empty((H,), dtype=torch.float32, device=dev)
-    # with a side stream the forward is one call (dism_hard_forward: the bigram half of the
-    # prepare overlaps the length-1 label scan); else prepare and readout run as two stages
     fused = args.streams == 2
-    names = ["labels", "lut", "carry"] + (["forward"] if fused else ["prepare", "readout"]) + \
-        ["dlut", "row_pairs", "queries", "keys", "key_pairs", "tau_reduce"]
-    side = torch.cuda.Stream(device=dev) if args.streams == 2 else None
+    names = ["labels", "lut", "carry"] + (["forward"] if fused else ["prepare", "readout"])
+    if not fwd_only:
+        names += ["dlut", "row_pairs", "queries", "keys", "key_pairs", "tau_reduce"]
+    side = torch.cuda.Stream(device=dev) if fused and not fwd_only else None
     fork, join = torch.cuda.Event(), torch.cuda.Event()
-    out = torch.empty((B, T, H, DV), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((B, T, H, DV), dtype=vdt, device=dev)
     lse2 = torch.empty((B, H, T), dtype=torch.float32, device=dev)
-    code = DTYPE_CODE[torch.bfloat16]
+    code = DTYPE_CODE[vdt]
     nbytes = _lib.workspace_bytes(B, T, H, D, DV, code)
     ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
     W = ws.data_ptr()
     hp = hard.data_ptr()
 
     def step(events=None):
-        """One fwd+bwd pass.  events: {stage: (start, end)} recorded on the stage's stream."""
+        """One pass.  events: {stage: (start, end)} recorded on the stage's stream."""
         def mark(name, which, strm=None):
             if events is not None and name in events:
                 events[name][which].record(strm if strm is not None else stream)
@@ -158,6 +226,8 @@ def main():
             mark("readout", 0)
             _lib.call("dism_hard_readout", *rd)
             mark("readout", 1)
+        if fwd_only:
+            return out, iq, ik
         bw = (*vec, tdo.data_ptr(), code, qp, kp, hp, cp, strip, lut.data_ptr())
         if side is not None:
             fork.record(stream)  # the forward's outputs are ready
@@ -193,18 +263,29 @@ def main():
         if side is not None:
             join.record(side)
             stream.wait_event(join)
-        return out
+        return out, iq, ik
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _, iq_t, ik_t = step()
+    torch.cuda.synchronize()
+    modes = row_modes(ws, tq, tv).cpu().numpy()
+    dense_rows = int((modes == 1).sum())
+
     def stage_events(only=None):
         return {nm: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                 for nm in names if only is None or nm in only}
-
-    # timed region: events only around the two label scans (the roofline kernels)
-    live = [stage_events(("queries", "keys")) for _ in range(args.steps)]
+    # roofline candidates: the label scans of the backward (HBM), the dense-row kernels
+    # (fp32 VALU: forward, queries, keys) and, forward-only, the forward
+    if fwd_only:
+        cand = ("forward",) if fused else ("readout",)
+    elif dense_rows:
+        cand = ("forward", "queries", "keys")
+    else:
+        cand = ("queries", "keys")
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    live = [stage_events(cand) for _ in range(args.steps)]
     t0 = time.perf_counter()
     start.record(stream)
     for s in range(args.steps):
@@ -215,8 +296,7 @@ def main():
     gpu_ms = start.elapsed_time(end)
     ms_step = gpu_ms / args.steps
     live_ms = {nm: float(np.mean([live[s][nm][0].elapsed_time(live[s][nm][1])
-                                  for s in range(args.steps)])) for nm in ("queries", "keys")}
-    # per-stage times from a separate instrumented pass (events between every stage)
+                                  for s in range(args.steps)])) for nm in cand}
     per = [stage_events() for _ in range(args.steps)]
     for s in range(args.steps):
         step(per[s])
@@ -225,22 +305,42 @@ def main():
                                   for s in range(args.steps)])) for nm in names}
     units = B * H * T
     value = units / (ms_step / 1e3)
-
-    # Roofline of the dominant single-kernel stage.  Algorithmic bytes per (b,h,t) unit: the
-    # rows the kernel must read once and write once (bf16 vectors, fp32 outputs), plus the
-    # combined-order entry and label of the unit's key and query (4 x 4 B).
-    order = 16
-    per_unit = {
-        "queries": 2 * D * 2 + 2 * DV * 2 + 3 * 4 + 4 * D + 4 + order,     # sq,sk,v,dO,lse2,G,nb -> dsq,rowtau
-        "keys": 2 * D * 2 + 2 * DV * 2 + 4 + 4 * D + 4 * DV + order,       # sq,sk,v,dO,lse2 -> dsk,dv
-    }
-    dom = max(per_unit, key=lambda x: live_ms[x])
-    kernel_of = {"queries": "scan_rows_kernel", "keys": "scan_keys_kernel"}
-    alg_bytes = per_unit[dom] * units
-    achieved = alg_bytes / (live_ms[dom] / 1e3)
-    traffic = measured_traffic(kernel_of[dom])
+    esz = 4 if vdt == torch.float32 else 2
+    order = 16  # combined-order entry and label of the unit's key and query (4 x 4 B)
+    dom = max(cand, key=lambda x: live_ms[x])
+    if dense_rows and dom in ("forward", "queries", "keys"):
+        # fp32 FMAs of the direct definition per valid pair: forward s, acc (R + DV); query rows
+        # s, e, dq (2R + DV); keys s, e, dk, dv (2R + 2DV); over the dense rows' valid pairs
+        pairs = valid_pairs(iq_t.cpu().numpy(), ik_t.cpu().numpy())
+        vp = float(pairs[(modes.reshape(-1) == 1)].sum())
+        fma = {"forward": D + DV, "queries": 2 * D + DV, "keys": 2 * D + 2 * DV}[dom]
+        flops = 2.0 * fma * vp
+        kern = {"forward": "dense_forward_kernel", "queries": "dense_rows_kernel",
+                "keys": "dense_keys_kernel"}[dom]
+        achieved = flops / (live_ms[dom] / 1e3)
+        roof = {"kernel": kern, "bound": "valu", "achieved": achieved / 1e12,
+                "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s", "frac": achieved / FP32_PEAK,
+                "traffic": None, "alg_flops_per_launch": flops, "valid_pairs": vp,
+                "launch_ms": live_ms[dom]}
+    else:
+        # HBM bytes per B*H*T unit that the stage must read and write once
+        per_unit = {
+            "queries": 2 * D * esz + 2 * DV * esz + 3 * 4 + 4 * D + 4 + order,
+            "keys": 2 * D * esz + 2 * DV * esz + 4 + 4 * D + 4 * DV + order,
+            "forward": 2 * D * esz + DV * esz + DV * esz + 4 + order,
+            "readout": 2 * D * esz + DV * esz + DV * esz + 4 + order,
+        }
+        kernel_of = {"queries": "scan_rows_kernel", "keys": "scan_keys_kernel",
+                     "forward": "dism_hard_forward (all kernels)",
+                     "readout": "dism_hard_readout (all kernels)"}
+        alg_bytes = per_unit[dom] * units
+        achieved = alg_bytes / (live_ms[dom] / 1e3)
+        roof = {"kernel": kernel_of[dom], "bound": "hbm", "achieved": achieved / 1e9,
+                "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": achieved / HBM_PEAK,
+                "traffic": measured_traffic(kernel_of[dom]) if args.config == 2 else None,
+                "alg_bytes_per_unit": per_unit[dom], "launch_ms": live_ms[dom]}
     result = {
-        "metric": "DISM fwd+bwd tokens/sec (B*H*T/s) at T=16k, 1 GPU",
+        "metric": METRIC,
         "value": value,
         "unit": "B*H*T/s",
         "n_gpus": 1,
@@ -251,57 +351,103 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32 (int32 labels, bf16 vectors)",
-        "data": "synthetic (BASELINE configs[2] generator, seed 20261203)",
-        "config": {"workload": "BASELINE configs[2]: hard DISM fwd+bwd, periodic heads",
-                   "B": B, "H": H, "T": T, "d_qk": D, "d_v": DV, "tau": args.tau,
-                   "carry_strip": strip, "global_batch": B, "seq_len": T,
-                   "parallelism": "single-gpu"},
+        "dtype": f"fp32 (int32 labels, {cfg['dtype']} vectors)",
+        "data": f"synthetic (BASELINE configs[{args.config}] generator, seed "
+                f"{20261201 + args.config})",
+        "config": {"workload": cfg["workload"], "B": B, "H": H, "T": T, "d_qk": D, "d_v": DV,
+                   "tau": args.tau, "carry_strip": strip, "forward_only": fwd_only,
+                   "global_batch": B, "seq_len": T, "parallelism": "single-gpu"},
+        "row_modes": {str(m): int((modes == m).sum()) for m in (0, 1, 2)},
         "kernel_ms": kern_ms,
-        "roofline": {"kernel": kernel_of[dom], "bound": "hbm", "achieved": achieved / 1e9,
-                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": achieved / HBM_PEAK,
-                     "traffic": traffic, "alg_bytes_per_unit": per_unit[dom],
-                     "launch_ms": live_ms[dom]},
+        "roofline": roof,
     }
-    # BASELINE.json's metric is quoted as a fraction of the integer-VALU roofline of the
-    # pairwise match recurrence: 2 int32 ops (symbol compare, length update) per causal pair
-    # per pass, two passes (forward, and the backward's recompute), at MI355X's int32 VALU
-    # peak (256 CUs x 4 SIMD x 16 lanes x 2.4 GHz = 39.3 T ops/s).  This build does not run
-    # that recurrence (label scans + bigram corrections do O(N) work per row), so the figure
-    # is the step time that recurrence would need at peak over the measured step time.
+    # BASELINE.json quotes its metric as a fraction of the integer-VALU roofline of the
+    # pairwise match recurrence (2 int32 ops -- compare, length update -- per causal pair per
+    # pass, two passes), at 256 CUs x 4 SIMD x 16 lanes x 2.4 GHz = 39.3 T int32 ops/s.  For
+    # sparse rows this build does not run that recurrence (label scans + bigram corrections
+    # are O(N) per row), so this is the time that recurrence would need at peak over the
+    # measured step: an algorithmic speed-up figure, not a hardware efficiency.
     pairs = T * (T + 1) / 2
-    int_ops = 4 * pairs * B * H
+    int_ops = (2 if fwd_only else 4) * pairs * B * H
     int_peak = 256 * 4 * 16 * 2.4e9
-    result["int_valu_roofline"] = {"ops": int_ops, "peak_ops_per_s": int_peak,
-                                   "t_roof_ms": int_ops / int_peak * 1e3,
-                                   "frac": (int_ops / int_peak * 1e3) / ms_step,
-                                   "note": "pairwise recurrence work (2 int ops per causal "
-                                           "pair per pass, fwd+bwd) at the int32 VALU peak "
-                                           "over the measured step"}
-    valu = measured_valu(kernel_of[dom])
-    if valu is not None:  # the label scans are VALU-issue bound: the second ceiling
-        insts, peak = valu
-        rate = insts / (live_ms[dom] / 1e3)
-        result["valu"] = {"kernel": kernel_of[dom], "insts_per_launch": insts,
-                          "achieved": rate / 1e9, "peak": peak / 1e9,
-                          "unit": "G wave64-instr/s", "frac": rate / peak}
+    result["pairwise_equiv"] = {"ops": int_ops, "peak_ops_per_s": int_peak,
+                                "t_roof_ms": int_ops / int_peak * 1e3,
+                                "ratio": (int_ops / int_peak * 1e3) / ms_step,
+                                "note": "time of the pairwise int32 recurrence at the VALU "
+                                        "peak over the measured step (not a hardware "
+                                        "efficiency; see roofline)"}
+    if args.config == 2:
+        valu = measured_valu(roof["kernel"])
+        if valu is not None:  # the label scans are VALU-issue bound: the second ceiling
+            insts, peak = valu
+            rate = insts / (live_ms[dom] / 1e3)
+            result["valu"] = {"kernel": roof["kernel"], "insts_per_launch": insts,
+                              "achieved": rate / 1e9, "peak": peak / 1e9,
+                              "unit": "G wave64-instr/s", "frac": rate / peak}
+    if args.config == 4:
+        # the metric's step for configs[4] is the whole layer (projections, the core, the
+        # output projection, forward and backward); the core's own step stays beside it
+        layer_ms = layer_step_ms(args)
+        result["core_ms_per_step"] = ms_step
+        result["ms_per_step"] = layer_ms
+        result["value"] = units / (layer_ms / 1e3)
+        result["config"]["d_model"] = 1280
+        result["data"] += " (core inputs: the layer's bf16 projections)"
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(q, k, v, do, args)
+        result["cpu_baseline"] = cpu_baseline(q, k, v, do, cfg, args)
     print(json.dumps(result), flush=True)
 
 
-def _time(fn, steps, warmup):
+def layer_arrays():
+    """configs[4] generator (numpy, seed 20261205): x ~ N(0, 0.02) [B, T, 1280]; projections
+    wq, wk [1280, H*8], wv [1280, H*128] ~ N(0, 1/1280); the output projection wo [H*128, 1280]
+    ~ N(0, 1/(H*128)); the upstream gradient dy ~ N(0, 1) [B, T, 1280]."""
+    c = CONFIGS[4]
+    B, T, H, D, DV, DM = c["B"], c["T"], c["H"], c["dqk"], c["dv"], 1280
+    rng = np.random.default_rng(20261201 + 4)
+    x = rng.standard_normal((B, T, DM), dtype=np.float32) * 0.02
+    wq, wk = (rng.standard_normal((DM, H * D), dtype=np.float32) / np.sqrt(DM) for _ in range(2))
+    wv = rng.standard_normal((DM, H * DV), dtype=np.float32) / np.sqrt(DM)
+    do = rng.standard_normal((B, T, H, DV), dtype=np.float32)
+    wo = rng.standard_normal((H * DV, DM), dtype=np.float32) / np.sqrt(H * DV)
+    dy = rng.standard_normal((B, T, DM), dtype=np.float32)
+    return x, wq, wk, wv, wo, do, dy
+
+
+def layer_step_ms(args):
+    """configs[4] layer step on the GPU: bf16 projections q = x wq, k = x wk, v = x wv, the
+    hard core through autograd (labels by the sign binarizer of q and k, sq = q, sk = k), the
+    output projection, and the backward of all of it from dy (weights' and tau's gradients).
+    Returns the mean ms per step over args.steps steps after args.warmup."""
     import torch
-    for _ in range(warmup):
-        fn()
+    import dism_amd
+    c = CONFIGS[4]
+    B, T, H, D, DV = c["B"], c["T"], c["H"], c["dqk"], c["dv"]
+    dev = torch.device("cuda:0")
+    x, wq, wk, wv, wo, _, dy = layer_arrays()
+    put = lambda a: torch.from_numpy(a).to(dev, torch.bfloat16)  # noqa: E731
+    x, dy = put(x), put(dy)
+    ws = [put(w).requires_grad_() for w in (wq, wk, wv, wo)]
+    tau = torch.full((H,), args.tau, dtype=torch.float32, device=dev, requires_grad=True)
+    hard = torch.ones((B, H), dtype=torch.bool, device=dev)
+
+    def step():
+        q = (x @ ws[0]).view(B, T, H, D)
+        k = (x @ ws[1]).view(B, T, H, D)
+        v = (x @ ws[2]).view(B, T, H, DV)
+        iq, ik = dism_amd.sign_labels(q.detach()), dism_amd.sign_labels(k.detach())
+        o = dism_amd.dism_core_hard(q, k, v, iq, ik, hard, tau)
+        (o.reshape(B, T, H * DV) @ ws[3]).backward(dy)
+    for _ in range(args.warmup):
+        step()
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
-    for _ in range(steps):
-        fn()
+    for _ in range(args.steps):
+        step()
     e.record()
     torch.cuda.synchronize()
-    return s.elapsed_time(e) / steps
+    return s.elapsed_time(e) / args.steps
 
 
 def _median_ms(fn, calls=20, samples=7, warmup=10):
@@ -506,37 +652,88 @@ def measured_valu(kernel):
         return None
 
 
-def cpu_baseline(q, k, v, do, args):
-    """CPU model (oracle/dism_cpu_model.c, the decomposed fp32 sequence the GPU reproduces)
-    fwd+bwd on the whole workload, OpenMP over (b,h) rows, repeated until >= 10 s of wall
-    time; threads = the host cores available to this process (at most 16)."""
-    import oracle
-    oracle.build()
-    from oracle import bf16_round
-    sq, sk, vv, dd = bf16_round(q), bf16_round(k), bf16_round(v), bf16_round(do)
-    Bs, _, Hs, _ = sq.shape
-    iq, ik = oracle.sign_labels(sq), oracle.sign_labels(sk)
-    tau = np.full(Hs, args.tau, np.float32)
-    hard = np.ones((Bs, Hs), bool)
+def _cpu_info():
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     try:
         avail = len(os.sched_getaffinity(0))
     except AttributeError:
         avail = os.cpu_count() or 1
+    return model, os.cpu_count(), avail
+
+
+def cpu_baseline(q, k, v, do, cfg, args):
+    """The CPU model (oracle/dism_cpu_model.c, the fp32 sequence the GPU reproduces: each row
+    by the same classification) on the same workload, OpenMP over (b,h) rows.  Threads: the
+    host cores allotted to this process (at most 16, the GPU box's CPU share for one GPU);
+    also a 1-thread figure.  Method of the reference's measure
+    (dism_v3/tools/bench_training.py:39-61): 10 warmup runs, median of 7 timed runs -- on a
+    bounded sample of the rows (whole batch entries and heads, the same T), chosen from a
+    first timed run so that all the runs take about 10-20 s; the sample is stated."""
+    import oracle
+    oracle.build()
+    from oracle import bf16_round
+    f32 = cfg["dtype"] == "f32"
+    rnd = (lambda a: np.ascontiguousarray(a, np.float32)) if f32 else bf16_round
+    model, nproc, avail = _cpu_info()
     threads = max(1, min(16, avail))
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        lut = oracle.log_weights(tau, args.T)
-        dl = oracle.dlog_weights(tau, args.T)
-        _, l2, _, _ = oracle.forward(sq, sk, vv, iq, ik, hard, lut, threads=threads)
-        oracle.backward(sq, sk, vv, dd, iq, ik, hard, lut, dl, l2, threads=threads)
-        reps += 1
-        dt = time.perf_counter() - t0
-        if dt >= 10.0:
-            break
-    units = reps * Bs * Hs * args.T
-    return {"value": units / dt, "unit": "B*H*T/s", "cores": threads, "kind": "port",
-            "sample": f"full workload B={Bs} H={Hs} T={args.T} fwd+bwd x{reps} "
-                      f"({dt:.1f} s wall, {threads} threads)"}
+    T = cfg["T"]
+
+    def sample(bs, hs):
+        sq, sk, vv, dd = (rnd(a[:bs, :, :hs]) for a in (q, k, v, do))
+        iq, ik = oracle.sign_labels(sq), oracle.sign_labels(sk)
+        tau = np.full(hs, args.tau, np.float32)
+        hard = np.ones((bs, hs), bool)
+        lut = oracle.log_weights(tau, T)
+        dl = None if cfg["fwd_only"] else oracle.dlog_weights(tau, T)
+        return sq, sk, vv, dd, iq, ik, hard, lut, dl
+
+    def run(x, th):
+        sq, sk, vv, dd, iq, ik, hard, lut, dl = x
+        _, l2, _, _ = oracle.forward(sq, sk, vv, iq, ik, hard, lut, threads=th)
+        if dl is not None:
+            oracle.backward(sq, sk, vv, dd, iq, ik, hard, lut, dl, l2, threads=th)
+
+    def measure(bs, hs, th, warm, reps):
+        x = sample(bs, hs)
+        for _ in range(warm):
+            run(x, th)
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            run(x, th)
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    B, H = cfg["B"], cfg["H"]
+    # the sample: whole rows, shrunk until one multi-thread run takes at most ~0.6 s
+    bs, hs = B, H
+    t1 = measure(bs, hs, threads, 0, 1)
+    while t1 > 0.6 and bs * hs > threads:
+        if bs > 1:
+            bs = (bs + 1) // 2
+        else:
+            hs = max(1, hs // 2)
+        t1 = measure(bs, hs, threads, 0, 1)
+    tm = measure(bs, hs, threads, 10, 7)
+    # one thread: a single row (or the whole workload if it is one row)
+    b1 = 1
+    t_one = measure(b1, 1, 1, 3, 3)
+    units = bs * hs * T
+    return {"value": units / tm, "unit": "B*H*T/s", "cores": threads, "kind": "port",
+            "one_thread_value": T / t_one, "nproc": nproc, "cores_allotted": avail,
+            "cpu_model": model,
+            "sample": f"B={bs} H={hs} of B={B} H={H}, T={T}, "
+                      f"{'forward' if cfg['fwd_only'] else 'fwd+bwd'}; median of 7 runs after "
+                      f"10 warmups ({tm * 1e3:.1f} ms/run, {threads} threads); one thread: "
+                      f"one row, median of 3 ({t_one * 1e3:.1f} ms)"}
 
 
 if __name__ == "__main__":

@@ -434,9 +434,12 @@ int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t
     // the scan takes the rows prepared in LDS, counting their bigram partners itself (phase
     // 1); after the join the scan takes the remaining rows from the plan's counts (phase 2),
     // then the pair kernels run.  Without a side stream the same launches run in order.
+    const hipStream_t s = S(stream);
+    // the row flags first, on the caller's stream: both halves read them
+    const hipError_t ce = dism::launch_classify(sa, s);
+    if (ce != hipSuccess) return hip_status(ce, "hard forward");
     SideLease lease;
     SideStream* side = lease.get();
-    const hipStream_t s = S(stream);
     hipStream_t ps = s;
     if (side) {
         if (hipEventRecord(side->fork, s) != hipSuccess ||

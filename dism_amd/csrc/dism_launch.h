@@ -217,8 +217,12 @@ hipError_t launch_packed_soft_zero(const PackedZero& z, hipStream_t s);
 // Position orders and bigram-pair plans of a prepare call: the LDS-resident kernel for the
 // rows it can take, the global-memory sort and plan for the others, then the owner lists.
 hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s);
-// the two independent halves of launch_prepare: the combined label order (what the label
-// scans need) and the bigram orders, pair plans and owner lists (what the pair kernels need)
+// the row modes' first step, the dense-row flags (dflag, and dcost cleared): both halves below
+// read them, so it runs before either is launched
+hipError_t launch_classify(const SortArgs& sa, hipStream_t s);
+// the two independent halves of launch_prepare (after launch_classify): the combined label
+// order (what the label scans need) and the bigram orders, pair plans and owner lists (what
+// the pair kernels need)
 hipError_t launch_prepare_labels(const SortArgs& sa, const PathArgs& pa, hipStream_t s);
 hipError_t launch_prepare_pairs(const SortArgs& sa, const PathArgs& pa, hipStream_t s);
 hipError_t launch_sort(const SortArgs& a, int role0, int roles, hipStream_t s);
@@ -245,7 +249,7 @@ hipError_t launch_pairs_keys(const PathArgs& a, int R, int DV, int dtype, hipStr
 // boundary rows (before the dense kernels), then the tile kernels for the flagged hard rows
 hipError_t launch_dense_classify(const int32_t* iq, const int32_t* ik, long BH, int n,
                                  int cls_n, int32_t* dflag, unsigned long long* dcost,
-                                 hipStream_t s);
+                                 uint16_t* dbound, hipStream_t s);
 hipError_t launch_walk_probe(const PathArgs& a, hipStream_t s);
 hipError_t launch_dense_prepare(const PathArgs& a, hipStream_t s);
 hipError_t launch_dense_forward(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);

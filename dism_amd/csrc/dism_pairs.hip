@@ -97,6 +97,26 @@ __device__ __forceinline__ void partner_range(const PathArgs& a, int bh, long so
     cnt_out = hi - lo;
 }
 
+// one step of a suffix walk at offset c: compares the PF label pairs (i - c - u, j - c - u),
+// advances c over the matching ones; true when all PF matched (the walk goes on)
+template <int PF>
+__device__ __forceinline__ bool walk_step(const int32_t* __restrict__ q,
+                                          const int32_t* __restrict__ k, int i, int j, int lo,
+                                          int& c) {
+    int qv[PF], kv[PF];
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+        const int iq = i - c - u, jk = j - c - u;
+        qv[u] = q[iq > 0 ? iq : 0];
+        kv[u] = k[jk > 0 ? jk : 0];
+    }
+    int run = 0;
+#pragma unroll
+    for (int u = 0; u < PF; ++u)
+        if (run == u && i - c - u >= lo && j - c - u >= 0 && qv[u] == kv[u]) ++run;
+    c += run;
+    return run == PF;
+}
 
 // Match length of a bigram pair (i, j >= 1, q[i-1] == k[j-1] known): match_length's suffix
 // walk without its first comparison.
@@ -112,25 +132,11 @@ __device__ __forceinline__ int pair_length(const int32_t* __restrict__ q,
     const int s0 = wb ? (i & ~63) : 0;
     const int lo = bound ? (i / strip) * strip : (s0 > dlo ? s0 : dlo);
     int c = i - 1 >= lo ? 2 : 1;
-    if (c == 2) {
-        // the walk compares WALK_PF label pairs per step, all loads in flight together
-        // (clamped indices; a comparison counts only while both positions are in range), so
-        // the usual short match costs one round trip instead of one per label
-        constexpr int WALK_PF = 4;
-        for (;;) {
-            int qv[WALK_PF], kv[WALK_PF];
-#pragma unroll
-            for (int u = 0; u < WALK_PF; ++u) {
-                const int iq = i - c - u, jk = j - c - u;
-                qv[u] = q[iq > 0 ? iq : 0];
-                kv[u] = k[jk > 0 ? jk : 0];
-            }
-            int run = 0;
-#pragma unroll
-            for (int u = 0; u < WALK_PF; ++u)
-                if (run == u && i - c - u >= lo && j - c - u >= 0 && qv[u] == kv[u]) ++run;
-            c += run;
-            if (run < WALK_PF) break;
+    // the walk compares a batch of label pairs per step, all loads in flight together
+    // (clamped indices; a comparison counts only while both positions are in range): 4 at
+    // first, so the usual short match costs one round trip, then 16 per step for long runs
+    if (c == 2 && walk_step<4>(q, k, i, j, lo, c)) {
+        while (walk_step<16>(q, k, i, j, lo, c)) {
         }
     }
     if (bound && lo > 0 && i - c < lo && j - c >= 0) {
@@ -281,14 +287,16 @@ static SortArgs sort_args(const SortArgs& sa, const PathArgs& pa) {
     return b;
 }
 
+hipError_t launch_classify(const SortArgs& sa, hipStream_t s) {
+    return launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n, sa.o.dflag,
+                                 sa.o.dcost, sa.o.dbound, s);
+}
+
 hipError_t launch_prepare_labels(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
     const SortArgs b = sort_args(sa, pa);
-    // the dense-row flags first: the label scans skip dense rows, the owner lists drop them
-    hipError_t e = launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n, sa.o.dflag, sa.o.dcost, s);
-    if (e != hipSuccess) return e;
     // prepare_lds_kernel role 0 orders every row: in LDS, or in global memory for rows whose
     // labels differ in more than one byte
-    e = b.lds_rows ? launch_prepare_lds(b, 0, 1, s) : launch_msort_labels(b, s);
+    hipError_t e = b.lds_rows ? launch_prepare_lds(b, 0, 1, s) : launch_msort_labels(b, s);
     return e != hipSuccess ? e : launch_ctab_balance(b, s);
 }
 
@@ -311,13 +319,14 @@ hipError_t launch_prepare_pairs(const SortArgs& sa, const PathArgs& pa, hipStrea
 hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
     const SortArgs b = sort_args(sa, pa);
     if (!b.lds_rows) {
-        const hipError_t e = launch_prepare_labels(sa, pa, s);
+        hipError_t e = launch_classify(sa, s);
+        if (e == hipSuccess) e = launch_prepare_labels(sa, pa, s);
         return e != hipSuccess ? e : launch_prepare_pairs(sa, pa, s);
     }
     // one stream: the dense-row flags, both LDS roles in one grid (64-block roles side by
     // side), then the bigram sorts of the other rows, the plan, the owner lists and the dense
     // rows' list and boundaries
-    hipError_t e = launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n, sa.o.dflag, sa.o.dcost, s);
+    hipError_t e = launch_classify(sa, s);
     if (e == hipSuccess) e = launch_prepare_lds(b, 0, 2, s);
     if (e == hipSuccess) e = launch_ctab_balance(b, s);
     if (e == hipSuccess) e = launch_sort(b, 1, 2, s);
@@ -456,27 +465,18 @@ __device__ __forceinline__ unsigned long long shfl_xor64(unsigned long long x, i
 // run's pairs' walks would cost.  Rows with S > N^2 get strip boundaries (mode 2,
 // dense_mode_kernel): their walks then stop within 64 rows (pair_length), so no row's walks
 // cost more than O(N^2) in all.  The estimate only picks the method; lengths stay exact.
+// Runs shorter than WALK_COUNTED are not counted: their pairs' walks take fewer than 16
+// comparisons each, and a row that is not dense has at most about N^2/64 label-equal pairs,
+// so together they cost under N^2/4; leaving them out keeps the per-row sum's atomics (one
+// cache line for all rows) to the rare long runs.
 constexpr int WALK_EXACT = 64;
+constexpr int WALK_COUNTED = 16;
 
 __device__ __forceinline__ int probe_run(const int32_t* __restrict__ q,
                                          const int32_t* __restrict__ k, int i, int j, int dlo) {
     int c = i - 1 >= dlo ? 2 : 1;
-    if (c == 2) {
-        constexpr int PF = 4;
-        while (c < WALK_EXACT) {
-            int qv[PF], kv[PF];
-#pragma unroll
-            for (int u = 0; u < PF; ++u) {
-                const int iq = i - c - u, jk = j - c - u;
-                qv[u] = q[iq > 0 ? iq : 0];
-                kv[u] = k[jk > 0 ? jk : 0];
-            }
-            int run = 0;
-#pragma unroll
-            for (int u = 0; u < PF; ++u)
-                if (run == u && i - c - u >= dlo && j - c - u >= 0 && qv[u] == kv[u]) ++run;
-            c += run;
-            if (run < PF) return c;
+    if (c == 2 && walk_step<4>(q, k, i, j, dlo, c)) {
+        while (c < WALK_EXACT && walk_step<16>(q, k, i, j, dlo, c)) {
         }
     }
     if (c < WALK_EXACT) return c;
@@ -508,7 +508,7 @@ __device__ __forceinline__ void probe_item(const PathArgs& a, int base, int k0, 
             const bool ends = i + 1 >= n || j + 1 >= n || next_reset || q[i + 1] != k[j + 1];
             if (ends) {
                 const unsigned long long l = (unsigned long long)probe_run(q, k, i, j, dlo);
-                cost += l * l / 2;
+                if (l >= WALK_COUNTED) cost += l * l / 2;
             }
         }
     }
