@@ -54,7 +54,9 @@ hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 struct Layout {
     int64_t corder, clab, ctab, bpos[2], blab[2], bplab[2], btab[2], shift, tmp[3];
     int64_t stage[2][2], bhcount[2], own[2], ocount, mode, onebyte;
-    int64_t pnb, prow, mcount, mdig, dflag, dlist, dcount, dbound, dcost, total;
+    int64_t pnb, prow, mcount, mdig, dflag, dlist, dcount, dbound, dcost;
+    int64_t lvent, lvmeta, lvqidx, lvkidx, lvcnt, lvq, lvT, lvP, lvU, lvQ, lvc;  // -1: none
+    int64_t total;
     int prow_stride;
 };
 
@@ -151,10 +153,25 @@ Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     L.pnb = take(BH * N * 4);
     L.prow = take(BH * N * L.prow_stride * 4);
     L.dflag = take(BH * 4);
-    L.dlist = take(2 * BH * 4);
+    L.dlist = take(3 * BH * 4);
     L.dcount = take(4 * 4);
     L.dbound = take(N <= dism::DENSE_MAX_N ? BH * dism::dense_row_entries((int)N) * 2 : 0);
     L.dcost = take(BH * 8);
+    // level rows (dism_levels.hip) only where they can occur
+    const bool lv = N <= dism::LEVEL_MAX_N && (int64_t)R * DV <= dism::LEVEL_RDV;
+    const int64_t lent = (int64_t)dism::LEVEL_BUDGET * N, lmat = dism::LEVEL_MAX * N;
+    const int64_t lseg = dism::level_segs(N) * R * DV * 4;
+    L.lvent = lv ? take(BH * lent * 4) : -1;
+    L.lvmeta = lv ? take(BH * dism::LEVEL_META * 4) : -1;
+    L.lvqidx = lv ? take(BH * lmat * 2) : -1;
+    L.lvkidx = lv ? take(BH * lmat * 2) : -1;
+    L.lvcnt = lv ? take(BH * lmat * 2) : -1;
+    L.lvq = lv ? take(BH * N * 16) : -1;
+    L.lvT = lv ? take(BH * lseg) : -1;
+    L.lvP = lv ? take(BH * lseg) : -1;
+    L.lvU = lv ? take(BH * lseg) : -1;
+    L.lvQ = lv ? take(BH * lseg) : -1;
+    L.lvc = lv ? take(BH * lent * 4) : -1;
     L.total = o;
     return L;
 }
@@ -192,6 +209,18 @@ dism::Orders orders(const Layout& L, void* ws) {
     o.dcount = at<int32_t>(ws, L.dcount);
     o.dbound = at<uint16_t>(ws, L.dbound);
     o.dcost = at<unsigned long long>(ws, L.dcost);
+    auto opt = [&](int64_t off) { return off < 0 ? nullptr : at<char>(ws, off); };
+    o.lvent = reinterpret_cast<int32_t*>(opt(L.lvent));
+    o.lvmeta = reinterpret_cast<int32_t*>(opt(L.lvmeta));
+    o.lvqidx = reinterpret_cast<uint16_t*>(opt(L.lvqidx));
+    o.lvkidx = reinterpret_cast<uint16_t*>(opt(L.lvkidx));
+    o.lvcnt = reinterpret_cast<uint16_t*>(opt(L.lvcnt));
+    o.lvq = reinterpret_cast<int4*>(opt(L.lvq));
+    o.lvT = reinterpret_cast<float*>(opt(L.lvT));
+    o.lvP = reinterpret_cast<float*>(opt(L.lvP));
+    o.lvU = reinterpret_cast<float*>(opt(L.lvU));
+    o.lvQ = reinterpret_cast<float*>(opt(L.lvQ));
+    o.lvc = reinterpret_cast<float*>(opt(L.lvc));
     return o;
 }
 
@@ -258,6 +287,7 @@ int32_t prepare_impl(const void* sq, const void* sk, const void* v, int32_t dtyp
     sa.pnb = at<int32_t>(workspace, L.pnb);
     dism::PathArgs pa = path(L, workspace, B, N, H, iq, ik, nullptr, nullptr, 0, nullptr, 0);
     pa.wlo = wlo;
+    pa.cls_n = (int)cls_n;
     return hip_status(dism::launch_prepare(sa, pa, S(stream)), "hard prepare");
 }
 
@@ -391,8 +421,11 @@ int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t
     if ((st2 = hip_status(dism::launch_pairs_finish(a, R, DV, dtype, S(stream)),
                           "hard readout pairs")))
         return st2;
-    return hip_status(dism::launch_dense_forward(a, R, DV, dtype, S(stream)),
-                      "hard readout dense rows");
+    if ((st2 = hip_status(dism::launch_dense_forward(a, R, DV, dtype, S(stream)),
+                          "hard readout dense rows")))
+        return st2;
+    return hip_status(dism::launch_level_forward(a, R, DV, dtype, S(stream)),
+                      "hard readout level rows");
 }
 
 int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t dtype,
@@ -465,7 +498,9 @@ int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t
         return st;
     if ((st = hip_status(dism::launch_pairs_finish(a, R, DV, dtype, s), "hard forward pairs")))
         return st;
-    return hip_status(dism::launch_dense_forward(a, R, DV, dtype, s), "hard forward dense rows");
+    if ((st = hip_status(dism::launch_dense_forward(a, R, DV, dtype, s), "hard forward dense rows")))
+        return st;
+    return hip_status(dism::launch_level_forward(a, R, DV, dtype, s), "hard forward level rows");
 }
 
 }  // extern "C"
@@ -600,8 +635,11 @@ int32_t dism_hard_backward_queries(const void* sq, const void* sk, const void* v
     if ((st = hip_status(dism::launch_scan_rows(a, R, DV, dtype, S(stream)),
                          "hard backward rows")))
         return st;
-    return hip_status(dism::launch_dense_rows(a, R, DV, dtype, S(stream)),
-                      "hard backward dense rows");
+    if ((st = hip_status(dism::launch_dense_rows(a, R, DV, dtype, S(stream)),
+                         "hard backward dense rows")))
+        return st;
+    return hip_status(dism::launch_level_rows(a, R, DV, dtype, S(stream)),
+                      "hard backward level rows");
 }
 
 int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, const void* dout,
@@ -622,8 +660,11 @@ int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, c
     if ((st = hip_status(dism::launch_scan_keys(a, R, DV, dtype, S(stream)),
                          "hard backward keys")))
         return st;
-    return hip_status(dism::launch_dense_keys(a, R, DV, dtype, S(stream)),
-                      "hard backward dense keys");
+    if ((st = hip_status(dism::launch_dense_keys(a, R, DV, dtype, S(stream)),
+                         "hard backward dense keys")))
+        return st;
+    return hip_status(dism::launch_level_keys(a, R, DV, dtype, S(stream)),
+                      "hard backward level keys");
 }
 
 int32_t dism_hard_backward_key_pairs(const void* sq, const void* sk, const void* v,
@@ -1042,7 +1083,8 @@ int32_t dism_hard_prefill(const void* sq, const void* sk, const void* v, int32_t
     a.lse2 = lse2;
     if ((st = hip_status(dism::launch_scan_forward(a, R, DV, dtype, s), what))) return st;
     if ((st = hip_status(dism::launch_pairs_finish(a, R, DV, dtype, s), what))) return st;
-    return hip_status(dism::launch_dense_forward(a, R, DV, dtype, s), what);
+    if ((st = hip_status(dism::launch_dense_forward(a, R, DV, dtype, s), what))) return st;
+    return hip_status(dism::launch_level_forward(a, R, DV, dtype, s), what);
 }
 
 int64_t dism_decoder_state_bytes(int64_t rows, int32_t R, int32_t DV, int64_t capacity,

@@ -149,19 +149,20 @@ __global__ __launch_bounds__(256) void dense_collide_kernel(const uint32_t* __re
     classify_finish(m, n, cn, bh, dflag, dcost);
 }
 
-// Row modes and lists (one workgroup, after the walk probe): mode 2 for the sparse rows
-// whose walk-cost estimate exceeds N^2; the mode-1 rows ascending in dlist[0..), the rows of
-// modes 1 and 2 ascending in dlist[BH..), their counts in dcount[0], dcount[1].
+// Row modes and lists (one workgroup, after the walk probe and the level lists): mode 2 for
+// the sparse rows whose walk-cost estimate exceeds N^2; the mode-1 rows ascending in
+// dlist[0..), the rows of modes 1 and 2 in dlist[BH..), the mode-3 rows in dlist[2 BH..),
+// their counts in dcount[0..2].
 __global__ __launch_bounds__(1024) void dense_mode_kernel(int32_t* __restrict__ dflag,
                                                           const unsigned long long* __restrict__ dcost,
                                                           int BH, int n,
                                                           int32_t* __restrict__ dlist,
                                                           int32_t* __restrict__ dcount) {
-    __shared__ int s_w[2][16];
-    __shared__ int s_base[2];
+    __shared__ int s_w[3][16];
+    __shared__ int s_base[3];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const unsigned long long nn = (unsigned long long)n * (unsigned long long)n;
-    if (tid < 2) s_base[tid] = 0;
+    if (tid < 3) s_base[tid] = 0;
     __syncthreads();
     for (int c0 = 0; c0 < BH; c0 += 1024) {
         const int x = c0 + tid;
@@ -170,29 +171,26 @@ __global__ __launch_bounds__(1024) void dense_mode_kernel(int32_t* __restrict__ 
             mode = 2;
             dflag[x] = 2;
         }
-        const unsigned long long m1 = __ballot(mode == 1), m2 = __ballot(mode != 0);
-        if (lane == 0) {
-            s_w[0][w] = __popcll(m1);
-            s_w[1][w] = __popcll(m2);
-        }
+        const unsigned long long ms[3] = {__ballot(mode == 1), __ballot(mode == 1 || mode == 2),
+                                          __ballot(mode == 3)};
+        if (lane < 3) s_w[lane][w] = __popcll(ms[lane]);
         __syncthreads();
-        int b1 = s_base[0], b2 = s_base[1];
-        for (int v = 0; v < w; ++v) {
-            b1 += s_w[0][v];
-            b2 += s_w[1][v];
-        }
+        int base[3] = {s_base[0], s_base[1], s_base[2]};
+        for (int v = 0; v < w; ++v)
+            for (int c = 0; c < 3; ++c) base[c] += s_w[c][v];
         const unsigned long long below = (1ull << lane) - 1ull;
-        if (mode == 1) dlist[b1 + __popcll(m1 & below)] = x;
-        if (mode != 0) dlist[BH + b2 + __popcll(m2 & below)] = x;
+        if (mode == 1) dlist[base[0] + __popcll(ms[0] & below)] = x;
+        if (mode == 1 || mode == 2) dlist[BH + base[1] + __popcll(ms[1] & below)] = x;
+        if (mode == 3) dlist[2 * BH + base[2] + __popcll(ms[2] & below)] = x;
         __syncthreads();
-        if (tid < 2) {
+        if (tid < 3) {
             int t = 0;
             for (int v = 0; v < 16; ++v) t += s_w[tid][v];
             s_base[tid] += t;
         }
         __syncthreads();
     }
-    if (tid < 2) dcount[tid] = s_base[tid];
+    if (tid < 3) dcount[tid] = s_base[tid];
 }
 
 // query i starts its match afresh (query reset or document start)
@@ -736,6 +734,8 @@ hipError_t launch_dense_classify(const int32_t* iq, const int32_t* ik, long BH, 
 }
 
 hipError_t launch_dense_prepare(const PathArgs& a, hipStream_t s) {
+    const hipError_t le = launch_level_prep(a, s);
+    if (le != hipSuccess) return le;
     hipLaunchKernelGGL(dense_mode_kernel, dim3(1), dim3(1024), 0, s, a.o.dflag, a.o.dcost,
                        a.B * a.H, a.n, a.o.dlist, a.o.dcount);
     hipError_t e = hipGetLastError();

@@ -54,12 +54,50 @@ struct Orders {
     // of each kind ascending and their counts, and the 16-bit boundary rows L[64s - 1, j],
     // j < 64s, of every 64-row query strip s >= 1 of the rows of modes 1 and 2
     // ([B*H][dense_row_entries(N)], only when N <= DENSE_MAX_N)
-    int32_t* dflag;       // row mode: 0 sparse, 1 dense, 2 sparse with strip-bounded walks
-    int32_t* dlist;       // mode-1 rows, then (at dlist + B*H) the rows of modes 1 and 2
-    int32_t* dcount;      // [0]: mode-1 rows, [1]: rows of modes 1 and 2
+    int32_t* dflag;       // row mode: 0 sparse, 1 dense, 2 sparse with strip-bounded walks,
+                          // 3 dense level row (dism_levels.hip)
+    int32_t* dlist;       // mode-1 rows, then (at dlist + B*H) the rows of modes 1 and 2, then
+                          // (at dlist + 2*B*H) the mode-3 rows
+    int32_t* dcount;      // [0]: mode-1 rows, [1]: rows of modes 1 and 2, [2]: mode-3 rows
     uint16_t* dbound;
     unsigned long long* dcost;  // [B*H] walk-cost estimate of the probe (dism_pairs.hip)
+    // level rows (mode 3, dism_levels.hip): dense rows whose sums are taken per match length.
+    // Null unless N <= LEVEL_MAX_N and R * DV <= LEVEL_RDV.  Per (b,h) row:
+    //   lvent  [LEVEL_BUDGET * N]  the kept entries e = 2p + s of levels 1, 2, ... in list
+    //                              order, LEVEL_START on a group's first entry
+    //   lvmeta [LEVEL_META]        level count, then off[0..LEVEL_MAX] (level l at
+    //                              [off[l-1], off[l])), then segbase[0..LEVEL_MAX] (level l's
+    //                              first segment of LEVEL_SEG entries)
+    //   lvqidx / lvkidx [LEVEL_MAX][N]  index of query / key position p in level l's list
+    //                              (valid for l up to its kept level count)
+    //   lvcnt  [LEVEL_MAX][N]      keys before query p in its level-l group
+    //   lvq    [N]                 per position {longest match Lq, its last key, kept levels
+    //                              of the query, kept levels of the key}
+    //   lvT, lvP [LEVEL_SEGS(N)][R*DV]  forward segment totals and prefixes ([r][d])
+    //   lvU, lvQ [LEVEL_SEGS(N)][R*DV]  key-side totals and suffixes ([d][r])
+    //   lvc    [LEVEL_BUDGET * N]  c_l of every query entry (backward)
+    int32_t* lvent;
+    int32_t* lvmeta;
+    uint16_t* lvqidx;
+    uint16_t* lvkidx;
+    uint16_t* lvcnt;
+    int4* lvq;
+    float* lvT;
+    float* lvP;
+    float* lvU;
+    float* lvQ;
+    float* lvc;
 };
+constexpr int LEVEL_MAX_N = 4096;   // longest level row (16-bit list indices and counts)
+constexpr int LEVEL_MAX = 32;       // most levels (longest match) of a level row
+constexpr int LEVEL_BUDGET = 16;    // kept entries per position over all levels
+constexpr int LEVEL_SEG = 32;       // list entries per segment
+constexpr int LEVEL_RDV = 512;      // largest R * DV of a level row
+constexpr int LEVEL_START = 0x40000000;
+constexpr int LEVEL_META = 2 * LEVEL_MAX + 4;
+__host__ __device__ inline long level_segs(long n) {
+    return (long)LEVEL_BUDGET * n / LEVEL_SEG + LEVEL_MAX;
+}
 
 constexpr int DENSE_MAX_N = 65536;   // longest row of the dense path (16-bit lengths)
 constexpr int DENSE_BUCKETS = 4096;  // label buckets of the classification
@@ -126,6 +164,9 @@ struct PathArgs {
     // query resets (inference prefill): per query the last reset position at or before it;
     // walks from that query stop there.  [B*H*N] or null.
     const int32_t* wlo;
+    // positions of each row the prepare's dense-row classification and level lists take (a
+    // prefill's rows are padded after the real tokens); 0: all n
+    int cls_n;
     // forward label scan: 0 = every row, pair counts from pnb; 1 = rows whose labels differ
     // in one byte (onebyte), with the pair counts computed in the scan (the plan may still be
     // running on another stream); 2 = the remaining rows, from pnb.  Phases 1/2 only for
@@ -251,6 +292,14 @@ hipError_t launch_dense_classify(const int32_t* iq, const int32_t* ik, long BH, 
                                  int cls_n, int32_t* dflag, unsigned long long* dcost,
                                  uint16_t* dbound, hipStream_t s);
 hipError_t launch_walk_probe(const PathArgs& a, hipStream_t s);
+// level lists of the dense rows that qualify (mode 1 -> 3; dism_sort.hip), before the row
+// lists of launch_dense_prepare
+hipError_t launch_level_prep(const PathArgs& a, hipStream_t s);
+// level rows: forward (segment prefixes, then the readout), backward query rows, backward
+// keys (dism_levels.hip); no-ops without level rows
+hipError_t launch_level_forward(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
+hipError_t launch_level_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
+hipError_t launch_level_keys(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_dense_prepare(const PathArgs& a, hipStream_t s);
 hipError_t launch_dense_forward(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_dense_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);

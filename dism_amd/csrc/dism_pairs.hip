@@ -218,7 +218,7 @@ __global__ __launch_bounds__(LIST_THREADS) void owner_lists_kernel(PathArgs a) {
     const int32_t* dense = a.o.dflag;  // dense rows' pairs belong to dism_dense.hip
     int before[3] = {0, 0, 0}, total[3] = {0, 0, 0};
     for (int r = tid; r < BH; r += LIST_THREADS) {
-        const bool drop = dense[r] == 1;
+        const bool drop = dense[r] == 1 || dense[r] == 3;
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             const int v = drop ? 0 : cnt[(long)r * 4 + c];

@@ -763,4 +763,210 @@ hipError_t launch_ctab_balance(const SortArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------------
+// Level lists (one 1024-thread workgroup per dense row, after the classification; rows of
+// N <= LEVEL_MAX_N whose labels are all below 256, fixed-length calls without resets).
+// Level l's list is the previous level's kept list without its entries at p = l - 2, stably
+// sorted by label[p - l + 1] (an lds_pass over the entries' labels, staged in LDS as bytes:
+// entry e's digit at level l is s_lab[e - 2(l - 1)]).  A group (equal digit and equal
+// previous group) is kept when one of its queries has a key before it.  Per level a block
+// scan gives every entry its group start, the keys before it in the group and the last of
+// them; kept groups are compacted (block scan) into the next level's input and written out
+// with the per-position indices and counts.  The row becomes mode 3 when a level keeps
+// nothing within LEVEL_MAX levels and LEVEL_BUDGET * N kept entries; otherwise it stays a
+// mode-1 (tile) row.  The oracle's levels_build computes the same lists.
+namespace {
+struct LvAgg {  // segmented aggregate of a run of list entries
+    int f, cnt, lk, gs;  // a group start inside; keys / last key position after the last
+                         // start; index of the last start (-1: none)
+};
+__device__ __forceinline__ LvAgg lv_op(LvAgg a, LvAgg b) {
+    return LvAgg{a.f | b.f, b.f ? b.cnt : a.cnt + b.cnt, b.f || b.lk >= 0 ? b.lk : a.lk,
+                 b.gs >= 0 ? b.gs : a.gs};
+}
+}  // namespace
+
+__global__ __launch_bounds__(SORT_THREADS) void level_prep_kernel(PathArgs a) {
+    constexpr int M2 = 2 * LEVEL_MAX_N;
+    __shared__ uint16_t s_e[2][M2];
+    __shared__ uint16_t s_g[2][M2];
+    __shared__ uint8_t s_lab[M2];
+    __shared__ uint8_t s_keep[M2];
+    __shared__ int wcnt[SORT_WAVES][RADIX];
+    __shared__ int scan[RADIX];
+    __shared__ unsigned long long lmask[SORT_WAVES][RADIX];
+    __shared__ LvAgg s_agg[SORT_WAVES];
+    __shared__ int s_cnt[SORT_WAVES];
+    __shared__ int s_bad;
+    // nv: the positions the lists take (a prefill's padding after them never pairs with
+    // them: its keys come after every real query)
+    const int bh = blockIdx.x, tid = threadIdx.x, n = a.n;
+    const int nv = a.cls_n > 0 && a.cls_n < n ? a.cls_n : n, n2 = 2 * nv;
+    if (a.o.dflag[bh] != 1) return;
+    const long so = (long)bh * n;
+    const int32_t* q = a.iq + so;
+    const int32_t* k = a.ik + so;
+    if (tid == 0) s_bad = 0;
+    __syncthreads();
+    int bad = 0;
+    for (int p = tid; p < nv; p += SORT_THREADS) {
+        const uint32_t lq = (uint32_t)q[p], lk = (uint32_t)k[p];
+        bad |= (lq >= 256u) | (lk >= 256u);
+        s_lab[2 * p] = (uint8_t)lk;
+        s_lab[2 * p + 1] = (uint8_t)lq;
+        s_e[0][2 * p] = (uint16_t)(2 * p);
+        s_e[0][2 * p + 1] = (uint16_t)(2 * p + 1);
+        s_g[0][2 * p] = 0;
+        s_g[0][2 * p + 1] = 0;
+    }
+    if (bad) atomicOr(&s_bad, 1);
+    __syncthreads();
+    if (s_bad) return;
+    int32_t* ent = a.o.lvent + (long)bh * LEVEL_BUDGET * n;
+    int32_t* meta = a.o.lvmeta + (long)bh * LEVEL_META;
+    uint16_t* qidx = a.o.lvqidx + (long)bh * LEVEL_MAX * n;
+    uint16_t* kidx = a.o.lvkidx + (long)bh * LEVEL_MAX * n;
+    uint16_t* qcnt = a.o.lvcnt + (long)bh * LEVEL_MAX * n;
+    int4* lq = a.o.lvq + so;
+    for (int p = tid; p < n; p += SORT_THREADS) lq[p] = make_int4(0, -1, 0, 0);
+    auto shi = [](int v, int l) { return __shfl(v, l); };
+    auto add = [](int x, int y) { return x + y; };
+    auto sha = [](LvAgg v, int l) {
+        return LvAgg{__shfl(v.f, l), __shfl(v.cnt, l), __shfl(v.lk, l), __shfl(v.gs, l)};
+    };
+    int cur = 0, m = n2, total = 0, segs = 0, nlev = -1;
+    if (tid == 0) {
+        meta[1] = 0;                    // off[0]
+        meta[LEVEL_MAX + 2] = 0;        // segbase[0]
+    }
+    for (int l = 1; l <= LEVEL_MAX + 1; ++l) {
+        const int oth = cur ^ 1;
+        // ---- drop the entries at p < l - 1 (order kept): cur -> oth
+        const int ept = (m + SORT_THREADS - 1) / SORT_THREADS;
+        int c0 = tid * ept, c1 = c0 + ept < m ? c0 + ept : m;
+        int keepn = 0;
+        for (int c = c0; c < c1; ++c) keepn += (s_e[cur][c] >> 1) >= l - 1;
+        int mi;
+        int base = block_exscan(keepn, add, 0, shi, s_cnt, false, &mi);
+        for (int c = c0; c < c1; ++c) {
+            const int e = s_e[cur][c];
+            if ((e >> 1) >= l - 1) {
+                s_e[oth][base] = (uint16_t)e;
+                s_g[oth][base] = s_g[cur][c];
+                ++base;
+            }
+        }
+        __syncthreads();
+        // ---- stable sort by label[p - l + 1]: oth -> cur
+        const int sh = 2 * (l - 1);
+        lds_pass(
+            mi, [&](int x) { return (int)s_lab[s_e[oth][x] - sh]; },
+            [&](int x, int dst) {
+                s_e[cur][dst] = s_e[oth][x];
+                s_g[cur][dst] = s_g[oth][x];
+            },
+            nullptr, wcnt, scan, lmask);
+        // ---- groups: start, keys before, last key; keep flags
+        const int ept2 = (mi + SORT_THREADS - 1) / SORT_THREADS;
+        c0 = tid * ept2;
+        c1 = c0 + ept2 < mi ? c0 + ept2 : mi;
+        auto is_start = [&](int c) {
+            if (c == 0) return true;
+            const int e = s_e[cur][c], f = s_e[cur][c - 1];
+            return s_lab[e - sh] != s_lab[f - sh] || s_g[cur][c] != s_g[cur][c - 1];
+        };
+        LvAgg loc{0, 0, -1, -1};
+        for (int c = c0; c < c1; ++c) {
+            const int e = s_e[cur][c];
+            const bool st = is_start(c);
+            const LvAgg one{st ? 1 : 0, (e & 1) ? 0 : 1, (e & 1) ? -1 : (e >> 1), st ? c : -1};
+            loc = lv_op(loc, one);
+        }
+        for (int c = tid; c < mi; c += SORT_THREADS) s_keep[c] = 0;
+        LvAgg dummy;
+        const LvAgg pre = block_exscan(loc, lv_op, LvAgg{0, 0, -1, -1}, sha, s_agg, false, &dummy);
+        {
+            LvAgg run = pre;
+            for (int c = c0; c < c1; ++c) {
+                const int e = s_e[cur][c];
+                const bool st = is_start(c);
+                if (st) run = LvAgg{1, 0, -1, c};
+                if ((e & 1) && run.cnt > 0) s_keep[run.gs] = 1;
+                if (!(e & 1)) {
+                    run.cnt += 1;
+                    run.lk = e >> 1;
+                }
+            }
+        }
+        __syncthreads();
+        // ---- compaction of the kept groups: cur -> oth (next level's input) and out
+        int kn = 0;
+        {
+            LvAgg run = pre;
+            for (int c = c0; c < c1; ++c) {
+                if (is_start(c)) run.gs = c;
+                kn += s_keep[run.gs];
+            }
+        }
+        int kt;
+        int kb = block_exscan(kn, add, 0, shi, s_cnt, false, &kt);
+        if (kt == 0) {
+            nlev = l - 1;
+            break;
+        }
+        if (l == LEVEL_MAX + 1 || total + kt > LEVEL_BUDGET * nv) break;  // not a level row
+        {
+            LvAgg run = pre;
+            for (int c = c0; c < c1; ++c) {
+                const int e = s_e[cur][c];
+                const bool st = is_start(c);
+                if (st) run = LvAgg{1, 0, -1, c};
+                if (s_keep[run.gs]) {
+                    const int idx = kb++;
+                    const int p = e >> 1;
+                    ent[total + idx] = e | (st ? LEVEL_START : 0);
+                    s_e[oth][idx] = (uint16_t)e;
+                    s_g[oth][idx] = (uint16_t)(idx - (c - run.gs));
+                    if (e & 1) {
+                        qidx[(long)(l - 1) * n + p] = (uint16_t)idx;
+                        qcnt[(long)(l - 1) * n + p] = (uint16_t)run.cnt;
+                        lq[p].z = l;
+                        if (run.cnt > 0) {
+                            lq[p].x = l;
+                            lq[p].y = run.lk;
+                        }
+                    } else {
+                        kidx[(long)(l - 1) * n + p] = (uint16_t)idx;
+                        lq[p].w = l;
+                    }
+                }
+                if (!(e & 1)) {
+                    run.cnt += 1;
+                    run.lk = e >> 1;
+                }
+            }
+        }
+        __syncthreads();
+        total += kt;
+        segs += (kt + LEVEL_SEG - 1) / LEVEL_SEG;
+        if (tid == 0) {
+            meta[1 + l] = total;
+            meta[LEVEL_MAX + 2 + l] = segs;
+        }
+        m = kt;
+        cur = oth;
+    }
+    if (nlev > 0 && tid == 0) {
+        meta[0] = nlev;
+        a.o.dflag[bh] = 3;
+    }
+}
+
+hipError_t launch_level_prep(const PathArgs& a, hipStream_t s) {
+    if (!a.o.lvent || a.dstart || a.wlo || a.n > LEVEL_MAX_N) return hipSuccess;
+    hipLaunchKernelGGL(level_prep_kernel, dim3((unsigned)(a.B * a.H)), dim3(SORT_THREADS), 0, s,
+                       a);
+    return hipGetLastError();
+}
+
 }  // namespace dism

@@ -78,6 +78,9 @@ def lib():
         L.orc_bucket_collisions.restype = ctypes.c_uint64
         L.orc_bucket_collisions.argtypes = [P, P, i64]
         L.orc_dense_rows.argtypes = [P, P, P, i32, i64, P]
+        L.orc_row_modes.argtypes = [P, P, i32, i64, i32, i32, P]
+        L.orc_level_row.restype = i32
+        L.orc_level_row.argtypes = [P, P, i64, i32, i32]
         _lib = L
     return _lib
 
@@ -178,6 +181,23 @@ def dense_rows(iq, ik, hard):
     return out.reshape(B, H)
 
 
+def row_modes(iq, ik, R, DV):
+    """Row modes of a fixed-length call without resets as the HIP path chooses them (every row
+    taken as hard): uint8 [B,H], 0 decomposed, 1 direct (dense), 3 levels (dense rows with
+    labels below 256, N <= 4096, R * DV <= 512 and at most 32 levels: level_count)."""
+    iq, ik = _i32(iq), _i32(ik)
+    B, H, N = iq.shape
+    out = np.empty(B * H, dtype=np.uint8)
+    lib().orc_row_modes(_p(iq), _p(ik), B * H, N, R, DV, _p(out))
+    return out.reshape(B, H)
+
+
+def level_count(q, k, R, DV):
+    """Levels of one row (its longest match) when it is a level row, else 0."""
+    q, k = _i32(q), _i32(k)
+    return int(lib().orc_level_row(_p(q), _p(k), q.shape[-1], R, DV))
+
+
 def packed_dense_flags(iq, ik, offsets):
     """Row classification of a packed call (B = 1): the HIP path classifies each head row of
     its document-tagged labels tag = rank * docs + d (rank: dense rank of the raw label among
@@ -219,10 +239,12 @@ def _dense_arg(dense, B, H):
 def forward(sq, sk, v, iq, ik, hard, lut, threads=0, direct=False, reset=None, dense=None):
     """CPU model forward.  Returns (O fp32 [B,N,H,DV], lse2 [B,H,N], Lmax, argmax).
 
-    direct=False: the sequence the HIP kernels reproduce bit for bit -- per row, the direct
-    (pairwise) definition for rows classified dense (dense_rows) and the decomposed one for
-    the others;  direct=True: the pairwise definition for every row.
-    dense: optional [B,H] (or scalar) override of the row classification.
+    direct=False: the sequence the HIP kernels reproduce bit for bit -- per row, the level
+    definition for level rows (row_modes 3), the direct (pairwise) definition for the other
+    rows classified dense (dense_rows) and the decomposed one for the rest;  direct=True: the
+    pairwise definition for every row.
+    dense: optional [B,H] (or scalar) override of the row modes (0 decomposed, 1 direct,
+    3 levels where the row qualifies, else direct).
     reset: optional [B,H,N] bool query resets (inference semantics: a reset query's match
     starts afresh at that query; keys stay)."""
     sq, sk, v, lut = _f32(sq), _f32(sk), _f32(v), _f32(lut)

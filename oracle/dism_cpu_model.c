@@ -506,6 +506,462 @@ void orc_dense_rows(const int32_t* iq, const int32_t* ik, const uint8_t* hard, i
         dense[bh] = (uint8_t)orc_dense_row(iq + (long)bh * N, ik + (long)bh * N, N, hard[bh]);
 }
 
+/* ---------------- level rows ----------------
+ * A dense row whose labels are all below 256, with N <= LEVEL_MAX_N, R * DV <= LEVEL_RDV, no
+ * query resets, and whose longest match is at most LEVEL_MAX (with at most LEVEL_BUDGET * N
+ * kept entries over all levels, below) is a "level row".  Its sums are taken per match
+ * length instead of per pair.
+ *
+ * Level l groups the 2N entries e = 2p + s (s = 0 key, 1 query at position p, p >= l - 1) by
+ * their l-gram (label[p - l + 1], ..., label[p]); a valid pair (j <= i) has L >= l exactly
+ * when key j and query i share a level-l group.  The level-l list is the level-(l-1) kept
+ * list without its entries at p = l - 2, stably sorted by label[p - l + 1] (level 1: all
+ * entries in e order, sorted by label): inside a group the entries stay in e order (a key
+ * before the query of its position).  A group is kept when one of its queries has a key
+ * before it; the others cannot hold a valid pair at this or any deeper level.  The levels
+ * stop at the first level with no kept group.
+ *
+ * Per query i and level l <= Lq (Lq = the longest match of i, lmax): n_l = keys before it in
+ * its group (the valid keys with L >= l); y_l = sq_i . M_l with M_l = sum over those keys
+ * of sk_j (x) v_j.  With p_l = exp2(LUT[l] - m), p_0 = 0, c_l = p_l - p_{l-1}:
+ *   sum over valid j of p(L_ij) x_j = sum over l of c_l * (sum over keys with L >= l of x_j).
+ * m = max(0, LUT[l] over the lengths l present, n_l > n_{l+1}), as the direct definition's.
+ *
+ * M_l comes from segments of LEVEL_SEG consecutive list entries: a query's M starts from the
+ * prefix P_s of its segment (when its group began in an earlier segment, else from zero) and
+ * runs an fma chain over the keys of its group before it in the segment.  T_s (the chain over
+ * the keys of a segment's last group piece when that group continues into the next segment)
+ * and P_{s+1} = P_s + T_s (P_{s+1} = T_s when the group began inside segment s) give the
+ * prefixes.  The backward's key side runs the mirror image over queries in descending order
+ * (U_s over the first piece, Q_{s-1} = Q_s + U_s).
+ *
+ * fp32 sequences (the HIP kernels of dism_levels.hip compute exactly these):
+ *   forward, query i: m as above; den = exp2(-m); for l = 1..Lq: den = fma(c_l, n_l, den);
+ *     acc[d] = fma(c_l, y_l[d], acc[d]) (acc from +0); y_l[d] = chain_r fma(sq[r], M[r][d]);
+ *     out = acc / den, lse2 = m + log2(den); jarg = the last key of i's level-Lq group before it.
+ *   backward, query i (p_l from l2 = lse2_i, cc = G[i + 1], F_l = p_l * (G[l] - cc), F_0 = 0,
+ *     dF_l = F_l - F_{l-1}): z_l[r] = lane tree of dO[d] * M[r][d] (level_tree),
+ *     w_l = chain_r fma(sq[r], z_l[r]); dq[r] = fma(c_l, z_l[r], dq[r]); u = fma(c_l, w_l, u);
+ *     vv = fma(dF_l, n_l, vv); ww = fma(dF_l, w_l, ww); z = fma(c_l, n_l, z); then rowtau
+ *     as the direct definition's.
+ *   backward, key j, levels l = 1..(its kept levels): K[d][r] = fma(a_i[r], dO_i[d], K) over
+ *     the queries after it in its group piece, descending, from Q_s or zero, a_i[r] =
+ *     c_l(i) * sq_i[r]; dv_l[d] = chain_r fma(sk[r], K[d][r]); dk_l[r] = level_tree of
+ *     v[d] * K[d][r]; dv = dv_1 + dv_2 + ..., dk likewise (left to right). */
+static float dot_chain(const float* a, const float* b, int n);
+
+#define LEVEL_MAX_N 4096L
+#define LEVEL_MAX 32
+#define LEVEL_BUDGET 16L
+#define LEVEL_SEG 32L
+#define LEVEL_RDV 512
+#define LEVEL_START 0x40000000
+
+typedef struct {
+    int nlev;
+    long off[LEVEL_MAX + 2];  /* level l (1-based) entries at [off[l-1], off[l]) */
+    int32_t* ent;             /* e | LEVEL_START at a group's first entry */
+} Levels;
+
+/* 1 (and L filled; free L->ent) when the labels make a level row; the caller checks N, R*DV
+ * and the absence of resets */
+static int levels_build(const int32_t* q, const int32_t* k, long N, Levels* L) {
+    L->ent = NULL;
+    L->nlev = 0;
+    if (N < 1 || N > LEVEL_MAX_N) return 0;
+    for (long x = 0; x < N; ++x)
+        if ((uint32_t)q[x] >= 256u || (uint32_t)k[x] >= 256u) return 0;
+    const long M2 = 2 * N, cap = LEVEL_BUDGET * N;
+    int32_t* cur = (int32_t*)malloc(sizeof(int32_t) * (size_t)M2);
+    int32_t* cg = (int32_t*)malloc(sizeof(int32_t) * (size_t)M2);
+    int32_t* in = (int32_t*)malloc(sizeof(int32_t) * (size_t)M2);
+    int32_t* ig = (int32_t*)malloc(sizeof(int32_t) * (size_t)M2);
+    int32_t* id = (int32_t*)malloc(sizeof(int32_t) * (size_t)M2);
+    int32_t* se = (int32_t*)malloc(sizeof(int32_t) * (size_t)M2);
+    int32_t* sg = (int32_t*)malloc(sizeof(int32_t) * (size_t)M2);
+    int32_t* sd = (int32_t*)malloc(sizeof(int32_t) * (size_t)M2);
+    L->ent = (int32_t*)malloc(sizeof(int32_t) * (size_t)cap);
+    long m = M2, total = 0;
+    int ok = 0;
+    for (long e = 0; e < M2; ++e) { cur[e] = (int32_t)e; cg[e] = 0; }
+    L->off[0] = 0;
+    for (int l = 1; l <= LEVEL_MAX + 1; ++l) {
+        long mi = 0;
+        for (long t = 0; t < m; ++t) {
+            const int32_t e = cur[t] & ~LEVEL_START;
+            const long p = e >> 1;
+            if (p < l - 1) continue;
+            in[mi] = e;
+            ig[mi] = cg[t];
+            id[mi] = ((e & 1) ? q : k)[p - l + 1];
+            ++mi;
+        }
+        long cnt[257];
+        memset(cnt, 0, sizeof(cnt));
+        for (long t = 0; t < mi; ++t) cnt[id[t] + 1]++;
+        for (int d = 0; d < 256; ++d) cnt[d + 1] += cnt[d];
+        for (long t = 0; t < mi; ++t) {
+            const long dst = cnt[id[t]]++;
+            se[dst] = in[t];
+            sg[dst] = ig[t];
+            sd[dst] = id[t];
+        }
+        long om = 0;
+        for (long t = 0; t < mi;) {
+            long te = t + 1;
+            while (te < mi && sd[te] == sd[t] && sg[te] == sg[t]) ++te;
+            int nk = 0, keep = 0;
+            for (long x = t; x < te; ++x) {
+                if (!(se[x] & 1)) ++nk;
+                else if (nk > 0) keep = 1;
+            }
+            if (keep) {
+                if (l <= LEVEL_MAX && total + om + (te - t) <= cap)
+                    for (long x = t; x < te; ++x) {
+                        L->ent[total + om + (x - t)] = se[x] | (x == t ? LEVEL_START : 0);
+                        cg[om + (x - t)] = (int32_t)om;  /* next level's group id */
+                    }
+                om += te - t;
+            }
+            t = te;
+        }
+        if (om == 0) { L->nlev = l - 1; ok = 1; break; }
+        if (l == LEVEL_MAX + 1 || total + om > cap) break;
+        for (long x = 0; x < om; ++x) cur[x] = L->ent[total + x];
+        m = om;
+        total += om;
+        L->off[l] = total;
+    }
+    free(cur); free(cg); free(in); free(ig); free(id); free(se); free(sg); free(sd);
+    if (!ok) { free(L->ent); L->ent = NULL; }
+    return ok;
+}
+
+/* the row's level count (>= 1), or 0 when it is not a level row (dense or not) */
+int orc_level_row(const int32_t* q, const int32_t* k, long N, int R, int DV) {
+    if ((long)R * DV > LEVEL_RDV) return 0;
+    if (!orc_dense_row(q, k, N, 1)) return 0;
+    Levels L;
+    if (!levels_build(q, k, N, &L)) return 0;
+    free(L.ent);
+    return L.nlev;
+}
+
+/* row mode as the HIP path chooses it: 0 decomposed, 1 direct, 3 levels */
+static int row_mode(const int32_t* q, const int32_t* k, long N, int R, int DV, int resets) {
+    if (!orc_dense_row(q, k, N, 1)) return 0;
+    if (resets || (long)R * DV > LEVEL_RDV) return 1;
+    Levels L;
+    if (!levels_build(q, k, N, &L)) return 1;
+    free(L.ent);
+    return 3;
+}
+
+void orc_row_modes(const int32_t* iq, const int32_t* ik, int BH, long N, int R, int DV,
+                   uint8_t* mode) {
+    for (int bh = 0; bh < BH; ++bh)
+        mode[bh] = (uint8_t)row_mode(iq + (long)bh * N, ik + (long)bh * N, N, R, DV, 0);
+}
+
+/* per (level, query or key position): index in the level list, -1 when not there; and
+ * per query the key count before it in its group */
+typedef struct {
+    int32_t* idx;   /* [nlev][2N] by entry e */
+    int32_t* nk;    /* [nlev][N] by query position */
+    int32_t* lastk; /* [nlev][N] last key position before the query in its group, -1 */
+} LevelMaps;
+
+static void level_maps(const Levels* L, long N, LevelMaps* Mp) {
+    const int nl = L->nlev;
+    Mp->idx = (int32_t*)malloc(sizeof(int32_t) * (size_t)(nl * 2 * N));
+    Mp->nk = (int32_t*)calloc((size_t)(nl * N), sizeof(int32_t));
+    Mp->lastk = (int32_t*)malloc(sizeof(int32_t) * (size_t)(nl * N));
+    for (long x = 0; x < nl * 2 * N; ++x) Mp->idx[x] = -1;
+    for (long x = 0; x < nl * N; ++x) Mp->lastk[x] = -1;
+    for (int l = 1; l <= nl; ++l) {
+        const int32_t* E = L->ent + L->off[l - 1];
+        const long m = L->off[l] - L->off[l - 1];
+        int nk = 0, lk = -1;
+        for (long t = 0; t < m; ++t) {
+            if (E[t] & LEVEL_START) { nk = 0; lk = -1; }
+            const int32_t e = E[t] & ~LEVEL_START;
+            Mp->idx[(long)(l - 1) * 2 * N + e] = (int32_t)t;
+            if (!(e & 1)) { ++nk; lk = e >> 1; }
+            else {
+                Mp->nk[(long)(l - 1) * N + (e >> 1)] = nk;
+                Mp->lastk[(long)(l - 1) * N + (e >> 1)] = lk;
+            }
+        }
+    }
+}
+
+static void level_maps_free(LevelMaps* Mp) { free(Mp->idx); free(Mp->nk); free(Mp->lastk); }
+
+/* lane tree of per-lane terms: lane t (t < 64) holds a[t]*b[t] (t < DV), then
+ * fma(a[t+64], b[t+64], .) (t + 64 < DV), else 0; t[l] = t[l] + t[l+m] for m = 32, ..., 1 */
+static float level_tree(const float* a, long sa, const float* b, long sb, int DV) {
+    float t[64];
+    for (int l = 0; l < 64; ++l) {
+        float x = l < DV ? a[l * sa] * b[l * sb] : 0.0f;
+        if (l + 64 < DV) x = fmaf(a[(l + 64) * sa], b[(l + 64) * sb], x);
+        t[l] = x;
+    }
+    for (int m = 32; m >= 1; m /= 2)
+        for (int l = 0; l < m; ++l) t[l] = t[l] + t[l + m];
+    return t[0];
+}
+
+/* forward prefixes of one level: P [nseg][R*DV], has [nseg] (1 when segment s's first
+ * piece continues a group of an earlier segment) */
+static void level_prefix(const Levels* L, int l, const float* sk, const float* v, int b, int h,
+                         long N, int H, int R, int DV, float* P, uint8_t* has) {
+    const int32_t* E = L->ent + L->off[l - 1];
+    const long m = L->off[l] - L->off[l - 1], nseg = (m + LEVEL_SEG - 1) / LEVEL_SEG;
+    const long RD = (long)R * DV;
+    float* T = (float*)malloc(sizeof(float) * (size_t)RD);
+    for (long s = 0; s < nseg; ++s) has[s] = 0;
+    for (long s = 0; s + 1 < nseg; ++s) {
+        const long beg = s * LEVEL_SEG, end = beg + LEVEL_SEG;
+        if (E[end] & LEVEL_START) continue;  /* no group crosses into s + 1 */
+        long ls = beg;
+        for (long x = beg; x < end; ++x)
+            if (E[x] & LEVEL_START) ls = x;
+        for (long e = 0; e < RD; ++e) T[e] = 0.0f;
+        for (long x = ls; x < end; ++x) {
+            const int32_t e = E[x] & ~LEVEL_START;
+            if (e & 1) continue;
+            const long krow = ((long)b * N + (e >> 1)) * H + h;
+            for (int r = 0; r < R; ++r)
+                for (int d = 0; d < DV; ++d)
+                    T[r * DV + d] = fmaf(sk[krow * R + r], v[krow * DV + d], T[r * DV + d]);
+        }
+        /* segment s wholly inside the group (first piece continuing, no start): add */
+        const int chain = has[s] && ls == beg && !(E[beg] & LEVEL_START);
+        for (long e = 0; e < RD; ++e)
+            P[(s + 1) * RD + e] = chain ? P[s * RD + e] + T[e] : T[e];
+        has[s + 1] = 1;
+    }
+    free(T);
+}
+
+/* M of query entry x of level l (list E), from the segment prefix */
+static void level_query_m(const int32_t* E, long x, const float* P, const uint8_t* has,
+                          const float* sk, const float* v, int b, int h, long N, int H, int R,
+                          int DV, float* M) {
+    const long RD = (long)R * DV, s = x / LEVEL_SEG, beg = s * LEVEL_SEG;
+    long ps = beg;
+    int start = 0;
+    for (long t = beg; t <= x; ++t)
+        if (E[t] & LEVEL_START) { ps = t; start = 1; }
+    for (long e = 0; e < RD; ++e) M[e] = (!start && has[s]) ? P[s * RD + e] : 0.0f;
+    for (long t = ps; t < x; ++t) {
+        const int32_t e = E[t] & ~LEVEL_START;
+        if (e & 1) continue;
+        const long krow = ((long)b * N + (e >> 1)) * H + h;
+        for (int r = 0; r < R; ++r)
+            for (int d = 0; d < DV; ++d)
+                M[r * DV + d] = fmaf(sk[krow * R + r], v[krow * DV + d], M[r * DV + d]);
+    }
+}
+
+static void level_forward_row(const float* sq, const float* sk, const float* v,
+                              const float* tab, int b, int h, long N, int H, int R, int DV,
+                              const Levels* L, float* out, float* lse2, int32_t* lmax,
+                              int32_t* jarg) {
+    const int nl = L->nlev;
+    const long RD = (long)R * DV;
+    LevelMaps Mp;
+    level_maps(L, N, &Mp);
+    float** P = (float**)malloc(sizeof(float*) * (size_t)nl);
+    uint8_t** has = (uint8_t**)malloc(sizeof(uint8_t*) * (size_t)nl);
+    for (int l = 1; l <= nl; ++l) {
+        const long m = L->off[l] - L->off[l - 1], nseg = (m + LEVEL_SEG - 1) / LEVEL_SEG;
+        P[l - 1] = (float*)malloc(sizeof(float) * (size_t)(nseg * RD));
+        has[l - 1] = (uint8_t*)malloc((size_t)nseg);
+        level_prefix(L, l, sk, v, b, h, N, H, R, DV, P[l - 1], has[l - 1]);
+    }
+    float* M = (float*)malloc(sizeof(float) * (size_t)RD);
+    float* acc = (float*)malloc(sizeof(float) * (size_t)DV);
+    for (long i = 0; i < N; ++i) {
+        const long row = ((long)b * N + i) * H + h;
+        int Lq = 0;
+        for (int l = 1; l <= nl; ++l)
+            if (Mp.idx[(long)(l - 1) * 2 * N + 2 * i + 1] >= 0 && Mp.nk[(long)(l - 1) * N + i] > 0)
+                Lq = l;
+        float m = 0.0f;
+        for (int l = 1; l <= Lq; ++l) {
+            const int n1 = Mp.nk[(long)(l - 1) * N + i];
+            const int n2 = l < Lq ? Mp.nk[(long)l * N + i] : 0;
+            if (n1 > n2 && tab[l] > m) m = tab[l];
+        }
+        float den = orc_exp2f(-m), pp = 0.0f;
+        for (int d = 0; d < DV; ++d) acc[d] = 0.0f;
+        const float* sqi = sq + row * R;
+        for (int l = 1; l <= Lq; ++l) {
+            const float p = orc_exp2f(tab[l] - m);
+            const float c = p - pp;
+            pp = p;
+            den = fmaf(c, (float)Mp.nk[(long)(l - 1) * N + i], den);
+            const long x = Mp.idx[(long)(l - 1) * 2 * N + 2 * i + 1];
+            level_query_m(L->ent + L->off[l - 1], x, P[l - 1], has[l - 1], sk, v, b, h, N, H, R,
+                          DV, M);
+            for (int d = 0; d < DV; ++d) {
+                float y = 0.0f;
+                for (int r = 0; r < R; ++r) y = fmaf(sqi[r], M[r * DV + d], y);
+                acc[d] = fmaf(c, y, acc[d]);
+            }
+        }
+        for (int d = 0; d < DV; ++d) out[row * DV + d] = acc[d] / den;
+        lse2[i] = m + orc_log2f(den);
+        if (lmax) lmax[i] = Lq;
+        if (jarg) jarg[i] = Lq ? Mp.lastk[(long)(Lq - 1) * N + i] : -1;
+    }
+    for (int l = 0; l < nl; ++l) { free(P[l]); free(has[l]); }
+    free(P); free(has); free(M); free(acc);
+    level_maps_free(&Mp);
+}
+
+/* c_l of query position i (l2 its lse2) */
+static float level_c(const float* tab, int l, float l2) {
+    const float p = orc_exp2f(tab[l] - l2);
+    return l > 1 ? p - orc_exp2f(tab[l - 1] - l2) : p - 0.0f;
+}
+
+static void level_backward_row(const float* sq, const float* sk, const float* v,
+                               const float* dout, const float* tab, const float* gt,
+                               const float* l2v, int b, int h, long N, int H, int R, int DV,
+                               const Levels* L, float* dsq, float* dsk, float* dv,
+                               float* rowtau) {
+    const int nl = L->nlev;
+    const long RD = (long)R * DV;
+    LevelMaps Mp;
+    level_maps(L, N, &Mp);
+    float** P = (float**)malloc(sizeof(float*) * (size_t)nl);
+    uint8_t** has = (uint8_t**)malloc(sizeof(uint8_t*) * (size_t)nl);
+    float** Q = (float**)malloc(sizeof(float*) * (size_t)nl);
+    uint8_t** hq = (uint8_t**)malloc(sizeof(uint8_t*) * (size_t)nl);
+    float* U = (float*)malloc(sizeof(float) * (size_t)RD);
+    float* a = (float*)malloc(sizeof(float) * (size_t)R);
+    for (int l = 1; l <= nl; ++l) {
+        const int32_t* E = L->ent + L->off[l - 1];
+        const long m = L->off[l] - L->off[l - 1], nseg = (m + LEVEL_SEG - 1) / LEVEL_SEG;
+        P[l - 1] = (float*)malloc(sizeof(float) * (size_t)(nseg * RD));
+        has[l - 1] = (uint8_t*)malloc((size_t)nseg);
+        level_prefix(L, l, sk, v, b, h, N, H, R, DV, P[l - 1], has[l - 1]);
+        /* key-side suffixes: K layout [d][r] */
+        Q[l - 1] = (float*)malloc(sizeof(float) * (size_t)(nseg * RD));
+        hq[l - 1] = (uint8_t*)calloc((size_t)nseg, 1);
+        for (long s = nseg - 1; s >= 1; --s) {
+            const long beg = s * LEVEL_SEG;
+            const long end = beg + LEVEL_SEG < m ? beg + LEVEL_SEG : m;
+            if (E[beg] & LEVEL_START) continue;  /* no group crosses from s - 1 */
+            long fe = end;
+            for (long x = end - 1; x > beg; --x)
+                if (E[x] & LEVEL_START) fe = x;
+            for (long e = 0; e < RD; ++e) U[e] = 0.0f;
+            for (long x = fe - 1; x >= beg; --x) {
+                const int32_t e = E[x] & ~LEVEL_START;
+                if (!(e & 1)) continue;
+                const long i = e >> 1;
+                const long row = ((long)b * N + i) * H + h;
+                const float c = level_c(tab, l, l2v[i]);
+                for (int r = 0; r < R; ++r) a[r] = c * sq[row * R + r];
+                for (int d = 0; d < DV; ++d)
+                    for (int r = 0; r < R; ++r)
+                        U[d * R + r] = fmaf(a[r], dout[row * DV + d], U[d * R + r]);
+            }
+            const int chain = hq[l - 1][s] && fe == end && end < m;
+            for (long e = 0; e < RD; ++e)
+                Q[l - 1][(s - 1) * RD + e] = chain ? Q[l - 1][s * RD + e] + U[e] : U[e];
+            hq[l - 1][s - 1] = 1;
+        }
+    }
+    float* M = (float*)malloc(sizeof(float) * (size_t)RD);
+    float* zl = (float*)malloc(sizeof(float) * (size_t)R);
+    float* dq = (float*)malloc(sizeof(float) * (size_t)R);
+    /* ---- query rows */
+    for (long i = 0; i < N; ++i) {
+        const long row = ((long)b * N + i) * H + h;
+        const float* sqi = sq + row * R;
+        const float* doi = dout + row * DV;
+        int Lq = 0;
+        for (int l = 1; l <= nl; ++l)
+            if (Mp.idx[(long)(l - 1) * 2 * N + 2 * i + 1] >= 0 && Mp.nk[(long)(l - 1) * N + i] > 0)
+                Lq = l;
+        const float l2 = l2v[i];
+        const float cc = gt[i + 1];
+        float u = 0.0f, vv = 0.0f, ww = 0.0f, z = 0.0f, pp = 0.0f, fp = 0.0f;
+        for (int r = 0; r < R; ++r) dq[r] = 0.0f;
+        for (int l = 1; l <= Lq; ++l) {
+            const float p = orc_exp2f(tab[l] - l2);
+            const float c = p - pp;
+            const float F = p * (gt[l] - cc);
+            const float dF = F - fp;
+            pp = p;
+            fp = F;
+            const long x = Mp.idx[(long)(l - 1) * 2 * N + 2 * i + 1];
+            level_query_m(L->ent + L->off[l - 1], x, P[l - 1], has[l - 1], sk, v, b, h, N, H, R,
+                          DV, M);
+            for (int r = 0; r < R; ++r) zl[r] = level_tree(doi, 1, M + (long)r * DV, 1, DV);
+            const float w = dot_chain(sqi, zl, R);
+            const float fn = (float)Mp.nk[(long)(l - 1) * N + i];
+            for (int r = 0; r < R; ++r) dq[r] = fmaf(c, zl[r], dq[r]);
+            u = fmaf(c, w, u);
+            vv = fmaf(dF, fn, vv);
+            ww = fmaf(dF, w, ww);
+            z = fmaf(c, fn, z);
+        }
+        for (int r = 0; r < R; ++r) dsq[row * R + r] = dq[r];
+        const float f = orc_exp2f(-l2);
+        const float mass = z + f;
+        const float mean = fmaf(-f, cc, vv) / mass;
+        rowtau[i] = fmaf(-u, mean, ww) / mass;
+    }
+    /* ---- keys */
+    float* K = M;  /* [d][r] */
+    float* dkl = dq;
+    for (long j = 0; j < N; ++j) {
+        const long krow = ((long)b * N + j) * H + h;
+        const float* skj = sk + krow * R;
+        const float* vj = v + krow * DV;
+        for (int l = 1; l <= nl; ++l) {
+            const long x = Mp.idx[(long)(l - 1) * 2 * N + 2 * j];
+            if (x < 0) break;
+            const int32_t* E = L->ent + L->off[l - 1];
+            const long m = L->off[l] - L->off[l - 1];
+            const long s = x / LEVEL_SEG, beg = s * LEVEL_SEG;
+            const long end = beg + LEVEL_SEG < m ? beg + LEVEL_SEG : m;
+            long pe = end;
+            for (long t = end - 1; t > x; --t)
+                if (E[t] & LEVEL_START) pe = t;
+            const int cont = pe == end && end < m && !(E[end] & LEVEL_START);
+            for (long e = 0; e < RD; ++e) K[e] = cont ? Q[l - 1][s * RD + e] : 0.0f;
+            for (long t = pe - 1; t > x; --t) {
+                const int32_t e = E[t] & ~LEVEL_START;
+                if (!(e & 1)) continue;
+                const long i = e >> 1;
+                const long row = ((long)b * N + i) * H + h;
+                const float c = level_c(tab, l, l2v[i]);
+                for (int r = 0; r < R; ++r) a[r] = c * sq[row * R + r];
+                for (int d = 0; d < DV; ++d)
+                    for (int r = 0; r < R; ++r)
+                        K[d * R + r] = fmaf(a[r], dout[row * DV + d], K[d * R + r]);
+            }
+            for (int r = 0; r < R; ++r) dkl[r] = level_tree(vj, 1, K + r, R, DV);
+            for (int d = 0; d < DV; ++d) {
+                float y = 0.0f;
+                for (int r = 0; r < R; ++r) y = fmaf(skj[r], K[d * R + r], y);
+                dv[krow * DV + d] = l == 1 ? y : dv[krow * DV + d] + y;
+            }
+            for (int r = 0; r < R; ++r)
+                dsk[krow * R + r] = l == 1 ? dkl[r] : dsk[krow * R + r] + dkl[r];
+        }
+    }
+    for (int l = 0; l < nl; ++l) { free(P[l]); free(has[l]); free(Q[l]); free(hq[l]); }
+    free(P); free(has); free(Q); free(hq); free(U); free(a); free(M); free(zl); free(dq);
+    level_maps_free(&Mp);
+}
+
 /* dtau_h: for each head, the B*N row terms in (b, i) order are cut into blocks of
  * `block` rows; each block is summed sequentially in double; block sums are then summed
  * sequentially in double; the result is rounded to float. */
@@ -690,7 +1146,16 @@ static void forward_impl(const float* sq, const float* sk, const float* v, const
             }
             continue;
         }
-        if (dense ? dense[bh] : orc_dense_row(q, k, N, 1)) {
+        const int mode = dense ? dense[bh] : row_mode(q, k, N, R, DV, wlo != NULL);
+        Levels lv;
+        if (mode == 3 && levels_build(q, k, N, &lv)) {
+            const long so = (long)bh * N;
+            level_forward_row(sq, sk, v, tab, b, h, N, H, R, DV, &lv, out, lse2 + so,
+                              lmax ? lmax + so : NULL, jarg ? jarg + so : NULL);
+            free(lv.ent);
+            continue;
+        }
+        if (mode == 1 || mode == 3) {
             const long so = (long)bh * N;
             direct_forward_row(sq, sk, v, q, k, tab, b, h, N, H, R, DV, out, lse2 + so,
                                lmax ? lmax + so : NULL, jarg ? jarg + so : NULL,
@@ -837,7 +1302,15 @@ void orc_backward_flags(const float* sq, const float* sk, const float* v, const 
             rowtau[(long)bh * N + x] = 0.0f;
         }
         if (!hard[bh]) continue;
-        if (dense ? dense[bh] : orc_dense_row(q, k, N, 1)) {
+        const int mode = dense ? dense[bh] : row_mode(q, k, N, R, DV, 0);
+        Levels lv;
+        if (mode == 3 && levels_build(q, k, N, &lv)) {
+            level_backward_row(sq, sk, v, dout, tab, gt, l2v, b, h, N, H, R, DV, &lv, dsq, dsk,
+                               dv, rowtau + (long)bh * N);
+            free(lv.ent);
+            continue;
+        }
+        if (mode == 1 || mode == 3) {
             direct_backward_row(sq, sk, v, dout, q, k, tab, gt, l2v, b, h, N, H, R, DV, dsq,
                                 dsk, dv, rowtau + (long)bh * N);
             continue;

@@ -329,7 +329,10 @@ def test_forward_with_query_resets_pinned_by_fp64():
         ref, l2d = dense.dense_forward(sq, sk, v, iq, ik, hard, tau, reset=reset)
         np.testing.assert_allclose(got, ref, atol=2e-6, rtol=2e-4)
         np.testing.assert_allclose(l2, l2d, atol=2e-5, rtol=2e-6)
-        plain = oracle.forward(sq, sk, v, iq, ik, hard, lut)[0]
+        # (calls with resets never take the level path, so the plain call is given the
+        # same row modes: direct for the dense rows)
+        plain = oracle.forward(sq, sk, v, iq, ik, hard, lut,
+                               dense=oracle.dense_rows(iq, ik, hard))[0]
         none = oracle.forward(sq, sk, v, iq, ik, hard, lut, reset=np.zeros_like(reset))[0]
         assert np.array_equal(plain.view(np.uint32), none.view(np.uint32))
         assert np.abs(plain - got).max() > 1e-3
