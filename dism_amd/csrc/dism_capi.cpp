@@ -55,7 +55,7 @@ struct Layout {
     int64_t corder, clab, ctab, bpos[2], blab[2], bplab[2], btab[2], shift, tmp[3];
     int64_t stage[2][2], bhcount[2], own[2], ocount, mode, onebyte;
     int64_t pnb, prow, mcount, mdig, dflag, dlist, dcount, dbound, dcost;
-    int64_t lvent, lvmeta, lvqidx, lvkidx, lvcnt, lvq, lvT, lvP, lvU, lvQ, lvc;  // -1: none
+    int64_t lvent, lvmeta, lvqidx, lvkidx, lvcnt, lvq, lvP, lvQ, lvY, lvZ, lvK;  // -1: none
     int64_t total;
     int prow_stride;
 };
@@ -167,11 +167,11 @@ Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     L.lvkidx = lv ? take(BH * lmat * 2) : -1;
     L.lvcnt = lv ? take(BH * lmat * 2) : -1;
     L.lvq = lv ? take(BH * N * 16) : -1;
-    L.lvT = lv ? take(BH * lseg) : -1;
     L.lvP = lv ? take(BH * lseg) : -1;
-    L.lvU = lv ? take(BH * lseg) : -1;
     L.lvQ = lv ? take(BH * lseg) : -1;
-    L.lvc = lv ? take(BH * lent * 4) : -1;
+    L.lvY = lv ? take(BH * lent * DV * 4) : -1;
+    L.lvZ = lv ? take(BH * lent * R * 4) : -1;
+    L.lvK = lv ? take(BH * lent * R * 4) : -1;
     L.total = o;
     return L;
 }
@@ -216,11 +216,11 @@ dism::Orders orders(const Layout& L, void* ws) {
     o.lvkidx = reinterpret_cast<uint16_t*>(opt(L.lvkidx));
     o.lvcnt = reinterpret_cast<uint16_t*>(opt(L.lvcnt));
     o.lvq = reinterpret_cast<int4*>(opt(L.lvq));
-    o.lvT = reinterpret_cast<float*>(opt(L.lvT));
     o.lvP = reinterpret_cast<float*>(opt(L.lvP));
-    o.lvU = reinterpret_cast<float*>(opt(L.lvU));
     o.lvQ = reinterpret_cast<float*>(opt(L.lvQ));
-    o.lvc = reinterpret_cast<float*>(opt(L.lvc));
+    o.lvY = reinterpret_cast<float*>(opt(L.lvY));
+    o.lvZ = reinterpret_cast<float*>(opt(L.lvZ));
+    o.lvK = reinterpret_cast<float*>(opt(L.lvK));
     return o;
 }
 

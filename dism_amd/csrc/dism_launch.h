@@ -73,20 +73,24 @@ struct Orders {
     //   lvcnt  [LEVEL_MAX][N]      keys before query p in its level-l group
     //   lvq    [N]                 per position {longest match Lq, its last key, kept levels
     //                              of the query, kept levels of the key}
-    //   lvT, lvP [LEVEL_SEGS(N)][R*DV]  forward segment totals and prefixes ([r][d])
-    //   lvU, lvQ [LEVEL_SEGS(N)][R*DV]  key-side totals and suffixes ([d][r])
-    //   lvc    [LEVEL_BUDGET * N]  c_l of every query entry (backward)
+    //   lvP    [level_segs(N)][R*DV]  forward segment totals T_s, each replaced by the
+    //                              prefix P_{s+1} ([r][d])
+    //   lvQ    [level_segs(N)][R*DV]  key-side totals U_s, each replaced by Q_{s-1} ([d][r])
+    //   lvY    [LEVEL_BUDGET * N][DV]  per list entry: the forward's y_l of a query, the
+    //                              backward's dv_l of a key
+    //   lvZ    [LEVEL_BUDGET * N][R]   the backward's z_l of a query
+    //   lvK    [LEVEL_BUDGET * N][R]   the backward's dk_l of a key
     int32_t* lvent;
     int32_t* lvmeta;
     uint16_t* lvqidx;
     uint16_t* lvkidx;
     uint16_t* lvcnt;
     int4* lvq;
-    float* lvT;
     float* lvP;
-    float* lvU;
     float* lvQ;
-    float* lvc;
+    float* lvY;
+    float* lvZ;
+    float* lvK;
 };
 constexpr int LEVEL_MAX_N = 4096;   // longest level row (16-bit list indices and counts)
 constexpr int LEVEL_MAX = 32;       // most levels (longest match) of a level row

@@ -16,14 +16,18 @@
 // Level lists are cut into segments of LEVEL_SEG entries.  level_seg_kernel forms, per
 // segment whose last group piece continues into the next segment, that piece's key sum T_s,
 // then per group the prefixes P (P_{s+1} = P_s + T_s, P_{s+1} = T_s where the group began in
-// segment s).  A query's M starts from its segment's P (when its group began in an earlier
-// segment) and adds the keys of its piece before it.  The key side mirrors this (U_s over a
-// segment's first piece, Q_{s-1} = Q_s + U_s, queries in descending order).
+// segment s).  level_scan_kernel then walks every segment with one wave: M starts from the
+// segment's P (when its first group began in an earlier segment), restarts at zero at each
+// group start, adds each key and is read by each query (its y_l, or z_l in the backward)
+// into a per-entry buffer.  The key side mirrors this (U_s over a segment's first piece,
+// Q_{s-1} = Q_s + U_s, the walk in descending order, dv_l and dk_l per key entry).  The
+// combine kernels then sum each query's (key's) levels in ascending order.
 //
-// Waves: one per query (forward, backward rows) or key (backward keys), lanes = value
-// columns (DV <= 128: CPL = 1 or 2 per lane); the segment lists are read with one vector
-// load and ballots.  Everything is a fixed fp32 sequence, restated by the oracle's
-// level_forward_row / level_backward_row (oracle/dism_cpu_model.c):
+// Lanes = value columns (DV <= 128: CPL = 1 or 2 per lane) in the walks: a segment's 32
+// entries are loaded at once (their rows by the entry's own lane, broadcast with readlane;
+// their value / gradient columns by every lane), then the walk runs in registers.
+// Everything is a fixed fp32 sequence, restated by the oracle's level_forward_row /
+// level_backward_row (oracle/dism_cpu_model.c):
 //   forward, query i: m = max(0, LUT[l] over the lengths present, n_l > n_{l+1});
 //     den = exp2(-m); for l = 1..Lq: den = fma(c_l, n_l, den);
 //     acc[d] = fma(c_l, y_l[d], acc[d]), y_l[d] = chain_r fma(sq[r], M[r][d]);
@@ -41,8 +45,10 @@
 
 namespace dism {
 
+constexpr int LV_SEG_THREADS = 1024;  // level_seg_kernel: one workgroup per (row, level)
 constexpr int LV_THREADS = 256;
-constexpr unsigned LV_GRID = 1024;  // persistent workgroups of the per-query / per-key kernels
+constexpr unsigned LV_GRID = 1024;    // persistent workgroups of the combine kernels
+constexpr int LV_MAX_SEGS = 2 * LEVEL_MAX_N / LEVEL_SEG;  // segments of one level list
 
 template <typename T>
 __device__ __forceinline__ float elem(const T* p) {
@@ -58,6 +64,29 @@ __device__ __forceinline__ float lane_tree(float x) {
     return x;
 }
 
+// N consecutive fp32 values (rows of N floats start at multiples of N floats)
+template <int N>
+__device__ __forceinline__ void store_f32_row_l(float* o, const float (&x)[N]) {
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (int c = 0; c < N / 4; ++c)
+            reinterpret_cast<float4*>(o)[c] = make_float4(x[4 * c], x[4 * c + 1], x[4 * c + 2],
+                                                          x[4 * c + 3]);
+    } else if constexpr (N % 2 == 0) {
+#pragma unroll
+        for (int c = 0; c < N / 2; ++c)
+            reinterpret_cast<float2*>(o)[c] = make_float2(x[2 * c], x[2 * c + 1]);
+    } else {
+#pragma unroll
+        for (int c = 0; c < N; ++c) o[c] = x[c];
+    }
+}
+
+__device__ __forceinline__ int rl(int x, int t) { return __builtin_amdgcn_readlane(x, t); }
+__device__ __forceinline__ float rlf(float x, int t) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), t));
+}
+
 // per-row views of the level state
 struct LvRow {
     const int32_t* ent;   // the row's kept entries, all levels
@@ -66,7 +95,7 @@ struct LvRow {
     const uint16_t* kidx;
     const uint16_t* cnt;
     int bh, b, h, n;
-    long so, row0;
+    long so, row0, ebase;  // ebase: the row's first entry slot (per-entry buffers)
     __device__ int off(int l) const { return meta[1 + l]; }           // level l+1 begins
     __device__ int segbase(int l) const { return meta[LEVEL_MAX + 2 + l]; }
 };
@@ -80,7 +109,8 @@ __device__ __forceinline__ LvRow lv_row(const PathArgs& a, int bh) {
     r.h = bh - r.b * a.H;
     r.so = (long)bh * n;
     r.row0 = (long)r.b * n * a.H + r.h;
-    r.ent = a.o.lvent + (long)bh * LEVEL_BUDGET * n;
+    r.ebase = (long)bh * LEVEL_BUDGET * n;
+    r.ent = a.o.lvent + r.ebase;
     r.meta = a.o.lvmeta + (long)bh * LEVEL_META;
     r.qidx = a.o.lvqidx + (long)bh * LEVEL_MAX * n;
     r.kidx = a.o.lvkidx + (long)bh * LEVEL_MAX * n;
@@ -88,59 +118,64 @@ __device__ __forceinline__ LvRow lv_row(const PathArgs& a, int bh) {
     return r;
 }
 
-// M (layout [r][column]) of the query at index x of a level list E (ml entries): from the
-// segment prefix Pl (this level's first segment) when its group began in an earlier segment,
-// plus its piece's keys before it.
+// One segment of a level list held by a wave: lane t < cnt holds entry t (ev with its
+// group-start flag, e without), its row (sk of a key, sq of a query) in rv, and for each
+// entry t every lane holds column lane + 64 c of its value row (keys) or gradient row
+// (queries), as `need` selects, in col[t][c].
 template <typename T, int R, int DV>
-__device__ __forceinline__ void query_m(const PathArgs& a, const LvRow& rw, const int32_t* E,
-                                        int ml, int x, const float* Pl, int lane,
-                                        float (&M)[R][(DV + 63) / 64]) {
-    constexpr int CPL = (DV + 63) / 64;
+struct SegData {
+    static constexpr int CPL = (DV + 63) / 64;
+    int ev, e, cnt;
+    float rv[R];
+    float col[LEVEL_SEG][CPL];
+};
+
+template <typename T, int R, int DV, bool KEYCOLS, bool QUERYCOLS>
+__device__ __forceinline__ void seg_load(const PathArgs& a, const LvRow& rw, const int32_t* E,
+                                         int ml, int beg, int lane, SegData<T, R, DV>& S) {
+    constexpr int CPL = SegData<T, R, DV>::CPL;
+    const T* sq = reinterpret_cast<const T*>(a.sq);
     const T* sk = reinterpret_cast<const T*>(a.sk);
     const T* v = reinterpret_cast<const T*>(a.v);
-    const int beg = x & ~(LEVEL_SEG - 1), xo = x - beg;
-    const int ev = (lane < LEVEL_SEG && beg + lane < ml) ? E[beg + lane] : 0;
-    const unsigned long long st = __ballot(lane <= xo && (ev & LEVEL_START));
-    unsigned long long km = __ballot(lane < xo && !(ev & 1));
-    bool cont = true;
-    if (st) {
-        const int ps = 63 - __clzll((long long)st);
-        km &= ~((1ull << ps) - 1ull);
-        cont = false;
-    }
+    const T* dout = reinterpret_cast<const T*>(a.dout);
+    S.cnt = ml - beg < LEVEL_SEG ? ml - beg : LEVEL_SEG;
+    const bool in = lane < S.cnt;
+    S.ev = in ? E[beg + lane] : 0;
+    S.e = S.ev & ~LEVEL_START;
+    const long row = rw.row0 + (long)(S.e >> 1) * a.H;
+    if (in) load_row<T, R>(((S.e & 1) ? sq : sk) + row * R, S.rv);
+    else
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-        const int col = lane + 64 * c;
+        for (int r = 0; r < R; ++r) S.rv[r] = 0.0f;
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            M[r][c] = (cont && col < DV)
-                          ? Pl[(long)(beg / LEVEL_SEG) * (R * DV) + r * DV + col] : 0.0f;
-    }
-    while (km) {
-        const int t = __builtin_ctzll(km);
-        km &= km - 1ull;
-        const int e = __builtin_amdgcn_readfirstlane(__shfl(ev, t)) & ~LEVEL_START;
-        const long krow = rw.row0 + (long)(e >> 1) * a.H;
-        float skr[R];
-        load_row<T, R>(sk + krow * R, skr);
+    for (int t = 0; t < LEVEL_SEG; ++t) {
+        const int et = rl(S.e, t);
+        const bool isq = et & 1;
+        const bool need = t < S.cnt && (isq ? QUERYCOLS : KEYCOLS);
+        const long rt = rw.row0 + (long)(et >> 1) * a.H;
+        const T* src = (isq ? dout : v) + rt * DV;
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
-            const int col = lane + 64 * c;
-            if (col < DV) {
-                const float vv = elem<T>(v + krow * DV + col);
-#pragma unroll
-                for (int r = 0; r < R; ++r) M[r][c] = __builtin_fmaf(skr[r], vv, M[r][c]);
-            }
+            const int cl = lane + 64 * c;
+            S.col[t][c] = (need && cl < DV) ? elem<T>(src + cl) : 0.0f;
         }
     }
 }
 
+// c_l of query position p (lse2 l2), level l: p_l - p_{l-1}
+__device__ __forceinline__ float level_c(const float* lut, int l, float l2) {
+    const float p = exp2_fp32(lut[l] - l2);
+    return l > 1 ? p - exp2_fp32(lut[l - 1] - l2) : p - 0.0f;
+}
+
 // ---------------------------------------------------------------------------------------
-// Segment totals and prefixes of one (level row, level): forward P over keys (KEYS false),
-// or the key side's c_l per query entry, U and Q (KEYS true).  Grid (B*H, LEVEL_MAX).
+// Segment totals and prefixes of one (level row, level): forward T / P over keys (KEYS
+// false), or the key side's U / Q over queries (KEYS true).  Grid (B*H, LEVEL_MAX).
 template <typename T, int R, int DV, bool KEYS>
-__global__ __launch_bounds__(LV_THREADS) void level_seg_kernel(PathArgs a) {
+__global__ __launch_bounds__(LV_SEG_THREADS) void level_seg_kernel(PathArgs a) {
     constexpr int CPL = (DV + 63) / 64, RD = R * DV;
+    constexpr int NW = LV_SEG_THREADS / 64;
+    __shared__ uint8_t s_any[LV_MAX_SEGS], s_first[LV_MAX_SEGS];
     const int BH = a.B * a.H;
     if ((int)blockIdx.x >= a.o.dcount[2]) return;
     const int bh = a.o.dlist[2 * BH + blockIdx.x];
@@ -148,36 +183,29 @@ __global__ __launch_bounds__(LV_THREADS) void level_seg_kernel(PathArgs a) {
     if (!a.hard[bh]) return;
     const LvRow rw = lv_row(a, bh);
     if (l > rw.meta[0]) return;
-    const int lane = lane_id(), w = wave_id(), tid = threadIdx.x;
+    const int lane = lane_id(), w = wave_id();
     const int o0 = rw.off(l - 1), ml = rw.off(l) - o0;
     const int nseg = (ml + LEVEL_SEG - 1) / LEVEL_SEG;
     const int32_t* E = rw.ent + o0;
     const long sbase = (long)bh * level_segs(a.n) + rw.segbase(l - 1);
-    const T* sq = reinterpret_cast<const T*>(a.sq);
-    const T* sk = reinterpret_cast<const T*>(a.sk);
-    const T* v = reinterpret_cast<const T*>(a.v);
-    const T* dout = reinterpret_cast<const T*>(a.dout);
-    float* tot = KEYS ? a.o.lvU : a.o.lvT;
-    float* pre = KEYS ? a.o.lvQ : a.o.lvP;
-    float* cl = a.o.lvc + (long)bh * LEVEL_BUDGET * a.n + o0;
+    // one buffer per direction: the totals, each overwritten by the prefix it produces once
+    // read (P_{s+1} into T_s's slot, Q_{s-1} into U_s's slot)
+    float* tot = KEYS ? a.o.lvQ : a.o.lvP;
+    float* pre = tot;
     const float* lut = a.lut + (long)rw.h * a.lut_stride;
-    if constexpr (KEYS) {
-        // c_l of every query entry of the level
-        for (int t = tid; t < ml; t += LV_THREADS) {
-            const int e = E[t] & ~LEVEL_START;
-            if (e & 1) {
-                const float l2 = a.lse2[rw.so + (e >> 1)];
-                const float p = exp2_fp32(lut[l] - l2);
-                cl[t] = l > 1 ? p - exp2_fp32(lut[l - 1] - l2) : p - 0.0f;
-            }
-        }
-        __syncthreads();
-    }
-    // ---- phase 1: totals of the pieces that cross a segment boundary
-    for (int s = w; s < nseg; s += LV_THREADS / 64) {
+    auto ix = [&](int seg, int r, int col) {
+        return (sbase + seg) * RD + (KEYS ? col * R + r : r * DV + col);
+    };
+    // ---- phase 1: segment flags; totals of the pieces that cross a segment boundary
+    for (int s = w; s < nseg; s += NW) {
         const int beg = s * LEVEL_SEG;
-        const int ev = (lane < LEVEL_SEG && beg + lane < ml) ? E[beg + lane] : 0;
-        const unsigned long long st = __ballot(lane < LEVEL_SEG && (ev & LEVEL_START));
+        SegData<T, R, DV> S;
+        seg_load<T, R, DV, !KEYS, KEYS>(a, rw, E, ml, beg, lane, S);
+        const unsigned long long st = __ballot(lane < S.cnt && (S.ev & LEVEL_START));
+        if (lane == 0) {
+            s_any[s] = st != 0ull;
+            s_first[s] = st & 1ull;
+        }
         float acc[R][CPL];
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -187,86 +215,61 @@ __global__ __launch_bounds__(LV_THREADS) void level_seg_kernel(PathArgs a) {
             // the last piece of s, when its group continues into s + 1
             if (s + 1 >= nseg || (E[beg + LEVEL_SEG] & LEVEL_START)) continue;
             const int ls = st ? 63 - __clzll((long long)st) : 0;
-            unsigned long long km = __ballot(lane >= ls && lane < LEVEL_SEG && !(ev & 1));
-            while (km) {
-                const int t = __builtin_ctzll(km);
-                km &= km - 1ull;
-                const int e = __builtin_amdgcn_readfirstlane(__shfl(ev, t)) & ~LEVEL_START;
-                const long krow = rw.row0 + (long)(e >> 1) * a.H;
-                float skr[R];
-                load_row<T, R>(sk + krow * R, skr);
 #pragma unroll
-                for (int c = 0; c < CPL; ++c) {
-                    const int col = lane + 64 * c;
-                    if (col < DV) {
-                        const float vv = elem<T>(v + krow * DV + col);
+            for (int t = 0; t < LEVEL_SEG; ++t) {
+                if (t >= ls && !(rl(S.e, t) & 1)) {
 #pragma unroll
-                        for (int r = 0; r < R; ++r)
-                            acc[r][c] = __builtin_fmaf(skr[r], vv, acc[r][c]);
+                    for (int r = 0; r < R; ++r) {
+                        const float x = rlf(S.rv[r], t);
+#pragma unroll
+                        for (int c = 0; c < CPL; ++c)
+                            acc[r][c] = __builtin_fmaf(x, S.col[t][c], acc[r][c]);
                     }
                 }
-            }
-#pragma unroll
-            for (int c = 0; c < CPL; ++c) {
-                const int col = lane + 64 * c;
-                if (col < DV)
-#pragma unroll
-                    for (int r = 0; r < R; ++r) tot[(sbase + s) * RD + r * DV + col] = acc[r][c];
             }
         } else {
             // the first piece of s, when its group began in an earlier segment
             if (s == 0 || (st & 1ull)) continue;
             const unsigned long long after = st & ~1ull;
-            const int fe = after ? __builtin_ctzll(after)
-                                 : (ml - beg < LEVEL_SEG ? ml - beg : LEVEL_SEG);
-            unsigned long long qm = __ballot(lane < fe && (ev & 1));
-            while (qm) {
-                const int t = 63 - __clzll((long long)qm);
-                qm &= ~(1ull << t);
-                const int e = __builtin_amdgcn_readfirstlane(__shfl(ev, t)) & ~LEVEL_START;
-                const long qrow = rw.row0 + (long)(e >> 1) * a.H;
-                const float c = cl[beg + t];
-                float ar[R];
-                load_row<T, R>(sq + qrow * R, ar);
+            const int fe = after ? __builtin_ctzll(after) : S.cnt;
+            float ar[R];
+            {
+                const bool isq = lane < S.cnt && (S.e & 1);
+                const float c = isq ? level_c(lut, l, a.lse2[rw.so + (S.e >> 1)]) : 0.0f;
 #pragma unroll
-                for (int r = 0; r < R; ++r) ar[r] = c * ar[r];
+                for (int r = 0; r < R; ++r) ar[r] = c * S.rv[r];
+            }
 #pragma unroll
-                for (int cc = 0; cc < CPL; ++cc) {
-                    const int col = lane + 64 * cc;
-                    if (col < DV) {
-                        const float dd = elem<T>(dout + qrow * DV + col);
+            for (int t = LEVEL_SEG - 1; t >= 0; --t) {
+                if (t < fe && (rl(S.e, t) & 1)) {
 #pragma unroll
-                        for (int r = 0; r < R; ++r)
-                            acc[r][cc] = __builtin_fmaf(ar[r], dd, acc[r][cc]);
+                    for (int r = 0; r < R; ++r) {
+                        const float x = rlf(ar[r], t);
+#pragma unroll
+                        for (int c = 0; c < CPL; ++c)
+                            acc[r][c] = __builtin_fmaf(x, S.col[t][c], acc[r][c]);
                     }
                 }
             }
+        }
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) {
-                const int col = lane + 64 * c;
-                if (col < DV)
+        for (int c = 0; c < CPL; ++c) {
+            const int col = lane + 64 * c;
+            if (col < DV)
 #pragma unroll
-                    for (int r = 0; r < R; ++r) tot[(sbase + s) * RD + col * R + r] = acc[r][c];
-            }
+                for (int r = 0; r < R; ++r) tot[ix(s, r, col)] = acc[r][c];
         }
     }
     __syncthreads();
     // ---- phase 2: one wave per chain of segments crossed by one group
-    for (int s = w; s < nseg; s += LV_THREADS / 64) {
-        const int beg = s * LEVEL_SEG;
-        const int ev = (lane < LEVEL_SEG && beg + lane < ml) ? E[beg + lane] : 0;
-        const unsigned long long st = __ballot(lane < LEVEL_SEG && (ev & LEVEL_START));
+    for (int s = w; s < nseg; s += NW) {
         float run[R][CPL];
-        auto add_tot = [&](int seg, bool first) {
+        auto load_tot = [&](int seg, float (&x)[R][CPL]) {
 #pragma unroll
             for (int c = 0; c < CPL; ++c) {
                 const int col = lane + 64 * c;
-                if (col < DV)
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        const long ix = (sbase + seg) * RD + (KEYS ? col * R + r : r * DV + col);
-                        run[r][c] = first ? tot[ix] : run[r][c] + tot[ix];
-                    }
+                for (int r = 0; r < R; ++r) x[r][c] = col < DV ? tot[ix(seg, r, col)] : 0.0f;
             }
         };
         auto store_pre = [&](int seg) {
@@ -275,56 +278,205 @@ __global__ __launch_bounds__(LV_THREADS) void level_seg_kernel(PathArgs a) {
                 const int col = lane + 64 * c;
                 if (col < DV)
 #pragma unroll
-                    for (int r = 0; r < R; ++r)
-                        pre[(sbase + seg) * RD + (KEYS ? col * R + r : r * DV + col)] = run[r][c];
+                    for (int r = 0; r < R; ++r) pre[ix(seg, r, col)] = run[r][c];
             }
-        };
-        // a segment holding no group start (the whole segment in one group)
-        auto inside = [&](int seg) {
-            const int b2 = seg * LEVEL_SEG;
-            const int e2 = (lane < LEVEL_SEG && b2 + lane < ml) ? E[b2 + lane] : 0;
-            return __ballot(lane < LEVEL_SEG && (e2 & LEVEL_START)) == 0ull;
         };
         if constexpr (!KEYS) {
-            // head: s holds a start and its last piece continues into s + 1
-            if (s + 1 >= nseg || (E[beg + LEVEL_SEG] & LEVEL_START) || !st) continue;
-            add_tot(s, true);
-            int t = s + 1;
-            store_pre(t);
-            while (t + 1 < nseg && !(E[(t + 1) * LEVEL_SEG] & LEVEL_START) && inside(t)) {
-                add_tot(t, false);
-                ++t;
-                store_pre(t);
+            // head: s holds a start and its last piece continues into s + 1; the chain runs
+            // on through the segments that hold no start
+            if (s + 1 >= nseg || s_first[s + 1] || !s_any[s]) continue;
+            int t1 = s + 1;
+            while (t1 + 1 < nseg && !s_first[t1 + 1] && !s_any[t1]) ++t1;
+            load_tot(s, run);
+            store_pre(s);  // P_{s+1}
+            for (int t = s + 1; t < t1; t += 4) {
+                float x[4][R][CPL];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (t + u < t1) load_tot(t + u, x[u]);
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (t + u < t1) {
+#pragma unroll
+                        for (int r = 0; r < R; ++r)
+#pragma unroll
+                            for (int c = 0; c < CPL; ++c) run[r][c] = run[r][c] + x[u][r][c];
+                        store_pre(t + u);  // P_{t+u+1}
+                    }
             }
         } else {
-            // head: s's first piece continues from s - 1, and s's group does not run through
-            // all of s into s + 1
-            if (s == 0 || (st & 1ull)) continue;
-            const bool through = !(st & ~1ull) && beg + LEVEL_SEG < ml &&
-                                 !(E[beg + LEVEL_SEG] & LEVEL_START);
-            if (through) continue;
-            add_tot(s, true);
-            int t = s - 1;
-            store_pre(t);
-            while (t >= 1 && inside(t)) {
-                add_tot(t, false);
-                --t;
-                store_pre(t);
+            // head: s's first piece continues from s - 1 and does not run through all of s
+            // into s + 1; the chain runs down through the segments that hold no start
+            if (s == 0 || s_first[s]) continue;
+            if (!s_any[s] && s + 1 < nseg && !s_first[s + 1]) continue;
+            int t1 = s - 1;
+            while (t1 >= 1 && !s_any[t1]) --t1;
+            load_tot(s, run);
+            store_pre(s);  // Q_{s-1}
+            for (int t = s - 1; t > t1; t -= 4) {
+                float x[4][R][CPL];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (t - u > t1) load_tot(t - u, x[u]);
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (t - u > t1) {
+#pragma unroll
+                        for (int r = 0; r < R; ++r)
+#pragma unroll
+                            for (int c = 0; c < CPL; ++c) run[r][c] = run[r][c] + x[u][r][c];
+                        store_pre(t - u);  // Q_{t-u-1}
+                    }
             }
         }
     }
 }
 
 // ---------------------------------------------------------------------------------------
-// forward: wave per query of the level rows
+// Segment walks: wave per (level row, segment of any level).  MODE 0: forward y_l per query
+// entry; 1: backward z_l per query entry; 2: backward dv_l, dk_l per key entry (descending).
+// Grid (B*H, ceil(level_segs(N) / 4)).
+template <typename T, int R, int DV, int MODE>
+__global__ __launch_bounds__(LV_THREADS) void level_scan_kernel(PathArgs a) {
+    constexpr int CPL = (DV + 63) / 64, RD = R * DV;
+    const int BH = a.B * a.H;
+    if ((int)blockIdx.x >= a.o.dcount[2]) return;
+    const int bh = __builtin_amdgcn_readfirstlane(a.o.dlist[2 * BH + blockIdx.x]);
+    if (!a.hard[bh]) return;
+    const LvRow rw = lv_row(a, bh);
+    const int nlev = rw.meta[0];
+    const int g = (int)blockIdx.y * (LV_THREADS / 64) + wave_id();
+    if (g >= rw.segbase(nlev)) return;
+    int l = 1;
+    while (rw.segbase(l) <= g) ++l;
+    const int lane = lane_id();
+    const int o0 = rw.off(l - 1), ml = rw.off(l) - o0;
+    const int s = g - rw.segbase(l - 1), beg = s * LEVEL_SEG;
+    const int32_t* E = rw.ent + o0;
+    const long sb = (long)bh * level_segs(a.n) + g;
+    const long eb = rw.ebase + o0 + beg;  // per-entry buffer slot of entry 0
+    SegData<T, R, DV> S;
+    seg_load<T, R, DV, true, MODE != 0>(a, rw, E, ml, beg, lane, S);
+    float M[R][CPL];
+    if constexpr (MODE != 2) {
+        const bool cont = !(rl(S.ev, 0) & LEVEL_START);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int col = lane + 64 * c;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                M[r][c] = (cont && col < DV) ? a.o.lvP[(sb - 1) * RD + r * DV + col] : 0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < LEVEL_SEG; ++t) {
+            if (t < S.cnt) {
+                const int ev = rl(S.ev, t);
+                if (t > 0 && (ev & LEVEL_START))
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+#pragma unroll
+                        for (int c = 0; c < CPL; ++c) M[r][c] = 0.0f;
+                if (!(ev & 1)) {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const float x = rlf(S.rv[r], t);
+#pragma unroll
+                        for (int c = 0; c < CPL; ++c)
+                            M[r][c] = __builtin_fmaf(x, S.col[t][c], M[r][c]);
+                    }
+                } else if constexpr (MODE == 0) {
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) {
+                        float y = 0.0f;
+#pragma unroll
+                        for (int r = 0; r < R; ++r) y = __builtin_fmaf(rlf(S.rv[r], t), M[r][c], y);
+                        const int col = lane + 64 * c;
+                        if (col < DV) a.o.lvY[(eb + t) * DV + col] = y;
+                    }
+                } else {
+                    float z[R];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float p = lane < DV ? S.col[t][0] * M[r][0] : 0.0f;
+                        if (CPL > 1 && lane + 64 < DV)
+                            p = __builtin_fmaf(S.col[t][CPL - 1], M[r][CPL - 1], p);
+                        z[r] = lane_tree(p);
+                    }
+                    if (lane == 0)
+#pragma unroll
+                        for (int r = 0; r < R; ++r) a.o.lvZ[(eb + t) * R + r] = z[r];
+                }
+            }
+        }
+    } else {
+        const float* lut = a.lut + (long)rw.h * a.lut_stride;
+        float ar[R];
+        {
+            const bool isq = lane < S.cnt && (S.e & 1);
+            const float c = isq ? level_c(lut, l, a.lse2[rw.so + (S.e >> 1)]) : 0.0f;
+#pragma unroll
+            for (int r = 0; r < R; ++r) ar[r] = c * S.rv[r];
+        }
+        const bool cont = beg + LEVEL_SEG < ml && !(E[beg + LEVEL_SEG] & LEVEL_START);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int col = lane + 64 * c;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                M[r][c] = (cont && col < DV) ? a.o.lvQ[(sb + 1) * RD + col * R + r] : 0.0f;
+        }
+#pragma unroll
+        for (int t = LEVEL_SEG - 1; t >= 0; --t) {
+            if (t < S.cnt) {
+                if (t + 1 < S.cnt && (rl(S.ev, t + 1) & LEVEL_START))
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+#pragma unroll
+                        for (int c = 0; c < CPL; ++c) M[r][c] = 0.0f;
+                const int ev = rl(S.ev, t);
+                if (ev & 1) {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const float x = rlf(ar[r], t);
+#pragma unroll
+                        for (int c = 0; c < CPL; ++c)
+                            M[r][c] = __builtin_fmaf(x, S.col[t][c], M[r][c]);
+                    }
+                } else {
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) {
+                        float y = 0.0f;
+#pragma unroll
+                        for (int r = 0; r < R; ++r) y = __builtin_fmaf(rlf(S.rv[r], t), M[r][c], y);
+                        const int col = lane + 64 * c;
+                        if (col < DV) a.o.lvY[(eb + t) * DV + col] = y;
+                    }
+                    float dk[R];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float p = lane < DV ? S.col[t][0] * M[r][0] : 0.0f;
+                        if (CPL > 1 && lane + 64 < DV)
+                            p = __builtin_fmaf(S.col[t][CPL - 1], M[r][CPL - 1], p);
+                        dk[r] = lane_tree(p);
+                    }
+                    if (lane == 0)
+#pragma unroll
+                        for (int r = 0; r < R; ++r) a.o.lvK[(eb + t) * R + r] = dk[r];
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// forward combine: wave per query (lanes = columns)
 template <typename T, int R, int DV>
-__global__ __launch_bounds__(LV_THREADS) void level_forward_kernel(PathArgs a) {
+__global__ __launch_bounds__(LV_THREADS) void level_fcombine_kernel(PathArgs a) {
     constexpr int CPL = (DV + 63) / 64;
     const int BH = a.B * a.H, n = a.n, lane = lane_id();
     const int cnt = __builtin_amdgcn_readfirstlane(a.o.dcount[2]);
     const long items = (long)cnt * n;
     const long nw = (long)gridDim.x * (LV_THREADS / 64);
-    const T* sq = reinterpret_cast<const T*>(a.sq);
     for (long x = (long)blockIdx.x * (LV_THREADS / 64) + wave_id(); x < items; x += nw) {
         const int bh = __builtin_amdgcn_readfirstlane(a.o.dlist[2 * BH + (int)(x / n)]);
         const int i = (int)(x % n);
@@ -343,28 +495,34 @@ __global__ __launch_bounds__(LV_THREADS) void level_forward_kernel(PathArgs a) {
                 if (lw > m) m = lw;
             }
         }
-        float sqr[R];
-        load_row<T, R>(sq + (rw.row0 + (long)i * a.H) * R, sqr);
         float den = exp2_fp32(-m), pp = 0.0f, acc[CPL];
 #pragma unroll
         for (int c = 0; c < CPL; ++c) acc[c] = 0.0f;
-        const float* P = a.o.lvP + (long)bh * level_segs(n) * (R * DV);
-        for (int l = 1; l <= Lq; ++l) {
-            const float p = exp2_fp32(lut[l] - m);
-            const float c = p - pp;
-            pp = p;
-            den = __builtin_fmaf(c, (float)cn[(long)(l - 1) * n], den);
-            const int o0 = rw.off(l - 1);
-            float M[R][CPL];
-            query_m<T, R, DV>(a, rw, rw.ent + o0, rw.off(l) - o0,
-                              rw.qidx[(long)(l - 1) * n + i],
-                              P + (long)rw.segbase(l - 1) * (R * DV), lane, M);
+        for (int l0 = 1; l0 <= Lq; l0 += 4) {
+            float y[4][CPL];
 #pragma unroll
-            for (int cc = 0; cc < CPL; ++cc) {
-                float y = 0.0f;
+            for (int u = 0; u < 4; ++u) {
+                const int l = l0 + u;
+                if (l <= Lq) {
+                    const long ei = rw.ebase + rw.off(l - 1) + rw.qidx[(long)(l - 1) * n + i];
 #pragma unroll
-                for (int r = 0; r < R; ++r) y = __builtin_fmaf(sqr[r], M[r][cc], y);
-                acc[cc] = __builtin_fmaf(c, y, acc[cc]);
+                    for (int c = 0; c < CPL; ++c) {
+                        const int col = lane + 64 * c;
+                        y[u][c] = col < DV ? a.o.lvY[ei * DV + col] : 0.0f;
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int l = l0 + u;
+                if (l <= Lq) {
+                    const float p = exp2_fp32(lut[l] - m);
+                    const float c = p - pp;
+                    pp = p;
+                    den = __builtin_fmaf(c, (float)cn[(long)(l - 1) * n], den);
+#pragma unroll
+                    for (int cc = 0; cc < CPL; ++cc) acc[cc] = __builtin_fmaf(c, y[u][cc], acc[cc]);
+                }
             }
         }
         const long orow = (rw.row0 + (long)i * a.H) * DV;
@@ -387,59 +545,41 @@ __global__ __launch_bounds__(LV_THREADS) void level_forward_kernel(PathArgs a) {
     }
 }
 
-// ---------------------------------------------------------------------------------------
-// backward, query rows (dSQ, rowtau): wave per query
+// backward rows combine: lane per query
 template <typename T, int R, int DV>
-__global__ __launch_bounds__(LV_THREADS) void level_rows_kernel(PathArgs a) {
-    constexpr int CPL = (DV + 63) / 64;
-    const int BH = a.B * a.H, n = a.n, lane = lane_id();
+__global__ __launch_bounds__(LV_THREADS) void level_rcombine_kernel(PathArgs a) {
+    const int BH = a.B * a.H, n = a.n;
     const int cnt = __builtin_amdgcn_readfirstlane(a.o.dcount[2]);
     const long items = (long)cnt * n;
-    const long nw = (long)gridDim.x * (LV_THREADS / 64);
     const T* sq = reinterpret_cast<const T*>(a.sq);
-    const T* dout = reinterpret_cast<const T*>(a.dout);
-    for (long x = (long)blockIdx.x * (LV_THREADS / 64) + wave_id(); x < items; x += nw) {
-        const int bh = __builtin_amdgcn_readfirstlane(a.o.dlist[2 * BH + (int)(x / n)]);
+    for (long x = (long)blockIdx.x * LV_THREADS + threadIdx.x; x < items;
+         x += (long)gridDim.x * LV_THREADS) {
+        const int bh = a.o.dlist[2 * BH + (int)(x / n)];
         const int i = (int)(x % n);
         if (!a.hard[bh]) continue;
         const LvRow rw = lv_row(a, bh);
-        const int Lq = __builtin_amdgcn_readfirstlane(a.o.lvq[rw.so + i].x);
+        const int Lq = a.o.lvq[rw.so + i].x;
         const float* lut = a.lut + (long)rw.h * a.lut_stride;
         const float* glut = a.dlut + (long)rw.h * a.lut_stride;
         const uint16_t* cn = rw.cnt + i;
         const long qrow = rw.row0 + (long)i * a.H;
-        float sqr[R], dor[CPL];
+        float sqr[R];
         load_row<T, R>(sq + qrow * R, sqr);
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            const int col = lane + 64 * c;
-            dor[c] = col < DV ? elem<T>(dout + qrow * DV + col) : 0.0f;
-        }
         const float l2 = a.lse2[rw.so + i];
         const float cc = glut[i + 1];
         float u = 0.0f, vv = 0.0f, ww = 0.0f, z = 0.0f, pp = 0.0f, fp = 0.0f, dq[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) dq[r] = 0.0f;
-        const float* P = a.o.lvP + (long)bh * level_segs(n) * (R * DV);
         for (int l = 1; l <= Lq; ++l) {
+            const long ei = rw.ebase + rw.off(l - 1) + rw.qidx[(long)(l - 1) * n + i];
+            float zl[R];
+            load_row<float, R>(a.o.lvZ + ei * R, zl);
             const float p = exp2_fp32(lut[l] - l2);
             const float c = p - pp;
             const float F = p * (glut[l] - cc);
             const float dF = F - fp;
             pp = p;
             fp = F;
-            const int o0 = rw.off(l - 1);
-            float M[R][CPL];
-            query_m<T, R, DV>(a, rw, rw.ent + o0, rw.off(l) - o0,
-                              rw.qidx[(long)(l - 1) * n + i],
-                              P + (long)rw.segbase(l - 1) * (R * DV), lane, M);
-            float zl[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float t = lane < DV ? dor[0] * M[r][0] : 0.0f;
-                if (CPL > 1 && lane + 64 < DV) t = __builtin_fmaf(dor[CPL - 1], M[r][CPL - 1], t);
-                zl[r] = lane_tree(t);
-            }
             float wl = 0.0f;
 #pragma unroll
             for (int r = 0; r < R; ++r) wl = __builtin_fmaf(sqr[r], zl[r], wl);
@@ -451,111 +591,66 @@ __global__ __launch_bounds__(LV_THREADS) void level_rows_kernel(PathArgs a) {
             ww = __builtin_fmaf(dF, wl, ww);
             z = __builtin_fmaf(c, fn, z);
         }
-        if (lane == 0) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) a.dsq[qrow * R + r] = dq[r];
-            const float f = exp2_fp32(-l2);
-            const float mass = z + f;
-            const float mean = __builtin_fmaf(-f, cc, vv) / mass;
-            a.rowtau[rw.so + i] = __builtin_fmaf(-u, mean, ww) / mass;
-        }
+        store_f32_row_l<R>(a.dsq + qrow * R, dq);
+        const float f = exp2_fp32(-l2);
+        const float mass = z + f;
+        const float mean = __builtin_fmaf(-f, cc, vv) / mass;
+        a.rowtau[rw.so + i] = __builtin_fmaf(-u, mean, ww) / mass;
     }
 }
 
-// ---------------------------------------------------------------------------------------
-// backward, keys (dSK, dV): wave per key
+// backward keys combine: wave per key (lanes = columns)
 template <typename T, int R, int DV>
-__global__ __launch_bounds__(LV_THREADS) void level_keys_kernel(PathArgs a) {
+__global__ __launch_bounds__(LV_THREADS) void level_kcombine_kernel(PathArgs a) {
     constexpr int CPL = (DV + 63) / 64;
     const int BH = a.B * a.H, n = a.n, lane = lane_id();
     const int cnt = __builtin_amdgcn_readfirstlane(a.o.dcount[2]);
     const long items = (long)cnt * n;
     const long nw = (long)gridDim.x * (LV_THREADS / 64);
-    const T* sq = reinterpret_cast<const T*>(a.sq);
-    const T* sk = reinterpret_cast<const T*>(a.sk);
-    const T* v = reinterpret_cast<const T*>(a.v);
-    const T* dout = reinterpret_cast<const T*>(a.dout);
     for (long x = (long)blockIdx.x * (LV_THREADS / 64) + wave_id(); x < items; x += nw) {
         const int bh = __builtin_amdgcn_readfirstlane(a.o.dlist[2 * BH + (int)(x / n)]);
         const int j = (int)(x % n);
         if (!a.hard[bh]) continue;
         const LvRow rw = lv_row(a, bh);
         const int Kk = __builtin_amdgcn_readfirstlane(a.o.lvq[rw.so + j].w);
-        const long krow = rw.row0 + (long)j * a.H;
-        float skr[R], vr[CPL], dvv[CPL], dk[R];
-        load_row<T, R>(sk + krow * R, skr);
+        float dvv[CPL], dk[R];
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            const int col = lane + 64 * c;
-            vr[c] = col < DV ? elem<T>(v + krow * DV + col) : 0.0f;
-            dvv[c] = 0.0f;
-        }
+        for (int c = 0; c < CPL; ++c) dvv[c] = 0.0f;
 #pragma unroll
         for (int r = 0; r < R; ++r) dk[r] = 0.0f;
-        const float* Q = a.o.lvQ + (long)bh * level_segs(n) * (R * DV);
-        for (int l = 1; l <= Kk; ++l) {
-            const int o0 = rw.off(l - 1), ml = rw.off(l) - o0;
-            const int32_t* E = rw.ent + o0;
-            const float* cl = a.o.lvc + (long)bh * LEVEL_BUDGET * n + o0;
-            const int xk = rw.kidx[(long)(l - 1) * n + j];
-            const int beg = xk & ~(LEVEL_SEG - 1), xo = xk - beg;
-            const int ev = (lane < LEVEL_SEG && beg + lane < ml) ? E[beg + lane] : 0;
-            const unsigned long long stm = __ballot(lane > xo && (ev & LEVEL_START));
-            const int pe = stm ? __builtin_ctzll(stm)
-                               : (ml - beg < LEVEL_SEG ? ml - beg : LEVEL_SEG);
-            const bool cont = !stm && beg + LEVEL_SEG < ml && !(E[beg + LEVEL_SEG] & LEVEL_START);
-            unsigned long long qm = __ballot(lane > xo && lane < pe && (ev & 1));
-            float K[R][CPL];
-            const float* Qs = Q + ((long)rw.segbase(l - 1) + beg / LEVEL_SEG) * (R * DV);
+        for (int l0 = 1; l0 <= Kk; l0 += 4) {
+            float y[4][CPL], d[4][R];
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) {
-                const int col = lane + 64 * c;
+            for (int u = 0; u < 4; ++u) {
+                const int l = l0 + u;
+                if (l <= Kk) {
+                    const long ei = rw.ebase + rw.off(l - 1) + rw.kidx[(long)(l - 1) * n + j];
 #pragma unroll
-                for (int r = 0; r < R; ++r) K[r][c] = (cont && col < DV) ? Qs[col * R + r] : 0.0f;
-            }
-            while (qm) {
-                const int t = 63 - __clzll((long long)qm);
-                qm &= ~(1ull << t);
-                const int e = __builtin_amdgcn_readfirstlane(__shfl(ev, t)) & ~LEVEL_START;
-                const long qrow = rw.row0 + (long)(e >> 1) * a.H;
-                const float c = cl[beg + t];
-                float ar[R];
-                load_row<T, R>(sq + qrow * R, ar);
-#pragma unroll
-                for (int r = 0; r < R; ++r) ar[r] = c * ar[r];
-#pragma unroll
-                for (int cc = 0; cc < CPL; ++cc) {
-                    const int col = lane + 64 * cc;
-                    if (col < DV) {
-                        const float dd = elem<T>(dout + qrow * DV + col);
-#pragma unroll
-                        for (int r = 0; r < R; ++r) K[r][cc] = __builtin_fmaf(ar[r], dd, K[r][cc]);
+                    for (int c = 0; c < CPL; ++c) {
+                        const int col = lane + 64 * c;
+                        y[u][c] = col < DV ? a.o.lvY[ei * DV + col] : 0.0f;
                     }
+                    load_row<float, R>(a.o.lvK + ei * R, d[u]);
                 }
             }
 #pragma unroll
-            for (int cc = 0; cc < CPL; ++cc) {
-                float y = 0.0f;
+            for (int u = 0; u < 4; ++u) {
+                const int l = l0 + u;
+                if (l <= Kk) {
 #pragma unroll
-                for (int r = 0; r < R; ++r) y = __builtin_fmaf(skr[r], K[r][cc], y);
-                dvv[cc] = l == 1 ? y : dvv[cc] + y;
-            }
+                    for (int c = 0; c < CPL; ++c) dvv[c] = l == 1 ? y[u][c] : dvv[c] + y[u][c];
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float t = lane < DV ? vr[0] * K[r][0] : 0.0f;
-                if (CPL > 1 && lane + 64 < DV) t = __builtin_fmaf(vr[CPL - 1], K[r][CPL - 1], t);
-                const float d = lane_tree(t);
-                dk[r] = l == 1 ? d : dk[r] + d;
+                    for (int r = 0; r < R; ++r) dk[r] = l == 1 ? d[u][r] : dk[r] + d[u][r];
+                }
             }
         }
+        const long krow = rw.row0 + (long)j * a.H;
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
             const int col = lane + 64 * c;
             if (col < DV) a.dv[krow * DV + col] = dvv[c];
         }
-        if (lane == 0)
-#pragma unroll
-            for (int r = 0; r < R; ++r) a.dsk[krow * R + r] = dk[r];
+        if (lane == 0) store_f32_row_l<R>(a.dsk + krow * R, dk);
     }
 }
 
@@ -563,19 +658,24 @@ __global__ __launch_bounds__(LV_THREADS) void level_keys_kernel(PathArgs a) {
 // launchers: (R, DV) pairs with R * DV <= LEVEL_RDV (other shapes never have level rows)
 template <typename T, int R, int DV>
 static hipError_t level_go(const PathArgs& a, int which, hipStream_t s) {
-    const dim3 sg((unsigned)(a.B * a.H), LEVEL_MAX);
+    const unsigned BH = (unsigned)(a.B * a.H);
+    const dim3 sg(BH, LEVEL_MAX);
+    const dim3 wg(BH, (unsigned)((level_segs(a.n) + 3) / 4));
     if (which == 0) {
-        hipLaunchKernelGGL((level_seg_kernel<T, R, DV, false>), sg, dim3(LV_THREADS), 0, s, a);
-        hipLaunchKernelGGL((level_forward_kernel<T, R, DV>), dim3(LV_GRID), dim3(LV_THREADS), 0,
+        hipLaunchKernelGGL((level_seg_kernel<T, R, DV, false>), sg, dim3(LV_SEG_THREADS), 0, s, a);
+        hipLaunchKernelGGL((level_scan_kernel<T, R, DV, 0>), wg, dim3(LV_THREADS), 0, s, a);
+        hipLaunchKernelGGL((level_fcombine_kernel<T, R, DV>), dim3(LV_GRID), dim3(LV_THREADS), 0,
                            s, a);
     } else if (which == 1) {
-        hipLaunchKernelGGL((level_seg_kernel<T, R, DV, false>), sg, dim3(LV_THREADS), 0, s, a);
-        hipLaunchKernelGGL((level_rows_kernel<T, R, DV>), dim3(LV_GRID), dim3(LV_THREADS), 0, s,
-                           a);
+        hipLaunchKernelGGL((level_seg_kernel<T, R, DV, false>), sg, dim3(LV_SEG_THREADS), 0, s, a);
+        hipLaunchKernelGGL((level_scan_kernel<T, R, DV, 1>), wg, dim3(LV_THREADS), 0, s, a);
+        hipLaunchKernelGGL((level_rcombine_kernel<T, R, DV>), dim3(LV_GRID / 4), dim3(LV_THREADS),
+                           0, s, a);
     } else {
-        hipLaunchKernelGGL((level_seg_kernel<T, R, DV, true>), sg, dim3(LV_THREADS), 0, s, a);
-        hipLaunchKernelGGL((level_keys_kernel<T, R, DV>), dim3(LV_GRID), dim3(LV_THREADS), 0, s,
-                           a);
+        hipLaunchKernelGGL((level_seg_kernel<T, R, DV, true>), sg, dim3(LV_SEG_THREADS), 0, s, a);
+        hipLaunchKernelGGL((level_scan_kernel<T, R, DV, 2>), wg, dim3(LV_THREADS), 0, s, a);
+        hipLaunchKernelGGL((level_kcombine_kernel<T, R, DV>), dim3(LV_GRID), dim3(LV_THREADS), 0,
+                           s, a);
     }
     return hipGetLastError();
 }

@@ -767,14 +767,15 @@ hipError_t launch_ctab_balance(const SortArgs& a, hipStream_t s) {
 // Level lists (one 1024-thread workgroup per dense row, after the classification; rows of
 // N <= LEVEL_MAX_N whose labels are all below 256, fixed-length calls without resets).
 // Level l's list is the previous level's kept list without its entries at p = l - 2, stably
-// sorted by label[p - l + 1] (an lds_pass over the entries' labels, staged in LDS as bytes:
-// entry e's digit at level l is s_lab[e - 2(l - 1)]).  A group (equal digit and equal
-// previous group) is kept when one of its queries has a key before it.  Per level a block
-// scan gives every entry its group start, the keys before it in the group and the last of
-// them; kept groups are compacted (block scan) into the next level's input and written out
-// with the per-position indices and counts.  The row becomes mode 3 when a level keeps
-// nothing within LEVEL_MAX levels and LEVEL_BUDGET * N kept entries; otherwise it stays a
-// mode-1 (tile) row.  The oracle's levels_build computes the same lists.
+// sorted by label[p - l + 1] (entry e's digit at level l is s_lab[e - 2(l - 1)], the labels
+// staged in LDS as bytes).  A group (equal digit and equal previous group) is kept when one
+// of its queries has a key before it.  Per level: the stable partition by digit (ballot
+// ranks for labels below 16, lds_pass otherwise), one block scan for every entry's group
+// start, keys before it in the group and the last of them, the keep flags, one block scan for
+// the kept entries (written out with the per-position indices and counts) and the next
+// level's input (kept, p >= l).  The row becomes mode 3 when a level keeps nothing within
+// LEVEL_MAX levels and LEVEL_BUDGET * N kept entries; otherwise it stays a mode-1 (tile)
+// row.  The oracle's levels_build computes the same lists.
 namespace {
 struct LvAgg {  // segmented aggregate of a run of list entries
     int f, cnt, lk, gs;  // a group start inside; keys / last key position after the last
@@ -783,6 +784,52 @@ struct LvAgg {  // segmented aggregate of a run of list entries
 __device__ __forceinline__ LvAgg lv_op(LvAgg a, LvAgg b) {
     return LvAgg{a.f | b.f, b.f ? b.cnt : a.cnt + b.cnt, b.f || b.lk >= 0 ? b.lk : a.lk,
                  b.gs >= 0 ? b.gs : a.gs};
+}
+
+// Stable counting pass over m elements with digits below nd <= 16 (per-wave contiguous
+// segments; ranks inside a 64-element group from one ballot per digit value).
+template <typename Dig, typename Emit>
+__device__ void small_pass(int m, int nd, Dig digit, Emit emit, int (*wcnt)[16], int* base_of) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int seg = ((m + SORT_WAVES - 1) / SORT_WAVES + 63) / 64 * 64;
+    const int beg = wave * seg;
+    const int end = beg + seg < m ? beg + seg : m;
+    const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    int cnt = 0;  // lane d < nd: this wave's count of digit d
+    for (int x0 = beg; x0 < end; x0 += 64) {
+        const int x = x0 + lane;
+        const int dg = x < end ? digit(x) : 16;
+        for (int d = 0; d < nd; ++d) {
+            const int c = __popcll(__ballot(dg == d));
+            if (lane == d) cnt += c;
+        }
+    }
+    if (lane < 16) wcnt[wave][lane] = cnt;
+    __syncthreads();
+    if (tid < 16) {  // exclusive scan over (digit, wave) into base_of[wave * 16 + digit]
+        int run = 0;
+        for (int d = 0; d < tid; ++d)
+            for (int w = 0; w < SORT_WAVES; ++w) run += wcnt[w][d];
+        for (int w = 0; w < SORT_WAVES; ++w) {
+            base_of[w * 16 + tid] = run;
+            run += wcnt[w][tid];
+        }
+    }
+    __syncthreads();
+    int base = lane < 16 ? base_of[wave * 16 + lane] : 0;
+    for (int x0 = beg; x0 < end; x0 += 64) {
+        const int x = x0 + lane;
+        const int dg = x < end ? digit(x) : 16;
+        int dst = 0;
+        for (int d = 0; d < nd; ++d) {
+            const unsigned long long mk = __ballot(dg == d);
+            const int bd = __shfl(base, d);
+            if (dg == d) dst = bd + __popcll(mk & below);
+            if (lane == d) base += __popcll(mk);
+        }
+        if (x < end) emit(x, dst);
+    }
+    __syncthreads();
 }
 }  // namespace
 
@@ -796,8 +843,8 @@ __global__ __launch_bounds__(SORT_THREADS) void level_prep_kernel(PathArgs a) {
     __shared__ int scan[RADIX];
     __shared__ unsigned long long lmask[SORT_WAVES][RADIX];
     __shared__ LvAgg s_agg[SORT_WAVES];
-    __shared__ int s_cnt[SORT_WAVES];
-    __shared__ int s_bad;
+    __shared__ Cnt4 s_c4[SORT_WAVES];
+    __shared__ uint32_t s_or;
     // nv: the positions the lists take (a prefill's padding after them never pairs with
     // them: its keys come after every real query)
     const int bh = blockIdx.x, tid = threadIdx.x, n = a.n;
@@ -806,12 +853,12 @@ __global__ __launch_bounds__(SORT_THREADS) void level_prep_kernel(PathArgs a) {
     const long so = (long)bh * n;
     const int32_t* q = a.iq + so;
     const int32_t* k = a.ik + so;
-    if (tid == 0) s_bad = 0;
+    if (tid == 0) s_or = 0;
     __syncthreads();
-    int bad = 0;
+    uint32_t orv = 0;
     for (int p = tid; p < nv; p += SORT_THREADS) {
         const uint32_t lq = (uint32_t)q[p], lk = (uint32_t)k[p];
-        bad |= (lq >= 256u) | (lk >= 256u);
+        orv |= lq | lk;
         s_lab[2 * p] = (uint8_t)lk;
         s_lab[2 * p + 1] = (uint8_t)lq;
         s_e[0][2 * p] = (uint16_t)(2 * p);
@@ -819,9 +866,13 @@ __global__ __launch_bounds__(SORT_THREADS) void level_prep_kernel(PathArgs a) {
         s_g[0][2 * p] = 0;
         s_g[0][2 * p + 1] = 0;
     }
-    if (bad) atomicOr(&s_bad, 1);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) orv |= (uint32_t)__shfl_xor((int)orv, o);
+    if ((tid & 63) == 0 && orv) atomicOr(&s_or, orv);
     __syncthreads();
-    if (s_bad) return;
+    const uint32_t used = s_or;
+    if (used >= 256u) return;   // labels of more than one byte: not a level row
+    const int nd = used < 16u ? (int)used + 1 : 0;  // small alphabet: ballot ranks (max < nd)
     int32_t* ent = a.o.lvent + (long)bh * LEVEL_BUDGET * n;
     int32_t* meta = a.o.lvmeta + (long)bh * LEVEL_META;
     uint16_t* qidx = a.o.lvqidx + (long)bh * LEVEL_MAX * n;
@@ -829,8 +880,10 @@ __global__ __launch_bounds__(SORT_THREADS) void level_prep_kernel(PathArgs a) {
     uint16_t* qcnt = a.o.lvcnt + (long)bh * LEVEL_MAX * n;
     int4* lq = a.o.lvq + so;
     for (int p = tid; p < n; p += SORT_THREADS) lq[p] = make_int4(0, -1, 0, 0);
-    auto shi = [](int v, int l) { return __shfl(v, l); };
-    auto add = [](int x, int y) { return x + y; };
+    auto sh4 = [](Cnt4 v, int l) {
+        return Cnt4{__shfl(v.x, l), __shfl(v.y, l), __shfl(v.z, l), __shfl(v.w, l)};
+    };
+    auto add4 = [](Cnt4 p, Cnt4 r) { return Cnt4{p.x + r.x, p.y + r.y, p.z + r.z, p.w + r.w}; };
     auto sha = [](LvAgg v, int l) {
         return LvAgg{__shfl(v.f, l), __shfl(v.cnt, l), __shfl(v.lk, l), __shfl(v.gs, l)};
     };
@@ -841,92 +894,78 @@ __global__ __launch_bounds__(SORT_THREADS) void level_prep_kernel(PathArgs a) {
     }
     for (int l = 1; l <= LEVEL_MAX + 1; ++l) {
         const int oth = cur ^ 1;
-        // ---- drop the entries at p < l - 1 (order kept): cur -> oth
-        const int ept = (m + SORT_THREADS - 1) / SORT_THREADS;
-        int c0 = tid * ept, c1 = c0 + ept < m ? c0 + ept : m;
-        int keepn = 0;
-        for (int c = c0; c < c1; ++c) keepn += (s_e[cur][c] >> 1) >= l - 1;
-        int mi;
-        int base = block_exscan(keepn, add, 0, shi, s_cnt, false, &mi);
-        for (int c = c0; c < c1; ++c) {
-            const int e = s_e[cur][c];
-            if ((e >> 1) >= l - 1) {
-                s_e[oth][base] = (uint16_t)e;
-                s_g[oth][base] = s_g[cur][c];
-                ++base;
-            }
-        }
-        __syncthreads();
-        // ---- stable sort by label[p - l + 1]: oth -> cur
         const int sh = 2 * (l - 1);
-        lds_pass(
-            mi, [&](int x) { return (int)s_lab[s_e[oth][x] - sh]; },
-            [&](int x, int dst) {
-                s_e[cur][dst] = s_e[oth][x];
-                s_g[cur][dst] = s_g[oth][x];
-            },
-            nullptr, wcnt, scan, lmask);
+        for (int c = tid; c < m; c += SORT_THREADS) s_keep[c] = 0;
+        // ---- stable partition by label[p - l + 1]: cur -> oth
+        auto dig = [&](int x) { return (int)s_lab[s_e[cur][x] - sh]; };
+        auto emit = [&](int x, int dst) {
+            s_e[oth][dst] = s_e[cur][x];
+            s_g[oth][dst] = s_g[cur][x];
+        };
+        if (nd) small_pass(m, nd, dig, emit, reinterpret_cast<int (*)[16]>(&wcnt[0][0]), scan);
+        else lds_pass(m, dig, emit, nullptr, wcnt, scan, lmask);
         // ---- groups: start, keys before, last key; keep flags
-        const int ept2 = (mi + SORT_THREADS - 1) / SORT_THREADS;
-        c0 = tid * ept2;
-        c1 = c0 + ept2 < mi ? c0 + ept2 : mi;
+        const int ept = (m + SORT_THREADS - 1) / SORT_THREADS;
+        const int c0 = tid * ept, c1 = c0 + ept < m ? c0 + ept : m;
         auto is_start = [&](int c) {
             if (c == 0) return true;
-            const int e = s_e[cur][c], f = s_e[cur][c - 1];
-            return s_lab[e - sh] != s_lab[f - sh] || s_g[cur][c] != s_g[cur][c - 1];
+            const int e = s_e[oth][c], f = s_e[oth][c - 1];
+            return s_lab[e - sh] != s_lab[f - sh] || s_g[oth][c] != s_g[oth][c - 1];
         };
         LvAgg loc{0, 0, -1, -1};
+        uint32_t starts = 0;  // bit c - c0: entry c starts a group
         for (int c = c0; c < c1; ++c) {
-            const int e = s_e[cur][c];
+            const int e = s_e[oth][c];
             const bool st = is_start(c);
+            starts |= (st ? 1u : 0u) << (c - c0);
             const LvAgg one{st ? 1 : 0, (e & 1) ? 0 : 1, (e & 1) ? -1 : (e >> 1), st ? c : -1};
             loc = lv_op(loc, one);
         }
-        for (int c = tid; c < mi; c += SORT_THREADS) s_keep[c] = 0;
         LvAgg dummy;
         const LvAgg pre = block_exscan(loc, lv_op, LvAgg{0, 0, -1, -1}, sha, s_agg, false, &dummy);
         {
             LvAgg run = pre;
             for (int c = c0; c < c1; ++c) {
-                const int e = s_e[cur][c];
-                const bool st = is_start(c);
-                if (st) run = LvAgg{1, 0, -1, c};
+                const int e = s_e[oth][c];
+                if ((starts >> (c - c0)) & 1u) run = LvAgg{1, 0, -1, c};
                 if ((e & 1) && run.cnt > 0) s_keep[run.gs] = 1;
-                if (!(e & 1)) {
-                    run.cnt += 1;
-                    run.lk = e >> 1;
-                }
+                if (!(e & 1)) ++run.cnt;
             }
         }
         __syncthreads();
-        // ---- compaction of the kept groups: cur -> oth (next level's input) and out
-        int kn = 0;
+        // ---- kept entries (x) and the next level's input (y: kept, p >= l)
+        Cnt4 kn{0, 0, 0, 0};
         {
-            LvAgg run = pre;
+            int gs = pre.gs;
             for (int c = c0; c < c1; ++c) {
-                if (is_start(c)) run.gs = c;
-                kn += s_keep[run.gs];
+                if ((starts >> (c - c0)) & 1u) gs = c;
+                const int kp = s_keep[gs];
+                kn.x += kp;
+                kn.y += kp && (s_e[oth][c] >> 1) >= l;
             }
         }
-        int kt;
-        int kb = block_exscan(kn, add, 0, shi, s_cnt, false, &kt);
-        if (kt == 0) {
+        Cnt4 kt;
+        Cnt4 kb = block_exscan(kn, add4, Cnt4{0, 0, 0, 0}, sh4, s_c4, false, &kt);
+        if (kt.x == 0) {
             nlev = l - 1;
             break;
         }
-        if (l == LEVEL_MAX + 1 || total + kt > LEVEL_BUDGET * nv) break;  // not a level row
+        if (l == LEVEL_MAX + 1 || total + kt.x > LEVEL_BUDGET * nv) break;  // not a level row
         {
             LvAgg run = pre;
             for (int c = c0; c < c1; ++c) {
-                const int e = s_e[cur][c];
-                const bool st = is_start(c);
+                const int e = s_e[oth][c];
+                const bool st = (starts >> (c - c0)) & 1u;
                 if (st) run = LvAgg{1, 0, -1, c};
                 if (s_keep[run.gs]) {
-                    const int idx = kb++;
+                    const int idx = kb.x++;
                     const int p = e >> 1;
                     ent[total + idx] = e | (st ? LEVEL_START : 0);
-                    s_e[oth][idx] = (uint16_t)e;
-                    s_g[oth][idx] = (uint16_t)(idx - (c - run.gs));
+                    if (p >= l) {  // next level's input (its group id: kept index of the start)
+                        s_e[cur][kb.y] = (uint16_t)e;
+                        s_g[cur][kb.y] = (uint16_t)(idx - (c - run.gs));
+                        ++kb.y;
+                    }
                     if (e & 1) {
                         qidx[(long)(l - 1) * n + p] = (uint16_t)idx;
                         qcnt[(long)(l - 1) * n + p] = (uint16_t)run.cnt;
@@ -947,14 +986,13 @@ __global__ __launch_bounds__(SORT_THREADS) void level_prep_kernel(PathArgs a) {
             }
         }
         __syncthreads();
-        total += kt;
-        segs += (kt + LEVEL_SEG - 1) / LEVEL_SEG;
+        total += kt.x;
+        segs += (kt.x + LEVEL_SEG - 1) / LEVEL_SEG;
         if (tid == 0) {
             meta[1 + l] = total;
             meta[LEVEL_MAX + 2 + l] = segs;
         }
-        m = kt;
-        cur = oth;
+        m = kt.y;
     }
     if (nlev > 0 && tid == 0) {
         meta[0] = nlev;
