@@ -126,6 +126,9 @@ def main():
                          "decoding at the nanochat layer shape; vocab: codebook argmax labels; "
                          "refshape: the reference's own benchmark shape (B16 H6 N2048 R32 DV64, "
                          "random-512 and identical labels, forward and backward timed apart)")
+    ap.add_argument("--graph", type=int, default=1, choices=(0, 1),
+                    help="1: time the step as a captured HIP graph (replayed --steps times); "
+                         "the eager step's time is reported beside it")
     ap.add_argument("--streams", type=int, default=2, choices=(1, 2),
                     help="2: the backward's key chain runs concurrently on a side stream")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
@@ -195,7 +198,11 @@ def bench_train(args):
     hp = hard.data_ptr()
 
     def step(events=None):
-        """One pass.  events: {stage: (start, end)} recorded on the stage's stream."""
+        """One pass.  events: {stage: (start, end)} recorded on the stage's stream.  Runs on the
+        current stream (a graph capture's stream while capturing)."""
+        stream = torch.cuda.current_stream(dev)
+        S = stream.cuda_stream
+
         def mark(name, which, strm=None):
             if events is not None and name in events:
                 events[name][which].record(strm if strm is not None else stream)
@@ -272,6 +279,7 @@ def bench_train(args):
     torch.cuda.synchronize()
     modes = row_modes(ws, tq, tv).cpu().numpy()
     dense_rows = int((modes == 1).sum())
+    level_rows = int((modes == 3).sum())
 
     def stage_events(only=None):
         return {nm: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -303,12 +311,51 @@ def bench_train(args):
     torch.cuda.synchronize()
     kern_ms = {nm: float(np.mean([per[s][nm][0].elapsed_time(per[s][nm][1])
                                   for s in range(args.steps)])) for nm in names}
+    eager_ms = ms_step
+    graph_ms = None
+    if args.graph:
+        # the same step captured once into a HIP graph (every launch, the side-stream fork and
+        # join included) and replayed: the small configs' steps are bounded by the host's
+        # launch rate otherwise.  Inputs, workspace and outputs are the same buffers.
+        g = torch.cuda.CUDAGraph()
+        cs = torch.cuda.Stream(device=dev)
+        cs.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(cs):
+            step()
+        torch.cuda.current_stream(dev).wait_stream(cs)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=cs):
+            step()
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        gs, ge = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        gs.record()
+        for _ in range(args.steps):
+            g.replay()
+        ge.record()
+        torch.cuda.synchronize()
+        graph_ms = gs.elapsed_time(ge) / args.steps
+        ms_step = graph_ms
     units = B * H * T
     value = units / (ms_step / 1e3)
     esz = 4 if vdt == torch.float32 else 2
     order = 16  # combined-order entry and label of the unit's key and query (4 x 4 B)
     dom = max(cand, key=lambda x: live_ms[x])
-    if dense_rows and dom in ("forward", "queries", "keys"):
+    if level_rows and not dense_rows:
+        # level rows: a chain of short launches (prepare lists, segment totals, walks,
+        # combines); the bound is the whole step's HBM traffic at its minimum -- every input
+        # read once, every output written once per (b,h,t) unit
+        fwd_b = 2 * D * esz + 2 * DV * esz + 4
+        bwd_b = 2 * D * esz + 2 * DV * esz + 4 + 8 * D + 4 * DV + 4
+        per_unit = fwd_b + (0 if fwd_only else bwd_b)
+        alg_bytes = per_unit * units
+        achieved = alg_bytes / (ms_step / 1e3)
+        roof = {"kernel": "whole step (level rows: all kernels)", "bound": "hbm",
+                "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK, "traffic": None, "alg_bytes_per_unit": per_unit,
+                "launch_ms": ms_step}
+    elif dense_rows and dom in ("forward", "queries", "keys"):
         # fp32 FMAs of the direct definition per valid pair: forward s, acc (R + DV); query rows
         # s, e, dq (2R + DV); keys s, e, dk, dv (2R + 2DV); over the dense rows' valid pairs
         pairs = valid_pairs(iq_t.cpu().numpy(), ik_t.cpu().numpy())
@@ -347,7 +394,9 @@ def bench_train(args):
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms_step,
-        "wall_ms_per_step": wall * 1e3 / args.steps,
+        "eager_ms_per_step": eager_ms,
+        "graph_ms_per_step": graph_ms,
+        "wall_ms_per_step_eager": wall * 1e3 / args.steps,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -357,7 +406,7 @@ def bench_train(args):
         "config": {"workload": cfg["workload"], "B": B, "H": H, "T": T, "d_qk": D, "d_v": DV,
                    "tau": args.tau, "carry_strip": strip, "forward_only": fwd_only,
                    "global_batch": B, "seq_len": T, "parallelism": "single-gpu"},
-        "row_modes": {str(m): int((modes == m).sum()) for m in (0, 1, 2)},
+        "row_modes": {str(m): int((modes == m).sum()) for m in (0, 1, 2, 3)},
         "kernel_ms": kern_ms,
         "roofline": roof,
     }
@@ -549,7 +598,7 @@ def bench_refshape(args):
         modes = row_modes(ws, sq, v).cpu()
         ref = REF_5090[kind]
         result[kind] = {"forward_ms": f_ms, "backward_ms": b_ms, "fwd_bwd_ms": fb_ms,
-                        "row_modes": {str(m): int((modes == m).sum()) for m in (0, 1, 2)},
+                        "row_modes": {str(m): int((modes == m).sum()) for m in (0, 1, 2, 3)},
                         "bht_per_s_fwd_bwd": B * H * N / (fb_ms / 1e3),
                         "rtx5090_ms": ref,
                         "speedup_vs_rtx5090": {"forward": ref["forward"] / f_ms,

@@ -55,7 +55,7 @@ struct Layout {
     int64_t corder, clab, ctab, bpos[2], blab[2], bplab[2], btab[2], shift, tmp[3];
     int64_t stage[2][2], bhcount[2], own[2], ocount, mode, onebyte;
     int64_t pnb, prow, mcount, mdig, dflag, dlist, dcount, dbound, dcost;
-    int64_t lvent, lvmeta, lvqidx, lvkidx, lvcnt, lvq, lvP, lvQ, lvY, lvZ, lvK;  // -1: none
+    int64_t lvent, lvlc, lvlf, lvlk, lvmeta, lvq, lvqidx, lvkidx, lvF, lvFk, lvP, lvQ, lvY, lvZ, lvK;  // -1: none
     int64_t total;
     int prow_stride;
 };
@@ -161,11 +161,15 @@ Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     const bool lv = N <= dism::LEVEL_MAX_N && (int64_t)R * DV <= dism::LEVEL_RDV;
     const int64_t lent = (int64_t)dism::LEVEL_BUDGET * N, lmat = dism::LEVEL_MAX * N;
     const int64_t lseg = dism::level_segs(N) * R * DV * 4;
-    L.lvent = lv ? take(BH * lent * 4) : -1;
+    L.lvent = lv ? take(BH * lmat * 2 * 4) : -1;
+    L.lvlc = lv ? take(BH * (dism::LEVEL_MAX + 2) * 4) : -1;
+    L.lvlf = lv ? take(BH * (dism::LEVEL_MAX + 1) * N) : -1;
+    L.lvlk = lv ? take(BH * lmat * 2) : -1;
     L.lvmeta = lv ? take(BH * dism::LEVEL_META * 4) : -1;
     L.lvqidx = lv ? take(BH * lmat * 2) : -1;
     L.lvkidx = lv ? take(BH * lmat * 2) : -1;
-    L.lvcnt = lv ? take(BH * lmat * 2) : -1;
+    L.lvF = lv ? take(BH * dism::level_segs(N)) : -1;
+    L.lvFk = lv ? take(BH * dism::level_segs(N)) : -1;
     L.lvq = lv ? take(BH * N * 16) : -1;
     L.lvP = lv ? take(BH * lseg) : -1;
     L.lvQ = lv ? take(BH * lseg) : -1;
@@ -211,10 +215,14 @@ dism::Orders orders(const Layout& L, void* ws) {
     o.dcost = at<unsigned long long>(ws, L.dcost);
     auto opt = [&](int64_t off) { return off < 0 ? nullptr : at<char>(ws, off); };
     o.lvent = reinterpret_cast<int32_t*>(opt(L.lvent));
+    o.lvlc = reinterpret_cast<int32_t*>(opt(L.lvlc));
+    o.lvlf = reinterpret_cast<uint8_t*>(opt(L.lvlf));
+    o.lvlk = reinterpret_cast<uint16_t*>(opt(L.lvlk));
     o.lvmeta = reinterpret_cast<int32_t*>(opt(L.lvmeta));
     o.lvqidx = reinterpret_cast<uint16_t*>(opt(L.lvqidx));
     o.lvkidx = reinterpret_cast<uint16_t*>(opt(L.lvkidx));
-    o.lvcnt = reinterpret_cast<uint16_t*>(opt(L.lvcnt));
+    o.lvF = reinterpret_cast<uint8_t*>(opt(L.lvF));
+    o.lvFk = reinterpret_cast<uint8_t*>(opt(L.lvFk));
     o.lvq = reinterpret_cast<int4*>(opt(L.lvq));
     o.lvP = reinterpret_cast<float*>(opt(L.lvP));
     o.lvQ = reinterpret_cast<float*>(opt(L.lvQ));
@@ -511,7 +519,7 @@ int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t
 // host code `scratch` only names the symbol: its device address comes from
 // hipGetSymbolAddress, once per device (with that device current), and only that address is
 // passed to kernels.
-constexpr int64_t NOALLOC_SCRATCH_BYTES = int64_t(128) << 20;
+constexpr int64_t NOALLOC_SCRATCH_BYTES = int64_t(256) << 20;
 static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
 
 namespace {

@@ -63,29 +63,41 @@ struct Orders {
     unsigned long long* dcost;  // [B*H] walk-cost estimate of the probe (dism_pairs.hip)
     // level rows (mode 3, dism_levels.hip): dense rows whose sums are taken per match length.
     // Null unless N <= LEVEL_MAX_N and R * DV <= LEVEL_RDV.  Per (b,h) row:
-    //   lvent  [LEVEL_BUDGET * N]  the kept entries e = 2p + s of levels 1, 2, ... in list
-    //                              order, LEVEL_START on a group's first entry
+    //   lvent  [LEVEL_MAX][2N]     level l's kept entries in list order (at (l - 1) 2N):
+    //                              entry e = 2p + s in the low LEVEL_EBITS bits, a query's
+    //                              count of keys before it in its group above them,
+    //                              LEVEL_START on a group's first entry
+    //   lvlc   [LEVEL_MAX + 2]     kept entries per level (per-level list construction)
+    //   lvlf   [LEVEL_MAX + 1][N]  per level and position: 1 query kept, 2 with a key before
+    //                              it, 4 key kept (per-level list construction)
+    //   lvlk   [LEVEL_MAX][N]      per level: a query's last key before it in its group
     //   lvmeta [LEVEL_META]        level count, then off[0..LEVEL_MAX] (level l at
     //                              [off[l-1], off[l])), then segbase[0..LEVEL_MAX] (level l's
     //                              first segment of LEVEL_SEG entries)
-    //   lvqidx / lvkidx [LEVEL_MAX][N]  index of query / key position p in level l's list
-    //                              (valid for l up to its kept level count)
-    //   lvcnt  [LEVEL_MAX][N]      keys before query p in its level-l group
     //   lvq    [N]                 per position {longest match Lq, its last key, kept levels
     //                              of the query, kept levels of the key}
-    //   lvP    [level_segs(N)][R*DV]  forward segment totals T_s, each replaced by the
-    //                              prefix P_{s+1} ([r][d])
-    //   lvQ    [level_segs(N)][R*DV]  key-side totals U_s, each replaced by Q_{s-1} ([d][r])
+    //   lvqidx / lvkidx [LEVEL_MAX][N]  index of query / key position p in level l's list
+    //                              (written by the segment walks; valid for l up to the
+    //                              position's kept level count)
+    //   lvF, lvFk [level_segs(N)]  per segment: bit 0 a group starts in it, bit 1 at its first
+    //                              entry (written by the forward / query-row and the key
+    //                              chains, which may run concurrently)
+    //   lvP    [level_segs(N)][R*DV]  forward segment totals T_s ([r][d])
+    //   lvQ    [level_segs(N)][R*DV]  key-side segment totals U_s ([d][r])
     //   lvY    [LEVEL_BUDGET * N][DV]  per list entry: the forward's y_l of a query, the
     //                              backward's dv_l of a key
     //   lvZ    [LEVEL_BUDGET * N][R]   the backward's z_l of a query
     //   lvK    [LEVEL_BUDGET * N][R]   the backward's dk_l of a key
     int32_t* lvent;
+    int32_t* lvlc;
+    uint8_t* lvlf;
+    uint16_t* lvlk;
     int32_t* lvmeta;
+    int4* lvq;
     uint16_t* lvqidx;
     uint16_t* lvkidx;
-    uint16_t* lvcnt;
-    int4* lvq;
+    uint8_t* lvF;
+    uint8_t* lvFk;
     float* lvP;
     float* lvQ;
     float* lvY;
@@ -98,6 +110,8 @@ constexpr int LEVEL_BUDGET = 16;    // kept entries per position over all levels
 constexpr int LEVEL_SEG = 32;       // list entries per segment
 constexpr int LEVEL_RDV = 512;      // largest R * DV of a level row
 constexpr int LEVEL_START = 0x40000000;
+constexpr int LEVEL_EBITS = 13;     // entry e < 2 LEVEL_MAX_N
+constexpr int LEVEL_EMASK = (1 << LEVEL_EBITS) - 1;
 constexpr int LEVEL_META = 2 * LEVEL_MAX + 4;
 __host__ __device__ inline long level_segs(long n) {
     return (long)LEVEL_BUDGET * n / LEVEL_SEG + LEVEL_MAX;

@@ -256,7 +256,7 @@ __global__ __launch_bounds__(LIST_THREADS) void owner_lists_kernel(PathArgs a) {
     int4* own = a.o.own[side];
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
-        const int m = dense[bh] == 1 ? 0 : cnt[(long)bh * 4 + c];
+        const int m = (dense[bh] == 1 || dense[bh] == 3) ? 0 : cnt[(long)bh * 4 + c];
         const int4* src = a.o.stage[side][c == 1 ? 1 : 0] + so;
         for (int k = tid; k < m; k += LIST_THREADS) {
             const int4 rec = src[c == 2 ? n - 1 - k : k];

@@ -518,6 +518,10 @@ __global__ __launch_bounds__(SORT_THREADS) void prepare_lds_kernel(SortArgs a) {
         a.o.onebyte[bh] = nd <= 1 ? 1 : 0;
         a.o.shift[bh] = 8 * dg;  // the top used byte (0 without any)
     }
+    // dense rows (classified before the prepare) have no bigram-pair work: role 1 skips them
+    // (the owner lists drop them; their label order, role 0, stays, e.g. for the decoder)
+    const int dmode = a.o.dflag[bh];
+    if (role == 1 && (dmode == 1 || dmode == 3)) return;
     if (!lds_ok) {
         // the global-memory path takes this row: its combined label order here (the LDS
         // pool as the passes' scratch), the bigram orders in sort_kernel roles 1-2
@@ -764,16 +768,17 @@ hipError_t launch_ctab_balance(const SortArgs& a, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Level lists (one 1024-thread workgroup per dense row, after the classification; rows of
-// N <= LEVEL_MAX_N whose labels are all below 256, fixed-length calls without resets).
+// Level lists, sequentially (one 1024-thread workgroup per dense row, after the
+// classification; rows of N <= LEVEL_MAX_N whose labels are all below 256 but not all below
+// 16 -- those go to level_lvl_kernel -- fixed-length calls without resets).
 // Level l's list is the previous level's kept list without its entries at p = l - 2, stably
 // sorted by label[p - l + 1] (entry e's digit at level l is s_lab[e - 2(l - 1)], the labels
 // staged in LDS as bytes).  A group (equal digit and equal previous group) is kept when one
-// of its queries has a key before it.  Per level: the stable partition by digit (ballot
-// ranks for labels below 16, lds_pass otherwise), one block scan for every entry's group
+// of its queries has a key before it.  Per level: the stable partition by digit
+// (lds_pass), one block scan for every entry's group
 // start, keys before it in the group and the last of them, the keep flags, one block scan for
-// the kept entries (written out with the per-position indices and counts) and the next
-// level's input (kept, p >= l).  The row becomes mode 3 when a level keeps nothing within
+// the kept entries (written out with their key counts) and the next level's input (kept,
+// p >= l).  The row becomes mode 3 when a level keeps nothing within
 // LEVEL_MAX levels and LEVEL_BUDGET * N kept entries; otherwise it stays a mode-1 (tile)
 // row.  The oracle's levels_build computes the same lists.
 namespace {
@@ -786,47 +791,70 @@ __device__ __forceinline__ LvAgg lv_op(LvAgg a, LvAgg b) {
                  b.gs >= 0 ? b.gs : a.gs};
 }
 
-// Stable counting pass over m elements with digits below nd <= 16 (per-wave contiguous
-// segments; ranks inside a 64-element group from one ballot per digit value).
+
+// A stable counting pass as lds_pass, with the ranks inside a 64-element group from ballot
+// matching of the 9-bit digit (no rank-mask scratch, so two level workgroups fit a CU).
 template <typename Dig, typename Emit>
-__device__ void small_pass(int m, int nd, Dig digit, Emit emit, int (*wcnt)[16], int* base_of) {
+__device__ void lv_pass(int m, Dig digit, Emit emit, int (*wcnt)[RADIX], int* scan) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int seg = ((m + SORT_WAVES - 1) / SORT_WAVES + 63) / 64 * 64;
     const int beg = wave * seg;
     const int end = beg + seg < m ? beg + seg : m;
     const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
-    int cnt = 0;  // lane d < nd: this wave's count of digit d
+    for (int e = tid; e < SORT_WAVES * RADIX; e += SORT_THREADS) (&wcnt[0][0])[e] = 0;
+    __syncthreads();
     for (int x0 = beg; x0 < end; x0 += 64) {
         const int x = x0 + lane;
-        const int dg = x < end ? digit(x) : 16;
-        for (int d = 0; d < nd; ++d) {
-            const int c = __popcll(__ballot(dg == d));
-            if (lane == d) cnt += c;
-        }
+        const int dig = x < end ? digit(x) : RADIX;
+        const unsigned long long eq = match_digit(dig);
+        if (dig < RADIX && !(eq & below)) wcnt[wave][dig] += __popcll(eq);
+        __builtin_amdgcn_wave_barrier();
     }
-    if (lane < 16) wcnt[wave][lane] = cnt;
     __syncthreads();
-    if (tid < 16) {  // exclusive scan over (digit, wave) into base_of[wave * 16 + digit]
-        int run = 0;
-        for (int d = 0; d < tid; ++d)
-            for (int w = 0; w < SORT_WAVES; ++w) run += wcnt[w][d];
+    if (tid < RADIX) {
+        int tot = 0;
+        for (int w = 0; w < SORT_WAVES; ++w) tot += wcnt[w][tid];
+        scan[tid] = tot;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int v0 = scan[4 * tid], v1 = scan[4 * tid + 1], v2 = scan[4 * tid + 2],
+                  v3 = scan[4 * tid + 3];
+        const int sum = v0 + v1 + v2 + v3;
+        int inc = sum;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int t = __shfl_up(inc, off);
+            if (lane >= off) inc += t;
+        }
+        int ex = inc - sum;
+        scan[4 * tid] = ex;
+        ex += v0;
+        scan[4 * tid + 1] = ex;
+        ex += v1;
+        scan[4 * tid + 2] = ex;
+        ex += v2;
+        scan[4 * tid + 3] = ex;
+    }
+    __syncthreads();
+    if (tid < RADIX) {
+        int run = scan[tid];
         for (int w = 0; w < SORT_WAVES; ++w) {
-            base_of[w * 16 + tid] = run;
-            run += wcnt[w][tid];
+            const int c = wcnt[w][tid];
+            wcnt[w][tid] = run;
+            run += c;
         }
     }
     __syncthreads();
-    int base = lane < 16 ? base_of[wave * 16 + lane] : 0;
     for (int x0 = beg; x0 < end; x0 += 64) {
         const int x = x0 + lane;
-        const int dg = x < end ? digit(x) : 16;
-        int dst = 0;
-        for (int d = 0; d < nd; ++d) {
-            const unsigned long long mk = __ballot(dg == d);
-            const int bd = __shfl(base, d);
-            if (dg == d) dst = bd + __popcll(mk & below);
-            if (lane == d) base += __popcll(mk);
-        }
+        const int dig = x < end ? digit(x) : RADIX;
+        const unsigned long long eq = match_digit(dig);
+        const int rank = __popcll(eq & below);
+        const int dst = dig < RADIX ? wcnt[wave][dig] + rank : 0;
+        __builtin_amdgcn_wave_barrier();
+        if (dig < RADIX && rank == 0) wcnt[wave][dig] += __popcll(eq);
+        __builtin_amdgcn_wave_barrier();
         if (x < end) emit(x, dst);
     }
     __syncthreads();
@@ -845,6 +873,10 @@ __global__ __launch_bounds__(SORT_THREADS) void level_prep_kernel(PathArgs a) {
     __shared__ LvAgg s_agg[SORT_WAVES];
     __shared__ Cnt4 s_c4[SORT_WAVES];
     __shared__ uint32_t s_or;
+    // per position: longest match, kept levels of the query / the key, the longest match's
+    // last key (0xFFFF: none); written out once at the end
+    __shared__ uint8_t s_lq[LEVEL_MAX_N], s_kq[LEVEL_MAX_N], s_kk[LEVEL_MAX_N];
+    __shared__ uint16_t s_jarg[LEVEL_MAX_N];
     // nv: the positions the lists take (a prefill's padding after them never pairs with
     // them: its keys come after every real query)
     const int bh = blockIdx.x, tid = threadIdx.x, n = a.n;
@@ -871,15 +903,16 @@ __global__ __launch_bounds__(SORT_THREADS) void level_prep_kernel(PathArgs a) {
     if ((tid & 63) == 0 && orv) atomicOr(&s_or, orv);
     __syncthreads();
     const uint32_t used = s_or;
-    if (used >= 256u) return;   // labels of more than one byte: not a level row
-    const int nd = used < 16u ? (int)used + 1 : 0;  // small alphabet: ballot ranks (max < nd)
-    int32_t* ent = a.o.lvent + (long)bh * LEVEL_BUDGET * n;
+    // labels of more than one byte: not a level row; below 16: level_lvl_kernel's rows
+    if (used >= 256u || used < 16u) return;
+    int32_t* ent = a.o.lvent + (long)bh * LEVEL_MAX * 2 * n;
     int32_t* meta = a.o.lvmeta + (long)bh * LEVEL_META;
-    uint16_t* qidx = a.o.lvqidx + (long)bh * LEVEL_MAX * n;
-    uint16_t* kidx = a.o.lvkidx + (long)bh * LEVEL_MAX * n;
-    uint16_t* qcnt = a.o.lvcnt + (long)bh * LEVEL_MAX * n;
-    int4* lq = a.o.lvq + so;
-    for (int p = tid; p < n; p += SORT_THREADS) lq[p] = make_int4(0, -1, 0, 0);
+    for (int p = tid; p < n; p += SORT_THREADS) {
+        s_lq[p] = 0;
+        s_kq[p] = 0;
+        s_kk[p] = 0;
+        s_jarg[p] = 0xFFFF;
+    }
     auto sh4 = [](Cnt4 v, int l) {
         return Cnt4{__shfl(v.x, l), __shfl(v.y, l), __shfl(v.z, l), __shfl(v.w, l)};
     };
@@ -902,8 +935,7 @@ __global__ __launch_bounds__(SORT_THREADS) void level_prep_kernel(PathArgs a) {
             s_e[oth][dst] = s_e[cur][x];
             s_g[oth][dst] = s_g[cur][x];
         };
-        if (nd) small_pass(m, nd, dig, emit, reinterpret_cast<int (*)[16]>(&wcnt[0][0]), scan);
-        else lds_pass(m, dig, emit, nullptr, wcnt, scan, lmask);
+        lds_pass(m, dig, emit, nullptr, wcnt, scan, lmask);
         // ---- groups: start, keys before, last key; keep flags
         const int ept = (m + SORT_THREADS - 1) / SORT_THREADS;
         const int c0 = tid * ept, c1 = c0 + ept < m ? c0 + ept : m;
@@ -960,23 +992,21 @@ __global__ __launch_bounds__(SORT_THREADS) void level_prep_kernel(PathArgs a) {
                 if (s_keep[run.gs]) {
                     const int idx = kb.x++;
                     const int p = e >> 1;
-                    ent[total + idx] = e | (st ? LEVEL_START : 0);
+                    ent[(long)(l - 1) * 2 * n + idx] =
+                        e | ((e & 1) ? run.cnt << LEVEL_EBITS : 0) | (st ? LEVEL_START : 0);
                     if (p >= l) {  // next level's input (its group id: kept index of the start)
                         s_e[cur][kb.y] = (uint16_t)e;
                         s_g[cur][kb.y] = (uint16_t)(idx - (c - run.gs));
                         ++kb.y;
                     }
                     if (e & 1) {
-                        qidx[(long)(l - 1) * n + p] = (uint16_t)idx;
-                        qcnt[(long)(l - 1) * n + p] = (uint16_t)run.cnt;
-                        lq[p].z = l;
+                        s_kq[p] = (uint8_t)l;
                         if (run.cnt > 0) {
-                            lq[p].x = l;
-                            lq[p].y = run.lk;
+                            s_lq[p] = (uint8_t)l;
+                            s_jarg[p] = (uint16_t)run.lk;
                         }
                     } else {
-                        kidx[(long)(l - 1) * n + p] = (uint16_t)idx;
-                        lq[p].w = l;
+                        s_kk[p] = (uint8_t)l;
                     }
                 }
                 if (!(e & 1)) {
@@ -994,7 +1024,238 @@ __global__ __launch_bounds__(SORT_THREADS) void level_prep_kernel(PathArgs a) {
         }
         m = kt.y;
     }
-    if (nlev > 0 && tid == 0) {
+    if (nlev <= 0) return;  // not a level row (uniform)
+    int4* lq = a.o.lvq + so;
+    for (int p = tid; p < n; p += SORT_THREADS)
+        lq[p] = make_int4(s_lq[p], s_jarg[p] == 0xFFFF ? -1 : (int)s_jarg[p], s_kq[p], s_kk[p]);
+    if (tid == 0) {
+        meta[0] = nlev;
+        a.o.dflag[bh] = 3;
+    }
+}
+
+// Level lists, one level per workgroup (grid (B*H, LEVEL_MAX + 1)), for rows whose labels
+// are all below 16.  The level-l list is the same as the sequential construction's: the
+// entries at p >= l - 1 ordered by their l-gram read oldest label first, then by e, without
+// the groups that hold no valid pair (a group's sub-groups hold none either, so the lists do
+// not depend on the previous level).  With b-bit symbols (b = 1, 2 or 4), byte k of the
+// l-gram key is the packed history s_h8[e - 2 S k] of S = 8 / b labels (the oldest of them
+// in its top bits, the last byte masked to the l-gram); LSD passes over the key bytes
+// (lds_pass) give the order.  The per-position flags and last keys go to lvlf / lvlk, the
+// kept count to lvlc[l]; level_finalize_kernel then takes the row to mode 3 or leaves it.
+__global__ __launch_bounds__(SORT_THREADS) void level_lvl_kernel(PathArgs a, int l0) {
+    constexpr int M2 = 2 * LEVEL_MAX_N;
+    // (under 80 KiB, so that two workgroups share a CU: the labels' bytes and later the
+    // per-position flags share one region, the keep flags use the idle order buffer)
+    __shared__ uint16_t s_e[2][M2];
+    __shared__ uint32_t s_u[LEVEL_MAX_N];   // s_lab (bytes), then s_fl
+    __shared__ uint8_t s_h8[M2];
+    __shared__ int wcnt[SORT_WAVES][RADIX];
+    __shared__ int scan[RADIX];
+    __shared__ LvAgg s_agg[SORT_WAVES];
+    __shared__ Cnt4 s_c4[SORT_WAVES];
+    __shared__ uint32_t s_or;
+    uint8_t* s_lab = reinterpret_cast<uint8_t*>(s_u);
+    uint32_t* s_fl = s_u;
+    const int bh = blockIdx.x, l = (int)blockIdx.y + l0, tid = threadIdx.x, n = a.n;
+    const int nv = a.cls_n > 0 && a.cls_n < n ? a.cls_n : n;
+    if (a.o.dflag[bh] != 1) return;
+    // a later launch's levels: nothing to do once an earlier level kept nothing
+    if (l0 > 1 && a.o.lvlc[(long)bh * (LEVEL_MAX + 2) + l0 - 1] == 0) {
+        if (tid == 0) a.o.lvlc[(long)bh * (LEVEL_MAX + 2) + l] = 0;
+        return;
+    }
+    const long so = (long)bh * n;
+    const int32_t* q = a.iq + so;
+    const int32_t* k = a.ik + so;
+    if (tid == 0) s_or = 0;
+    __syncthreads();
+    uint32_t orv = 0;
+    for (int p = tid; p < nv; p += SORT_THREADS) {
+        const uint32_t lq = (uint32_t)q[p], lk = (uint32_t)k[p];
+        orv |= lq | lk;
+        s_lab[2 * p] = (uint8_t)lk;
+        s_lab[2 * p + 1] = (uint8_t)lq;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) orv |= (uint32_t)__shfl_xor((int)orv, o);
+    if ((tid & 63) == 0 && orv) atomicOr(&s_or, orv);
+    __syncthreads();
+    const uint32_t used = s_or;
+    if (used >= 16u) return;  // the sequential construction's rows
+    const int b = used < 2u ? 1 : used < 4u ? 2 : 4, S = 8 / b;
+    int32_t* cnts = a.o.lvlc + (long)bh * (LEVEL_MAX + 2);
+    uint8_t* lf = a.o.lvlf + ((long)bh * (LEVEL_MAX + 1) + (l - 1)) * n;
+    const int e0 = 2 * (l - 1), m = 2 * nv - e0;
+    if (m <= 0) {
+        for (int p = tid; p < n; p += SORT_THREADS) lf[p] = 0;
+        if (tid == 0) cnts[l] = 0;
+        return;
+    }
+    for (int e = tid; e < 2 * nv; e += SORT_THREADS) {
+        const int qp = e >> 1, side = e & 1;
+        uint32_t h = 0;
+        for (int u = 0; u < S && qp - u >= 0; ++u) h |= (uint32_t)s_lab[2 * (qp - u) + side] << (b * u);
+        s_h8[e] = (uint8_t)h;
+    }
+    for (int x = tid; x < m; x += SORT_THREADS) s_e[0][x] = (uint16_t)(e0 + x);
+    __syncthreads();
+    for (int p = tid; p < nv; p += SORT_THREADS) s_fl[p] = 0u;  // (the labels are in s_h8 now)
+    const int nbytes = (l + S - 1) / S;
+    const int lastmask = (l % S) ? (1 << (b * (l - S * (nbytes - 1)))) - 1 : 0xFF;
+    auto kbyte = [&](int e, int kk) {
+        const int v = s_h8[e - 2 * S * kk];
+        return kk == nbytes - 1 ? (v & lastmask) : v;
+    };
+    int cur = 0;
+    for (int kk = 0; kk < nbytes; ++kk) {
+        const int nx = cur ^ 1;
+        lv_pass(
+            m, [&](int x) { return kbyte(s_e[cur][x], kk); },
+            [&](int x, int dst) { s_e[nx][dst] = s_e[cur][x]; }, wcnt, scan);
+        cur = nx;
+    }
+    uint8_t* s_keep = reinterpret_cast<uint8_t*>(s_e[cur ^ 1]);
+    // ---- groups, keep flags, compaction (as the sequential construction's level step)
+    const int ept = (m + SORT_THREADS - 1) / SORT_THREADS;
+    const int c0 = tid * ept, c1 = c0 + ept < m ? c0 + ept : m;
+    auto is_start = [&](int c) {
+        if (c == 0) return true;
+        const int e = s_e[cur][c], f = s_e[cur][c - 1];
+        for (int kk = 0; kk < nbytes; ++kk)
+            if (kbyte(e, kk) != kbyte(f, kk)) return true;
+        return false;
+    };
+    for (int c = tid; c < m; c += SORT_THREADS) s_keep[c] = 0;
+    LvAgg loc{0, 0, -1, -1};
+    uint32_t starts = 0;
+    for (int c = c0; c < c1; ++c) {
+        const int e = s_e[cur][c];
+        const bool st = is_start(c);
+        starts |= (st ? 1u : 0u) << (c - c0);
+        const LvAgg one{st ? 1 : 0, (e & 1) ? 0 : 1, (e & 1) ? -1 : (e >> 1), st ? c : -1};
+        loc = lv_op(loc, one);
+    }
+    auto sha = [](LvAgg v, int ln) {
+        return LvAgg{__shfl(v.f, ln), __shfl(v.cnt, ln), __shfl(v.lk, ln), __shfl(v.gs, ln)};
+    };
+    LvAgg dummy;
+    const LvAgg pre = block_exscan(loc, lv_op, LvAgg{0, 0, -1, -1}, sha, s_agg, false, &dummy);
+    {
+        LvAgg run = pre;
+        for (int c = c0; c < c1; ++c) {
+            const int e = s_e[cur][c];
+            if ((starts >> (c - c0)) & 1u) run = LvAgg{1, 0, -1, c};
+            if ((e & 1) && run.cnt > 0) s_keep[run.gs] = 1;
+            if (!(e & 1)) ++run.cnt;
+        }
+    }
+    __syncthreads();
+    Cnt4 kn{0, 0, 0, 0};
+    {
+        int gs = pre.gs;
+        for (int c = c0; c < c1; ++c) {
+            if ((starts >> (c - c0)) & 1u) gs = c;
+            kn.x += s_keep[gs];
+        }
+    }
+    auto sh4 = [](Cnt4 v, int ln) {
+        return Cnt4{__shfl(v.x, ln), __shfl(v.y, ln), __shfl(v.z, ln), __shfl(v.w, ln)};
+    };
+    auto add4 = [](Cnt4 x, Cnt4 y) { return Cnt4{x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w}; };
+    Cnt4 kt;
+    Cnt4 kb = block_exscan(kn, add4, Cnt4{0, 0, 0, 0}, sh4, s_c4, false, &kt);
+    if (l <= LEVEL_MAX && kt.x > 0) {
+        int32_t* ent = a.o.lvent + (long)bh * LEVEL_MAX * 2 * n + (long)(l - 1) * 2 * n;
+        uint16_t* lk = a.o.lvlk + ((long)bh * LEVEL_MAX + (l - 1)) * n;
+        LvAgg run = pre;
+        for (int c = c0; c < c1; ++c) {
+            const int e = s_e[cur][c];
+            const bool st = (starts >> (c - c0)) & 1u;
+            if (st) run = LvAgg{1, 0, -1, c};
+            if (s_keep[run.gs]) {
+                const int idx = kb.x++;
+                const int p = e >> 1;
+                ent[idx] = e | ((e & 1) ? run.cnt << LEVEL_EBITS : 0) | (st ? LEVEL_START : 0);
+                if (e & 1) {
+                    atomicOr(&s_fl[p], run.cnt > 0 ? 3u : 1u);
+                    if (run.cnt > 0) lk[p] = (uint16_t)run.lk;
+                } else {
+                    atomicOr(&s_fl[p], 4u);
+                }
+            }
+            if (!(e & 1)) {
+                run.cnt += 1;
+                run.lk = e >> 1;
+            }
+        }
+    }
+    __syncthreads();
+    for (int p = tid; p < n; p += SORT_THREADS) lf[p] = p < nv ? (uint8_t)s_fl[p] : 0;
+    if (tid == 0) cnts[l] = kt.x;
+}
+
+// Mode 3 for the rows level_lvl_kernel built whose levels end within LEVEL_MAX and the
+// budget; the level offsets, segment bases and per-position summaries.
+__global__ __launch_bounds__(256) void level_finalize_kernel(PathArgs a) {
+    __shared__ uint32_t s_or;
+    __shared__ int s_nlev;
+    const int bh = blockIdx.x, tid = threadIdx.x, n = a.n;
+    const int nv = a.cls_n > 0 && a.cls_n < n ? a.cls_n : n;
+    if (a.o.dflag[bh] != 1) return;
+    const long so = (long)bh * n;
+    if (tid == 0) s_or = 0;
+    __syncthreads();
+    uint32_t orv = 0;
+    for (int p = tid; p < nv; p += 256) orv |= (uint32_t)a.iq[so + p] | (uint32_t)a.ik[so + p];
+    if (orv) atomicOr(&s_or, orv);
+    __syncthreads();
+    if (s_or >= 16u) return;
+    const int32_t* cnts = a.o.lvlc + (long)bh * (LEVEL_MAX + 2);
+    int32_t* meta = a.o.lvmeta + (long)bh * LEVEL_META;
+    if (tid < 64) {  // lane l - 1 holds level l's count
+        const int c = tid < LEVEL_MAX + 1 ? cnts[tid + 1] : 0;
+        const unsigned long long z = __ballot(tid < LEVEL_MAX + 1 && c == 0);
+        int nlev = z ? __builtin_ctzll(z) : -1, total = 0;
+        if (nlev > 0) {
+            int segs = 0;
+            meta[1] = 0;
+            meta[LEVEL_MAX + 2] = 0;
+            for (int l = 1; l <= nlev; ++l) {
+                const int cl = __shfl(c, l - 1);
+                total += cl;
+                segs += (cl + LEVEL_SEG - 1) / LEVEL_SEG;
+                if (tid == 0) {
+                    meta[1 + l] = total;
+                    meta[LEVEL_MAX + 2 + l] = segs;
+                }
+            }
+            if (total > LEVEL_BUDGET * nv) nlev = -1;
+        }
+        if (tid == 0) s_nlev = nlev;
+    }
+    __syncthreads();
+    const int nlev = s_nlev;
+    if (nlev <= 0) return;
+    const uint8_t* lf = a.o.lvlf + (long)bh * (LEVEL_MAX + 1) * n;
+    const uint16_t* lk = a.o.lvlk + (long)bh * LEVEL_MAX * n;
+    for (int p = tid; p < n; p += 256) {
+        int kq = 0, lq = 0, kk = 0;
+        for (int l0 = 1; l0 <= nlev; l0 += 8) {  // eight levels' loads in flight
+            int f[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) f[u] = l0 + u <= nlev ? lf[(long)(l0 + u - 1) * n + p] : 0;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (f[u] & 1) kq = l0 + u;
+                if (f[u] & 2) lq = l0 + u;
+                if (f[u] & 4) kk = l0 + u;
+            }
+        }
+        a.o.lvq[so + p] = make_int4(lq, lq > 0 ? (int)lk[(long)(lq - 1) * n + p] : -1, kq, kk);
+    }
+    __syncthreads();
+    if (tid == 0) {
         meta[0] = nlev;
         a.o.dflag[bh] = 3;
     }
@@ -1002,8 +1263,13 @@ __global__ __launch_bounds__(SORT_THREADS) void level_prep_kernel(PathArgs a) {
 
 hipError_t launch_level_prep(const PathArgs& a, hipStream_t s) {
     if (!a.o.lvent || a.dstart || a.wlo || a.n > LEVEL_MAX_N) return hipSuccess;
-    hipLaunchKernelGGL(level_prep_kernel, dim3((unsigned)(a.B * a.H)), dim3(SORT_THREADS), 0, s,
-                       a);
+    const unsigned BH = (unsigned)(a.B * a.H);
+    // levels 1..16, then 17..33 (those exit at once when level 16 kept nothing)
+    hipLaunchKernelGGL(level_lvl_kernel, dim3(BH, 16), dim3(SORT_THREADS), 0, s, a, 1);
+    hipLaunchKernelGGL(level_lvl_kernel, dim3(BH, LEVEL_MAX + 1 - 16), dim3(SORT_THREADS), 0, s,
+                       a, 17);
+    hipLaunchKernelGGL(level_finalize_kernel, dim3(BH), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(level_prep_kernel, dim3(BH), dim3(SORT_THREADS), 0, s, a);
     return hipGetLastError();
 }
 

@@ -113,7 +113,7 @@ int32_t dism_hard_prepare(const void* sq, const void* sk, const void* v, int32_t
  * bit), with its workspace in a device array inside the library instead of a caller buffer,
  * and every launch on `stream` (no side stream).  No reference counterpart: for callers that
  * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  The array holds dism_hard_forward_noalloc_max_bytes() bytes (128 MiB) on every
+ * hipMalloc).  The array holds dism_hard_forward_noalloc_max_bytes() bytes (256 MiB) on every
  * device the library runs on, until the process ends; shapes whose
  * dism_hard_workspace_bytes exceeds it fail with DISM_ERR_INVALID.  All calls on one device
  * share the array: calls that overlap in time on one device (other streams, other threads)

@@ -82,7 +82,7 @@ def test_noalloc_forward_rejects_large_shapes():
     from dism_amd import _lib
     lib = _lib.load()
     limit = lib.dism_hard_forward_noalloc_max_bytes()
-    assert limit == 128 << 20
+    assert limit == 256 << 20
     b, n, h, r, dv = 4, 16384, 16, 8, 64
     assert _lib.workspace_bytes(b, n, h, r, dv, 0) > limit
     null = ctypes.c_void_p(16)  # never dereferenced: the size check comes first
