@@ -24,6 +24,7 @@ from . import _lib
 from ._checks import DTYPE_CODE, check_ctas, require
 from .hard_backward import backward_hard
 from .hard_forward import _forward_core, _packed_forward_core, hard_dlog_weights
+from .labels import vocab_labels_op
 from .varlen import VarlenLayout, packed_backward
 
 
@@ -169,6 +170,34 @@ def dism_core(q, k, sq, sk, v, q_lse, k_lse, idx_q, idx_k, direction, hard, rtau
             "soft rows need the soft DISM core, which the MI355X hard core does not provide")
     out = dism_core_hard(sq, sk, v, idx_q, idx_k, hard, rtau, layout=layout)
     return _SoftOperands.apply(out, q, k, q_lse, k_lse)
+
+
+def voc_dism(q, k, sq, sk, v, q_vocab, k_vocab, rtau, *, direction, hard, cu_seqlens=None,
+             layout=None, ctas=0, beta=1.0, hard_planner=None, all_hard=None):
+    """The reference's vocabulary entry (flash_dism/__init__.py:43-56, voc.py:7-40) for rows
+    that are all hard: q, k bf16 [B,N,H,D] are labelled by the exact codebook argmax against
+    q_vocab / k_vocab ([H,V,D] or shared [V,D], D in {32, 64, 128}; first index on ties) --
+    the indices the reference's interpolation kernel returns for its hard rows
+    (flash_dism/emb_kernel.py:96-156, reference oracle dism_v3_ref.py:159-162) -- and the
+    hard core runs on sq, sk, v with those labels (dism_core).  The interpolated embeddings
+    and their normalizers feed only the soft core, so for hard rows q, k, q_vocab and k_vocab
+    receive zero gradients and ``beta`` (the soft gate's vocabulary temperature, a positive
+    finite scalar or 0-dim tensor) does not change the result.  Soft rows raise
+    NotImplementedError; under torch.compile pass ``all_hard=True`` (see dism_core)."""
+    if hard_planner is not None:
+        raise NotImplementedError("the asynchronous hard planner is not part of the MI355X "
+                                  "hard core")
+    if not torch.compiler.is_compiling():
+        bv = float(beta.detach().item()) if isinstance(beta, torch.Tensor) else float(beta)
+        require(bv > 0.0 and bv != float("inf"), "beta must be a positive finite temperature")
+    require(q.dim() == 4 and tuple(k.shape) == tuple(q.shape), "q and k must be [B,N,H,D]")
+    idx_q = vocab_labels_op(q.detach().contiguous(), q_vocab.detach().contiguous())
+    idx_k = vocab_labels_op(k.detach().contiguous(), k_vocab.detach().contiguous())
+    b, n, h = sq.shape[0], sq.shape[1], sq.shape[2]
+    lse = torch.zeros((b, h, n), dtype=torch.float32, device=sq.device)
+    out = dism_core(q, k, sq, sk, v, lse, lse, idx_q, idx_k, direction, hard, rtau,
+                    cu_seqlens=cu_seqlens, layout=layout, ctas=ctas, all_hard=all_hard)
+    return _SoftOperands.apply(out, q_vocab, k_vocab, lse, lse)
 
 
 class _SoftOperands(torch.autograd.Function):

@@ -53,6 +53,19 @@ def vocab_labels(x, vocab, *, return_exact_count=False):
     return (out, scratch[:1]) if return_exact_count else out
 
 
+@torch.library.custom_op("dism_amd::vocab_labels", mutates_args=())
+def vocab_labels_op(x: torch.Tensor, vocab: torch.Tensor) -> torch.Tensor:
+    """vocab_labels as a torch.library operator (opaque to torch.compile, no autograd: the
+    argmax is piecewise constant)."""
+    return vocab_labels(x, vocab)
+
+
+@vocab_labels_op.register_fake
+def _vocab_labels_fake(x, vocab):
+    b, n, h, _ = x.shape
+    return x.new_empty((b, h, n), dtype=torch.int32)
+
+
 def vocab_argmax_labels(q, k, q_vocab, k_vocab):
     """(idx_q, idx_k) = codebook argmax labels of q against q_vocab and of k against k_vocab,
     the hard labels of dism_v3/python/flash_dism/reference/dism_v3_ref.py:159-162."""
