@@ -54,7 +54,7 @@ hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 struct Layout {
     int64_t corder, clab, ctab, bpos[2], blab[2], bplab[2], btab[2], shift, tmp[3];
     int64_t stage[2][2], bhcount[2], own[2], ocount, mode, onebyte;
-    int64_t pnb, prow, mcount, mdig, dflag, dlist, dcount, dbound, dcost;
+    int64_t pnb, prow, mcount, mdig, dflag, dlist, dcount, dbound, dcost, runs, runcnt;
     int64_t lvent, lvlc, lvlf, lvlk, lvmeta, lvq, lvqidx, lvkidx, lvF, lvFk, lvP, lvQ, lvY, lvZ, lvK;  // -1: none
     int64_t total;
     int prow_stride;
@@ -157,6 +157,8 @@ Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     L.dcount = take(4 * 4);
     L.dbound = take(N <= dism::DENSE_MAX_N ? BH * dism::dense_row_entries((int)N) * 2 : 0);
     L.dcost = take(BH * 8);
+    L.runs = take(BH * dism::RUN_CAP * 16);
+    L.runcnt = take(BH * 4);
     // level rows (dism_levels.hip) only where they can occur
     const bool lv = N <= dism::LEVEL_MAX_N && (int64_t)R * DV <= dism::LEVEL_RDV;
     const int64_t lent = (int64_t)dism::LEVEL_BUDGET * N, lmat = dism::LEVEL_MAX * N;
@@ -213,6 +215,8 @@ dism::Orders orders(const Layout& L, void* ws) {
     o.dcount = at<int32_t>(ws, L.dcount);
     o.dbound = at<uint16_t>(ws, L.dbound);
     o.dcost = at<unsigned long long>(ws, L.dcost);
+    o.runs = at<int4>(ws, L.runs);
+    o.runcnt = at<int32_t>(ws, L.runcnt);
     auto opt = [&](int64_t off) { return off < 0 ? nullptr : at<char>(ws, off); };
     o.lvent = reinterpret_cast<int32_t*>(opt(L.lvent));
     o.lvlc = reinterpret_cast<int32_t*>(opt(L.lvlc));

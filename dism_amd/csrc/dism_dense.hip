@@ -80,7 +80,8 @@ __device__ __forceinline__ void count_buckets(const int32_t* __restrict__ iq,
 // the row's flag from its collision count t (a 256-thread block's partial sums m)
 __device__ __forceinline__ void classify_finish(unsigned long long m, int n, int cn, long bh,
                                                 int32_t* __restrict__ dflag,
-                                                unsigned long long* __restrict__ dcost) {
+                                                unsigned long long* __restrict__ dcost,
+                                                int32_t* __restrict__ runcnt) {
     __shared__ unsigned long long s_red[4];
     const int tid = threadIdx.x;
 #pragma unroll
@@ -89,6 +90,7 @@ __device__ __forceinline__ void classify_finish(unsigned long long m, int n, int
     __syncthreads();
     if (tid == 0) {
         dcost[bh] = 0ull;  // the walk probe adds to it
+        if (runcnt) runcnt[bh] = 0;  // and lists the long runs
         const unsigned long long t = s_red[0] + s_red[1] + s_red[2] + s_red[3];
         dflag[bh] =
             (n <= DENSE_MAX_N && t * 64ull > (unsigned long long)cn * (unsigned long long)cn)
@@ -100,7 +102,8 @@ __device__ __forceinline__ void classify_finish(unsigned long long m, int n, int
 // rows are padded after the real tokens).  Rows longer than DENSE_MAX_N are never dense.
 __global__ __launch_bounds__(256) void dense_classify_kernel(
     const int32_t* __restrict__ iq, const int32_t* __restrict__ ik, int n, int cn,
-    int32_t* __restrict__ dflag, unsigned long long* __restrict__ dcost) {
+    int32_t* __restrict__ dflag, unsigned long long* __restrict__ dcost,
+    int32_t* __restrict__ runcnt) {
     __shared__ uint32_t s_cnt[2][DENSE_BUCKETS];
     const long bh = blockIdx.x;
     unsigned long long m = 0;
@@ -109,7 +112,7 @@ __global__ __launch_bounds__(256) void dense_classify_kernel(
         for (int x = threadIdx.x; x < DENSE_BUCKETS; x += 256)
             m += (unsigned long long)s_cnt[0][x] * s_cnt[1][x];
     }
-    classify_finish(m, n, cn, bh, dflag, dcost);
+    classify_finish(m, n, cn, bh, dflag, dcost, runcnt);
 }
 
 // Long rows (cn > DENSE_CLS_SEG): workgroup per (row, segment of DENSE_CLS_SEG positions)
@@ -134,7 +137,8 @@ __global__ __launch_bounds__(256) void dense_count_kernel(const int32_t* __restr
 __global__ __launch_bounds__(256) void dense_collide_kernel(const uint32_t* __restrict__ part,
                                                             long part_stride, int segs, int n,
                                                             int cn, int32_t* __restrict__ dflag,
-                                                            unsigned long long* __restrict__ dcost) {
+                                                            unsigned long long* __restrict__ dcost,
+                                                            int32_t* __restrict__ runcnt) {
     const long bh = blockIdx.x;
     const uint32_t* p = part + bh * part_stride;
     unsigned long long m = 0;
@@ -146,7 +150,7 @@ __global__ __launch_bounds__(256) void dense_collide_kernel(const uint32_t* __re
         }
         m += (unsigned long long)cq * ck;
     }
-    classify_finish(m, n, cn, bh, dflag, dcost);
+    classify_finish(m, n, cn, bh, dflag, dcost, runcnt);
 }
 
 // Row modes and lists (one workgroup, after the walk probe and the level lists): mode 2 for
@@ -711,12 +715,12 @@ __global__ __launch_bounds__(DENSE_THREADS) void dense_keys_kernel(PathArgs a) {
 // ---------------------------------------------------------------------------------------
 hipError_t launch_dense_classify(const int32_t* iq, const int32_t* ik, long BH, int n,
                                  int cls_n, int32_t* dflag, unsigned long long* dcost,
-                                 uint16_t* dbound, hipStream_t s) {
+                                 uint16_t* dbound, int32_t* runcnt, hipStream_t s) {
     const int cn = cls_n > 0 && cls_n < n ? cls_n : n;
     const int segs = (cn + DENSE_CLS_SEG - 1) / DENSE_CLS_SEG;
     if (segs <= 1 || n > DENSE_MAX_N || !dbound) {
         hipLaunchKernelGGL(dense_classify_kernel, dim3((unsigned)BH), dim3(256), 0, s, iq, ik,
-                           n, cn, dflag, dcost);
+                           n, cn, dflag, dcost, runcnt);
         return hipGetLastError();
     }
     // the segment counts go to the rows' boundary-row space, written later by the prepare
@@ -729,7 +733,7 @@ hipError_t launch_dense_classify(const int32_t* iq, const int32_t* ik, long BH, 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(dense_collide_kernel, dim3((unsigned)BH), dim3(256), 0, s, part, stride,
-                       segs, n, cn, dflag, dcost);
+                       segs, n, cn, dflag, dcost, runcnt);
     return hipGetLastError();
 }
 

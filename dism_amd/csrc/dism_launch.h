@@ -61,6 +61,13 @@ struct Orders {
     int32_t* dcount;      // [0]: mode-1 rows, [1]: rows of modes 1 and 2, [2]: mode-3 rows
     uint16_t* dbound;
     unsigned long long* dcost;  // [B*H] walk-cost estimate of the probe (dism_pairs.hip)
+    // long runs (dism_pairs.hip): per row, the run ends (diagonal i - j, end query i, exact
+    // length) of the diagonal match runs of at least RUN_MIN labels, as the walk probe finds
+    // them ([B*H][RUN_CAP] records, count in runcnt[B*H], cleared by the classification);
+    // a pair walk that reaches RUN_MIN labels takes its length from its run's end.  Only for
+    // calls without resets or documents.
+    int4* runs;
+    int32_t* runcnt;
     // level rows (mode 3, dism_levels.hip): dense rows whose sums are taken per match length.
     // Null unless N <= LEVEL_MAX_N and R * DV <= LEVEL_RDV.  Per (b,h) row:
     //   lvent  [LEVEL_MAX][2N]     level l's kept entries in list order (at (l - 1) 2N):
@@ -118,6 +125,8 @@ __host__ __device__ inline long level_segs(long n) {
 }
 
 constexpr int DENSE_MAX_N = 65536;   // longest row of the dense path (16-bit lengths)
+constexpr int RUN_MIN = 64;          // runs at least this long are listed (walks stop there)
+constexpr int RUN_CAP = 4096;        // listed runs per row (more: the walks run in full)
 constexpr int DENSE_BUCKETS = 4096;  // label buckets of the classification
 __host__ __device__ inline long dense_strip_offset(int s) { return 32L * s * (s - 1); }
 __host__ __device__ inline long dense_row_entries(int n) {
@@ -308,7 +317,7 @@ hipError_t launch_pairs_keys(const PathArgs& a, int R, int DV, int dtype, hipStr
 // boundary rows (before the dense kernels), then the tile kernels for the flagged hard rows
 hipError_t launch_dense_classify(const int32_t* iq, const int32_t* ik, long BH, int n,
                                  int cls_n, int32_t* dflag, unsigned long long* dcost,
-                                 uint16_t* dbound, hipStream_t s);
+                                 uint16_t* dbound, int32_t* runcnt, hipStream_t s);
 hipError_t launch_walk_probe(const PathArgs& a, hipStream_t s);
 // level lists of the dense rows that qualify (mode 1 -> 3; dism_sort.hip), before the row
 // lists of launch_dense_prepare

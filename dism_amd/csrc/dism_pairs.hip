@@ -125,19 +125,61 @@ __device__ __forceinline__ bool walk_step(const int32_t* __restrict__ q,
 // wb: the row's 16-bit strip boundaries (rows whose walks the probe found long, mode 2): the
 // walk stops at its 64-row strip's first row i0 and adds L[i0 - 1, j - c] from the boundary
 // row (unless a reset or document start at or above i0 ends the walk first).
+// The listed long runs of a row (sorted by diagonal, then end), or none.
+struct RunList {
+    const int4* p;
+    int n;
+};
+__device__ __forceinline__ RunList runs_of(const PathArgs& a, int bh) {
+    RunList r{nullptr, 0};
+    if (a.o.runs && !a.wlo && !a.dstart && !a.bound) {
+        const int c = a.o.runcnt[bh];
+        if (c <= RUN_CAP) {  // a complete list
+            r.p = a.o.runs + (long)bh * RUN_CAP;
+            r.n = c;
+        }
+    }
+    return r;
+}
+
+// length of the pair (i, j) inside a listed run: the run on diagonal i - j whose end is the
+// first at or after i; -1 when there is none covering i
+__device__ __forceinline__ int run_length(const RunList& rl, int i, int j) {
+    const int d = i - j;
+    int lo = 0, hi = rl.n;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        const int4 r = rl.p[mid];
+        if (r.x < d || (r.x == d && r.y < i)) lo = mid + 1;
+        else hi = mid;
+    }
+    if (lo < rl.n) {
+        const int4 r = rl.p[lo];
+        if (r.x == d && r.y - r.z < i) return r.z - (r.y - i);
+    }
+    return -1;
+}
+
 __device__ __forceinline__ int pair_length(const int32_t* __restrict__ q,
                                            const int32_t* __restrict__ k, int i, int j,
                                            const int32_t* __restrict__ bound, int strip, int n,
-                                           int dlo, const uint16_t* __restrict__ wb = nullptr) {
+                                           int dlo, const uint16_t* __restrict__ wb = nullptr,
+                                           RunList rl = RunList{nullptr, 0}) {
     const int s0 = wb ? (i & ~63) : 0;
     const int lo = bound ? (i / strip) * strip : (s0 > dlo ? s0 : dlo);
     int c = i - 1 >= lo ? 2 : 1;
     // the walk compares a batch of label pairs per step, all loads in flight together
     // (clamped indices; a comparison counts only while both positions are in range): 4 at
-    // first, so the usual short match costs one round trip, then 16 per step for long runs
+    // first, so the usual short match costs one round trip, then 16 per step for long runs;
+    // a walk that reaches RUN_MIN labels takes its length from its run's listed end
     if (c == 2 && walk_step<4>(q, k, i, j, lo, c)) {
-        while (walk_step<16>(q, k, i, j, lo, c)) {
+        bool on = true;
+        while (on && c < RUN_MIN) on = walk_step<16>(q, k, i, j, lo, c);
+        if (on && rl.n > 0 && !wb) {
+            const int L = run_length(rl, i, j);
+            if (L >= c) return L;
         }
+        while (on) on = walk_step<16>(q, k, i, j, lo, c);
     }
     if (bound && lo > 0 && i - c < lo && j - c >= 0) {
         const int jj = j - c;
@@ -289,7 +331,7 @@ static SortArgs sort_args(const SortArgs& sa, const PathArgs& pa) {
 
 hipError_t launch_classify(const SortArgs& sa, hipStream_t s) {
     return launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n, sa.o.dflag,
-                                 sa.o.dcost, sa.o.dbound, s);
+                                 sa.o.dcost, sa.o.dbound, sa.o.runcnt, s);
 }
 
 hipError_t launch_prepare_labels(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {
@@ -312,7 +354,7 @@ hipError_t launch_prepare_pairs(const SortArgs& sa, const PathArgs& pa, hipStrea
         if (e == hipSuccess) e = launch_prepare_lds(b, 1, 1, s);
     }
     if (e == hipSuccess) e = launch_owner_lists(pa, s);
-    if (e == hipSuccess && pa.n <= DENSE_MAX_N) e = launch_walk_probe(pa, s);
+    if (e == hipSuccess) e = launch_walk_probe(pa, s);
     return e != hipSuccess ? e : launch_dense_prepare(pa, s);
 }
 
@@ -332,7 +374,7 @@ hipError_t launch_prepare(const SortArgs& sa, const PathArgs& pa, hipStream_t s)
     if (e == hipSuccess) e = launch_sort(b, 1, 2, s);
     if (e == hipSuccess) e = launch_pair_plan(pa, s);
     if (e == hipSuccess) e = launch_owner_lists(pa, s);
-    if (e == hipSuccess && pa.n <= DENSE_MAX_N) e = launch_walk_probe(pa, s);
+    if (e == hipSuccess) e = launch_walk_probe(pa, s);
     return e != hipSuccess ? e : launch_dense_prepare(pa, s);
 }
 
@@ -472,21 +514,15 @@ __device__ __forceinline__ unsigned long long shfl_xor64(unsigned long long x, i
 constexpr int WALK_EXACT = 64;
 constexpr int WALK_COUNTED = 16;
 
+// the run's exact length (its walk, once per run end)
 __device__ __forceinline__ int probe_run(const int32_t* __restrict__ q,
                                          const int32_t* __restrict__ k, int i, int j, int dlo) {
     int c = i - 1 >= dlo ? 2 : 1;
     if (c == 2 && walk_step<4>(q, k, i, j, dlo, c)) {
-        while (c < WALK_EXACT && walk_step<16>(q, k, i, j, dlo, c)) {
+        while (walk_step<16>(q, k, i, j, dlo, c)) {
         }
     }
-    if (c < WALK_EXACT) return c;
-    int est = c;
-    for (int o = 2 * WALK_EXACT;; o *= 2) {
-        const int ii = i - (o - 1), jj = j - (o - 1);
-        if (ii < dlo || jj < 0 || q[ii] != k[jj]) break;
-        est = o;
-    }
-    return est;
+    return c;
 }
 
 template <int G>
@@ -500,6 +536,7 @@ __device__ __forceinline__ void probe_item(const PathArgs& a, int base, int k0, 
     const int32_t* k = a.ik + s.so;
     const int dlo = walk_lo(a, s.so, i);
     const bool next_reset = i + 1 < n && walk_lo(a, s.so, i + 1) == i + 1;
+    const bool listed = a.o.runs && !a.wlo && !a.dstart;
     unsigned long long cost = 0;
     for (int c0 = 0; c0 < s.maxcnt; c0 += G) {
         const int kq = c0 + sub;
@@ -507,8 +544,14 @@ __device__ __forceinline__ void probe_item(const PathArgs& a, int base, int k0, 
             const int j = kb[s.lo + kq];
             const bool ends = i + 1 >= n || j + 1 >= n || next_reset || q[i + 1] != k[j + 1];
             if (ends) {
-                const unsigned long long l = (unsigned long long)probe_run(q, k, i, j, dlo);
+                const int lr = probe_run(q, k, i, j, dlo);
+                const unsigned long long l = (unsigned long long)lr;
                 if (l >= WALK_COUNTED) cost += l * l / 2;
+                if (lr >= RUN_MIN && listed) {
+                    const int slot = atomicAdd(&a.o.runcnt[s.bh], 1);
+                    if (slot < RUN_CAP)
+                        a.o.runs[(long)s.bh * RUN_CAP + slot] = make_int4(i - j, i, lr, 0);
+                }
             }
         }
     }
@@ -523,8 +566,56 @@ __global__ __launch_bounds__(64 * WAVES) void walk_probe_kernel(PathArgs a) {
     });
 }
 
+// The listed runs of each row sorted by (diagonal, end): one workgroup per row, a bitonic
+// sort in LDS (lists of at most RUN_CAP records; a longer list is not used).
+__global__ __launch_bounds__(1024) void run_sort_kernel(PathArgs a) {
+    __shared__ unsigned long long s_k[RUN_CAP];
+    __shared__ int s_l[RUN_CAP];
+    const int bh = blockIdx.x, tid = threadIdx.x;
+    const int cnt = a.o.runcnt[bh];
+    if (cnt <= 1 || cnt > RUN_CAP) return;
+    int4* runs = a.o.runs + (long)bh * RUN_CAP;
+    int m = 1;
+    while (m < cnt) m <<= 1;
+    for (int x = tid; x < m; x += 1024) {
+        if (x < cnt) {
+            const int4 r = runs[x];
+            s_k[x] = ((unsigned long long)(uint32_t)r.x << 32) | (uint32_t)r.y;
+            s_l[x] = r.z;
+        } else {
+            s_k[x] = ~0ull;
+            s_l[x] = 0;
+        }
+    }
+    __syncthreads();
+    for (int size = 2; size <= m; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int x = tid; x < m; x += 1024) {
+                const int y = x ^ stride;
+                if (y > x) {
+                    const bool up = (x & size) == 0;
+                    const unsigned long long kx = s_k[x], ky = s_k[y];
+                    if ((kx > ky) == up) {
+                        s_k[x] = ky;
+                        s_k[y] = kx;
+                        const int t = s_l[x];
+                        s_l[x] = s_l[y];
+                        s_l[y] = t;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int x = tid; x < cnt; x += 1024)
+        runs[x] = make_int4((int)(s_k[x] >> 32), (int)(uint32_t)s_k[x], s_l[x], 0);
+}
+
 hipError_t launch_walk_probe(const PathArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(walk_probe_kernel, dim3(PAIR_GRID), dim3(64 * WAVES), 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !a.o.runs || a.wlo || a.dstart) return e;
+    hipLaunchKernelGGL(run_sort_kernel, dim3((unsigned)(a.B * a.H)), dim3(1024), 0, s, a);
     return hipGetLastError();
 }
 
@@ -542,6 +633,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
     const int32_t* k = a.ik + s.so;
     const int32_t* bnd = s.hard ? bound_of(a, s.bh) : nullptr;
     const uint16_t* wb = bnd ? nullptr : walk_bound_of(a, s.bh);
+    const RunList rl = runs_of(a, s.bh);
     const float* lut = a.lut + (long)s.h * a.lut_stride;
     const T* sq = reinterpret_cast<const T*>(a.sq);
     const T* sk = reinterpret_cast<const T*>(a.sk);
@@ -582,7 +674,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
         }
         float skr[R];
         load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
-        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb) : 1;
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb, rl) : 1;
         const float lw = lut[L];
         float mm = has && lw > m0 ? lw : m0;
         key = has ? (((unsigned long long)(unsigned)L << 32) | (unsigned)j) : 0ull;
@@ -629,7 +721,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
             const int kq = c0 + sub;
             if (kq < cnt) {
                 const int j = kb[lo + kq];
-                const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb);
+                const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb, rl);
                 const float lw = lut[L];
                 if (lw > m0) atomicMax(&S.m[sl], __float_as_uint(lw));
                 atomicMax(&S.key[sl], ((unsigned long long)(unsigned)L << 32) | (unsigned)j);
@@ -646,7 +738,7 @@ __device__ __forceinline__ void finish_item(const PathArgs& a, int base, int k0,
             const int kq = c0 + sub;
             if (kq < cnt) {
                 const int j = kb[lo + kq];
-                const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb);
+                const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb, rl);
                 const float p = exp2_fp32(lut[L] - m);
                 float skr[R];
                 load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
@@ -752,6 +844,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
     const int32_t* k = a.ik + s.so;
     const int32_t* bnd = s.hard ? bound_of(a, s.bh) : nullptr;
     const uint16_t* wb = bnd ? nullptr : walk_bound_of(a, s.bh);
+    const RunList rl = runs_of(a, s.bh);
     const float* lut = a.lut + (long)s.h * a.lut_stride;
     const float* glut = a.dlut + (long)s.h * a.lut_stride;
     const T* sq = reinterpret_cast<const T*>(a.sq);
@@ -786,7 +879,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
         }
         float skr[R];
         load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
-        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb) : 1;
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb, rl) : 1;
         float sdot = 0.0f;
 #pragma unroll
         for (int r = 0; r < R; ++r) sdot = __builtin_fmaf(sqr[r], skr[r], sdot);
@@ -827,7 +920,7 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
         const int kq = c0 + sub;
         if (kq < cnt) {
             const int j = kb[lo + kq];
-            const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb);
+            const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb, rl);
             float skr[R];
             load_row<T, R>(sk + (s.row0 + (long)j * a.H) * R, skr);
             float sdot = 0.0f;
@@ -928,6 +1021,7 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
     const int32_t* k = a.ik + s.so;
     const int32_t* bnd = s.hard ? bound_of(a, s.bh) : nullptr;
     const uint16_t* wb = bnd ? nullptr : walk_bound_of(a, s.bh);
+    const RunList rl = runs_of(a, s.bh);
     const float* lut = a.lut + (long)s.h * a.lut_stride;
     const float lut1 = lut[1];
     const T* sq = reinterpret_cast<const T*>(a.sq);
@@ -971,7 +1065,7 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
         const float l2 = a.lse2[s.so + i];
         float sqr[R];
         load_row<T, R>(sq + (s.row0 + (long)i * a.H) * R, sqr);
-        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb) : 1;
+        const int L = has ? pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb, rl) : 1;
         const float p = exp2_fp32(lut[L] - l2);
         float sdot = 0.0f;
 #pragma unroll
@@ -1009,7 +1103,7 @@ __device__ __forceinline__ void keys_item(const PathArgs& a, int base, int k0, i
         const int kq = c0 + sub;
         if (kq < cnt) {
             const int i = qb[lo + kq];
-            const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb);
+            const int L = pair_length(q, k, i, j, bnd, a.strip, n, walk_lo(a, s.so, i), wb, rl);
             const float l2 = a.lse2[s.so + i];
             const float p = exp2_fp32(lut[L] - l2);
             float sqr[R];

@@ -171,10 +171,12 @@ def _periodic_row(n, period, rng):
 
 
 def test_long_repeats_take_strip_bounded_walks():
-    """Rows with few label collisions but long repeats (a random 256-symbol pattern of period
-    200, and the same with one mutated position per period) are not dense; the walk probe
-    gives them strip boundaries (mode 2) so their bigram walks stop within 64 rows.  Lengths
-    stay exact: bit for bit against the CPU model's unbounded walks."""
+    """Rows with few label collisions but long repeats are not dense.  A random 256-symbol
+    pattern of period 200 (every run as long as the row allows: walk cost far above N^2)
+    gets strip boundaries from the walk probe (mode 2), so its bigram walks stop within 64
+    rows; the same pattern broken once per period (runs of at most 233 labels, cost below
+    N^2) stays mode 0 and its walks past RUN_MIN labels take their lengths from the probe's
+    list of run ends.  Lengths stay exact: bit for bit against the CPU model's walks."""
     import dism_amd
     from dism_amd.hard_forward import row_modes
     n, b, h = 4096, 1, 4
@@ -198,4 +200,4 @@ def test_long_repeats_take_strip_bounded_walks():
     _, _, state = dism_amd.forward_hard(*t, dev(q), dev(k), dev(hard), dev(tau),
                                         save_state=True)
     modes = host(row_modes(state["workspace"], t[0], t[2]))
-    assert modes.tolist() == [[0, 2, 2, 0]], modes
+    assert modes.tolist() == [[0, 2, 0, 0]], modes
