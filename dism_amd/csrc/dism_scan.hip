@@ -124,17 +124,15 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
     auto& s_r = s_r_all[wave_id()];
     __shared__ int s_slot_all[WAVES][WIN];
     auto& s_slot = s_slot_all[wave_id()];
-    // predecessor-label histogram of the current label group's keys, two 16-bit counts per
-    // word (one-byte labels), for the pair counts computed here (fwd_phase 1)
-    __shared__ uint32_t s_h_all[WAVES][128];
+    // predecessor-label histogram of the current label group's keys, one 32-bit count per
+    // predecessor byte (one-byte labels), for the pair counts computed here (fwd_phase 1)
+    __shared__ uint32_t s_h_all[WAVES][256];
     uint32_t* s_h = s_h_all[wave_id()];
     Item it;
     if (!scan_item(a, it)) return;
     // fwd_phase 1: rows whose labels differ in one byte, pair counts from the histogram;
     // 2: the other rows, pair counts from the plan (pnb); 0: every row from pnb
-    // (phase 1's per-wave histogram holds 16-bit counts: rows of 65536 and more keys take
-    // their pair counts from the plan, in phase 2)
-    const int onebyte = a.fwd_phase ? (a.o.onebyte[it.bh] && a.n < 65536) : 0;
+    const int onebyte = a.fwd_phase ? a.o.onebyte[it.bh] : 0;
     if ((a.fwd_phase == 1 && !onebyte) || (a.fwd_phase == 2 && onebyte)) return;
     const bool hist_nb = a.fwd_phase == 1;
     const int lshift = hist_nb ? a.o.shift[it.bh] : 0;
@@ -217,7 +215,7 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
             for (int c = 0; c < COLS; ++c) M[r][c] = 0.0f;
         int carry_cnt = 0, carry_last = -1;
         if (hist_nb) {
-            for (int x = lane; x < 128; x += 64) s_h[x] = 0u;
+            for (int x = lane; x < 256; x += 64) s_h[x] = 0u;
             asm volatile("" ::: "memory");
         }
         do {
@@ -248,7 +246,7 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
                 // histogram
                 const int pl = nbC;
                 int c = 0;
-                if (isq && pl >= 0) c = (int)((s_h[pl >> 1] >> (16 * (pl & 1))) & 0xffffu);
+                if (isq && pl >= 0) c = (int)s_h[pl];
                 // only keys before the window's last query can count
                 const unsigned long long qv = __ballot(isq && pl >= 0);
                 unsigned long long kv = __ballot(ok && !isq && pl >= 0);
@@ -260,7 +258,7 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
                 }
                 nb = isq ? c : 0;
                 asm volatile("" ::: "memory");
-                if (ok && !isq && pl >= 0) atomicAdd(&s_h[pl >> 1], 1u << (16 * (pl & 1)));
+                if (ok && !isq && pl >= 0) atomicAdd(&s_h[pl], 1u);
                 asm volatile("" ::: "memory");
             }
             const float m = (cnt > 0 && lut1 > 0.0f) ? lut1 : 0.0f;

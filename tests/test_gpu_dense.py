@@ -141,8 +141,8 @@ def test_dense_rows_with_non_finite_vectors():
 
 
 def test_phase1_counts_rows_past_65535():
-    """Rows of N >= 65536 take their bigram counts from the plan (the fused forward's phase-1
-    histogram holds 16-bit counts): 65792 keys share one (predecessor, label) bigram."""
+    """A row of N > 65535 whose keys share one (predecessor, label) bigram: 65792 keys, more
+    than a 16-bit count holds; the fused forward's phase-1 histogram counts them in 32 bits."""
     n = 65792
     q = np.ones((1, 1, n), np.int32)
     k = np.full((1, 1, n), 7, np.int32)
