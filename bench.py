@@ -406,7 +406,7 @@ def bench_train(args):
         "config": {"workload": cfg["workload"], "B": B, "H": H, "T": T, "d_qk": D, "d_v": DV,
                    "tau": args.tau, "carry_strip": strip, "forward_only": fwd_only,
                    "global_batch": B, "seq_len": T, "parallelism": "single-gpu"},
-        "row_modes": {str(m): int((modes == m).sum()) for m in (0, 1, 2, 3)},
+        "row_modes": {str(m): int((modes == m).sum()) for m in (0, 1, 2, 3, 4)},
         "kernel_ms": kern_ms,
         "roofline": roof,
     }
@@ -497,6 +497,21 @@ def layer_step_ms(args):
     e.record()
     torch.cuda.synchronize()
     return s.elapsed_time(e) / args.steps
+
+
+def _time(fn, steps, warmup):
+    """Mean ms per call of `fn` over `steps` calls between CUDA events, after `warmup` calls."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
 
 
 def _median_ms(fn, calls=20, samples=7, warmup=10):
@@ -598,7 +613,7 @@ def bench_refshape(args):
         modes = row_modes(ws, sq, v).cpu()
         ref = REF_5090[kind]
         result[kind] = {"forward_ms": f_ms, "backward_ms": b_ms, "fwd_bwd_ms": fb_ms,
-                        "row_modes": {str(m): int((modes == m).sum()) for m in (0, 1, 2, 3)},
+                        "row_modes": {str(m): int((modes == m).sum()) for m in (0, 1, 2, 3, 4)},
                         "bht_per_s_fwd_bwd": B * H * N / (fb_ms / 1e3),
                         "rtx5090_ms": ref,
                         "speedup_vs_rtx5090": {"forward": ref["forward"] / f_ms,

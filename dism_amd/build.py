@@ -19,7 +19,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("DISM_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["dism_aux.hip", "dism_sort.hip", "dism_msort.hip", "dism_pairs.hip", "dism_scan.hip",
-           "dism_packed.hip", "dism_dense.hip", "dism_levels.hip", "dism_decode.hip", "dism_vocab.hip", "dism_capi.cpp"]
+           "dism_packed.hip", "dism_dense.hip", "dism_levels.hip", "dism_prefix.hip", "dism_prefix_rows.hip", "dism_prefix_keys.hip", "dism_decode.hip", "dism_vocab.hip", "dism_capi.cpp"]
 
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",

@@ -56,6 +56,7 @@ struct Layout {
     int64_t stage[2][2], bhcount[2], own[2], ocount, mode, onebyte;
     int64_t pnb, prow, mcount, mdig, dflag, dlist, dcount, dbound, dcost, runs, runcnt;
     int64_t lvent, lvlc, lvlf, lvlk, lvmeta, lvq, lvqidx, lvkidx, lvF, lvFk, lvP, lvQ, lvY, lvZ, lvK;  // -1: none
+    int64_t pxT, pxB, pxU, pxS, pxR, pxK, pxKR;  // -1: none
     int64_t total;
     int prow_stride;
 };
@@ -153,7 +154,7 @@ Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     L.pnb = take(BH * N * 4);
     L.prow = take(BH * N * L.prow_stride * 4);
     L.dflag = take(BH * 4);
-    L.dlist = take(3 * BH * 4);
+    L.dlist = take(4 * BH * 4);
     L.dcount = take(4 * 4);
     L.dbound = take(N <= dism::DENSE_MAX_N ? BH * dism::dense_row_entries((int)N) * 2 : 0);
     L.dcost = take(BH * 8);
@@ -178,6 +179,16 @@ Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     L.lvY = lv ? take(BH * lent * DV * 4) : -1;
     L.lvZ = lv ? take(BH * lent * R * 4) : -1;
     L.lvK = lv ? take(BH * lent * R * 4) : -1;
+    // prefix rows (dism_prefix.hip) wherever dense rows can occur
+    const bool px = N <= dism::DENSE_MAX_N;
+    const int64_t pseg = px ? (int64_t)dism::px_segs((int)N) : 0;
+    L.pxT = px ? take(BH * pseg * R * DV * 4) : -1;
+    L.pxB = px ? take(BH * pseg * R * DV * 4) : -1;
+    L.pxU = px ? take(BH * pseg * R * DV * 4) : -1;
+    L.pxS = px ? take(BH * pseg * 16) : -1;
+    L.pxR = px ? take(BH * pseg * 16) : -1;
+    L.pxK = px ? take(BH * pseg * 8) : -1;
+    L.pxKR = px ? take(BH * pseg * 8) : -1;
     L.total = o;
     return L;
 }
@@ -233,6 +244,13 @@ dism::Orders orders(const Layout& L, void* ws) {
     o.lvY = reinterpret_cast<float*>(opt(L.lvY));
     o.lvZ = reinterpret_cast<float*>(opt(L.lvZ));
     o.lvK = reinterpret_cast<float*>(opt(L.lvK));
+    o.pxT = reinterpret_cast<float*>(opt(L.pxT));
+    o.pxB = reinterpret_cast<float*>(opt(L.pxB));
+    o.pxU = reinterpret_cast<float*>(opt(L.pxU));
+    o.pxS = reinterpret_cast<float4*>(opt(L.pxS));
+    o.pxR = reinterpret_cast<float4*>(opt(L.pxR));
+    o.pxK = reinterpret_cast<float2*>(opt(L.pxK));
+    o.pxKR = reinterpret_cast<float2*>(opt(L.pxKR));
     return o;
 }
 
@@ -294,6 +312,7 @@ int32_t prepare_impl(const void* sq, const void* sk, const void* v, int32_t dtyp
     sa.BH = B * H;
     sa.n = (int)N;
     sa.cls_n = (int)cls_n;
+    sa.prefix = wlo == nullptr && (cls_n <= 0 || cls_n >= N) ? 1 : 0;
     for (int t = 0; t < 3; ++t) sa.tmp[t] = at<int32_t>(workspace, L.tmp[t]);
     sa.o = orders(L, workspace);
     sa.pnb = at<int32_t>(workspace, L.pnb);
@@ -436,8 +455,11 @@ int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t
     if ((st2 = hip_status(dism::launch_dense_forward(a, R, DV, dtype, S(stream)),
                           "hard readout dense rows")))
         return st2;
-    return hip_status(dism::launch_level_forward(a, R, DV, dtype, S(stream)),
-                      "hard readout level rows");
+    if ((st2 = hip_status(dism::launch_level_forward(a, R, DV, dtype, S(stream)),
+                          "hard readout level rows")))
+        return st2;
+    return hip_status(dism::launch_prefix_forward(a, R, DV, dtype, S(stream)),
+                      "hard readout prefix rows");
 }
 
 int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t dtype,
@@ -465,6 +487,7 @@ int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t
     for (int t = 0; t < 3; ++t) sa.tmp[t] = at<int32_t>(workspace, L.tmp[t]);
     sa.o = orders(L, workspace);
     sa.pnb = at<int32_t>(workspace, L.pnb);
+    sa.prefix = 1;
     dism::PathArgs a = path(L, workspace, B, N, H, iq, ik, hard, boundary, strip, lut, lut_stride);
     a.sq = sq;
     a.sk = sk;
@@ -512,7 +535,10 @@ int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t
         return st;
     if ((st = hip_status(dism::launch_dense_forward(a, R, DV, dtype, s), "hard forward dense rows")))
         return st;
-    return hip_status(dism::launch_level_forward(a, R, DV, dtype, s), "hard forward level rows");
+    if ((st = hip_status(dism::launch_level_forward(a, R, DV, dtype, s),
+                         "hard forward level rows")))
+        return st;
+    return hip_status(dism::launch_prefix_forward(a, R, DV, dtype, s), "hard forward prefix rows");
 }
 
 }  // extern "C"
@@ -650,8 +676,11 @@ int32_t dism_hard_backward_queries(const void* sq, const void* sk, const void* v
     if ((st = hip_status(dism::launch_dense_rows(a, R, DV, dtype, S(stream)),
                          "hard backward dense rows")))
         return st;
-    return hip_status(dism::launch_level_rows(a, R, DV, dtype, S(stream)),
-                      "hard backward level rows");
+    if ((st = hip_status(dism::launch_level_rows(a, R, DV, dtype, S(stream)),
+                         "hard backward level rows")))
+        return st;
+    return hip_status(dism::launch_prefix_rows(a, R, DV, dtype, S(stream)),
+                      "hard backward prefix rows");
 }
 
 int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, const void* dout,
@@ -675,8 +704,11 @@ int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, c
     if ((st = hip_status(dism::launch_dense_keys(a, R, DV, dtype, S(stream)),
                          "hard backward dense keys")))
         return st;
-    return hip_status(dism::launch_level_keys(a, R, DV, dtype, S(stream)),
-                      "hard backward level keys");
+    if ((st = hip_status(dism::launch_level_keys(a, R, DV, dtype, S(stream)),
+                         "hard backward level keys")))
+        return st;
+    return hip_status(dism::launch_prefix_keys(a, R, DV, dtype, S(stream)),
+                      "hard backward prefix keys");
 }
 
 int32_t dism_hard_backward_key_pairs(const void* sq, const void* sk, const void* v,
@@ -1096,7 +1128,9 @@ int32_t dism_hard_prefill(const void* sq, const void* sk, const void* v, int32_t
     if ((st = hip_status(dism::launch_scan_forward(a, R, DV, dtype, s), what))) return st;
     if ((st = hip_status(dism::launch_pairs_finish(a, R, DV, dtype, s), what))) return st;
     if ((st = hip_status(dism::launch_dense_forward(a, R, DV, dtype, s), what))) return st;
-    return hip_status(dism::launch_level_forward(a, R, DV, dtype, s), what);
+    const hipError_t le = dism::launch_level_forward(a, R, DV, dtype, s);
+    if (le != hipSuccess) return hip_status(le, what);
+    return hip_status(dism::launch_prefix_forward(a, R, DV, dtype, s), what);
 }
 
 int64_t dism_decoder_state_bytes(int64_t rows, int32_t R, int32_t DV, int64_t capacity,

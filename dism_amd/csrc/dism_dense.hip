@@ -155,18 +155,19 @@ __global__ __launch_bounds__(256) void dense_collide_kernel(const uint32_t* __re
 
 // Row modes and lists (one workgroup, after the walk probe and the level lists): mode 2 for
 // the sparse rows whose walk-cost estimate exceeds N^2; the mode-1 rows ascending in
-// dlist[0..), the rows of modes 1 and 2 in dlist[BH..), the mode-3 rows in dlist[2 BH..),
-// their counts in dcount[0..2].
+// dlist[0..), the rows of modes 1 and 2 in dlist[BH..), the mode-3 rows in dlist[2 BH..), the
+// mode-4 rows in dlist[3 BH..), their counts in dcount[0..3].
 __global__ __launch_bounds__(1024) void dense_mode_kernel(int32_t* __restrict__ dflag,
                                                           const unsigned long long* __restrict__ dcost,
                                                           int BH, int n,
                                                           int32_t* __restrict__ dlist,
                                                           int32_t* __restrict__ dcount) {
-    __shared__ int s_w[3][16];
-    __shared__ int s_base[3];
+    constexpr int NL = 4;
+    __shared__ int s_w[NL][16];
+    __shared__ int s_base[NL];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const unsigned long long nn = (unsigned long long)n * (unsigned long long)n;
-    if (tid < 3) s_base[tid] = 0;
+    if (tid < NL) s_base[tid] = 0;
     __syncthreads();
     for (int c0 = 0; c0 < BH; c0 += 1024) {
         const int x = c0 + tid;
@@ -175,26 +176,27 @@ __global__ __launch_bounds__(1024) void dense_mode_kernel(int32_t* __restrict__ 
             mode = 2;
             dflag[x] = 2;
         }
-        const unsigned long long ms[3] = {__ballot(mode == 1), __ballot(mode == 1 || mode == 2),
-                                          __ballot(mode == 3)};
-        if (lane < 3) s_w[lane][w] = __popcll(ms[lane]);
+        const unsigned long long ms[NL] = {__ballot(mode == 1), __ballot(mode == 1 || mode == 2),
+                                           __ballot(mode == 3), __ballot(mode == 4)};
+        if (lane < NL) s_w[lane][w] = __popcll(ms[lane]);
         __syncthreads();
-        int base[3] = {s_base[0], s_base[1], s_base[2]};
+        int base[NL] = {s_base[0], s_base[1], s_base[2], s_base[3]};
         for (int v = 0; v < w; ++v)
-            for (int c = 0; c < 3; ++c) base[c] += s_w[c][v];
+            for (int c = 0; c < NL; ++c) base[c] += s_w[c][v];
         const unsigned long long below = (1ull << lane) - 1ull;
         if (mode == 1) dlist[base[0] + __popcll(ms[0] & below)] = x;
         if (mode == 1 || mode == 2) dlist[BH + base[1] + __popcll(ms[1] & below)] = x;
         if (mode == 3) dlist[2 * BH + base[2] + __popcll(ms[2] & below)] = x;
+        if (mode == 4) dlist[3 * BH + base[3] + __popcll(ms[3] & below)] = x;
         __syncthreads();
-        if (tid < 3) {
+        if (tid < NL) {
             int t = 0;
             for (int v = 0; v < 16; ++v) t += s_w[tid][v];
             s_base[tid] += t;
         }
         __syncthreads();
     }
-    if (tid < 3) dcount[tid] = s_base[tid];
+    if (tid < NL) dcount[tid] = s_base[tid];
 }
 
 // query i starts its match afresh (query reset or document start)

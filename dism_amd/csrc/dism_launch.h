@@ -55,10 +55,12 @@ struct Orders {
     // j < 64s, of every 64-row query strip s >= 1 of the rows of modes 1 and 2
     // ([B*H][dense_row_entries(N)], only when N <= DENSE_MAX_N)
     int32_t* dflag;       // row mode: 0 sparse, 1 dense, 2 sparse with strip-bounded walks,
-                          // 3 dense level row (dism_levels.hip)
+                          // 3 dense level row (dism_levels.hip), 4 dense prefix row
+                          // (dism_prefix.hip)
     int32_t* dlist;       // mode-1 rows, then (at dlist + B*H) the rows of modes 1 and 2, then
-                          // (at dlist + 2*B*H) the mode-3 rows
-    int32_t* dcount;      // [0]: mode-1 rows, [1]: rows of modes 1 and 2, [2]: mode-3 rows
+                          // (at dlist + 2*B*H) the mode-3 rows, (at dlist + 3*B*H) the mode-4
+    int32_t* dcount;      // [0]: mode-1 rows, [1]: rows of modes 1 and 2, [2]: mode-3 rows,
+                          // [3]: mode-4 rows
     uint16_t* dbound;
     unsigned long long* dcost;  // [B*H] walk-cost estimate of the probe (dism_pairs.hip)
     // long runs (dism_pairs.hip): per row, the run ends (diagonal i - j, end query i, exact
@@ -110,6 +112,26 @@ struct Orders {
     float* lvY;
     float* lvZ;
     float* lvK;
+    // prefix rows (mode 4, dism_prefix.hip): dense rows in which every label has one
+    // predecessor label, so every valid pair's match runs to the key's row start.  Per (b,h)
+    // row, per segment s of PREFIX_SEG entries of the combined order ([px_segs(N)]):
+    //   pxT, pxB [..][R*DV]  the forward's / query side's weighted key sums of the segment's
+    //                        last group piece ([r][d]), overwritten by the chain with the
+    //                        state before the segment (pxB: the d ln W / d tau weighted ones)
+    //   pxU      [..][R*DV]  the key side's query sums of the first piece, then the state
+    //                        after the segment
+    //   pxS      [..]        {M, S, SG, (last key + 1) | PX_HAS | PX_RESET} per segment
+    //   pxR      [..]        the state before the segment {mu, PS, PSG, last key}
+    //   pxK      [..]        key side {lambda, has | restart << 1}
+    //   pxKR     [..]        the state after the segment {nu, has}
+    // Null unless N <= DENSE_MAX_N.
+    float* pxT;
+    float* pxB;
+    float* pxU;
+    float4* pxS;
+    float4* pxR;
+    float2* pxK;
+    float2* pxKR;
 };
 constexpr int LEVEL_MAX_N = 4096;   // longest level row (16-bit list indices and counts)
 constexpr int LEVEL_MAX = 32;       // most levels (longest match) of a level row
@@ -123,6 +145,13 @@ constexpr int LEVEL_META = 2 * LEVEL_MAX + 4;
 __host__ __device__ inline long level_segs(long n) {
     return (long)LEVEL_BUDGET * n / LEVEL_SEG + LEVEL_MAX;
 }
+
+// row modes computed whole by the dense, level or prefix kernels: no bigram-pair plan (the
+// prepare's role 1 skips them, so their staged owner records and counts are not written)
+__host__ __device__ inline bool pairless_mode(int m) { return m == 1 || m == 3 || m == 4; }
+
+constexpr int PREFIX_SEG = 64;       // combined-order entries per prefix-row segment
+__host__ __device__ inline int px_segs(int n) { return (2 * n + PREFIX_SEG - 1) / PREFIX_SEG; }
 
 constexpr int DENSE_MAX_N = 65536;   // longest row of the dense path (16-bit lengths)
 constexpr int RUN_MIN = 64;          // runs at least this long are listed (walks stop there)
@@ -149,6 +178,8 @@ struct SortArgs {
     int role_base;          // first role of a launch (blockIdx.y + role_base)
     int lds_rows;           // rows with one label byte go to prepare_lds_kernel (sort skips them)
     int cls_n;              // positions the dense-row classification counts (0: all n)
+    int prefix;             // 1: dense rows may become prefix rows (fixed-length rows of all
+                            // n positions, no resets or documents; o.pxT set)
 };
 
 // Per query row record (prow, valid when the row's bigram pair count pnb > 0):
@@ -327,6 +358,14 @@ hipError_t launch_level_prep(const PathArgs& a, hipStream_t s);
 hipError_t launch_level_forward(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_level_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_level_keys(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
+// prefix rows: the classification (mode 1 -> 4, right after the dense-row flags), forward
+// (segment totals, chain, readout), backward query rows, backward keys (dism_prefix.hip);
+// no-ops without prefix rows
+hipError_t launch_prefix_check(const int32_t* iq, const int32_t* ik, long BH, int n,
+                               int32_t* dflag, hipStream_t s);
+hipError_t launch_prefix_forward(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
+hipError_t launch_prefix_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
+hipError_t launch_prefix_keys(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_dense_prepare(const PathArgs& a, hipStream_t s);
 hipError_t launch_dense_forward(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_dense_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);

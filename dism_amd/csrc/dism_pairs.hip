@@ -260,7 +260,7 @@ __global__ __launch_bounds__(LIST_THREADS) void owner_lists_kernel(PathArgs a) {
     const int32_t* dense = a.o.dflag;  // dense rows' pairs belong to dism_dense.hip
     int before[3] = {0, 0, 0}, total[3] = {0, 0, 0};
     for (int r = tid; r < BH; r += LIST_THREADS) {
-        const bool drop = dense[r] == 1 || dense[r] == 3;
+        const bool drop = pairless_mode(dense[r]);
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             const int v = drop ? 0 : cnt[(long)r * 4 + c];
@@ -298,7 +298,7 @@ __global__ __launch_bounds__(LIST_THREADS) void owner_lists_kernel(PathArgs a) {
     int4* own = a.o.own[side];
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
-        const int m = (dense[bh] == 1 || dense[bh] == 3) ? 0 : cnt[(long)bh * 4 + c];
+        const int m = pairless_mode(dense[bh]) ? 0 : cnt[(long)bh * 4 + c];
         const int4* src = a.o.stage[side][c == 1 ? 1 : 0] + so;
         for (int k = tid; k < m; k += LIST_THREADS) {
             const int4 rec = src[c == 2 ? n - 1 - k : k];
@@ -330,8 +330,12 @@ static SortArgs sort_args(const SortArgs& sa, const PathArgs& pa) {
 }
 
 hipError_t launch_classify(const SortArgs& sa, hipStream_t s) {
-    return launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n, sa.o.dflag,
-                                 sa.o.dcost, sa.o.dbound, sa.o.runcnt, s);
+    const hipError_t e = launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n,
+                                               sa.o.dflag, sa.o.dcost, sa.o.dbound, sa.o.runcnt,
+                                               s);
+    if (e != hipSuccess || !sa.prefix || !sa.o.pxT || sa.n > DENSE_MAX_N) return e;
+    if (sa.cls_n > 0 && sa.cls_n < sa.n) return e;
+    return launch_prefix_check(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.o.dflag, s);
 }
 
 hipError_t launch_prepare_labels(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {

@@ -85,7 +85,7 @@ __device__ __forceinline__ bool scan_item(const PathArgs& a, Item& it) {
     // dense hard rows are computed whole by the tile kernels (dism_dense.hip) or the level
     // kernels (dism_levels.hip)
     const int dmode = a.o.dflag[it.bh];
-    if ((dmode == 1 || dmode == 3) && a.hard[it.bh]) return false;
+    if (pairless_mode(dmode) && a.hard[it.bh]) return false;
     it.bucket = item & 255;
     it.b = it.bh / a.H;
     it.h = it.bh - it.b * a.H;

@@ -521,7 +521,7 @@ __global__ __launch_bounds__(SORT_THREADS) void prepare_lds_kernel(SortArgs a) {
     // dense rows (classified before the prepare) have no bigram-pair work: role 1 skips them
     // (the owner lists drop them; their label order, role 0, stays, e.g. for the decoder)
     const int dmode = a.o.dflag[bh];
-    if (role == 1 && (dmode == 1 || dmode == 3)) return;
+    if (role == 1 && pairless_mode(dmode)) return;
     if (!lds_ok) {
         // the global-memory path takes this row: its combined label order here (the LDS
         // pool as the passes' scratch), the bigram orders in sort_kernel roles 1-2

@@ -81,6 +81,8 @@ def lib():
         L.orc_row_modes.argtypes = [P, P, i32, i64, i32, i32, P]
         L.orc_level_row.restype = i32
         L.orc_level_row.argtypes = [P, P, i64, i32, i32]
+        L.orc_prefix_row.restype = i32
+        L.orc_prefix_row.argtypes = [P, P, i64]
         _lib = L
     return _lib
 
@@ -184,12 +186,20 @@ def dense_rows(iq, ik, hard):
 def row_modes(iq, ik, R, DV):
     """Row modes of a fixed-length call without resets as the HIP path chooses them (every row
     taken as hard): uint8 [B,H], 0 decomposed, 1 direct (dense), 3 levels (dense rows with
-    labels below 256, N <= 4096, R * DV <= 512 and at most 32 levels: level_count)."""
+    labels below 256, N <= 4096, R * DV <= 512 and at most 32 levels: level_count), 4 prefix
+    (dense rows whose every label has one predecessor label: prefix_row)."""
     iq, ik = _i32(iq), _i32(ik)
     B, H, N = iq.shape
     out = np.empty(B * H, dtype=np.uint8)
     lib().orc_row_modes(_p(iq), _p(ik), B * H, N, R, DV, _p(out))
     return out.reshape(B, H)
+
+
+def prefix_row(q, k):
+    """1 when one row (q, k [N]) is a prefix row: dense, and every label has one predecessor
+    label over both sides (so every valid pair's match runs to the key's row start)."""
+    q, k = _i32(q), _i32(k)
+    return int(lib().orc_prefix_row(_p(q), _p(k), q.shape[-1]))
 
 
 def level_count(q, k, R, DV):
@@ -239,12 +249,13 @@ def _dense_arg(dense, B, H):
 def forward(sq, sk, v, iq, ik, hard, lut, threads=0, direct=False, reset=None, dense=None):
     """CPU model forward.  Returns (O fp32 [B,N,H,DV], lse2 [B,H,N], Lmax, argmax).
 
-    direct=False: the sequence the HIP kernels reproduce bit for bit -- per row, the level
-    definition for level rows (row_modes 3), the direct (pairwise) definition for the other
+    direct=False: the sequence the HIP kernels reproduce bit for bit -- per row, the prefix
+    definition for prefix rows (row_modes 4), the level definition for level rows (3), the direct (pairwise) definition for the other
     rows classified dense (dense_rows) and the decomposed one for the rest;  direct=True: the
     pairwise definition for every row.
     dense: optional [B,H] (or scalar) override of the row modes (0 decomposed, 1 direct,
-    3 levels where the row qualifies, else direct).
+    3 levels where the row qualifies, else direct, 4 the prefix definition, which assumes a
+    prefix row).
     reset: optional [B,H,N] bool query resets (inference semantics: a reset query's match
     starts afresh at that query; keys stay)."""
     sq, sk, v, lut = _f32(sq), _f32(sk), _f32(v), _f32(lut)

@@ -647,9 +647,459 @@ int orc_level_row(const int32_t* q, const int32_t* k, long N, int R, int DV) {
     return L.nlev;
 }
 
-/* row mode as the HIP path chooses it: 0 decomposed, 1 direct, 3 levels */
+/* ---------------- prefix rows ----------------
+ * A hard row is a prefix row when it is dense (orc_dense_row), has no query resets, and
+ * every label has one predecessor label: for all positions p, p' >= 1 on either side whose
+ * labels are equal, the labels at p - 1 and p' - 1 (on the same sides) are equal too
+ * (all-identical labels, a period of distinct labels; checked per label bucket,
+ * prefix_labels).  Then a valid pair (i, j <= i,
+ * iq[i] == ik[j]) with j >= 1 has iq[i-1] == ik[j-1], and by induction on j its match
+ * reaches the key's row start: L_ij = j + 1.  The weight exp2(LUT[j+1] - m) of a pair is
+ * then a function of the key, and a query's sum over its valid keys is a prefix sum over
+ * its label group -- with a running maximum, because LUT[j+1] grows with j past the fp32
+ * range of exp2 on long rows.
+ *
+ * The list is the combined label order: the 2N entries e = 2p + s (s = 0 key, 1 query at
+ * position p) sorted by (label, p, s), so a label group is a run of entries and a query's
+ * valid keys are the keys before it in its run.  Segments of PREFIX_SEG entries.  With
+ * l_t = LUT[p_t + 1] for a key entry t:
+ *
+ * forward, per segment s:  over the keys t of its last piece (the entries of the group of
+ *   its last entry that lie in s), ascending: M_s = max l_t; w = exp2(l_t - M_s);
+ *   T_s[r][d] = fma(w * sk_t[r], v_t[d], T_s[r][d]); S_s = S_s + w; K_s = p of the last key.
+ * prefix chain, s ascending, state (mu = 0, P = 0, PS = 0, lk = -1):  Pre_s = state; when
+ *   the last piece's group starts in s (at or after its first entry) the state restarts;
+ *   when the piece has keys: mu' = max(mu, M_s), g = exp2(mu - mu'), h = exp2(M_s - mu'),
+ *   P[e] = fma(h, T_s[e], P[e] * g), PS = fma(h, S_s, PS * g), mu = mu', lk = K_s.
+ * query at entry x of segment s: it starts from Pre_s when its group began before s, else
+ *   from the empty state; its own keys are those of its group in s before it.
+ *   m = max(mu, l_t over its own keys); f = exp2(mu - m);
+ *   y[d] = (chain_r fma(sq[r], P[r][d])) * f (0 from the empty state);
+ *   den = fma(PS, f, exp2(-m)); own keys ascending: p = exp2(l_t - m); den = den + p;
+ *   s = chain_r fma(sq[r], sk_t[r]); y[d] = fma(p * s, v_t[d], y[d]);
+ *   out = y / den; lse2 = m + log2(den); jarg = its last valid key (own, else lk); lmax =
+ *   jarg + 1 (0 with no key).
+ *
+ * backward, query side (l2 = lse2_i, c = G[i + 1], G the d ln W / d tau table): the same
+ *   segments and chain carry also sums weighted by G - G0_s, centred on the G of the piece's
+ *   last key (G grows like L, so uncentred sums would cancel): TB_s[r][d] =
+ *   fma((w * (G_t - G0_s)) * sk_t[r], v_t[d], .), SG_s = fma(w, G_t - G0_s, .); the chain
+ *   recentres its state first: PB[e] = fma(h, TB_s[e], fma(gam - G0_s, P[e], PB[e]) * g),
+ *   PSG = fma(h, SG_s, fma(gam - G0_s, PS, PSG) * g), gam = G0_s.  kappa = exp2(mu - l2);
+ *   zP[r] = lane_reduce(dO, P[r]), zB[r] = lane_reduce(dO, PB[r]) (0 from the empty state);
+ *   dq[r] = zP[r] * kappa;  u0 = wave_tree(sq[r] * zP[r]) * kappa,
+ *   W0 = wave_tree(sq[r] * zB[r]) * kappa (term r on lane r * 64/R);  z0 = PS * kappa;
+ *   cg = c - gam; vv0 = fma(-cg, z0, PSG * kappa); w0 = fma(-cg, u0, W0).  Own keys, lane = entry slot in
+ *   the segment: p = exp2(l_t - l2); s = chain_r(sq . sk_t); e = chain_d(dO . v_t);
+ *   ps = p * s; pe = p * e; pse = ps * e; g = G_t - c;  u = u0 + wave_tree(pse),
+ *   vv = vv0 + wave_tree(p * g), w = w0 + wave_tree(pse * g), z = z0 + wave_tree(p),
+ *   dq[r] = dq[r] + lane_tree(pe * sk_t[r]);  rowtau as the direct definition's.
+ * backward, key side, per segment s: over the queries of its first piece (the entries of the
+ *   group of its first entry that lie in s), descending: lam_s = min l2_i;
+ *   w = exp2(lam_s - l2_i); U_s[r][d] = fma(w * sq_i[r], dO_i[d], U_s[r][d]).
+ *   suffix chain, s descending, state (none):  Suf_s = state; when the first piece's group
+ *   ends in s the state restarts; when the piece has queries: the first sets (nu = lam_s,
+ *   Q = U_s), later ones nu' = min(nu, lam_s), g = exp2(nu' - nu), h = exp2(nu' - lam_s),
+ *   Q[e] = fma(h, U_s[e], Q[e] * g), nu = nu'.
+ *   key at entry x of s: from Suf_s when its group continues past s: phi = exp2(l_j - nu),
+ *   dv[d] = (chain_r fma(sk[r], Q[r][d])) * phi, dk[r] = lane_reduce(v, Q[r]) * phi (else
+ *   0); own queries (its group's queries after it in s), lane = slot:
+ *   p = exp2(l_j - l2_i); s, e, ps, pe as above; dk[r] = dk[r] + lane_tree(pe * sq_i[r]);
+ *   ascending: dv[d] = fma(ps, dO_i[d], dv[d]).
+ * wave_tree: xor butterfly t[l] = t[l] + t[l ^ o], o = 32, ..., 1, over 64 lanes (0 where no
+ * term); lane_tree: lane_reduce's order over per-lane terms. */
+#define PREFIX_SEG 64L
+
+static float lane_reduce(const float* a, const float* b, int DV, int R);
+
+/* 1 when every label bucket (label_bucket, the classification's hash) holds one label over
+ * both sides and one predecessor label over the positions >= 1 of both sides -- every label
+ * then has one predecessor label.  (A row whose distinct labels share a bucket is not taken,
+ * whatever its predecessors: the HIP check keeps one slot per bucket.) */
+static int prefix_labels(const int32_t* q, const int32_t* k, long N) {
+    uint64_t* lab = (uint64_t*)calloc(4096, sizeof(uint64_t));
+    uint64_t* pred = (uint64_t*)calloc(4096, sizeof(uint64_t));
+    int ok = 1;
+    for (long p = 0; p < N && ok; ++p)
+        for (int side = 0; side < 2 && ok; ++side) {
+            const int32_t* L = side ? k : q;
+            const uint32_t b = label_bucket(L[p]);
+            const uint64_t t = (1ull << 32) | (uint32_t)L[p];
+            if (!lab[b]) lab[b] = t;
+            else if (lab[b] != t) ok = 0;
+            if (p >= 1 && ok) {
+                const uint64_t u = (1ull << 32) | (uint32_t)L[p - 1];
+                if (!pred[b]) pred[b] = u;
+                else if (pred[b] != u) ok = 0;
+            }
+        }
+    free(lab);
+    free(pred);
+    return ok;
+}
+
+int orc_prefix_row(const int32_t* q, const int32_t* k, long N) {
+    return orc_dense_row(q, k, N, 1) && prefix_labels(q, k, N);
+}
+
+static int cmp_entry(const void* a, const void* b, void* ctx) {
+    const int32_t* const* lab = (const int32_t* const*)ctx;
+    const int32_t x = *(const int32_t*)a, y = *(const int32_t*)b;
+    const uint32_t lx = (uint32_t)lab[x & 1][x >> 1], ly = (uint32_t)lab[y & 1][y >> 1];
+    if (lx != ly) return lx < ly ? -1 : 1;
+    return x < y ? -1 : x > y;
+}
+
+/* the combined label order E[2N] and, per entry, its group's start gs and end ge */
+static void prefix_list(const int32_t* q, const int32_t* k, long N, int32_t* E, int32_t* gs,
+                        int32_t* ge) {
+    const int32_t* lab[2] = {k, q};
+    const long M2 = 2 * N;
+    for (long e = 0; e < M2; ++e) E[e] = (int32_t)e;
+    qsort_r(E, (size_t)M2, sizeof(int32_t), cmp_entry, (void*)lab);
+    for (long x = 0; x < M2; ++x) {
+        const int same = x > 0 && lab[E[x] & 1][E[x] >> 1] == lab[E[x - 1] & 1][E[x - 1] >> 1];
+        gs[x] = same ? gs[x - 1] : (int32_t)x;
+    }
+    for (long x = M2 - 1; x >= 0; --x) {
+        const int same = x + 1 < M2 &&
+                         lab[E[x] & 1][E[x] >> 1] == lab[E[x + 1] & 1][E[x + 1] >> 1];
+        ge[x] = same ? ge[x + 1] : (int32_t)(x + 1);
+    }
+}
+
+/* xor-butterfly sum of 64 lane terms (lane 0's result; every lane's is the same) */
+static float wave_tree(const float* t0) {
+    float t[64], u[64];
+    memcpy(t, t0, sizeof(t));
+    for (int o = 32; o >= 1; o /= 2) {
+        for (int l = 0; l < 64; ++l) u[l] = t[l] + t[l ^ o];
+        memcpy(t, u, sizeof(t));
+    }
+    return t[0];
+}
+
+/* lane_reduce's order over 64 per-lane terms t[l] (read with stride st) */
+static float lane_tree(const float* t0, long st, int R) {
+    float t[64];
+    const int G = 64 / R;
+    for (int l = 0; l < 64; ++l) t[l] = t0[l * st];
+    for (int m = 32; m >= G; m /= 2)
+        for (int l = 0; l < m; ++l) t[l] = t[l] + t[l + m];
+    for (int sz = 1; sz < G; sz *= 2)
+        for (int g = 0; g < G; g += 2 * sz) t[g] = t[g] + t[g + sz];
+    return t[0];
+}
+
+/* segment totals over each segment's last piece and the prefix chain, in place: on return
+ * P[s] (and PB[s] when non-null), mu[s], PS[s], PSG[s], gam[s], lk[s] hold the state Pre_s */
+static void prefix_chain(const int32_t* E, const int32_t* gs, long N, const float* tab,
+                         const float* gt, const float* sk, const float* v, int b, int h,
+                         int H, int R, int DV, float* P, float* PB, float* mu, float* PS,
+                         float* PSG, float* gam, int32_t* lk) {
+    const long M2 = 2 * N, nseg = (M2 + PREFIX_SEG - 1) / PREFIX_SEG, RD = (long)R * DV;
+    float* T = (float*)malloc(sizeof(float) * (size_t)RD);
+    float* TB = (float*)malloc(sizeof(float) * (size_t)RD);
+    float* st = (float*)calloc((size_t)RD, sizeof(float));
+    float* sb = (float*)calloc((size_t)RD, sizeof(float));
+    float smu = 0.0f, sps = 0.0f, spsg = 0.0f, sgam = 0.0f;
+    int32_t slk = -1;
+    for (long s = 0; s < nseg; ++s) {
+        const long x0 = s * PREFIX_SEG, end = x0 + PREFIX_SEG < M2 ? x0 + PREFIX_SEG : M2;
+        const long lo = gs[end - 1] > x0 ? gs[end - 1] : x0;
+        float M = 0.0f, S = 0.0f, SG = 0.0f;
+        int has = 0;
+        int32_t K = -1;
+        for (long t = lo; t < end; ++t)
+            if (!(E[t] & 1)) {
+                const float l = tab[(E[t] >> 1) + 1];
+                if (!has || l > M) M = l;
+                has = 1;
+            }
+        for (long t = lo; t < end; ++t)
+            if (!(E[t] & 1)) K = E[t] >> 1;
+        const float G0 = PB && has ? gt[K + 1] : 0.0f;  /* the segment's centre */
+        for (long e = 0; e < RD; ++e) { T[e] = 0.0f; TB[e] = 0.0f; }
+        for (long t = lo; t < end; ++t) {
+            if (E[t] & 1) continue;
+            const long p = E[t] >> 1, row = ((long)b * N + p) * H + h;
+            const float w = orc_exp2f(tab[p + 1] - M);
+            const float dg = PB ? gt[p + 1] - G0 : 0.0f;
+            const float wg = w * dg;
+            for (int r = 0; r < R; ++r) {
+                const float a = w * sk[row * R + r];
+                for (int d = 0; d < DV; ++d)
+                    T[(long)r * DV + d] = fmaf(a, v[row * DV + d], T[(long)r * DV + d]);
+                if (PB) {
+                    const float c = wg * sk[row * R + r];
+                    for (int d = 0; d < DV; ++d)
+                        TB[(long)r * DV + d] = fmaf(c, v[row * DV + d], TB[(long)r * DV + d]);
+                }
+            }
+            S = S + w;
+            if (PB) SG = fmaf(w, dg, SG);
+        }
+        /* Pre_s */
+        memcpy(P + s * RD, st, sizeof(float) * (size_t)RD);
+        if (PB) memcpy(PB + s * RD, sb, sizeof(float) * (size_t)RD);
+        mu[s] = smu;
+        PS[s] = sps;
+        if (PSG) PSG[s] = spsg;
+        if (gam) gam[s] = sgam;
+        lk[s] = slk;
+        if (gs[end - 1] >= x0) {
+            smu = 0.0f; sps = 0.0f; spsg = 0.0f; sgam = 0.0f; slk = -1;
+            for (long e = 0; e < RD; ++e) { st[e] = 0.0f; sb[e] = 0.0f; }
+        }
+        if (has) {
+            const float m2 = M > smu ? M : smu;
+            const float g = orc_exp2f(smu - m2), hh = orc_exp2f(M - m2);
+            const float dG = sgam - G0;  /* recentre the state on this segment's centre */
+            for (long e = 0; e < RD; ++e) {
+                if (PB) sb[e] = fmaf(hh, TB[e], fmaf(dG, st[e], sb[e]) * g);
+                st[e] = fmaf(hh, T[e], st[e] * g);
+            }
+            if (PB) spsg = fmaf(hh, SG, fmaf(dG, sps, spsg) * g);
+            sps = fmaf(hh, S, sps * g);
+            if (PB) sgam = G0;
+            smu = m2;
+            slk = K;
+        }
+    }
+    free(T); free(TB); free(st); free(sb);
+}
+
+static void prefix_forward_row(const float* sq, const float* sk, const float* v,
+                               const int32_t* q, const int32_t* k, const float* tab, int b,
+                               int h, long N, int H, int R, int DV, float* out, float* lse2,
+                               int32_t* lmax, int32_t* jarg) {
+    const long M2 = 2 * N, nseg = (M2 + PREFIX_SEG - 1) / PREFIX_SEG, RD = (long)R * DV;
+    int32_t* E = (int32_t*)malloc(sizeof(int32_t) * (size_t)M2);
+    int32_t* gs = (int32_t*)malloc(sizeof(int32_t) * (size_t)M2);
+    int32_t* ge = (int32_t*)malloc(sizeof(int32_t) * (size_t)M2);
+    float* P = (float*)malloc(sizeof(float) * (size_t)(nseg * RD));
+    float* mu = (float*)malloc(sizeof(float) * (size_t)nseg);
+    float* PS = (float*)malloc(sizeof(float) * (size_t)nseg);
+    int32_t* lk = (int32_t*)malloc(sizeof(int32_t) * (size_t)nseg);
+    float* y = (float*)malloc(sizeof(float) * (size_t)DV);
+    prefix_list(q, k, N, E, gs, ge);
+    prefix_chain(E, gs, N, tab, NULL, sk, v, b, h, H, R, DV, P, NULL, mu, PS, NULL, NULL, lk);
+    for (long x = 0; x < M2; ++x) {
+        if (!(E[x] & 1)) continue;
+        const long i = E[x] >> 1, s = x / PREFIX_SEG, x0 = s * PREFIX_SEG;
+        const long row = ((long)b * N + i) * H + h;
+        const int use = gs[x] < x0;
+        const long lo = use ? x0 : gs[x];
+        const float bmu = use ? mu[s] : 0.0f, bps = use ? PS[s] : 0.0f;
+        int32_t jb = use ? lk[s] : -1;
+        float m = bmu;
+        for (long t = lo; t < x; ++t)
+            if (!(E[t] & 1) && tab[(E[t] >> 1) + 1] > m) m = tab[(E[t] >> 1) + 1];
+        const float f = orc_exp2f(bmu - m);
+        const float* sqi = sq + row * R;
+        for (int d = 0; d < DV; ++d) {
+            float a = 0.0f;
+            if (use)
+                for (int r = 0; r < R; ++r) a = fmaf(sqi[r], P[s * RD + (long)r * DV + d], a);
+            y[d] = a * f;
+        }
+        float den = fmaf(bps, f, orc_exp2f(-m));
+        for (long t = lo; t < x; ++t) {
+            if (E[t] & 1) continue;
+            const long j = E[t] >> 1, krow = ((long)b * N + j) * H + h;
+            const float p = orc_exp2f(tab[j + 1] - m);
+            den = den + p;
+            const float ps = p * dot_chain(sqi, sk + krow * R, R);
+            for (int d = 0; d < DV; ++d) y[d] = fmaf(ps, v[krow * DV + d], y[d]);
+            jb = (int32_t)j;
+        }
+        for (int d = 0; d < DV; ++d) out[row * DV + d] = y[d] / den;
+        lse2[i] = m + orc_log2f(den);
+        if (lmax) lmax[i] = jb >= 0 ? jb + 1 : 0;
+        if (jarg) jarg[i] = jb;
+    }
+    free(E); free(gs); free(ge); free(P); free(mu); free(PS); free(lk); free(y);
+}
+
+static void prefix_backward_row(const float* sq, const float* sk, const float* v,
+                                const float* dout, const int32_t* q, const int32_t* k,
+                                const float* tab, const float* gt, const float* l2v, int b,
+                                int h, long N, int H, int R, int DV, float* dsq, float* dsk,
+                                float* dv, float* rowtau) {
+    const long M2 = 2 * N, nseg = (M2 + PREFIX_SEG - 1) / PREFIX_SEG, RD = (long)R * DV;
+    const int G = 64 / R;
+    int32_t* E = (int32_t*)malloc(sizeof(int32_t) * (size_t)M2);
+    int32_t* gs = (int32_t*)malloc(sizeof(int32_t) * (size_t)M2);
+    int32_t* ge = (int32_t*)malloc(sizeof(int32_t) * (size_t)M2);
+    float* P = (float*)malloc(sizeof(float) * (size_t)(nseg * RD));
+    float* PB = (float*)malloc(sizeof(float) * (size_t)(nseg * RD));
+    float* Q = (float*)malloc(sizeof(float) * (size_t)(nseg * RD));
+    float* mu = (float*)malloc(sizeof(float) * (size_t)nseg);
+    float* PS = (float*)malloc(sizeof(float) * (size_t)nseg);
+    float* PSG = (float*)malloc(sizeof(float) * (size_t)nseg);
+    float* gam = (float*)malloc(sizeof(float) * (size_t)nseg);
+    float* nu = (float*)malloc(sizeof(float) * (size_t)nseg);
+    uint8_t* qh = (uint8_t*)malloc((size_t)nseg);
+    int32_t* lk = (int32_t*)malloc(sizeof(int32_t) * (size_t)nseg);
+    float* U = (float*)malloc(sizeof(float) * (size_t)RD);
+    float* st = (float*)calloc((size_t)RD, sizeof(float));
+    float* X = (float*)malloc(sizeof(float) * (size_t)(64 * R));
+    float *zP = (float*)malloc(sizeof(float) * (size_t)R), *zB = (float*)malloc(sizeof(float) * (size_t)R);
+    float* col = (float*)malloc(sizeof(float) * (size_t)DV);
+    prefix_list(q, k, N, E, gs, ge);
+    prefix_chain(E, gs, N, tab, gt, sk, v, b, h, H, R, DV, P, PB, mu, PS, PSG, gam, lk);
+    /* ---- query side */
+    for (long x = 0; x < M2; ++x) {
+        if (!(E[x] & 1)) continue;
+        const long i = E[x] >> 1, s = x / PREFIX_SEG, x0 = s * PREFIX_SEG;
+        const long row = ((long)b * N + i) * H + h;
+        const float* sqi = sq + row * R;
+        const float* doi = dout + row * DV;
+        const float l2 = l2v[i], c = gt[i + 1];
+        const int use = gs[x] < x0;
+        const long lo = use ? x0 : gs[x];
+        const float kap = orc_exp2f((use ? mu[s] : 0.0f) - l2);
+        float t1[64], t2[64];
+        for (int r = 0; r < R; ++r) {
+            if (use) {
+                for (int d = 0; d < DV; ++d) col[d] = P[s * RD + (long)r * DV + d];
+                zP[r] = lane_reduce(doi, col, DV, R);
+                for (int d = 0; d < DV; ++d) col[d] = PB[s * RD + (long)r * DV + d];
+                zB[r] = lane_reduce(doi, col, DV, R);
+            } else {
+                zP[r] = 0.0f;
+                zB[r] = 0.0f;
+            }
+        }
+        for (int l = 0; l < 64; ++l) { t1[l] = 0.0f; t2[l] = 0.0f; }
+        for (int r = 0; r < R; ++r) { t1[r * G] = sqi[r] * zP[r]; t2[r * G] = sqi[r] * zB[r]; }
+        const float u0 = wave_tree(t1) * kap, W0 = wave_tree(t2) * kap;
+        const float z0 = (use ? PS[s] : 0.0f) * kap, zg0 = (use ? PSG[s] : 0.0f) * kap;
+        const float cg = c - (use ? gam[s] : 0.0f);
+        const float vv0 = fmaf(-cg, z0, zg0), w0 = fmaf(-cg, u0, W0);
+        float A[64], Bt[64], C[64], D[64];
+        for (int l = 0; l < 64; ++l) {
+            A[l] = 0.0f; Bt[l] = 0.0f; C[l] = 0.0f; D[l] = 0.0f;
+            for (int r = 0; r < R; ++r) X[l * R + r] = 0.0f;
+            const long t = x0 + l;
+            if (t < lo || t >= x || (E[t] & 1)) continue;
+            const long j = E[t] >> 1, krow = ((long)b * N + j) * H + h;
+            const float p = orc_exp2f(tab[j + 1] - l2);
+            const float sv = dot_chain(sqi, sk + krow * R, R);
+            const float ev = dot_chain(doi, v + krow * DV, DV);
+            const float ps = p * sv, pe = p * ev, pse = ps * ev, g = gt[j + 1] - c;
+            A[l] = pse; Bt[l] = p * g; C[l] = pse * g; D[l] = p;
+            for (int r = 0; r < R; ++r) X[l * R + r] = pe * sk[krow * R + r];
+        }
+        const float u = u0 + wave_tree(A), vv = vv0 + wave_tree(Bt);
+        const float w = w0 + wave_tree(C), z = z0 + wave_tree(D);
+        for (int r = 0; r < R; ++r) dsq[row * R + r] = zP[r] * kap + lane_tree(X + r, R, R);
+        const float f = orc_exp2f(-l2), mass = z + f;
+        const float mean = fmaf(-f, c, vv) / mass;
+        rowtau[i] = fmaf(-u, mean, w) / mass;
+    }
+    /* ---- key side: suffix chain over each segment's first piece */
+    {
+        int has = 0;
+        float snu = 0.0f;
+        for (long s = nseg - 1; s >= 0; --s) {
+            const long x0 = s * PREFIX_SEG, end = x0 + PREFIX_SEG < M2 ? x0 + PREFIX_SEG : M2;
+            const long hi = ge[x0] < end ? ge[x0] : end;
+            float lam = 0.0f;
+            int hu = 0;
+            for (long t = x0; t < hi; ++t)
+                if (E[t] & 1) {
+                    const float l2 = l2v[E[t] >> 1];
+                    if (!hu || l2 < lam) lam = l2;
+                    hu = 1;
+                }
+            for (long e = 0; e < RD; ++e) U[e] = 0.0f;
+            for (long t = hi - 1; t >= x0; --t) {
+                if (!(E[t] & 1)) continue;
+                const long i = E[t] >> 1, row = ((long)b * N + i) * H + h;
+                const float wq = orc_exp2f(lam - l2v[i]);
+                for (int r = 0; r < R; ++r) {
+                    const float a = wq * sq[row * R + r];
+                    for (int d = 0; d < DV; ++d)
+                        U[(long)r * DV + d] = fmaf(a, dout[row * DV + d], U[(long)r * DV + d]);
+                }
+            }
+            memcpy(Q + s * RD, st, sizeof(float) * (size_t)RD);
+            nu[s] = snu;
+            qh[s] = (uint8_t)has;
+            if (ge[x0] <= end) {
+                has = 0;
+                snu = 0.0f;
+                for (long e = 0; e < RD; ++e) st[e] = 0.0f;
+            }
+            if (hu) {
+                if (!has) {
+                    snu = lam;
+                    memcpy(st, U, sizeof(float) * (size_t)RD);
+                    has = 1;
+                } else {
+                    const float n2 = lam < snu ? lam : snu;
+                    const float g = orc_exp2f(n2 - snu), hh = orc_exp2f(n2 - lam);
+                    for (long e = 0; e < RD; ++e) st[e] = fmaf(hh, U[e], st[e] * g);
+                    snu = n2;
+                }
+            }
+        }
+    }
+    for (long x = 0; x < M2; ++x) {
+        if (E[x] & 1) continue;
+        const long j = E[x] >> 1, s = x / PREFIX_SEG, x0 = s * PREFIX_SEG;
+        const long end = x0 + PREFIX_SEG < M2 ? x0 + PREFIX_SEG : M2;
+        const long krow = ((long)b * N + j) * H + h;
+        const float* skj = sk + krow * R;
+        const float* vj = v + krow * DV;
+        const float lj = tab[j + 1];
+        const int use = ge[x] > end && qh[s];
+        const long hi = ge[x] < end ? ge[x] : end;
+        float* dkj = dsk + krow * R;
+        float* dvj = dv + krow * DV;
+        const float phi = use ? orc_exp2f(lj - nu[s]) : 0.0f;
+        for (int d = 0; d < DV; ++d) {
+            float a = 0.0f;
+            if (use)
+                for (int r = 0; r < R; ++r) a = fmaf(skj[r], Q[s * RD + (long)r * DV + d], a);
+            dvj[d] = use ? a * phi : 0.0f;
+        }
+        for (int r = 0; r < R; ++r) {
+            if (use) {
+                for (int d = 0; d < DV; ++d) col[d] = Q[s * RD + (long)r * DV + d];
+                dkj[r] = lane_reduce(vj, col, DV, R) * phi;
+            } else {
+                dkj[r] = 0.0f;
+            }
+        }
+        for (int l = 0; l < 64; ++l) {
+            for (int r = 0; r < R; ++r) X[l * R + r] = 0.0f;
+            const long t = x0 + l;
+            if (t <= x || t >= hi || !(E[t] & 1)) continue;
+            const long i = E[t] >> 1, row = ((long)b * N + i) * H + h;
+            const float p = orc_exp2f(lj - l2v[i]);
+            const float ev = dot_chain(dout + row * DV, vj, DV);
+            const float pe = p * ev;
+            for (int r = 0; r < R; ++r) X[l * R + r] = pe * sq[row * R + r];
+        }
+        for (int r = 0; r < R; ++r) dkj[r] = dkj[r] + lane_tree(X + r, R, R);
+        for (long t = x + 1; t < hi; ++t) {
+            if (!(E[t] & 1)) continue;
+            const long i = E[t] >> 1, row = ((long)b * N + i) * H + h;
+            const float p = orc_exp2f(lj - l2v[i]);
+            const float ps = p * dot_chain(sq + row * R, skj, R);
+            for (int d = 0; d < DV; ++d) dvj[d] = fmaf(ps, dout[row * DV + d], dvj[d]);
+        }
+    }
+    free(E); free(gs); free(ge); free(P); free(PB); free(Q); free(mu); free(PS); free(PSG); free(gam);
+    free(nu); free(qh); free(lk); free(U); free(st); free(X); free(zP); free(zB); free(col);
+}
+
+/* row mode as the HIP path chooses it: 0 decomposed, 1 direct, 3 levels, 4 prefix */
 static int row_mode(const int32_t* q, const int32_t* k, long N, int R, int DV, int resets) {
     if (!orc_dense_row(q, k, N, 1)) return 0;
+    if (!resets && prefix_labels(q, k, N)) return 4;
     if (resets || (long)R * DV > LEVEL_RDV) return 1;
     Levels L;
     if (!levels_build(q, k, N, &L)) return 1;
@@ -1155,6 +1605,12 @@ static void forward_impl(const float* sq, const float* sk, const float* v, const
             free(lv.ent);
             continue;
         }
+        if (mode == 4) {
+            const long so = (long)bh * N;
+            prefix_forward_row(sq, sk, v, q, k, tab, b, h, N, H, R, DV, out, lse2 + so,
+                               lmax ? lmax + so : NULL, jarg ? jarg + so : NULL);
+            continue;
+        }
         if (mode == 1 || mode == 3) {
             const long so = (long)bh * N;
             direct_forward_row(sq, sk, v, q, k, tab, b, h, N, H, R, DV, out, lse2 + so,
@@ -1308,6 +1764,11 @@ void orc_backward_flags(const float* sq, const float* sk, const float* v, const 
             level_backward_row(sq, sk, v, dout, tab, gt, l2v, b, h, N, H, R, DV, &lv, dsq, dsk,
                                dv, rowtau + (long)bh * N);
             free(lv.ent);
+            continue;
+        }
+        if (mode == 4) {
+            prefix_backward_row(sq, sk, v, dout, q, k, tab, gt, l2v, b, h, N, H, R, DV, dsq,
+                                dsk, dv, rowtau + (long)bh * N);
             continue;
         }
         if (mode == 1 || mode == 3) {

@@ -5,7 +5,8 @@ points with the key chain on a side stream, the tau reduction -- replayed severa
 the program's own eager work and synchronizations between the replays.  Every replay must
 reproduce the eager step bit for bit (no launch of the path records a memset node; a node
 that misbehaves on replays after the first would show here).  Row kinds: level rows (alphabet
-4), sparse rows (8-bit labels), dense tile rows (identical labels)."""
+4), sparse rows (8-bit labels), prefix rows (identical labels), dense tile rows (long runs of
+one label with two predecessors)."""
 import numpy as np
 import pytest
 import torch
@@ -23,9 +24,12 @@ class Step:
         g = torch.Generator(device="cpu").manual_seed(seed)
         q = torch.randn(B, T, H, D, generator=g)
         k = torch.randn(B, T, H, D, generator=g)
-        if pattern == "equal":
+        if pattern in ("equal", "direct"):
             q = q.abs()
             k = k.abs()
+        if pattern == "direct":  # label 255 with two predecessors: a direct dense row
+            q[:, ::97, :, 0] *= -1
+            k[:, ::89, :, 0] *= -1
         self.tq = q.to(dev, torch.bfloat16).contiguous()
         self.tk = k.to(dev, torch.bfloat16).contiguous()
         self.tv = torch.randn(B, T, H, DV, generator=g).to(dev, torch.bfloat16).contiguous()
@@ -86,7 +90,7 @@ class Step:
 
 
 @pytest.mark.parametrize("shape", [(2, 512, 4, 2, 64, "level"), (1, 1024, 4, 8, 64, "sparse"),
-                                   (1, 512, 2, 8, 64, "equal")])
+                                   (1, 512, 2, 8, 64, "equal"), (1, 512, 2, 8, 64, "direct")])
 def test_graph_replays_match_eager(shape):
     *dims, pattern = shape
     print(f"graph replay {shape}", flush=True)
@@ -96,7 +100,7 @@ def test_graph_replays_match_eager(shape):
     torch.cuda.synchronize()
     want = st.results()
     modes = st.dism_amd.hard_forward.row_modes(st.ws, st.tq, st.tv).cpu().numpy()
-    expect = {"level": 3, "sparse": 0, "equal": 1}[pattern]
+    expect = {"level": 3, "sparse": 0, "equal": 4, "direct": 1}[pattern]
     assert (modes == expect).all(), modes
     g = torch.cuda.CUDAGraph()
     cs = torch.cuda.Stream()
