@@ -670,17 +670,18 @@ int32_t dism_hard_backward_queries(const void* sq, const void* sk, const void* v
     a.dlut = dlut;
     a.dsq = dsq;
     a.rowtau = rowtau;
-    if ((st = hip_status(dism::launch_scan_rows(a, R, DV, dtype, S(stream)),
-                         "hard backward rows")))
-        return st;
+    // the dense, level and prefix rows first: their kernels mostly find no rows, and such
+    // launches drain fastest before the label scan fills the device
     if ((st = hip_status(dism::launch_dense_rows(a, R, DV, dtype, S(stream)),
                          "hard backward dense rows")))
         return st;
     if ((st = hip_status(dism::launch_level_rows(a, R, DV, dtype, S(stream)),
                          "hard backward level rows")))
         return st;
-    return hip_status(dism::launch_prefix_rows(a, R, DV, dtype, S(stream)),
-                      "hard backward prefix rows");
+    if ((st = hip_status(dism::launch_prefix_rows(a, R, DV, dtype, S(stream)),
+                         "hard backward prefix rows")))
+        return st;
+    return hip_status(dism::launch_scan_rows(a, R, DV, dtype, S(stream)), "hard backward rows");
 }
 
 int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, const void* dout,
@@ -698,17 +699,16 @@ int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, c
     if (!dsk || !dv) return fail(DISM_ERR_INVALID, "hard backward: null pointer");
     a.dsk = dsk;
     a.dv = dv;
-    if ((st = hip_status(dism::launch_scan_keys(a, R, DV, dtype, S(stream)),
-                         "hard backward keys")))
-        return st;
     if ((st = hip_status(dism::launch_dense_keys(a, R, DV, dtype, S(stream)),
                          "hard backward dense keys")))
         return st;
     if ((st = hip_status(dism::launch_level_keys(a, R, DV, dtype, S(stream)),
                          "hard backward level keys")))
         return st;
-    return hip_status(dism::launch_prefix_keys(a, R, DV, dtype, S(stream)),
-                      "hard backward prefix keys");
+    if ((st = hip_status(dism::launch_prefix_keys(a, R, DV, dtype, S(stream)),
+                         "hard backward prefix keys")))
+        return st;
+    return hip_status(dism::launch_scan_keys(a, R, DV, dtype, S(stream)), "hard backward keys");
 }
 
 int32_t dism_hard_backward_key_pairs(const void* sq, const void* sk, const void* v,

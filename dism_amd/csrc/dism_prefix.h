@@ -309,46 +309,51 @@ __global__ __launch_bounds__(PX_CHAIN_THREADS) void prefix_chain_kernel(PathArgs
     __shared__ float2 s_gh[PX_MAX_SEGS];
     __shared__ float s_dg[KIND == 1 ? PX_MAX_SEGS : 1];
     __shared__ uint8_t s_op[PX_MAX_SEGS];
+    // the segments' records (and, KIND 1, the centre G0 of each), loaded in parallel so that
+    // the sequential scalar chain below reads LDS only
+    __shared__ float4 s_in[PX_MAX_SEGS];
+    __shared__ float s_g0[KIND == 1 ? PX_MAX_SEGS : 1];
+    __shared__ float2 s_m[PX_MAX_SEGS];
     const int bh = blockIdx.x, tid = threadIdx.x;
     if (a.o.dflag[bh] != 4 || !a.hard[bh]) return;
     const int nseg = px_segs(a.n);
     const long sb = (long)bh * nseg;
+    for (int s = tid; s < nseg; s += PX_CHAIN_THREADS) {
+        if constexpr (KIND < 2) {
+            const float4 t = a.o.pxS[sb + s];
+            s_in[s] = t;
+            if constexpr (KIND == 1) {
+                const int fl = __float_as_int(t.w);
+                s_g0[s] = (fl & PX_HAS)
+                              ? a.dlut[(long)(bh % a.H) * a.lut_stride + (fl & 0xFFFFF)]
+                              : 0.0f;
+            }
+        } else {
+            const float2 t = a.o.pxK[sb + s];
+            s_in[s] = make_float4(t.x, t.y, 0.0f, 0.0f);
+        }
+    }
+    __syncthreads();
+    // (1) thread 0: the running maximum (minimum) alone, the base after a restart and the
+    // value after each segment; (2) all threads: the factors g, h; (3) thread 0: the scalar
+    // sums and the records of the state before (after) each segment
     if (tid == 0) {
         if constexpr (KIND < 2) {
-            // KIND 0 keeps the last key in .w, KIND 1 the centre gam of the G-weighted sums
-            const float* dl = KIND == 1 ? a.dlut + (long)(bh % a.H) * a.lut_stride : nullptr;
-            float mu = 0.0f, PS = 0.0f, PSG = 0.0f, gam = 0.0f;
-            int lk = -1;
-            const bool wr = blockIdx.y == 0;
+            float mu = 0.0f;
             for (int s = 0; s < nseg; ++s) {
-                const float4 t = a.o.pxS[sb + s];
+                const float4 t = s_in[s];
                 const int fl = __float_as_int(t.w);
-                if (wr)
-                    a.o.pxR[sb + s] =
-                        make_float4(mu, PS, PSG, KIND == 1 ? gam : __int_as_float(lk));
                 int op = 0;
                 if (fl & PX_RESET) {
-                    mu = 0.0f; PS = 0.0f; PSG = 0.0f; gam = 0.0f; lk = -1;
+                    mu = 0.0f;
                     op |= 1;
                 }
-                float g = 1.0f, h = 1.0f, dG = 0.0f;
+                const float mb = mu;
                 if (fl & PX_HAS) {
-                    const float m2 = t.x > mu ? t.x : mu;
-                    g = exp2_fp32(mu - m2);
-                    h = exp2_fp32(t.x - m2);
-                    lk = (fl & 0xFFFFF) - 1;
-                    if constexpr (KIND == 1) {
-                        const float g0 = dl[lk + 1];
-                        dG = gam - g0;
-                        PSG = __builtin_fmaf(h, t.z, __builtin_fmaf(dG, PS, PSG) * g);
-                        gam = g0;
-                    }
-                    PS = __builtin_fmaf(h, t.y, PS * g);
-                    mu = m2;
+                    mu = t.x > mu ? t.x : mu;
                     op |= 2;
                 }
-                s_gh[s] = make_float2(g, h);
-                s_dg[s] = dG;
+                s_m[s] = make_float2(mb, mu);
                 s_op[s] = (uint8_t)op;
             }
         } else {
@@ -356,7 +361,7 @@ __global__ __launch_bounds__(PX_CHAIN_THREADS) void prefix_chain_kernel(PathArgs
             int has = 0;
             const bool wr = blockIdx.y == 0;
             for (int s = nseg - 1; s >= 0; --s) {
-                const float2 t = a.o.pxK[sb + s];
+                const float4 t = s_in[s];
                 const int fl = __float_as_int(t.y);
                 if (wr) a.o.pxKR[sb + s] = make_float2(nu, __int_as_float(has));
                 int op = 0;
@@ -365,26 +370,72 @@ __global__ __launch_bounds__(PX_CHAIN_THREADS) void prefix_chain_kernel(PathArgs
                     nu = 0.0f;
                     op |= 1;
                 }
-                float g = 1.0f, h = 1.0f;
+                const float nb = nu;
                 if (fl & 1) {
                     if (!has) {
                         nu = t.x;
                         has = 1;
                         op |= 4;
                     } else {
-                        const float n2 = t.x < nu ? t.x : nu;
-                        g = exp2_fp32(n2 - nu);
-                        h = exp2_fp32(n2 - t.x);
-                        nu = n2;
+                        nu = t.x < nu ? t.x : nu;
                         op |= 2;
                     }
                 }
-                s_gh[s] = make_float2(g, h);
+                s_m[s] = make_float2(nb, nu);
                 s_op[s] = (uint8_t)op;
             }
         }
     }
     __syncthreads();
+    for (int s = tid; s < nseg; s += PX_CHAIN_THREADS) {
+        const int op = s_op[s];
+        const float2 m = s_m[s];
+        float g = 1.0f, h = 1.0f;
+        if (op & 2) {
+            if constexpr (KIND < 2) {
+                g = exp2_fp32(m.x - m.y);
+                h = exp2_fp32(s_in[s].x - m.y);
+            } else {
+                g = exp2_fp32(m.y - m.x);
+                h = exp2_fp32(m.y - s_in[s].x);
+            }
+        }
+        s_gh[s] = make_float2(g, h);
+    }
+    __syncthreads();
+    if constexpr (KIND < 2) {
+        if (tid == 0) {
+            // KIND 0 keeps the last key in .w, KIND 1 the centre gam of the G-weighted sums
+            float PS = 0.0f, PSG = 0.0f, gam = 0.0f, mu = 0.0f;
+            int lk = -1;
+            const bool wr = blockIdx.y == 0;
+            for (int s = 0; s < nseg; ++s) {
+                const float4 t = s_in[s];
+                const int fl = __float_as_int(t.w);
+                if (wr)
+                    a.o.pxR[sb + s] =
+                        make_float4(mu, PS, PSG, KIND == 1 ? gam : __int_as_float(lk));
+                if (fl & PX_RESET) {
+                    PS = 0.0f; PSG = 0.0f; gam = 0.0f; lk = -1;
+                }
+                float dG = 0.0f;
+                if (fl & PX_HAS) {
+                    const float2 gh = s_gh[s];
+                    lk = (fl & 0xFFFFF) - 1;
+                    if constexpr (KIND == 1) {
+                        const float g0 = s_g0[s];
+                        dG = gam - g0;
+                        PSG = __builtin_fmaf(gh.y, t.z, __builtin_fmaf(dG, PS, PSG) * gh.x);
+                        gam = g0;
+                    }
+                    PS = __builtin_fmaf(gh.y, t.y, PS * gh.x);
+                }
+                mu = s_m[s].y;
+                if constexpr (KIND == 1) s_dg[s] = dG;
+            }
+        }
+        __syncthreads();
+    }
     float* A = KIND == 2 ? a.o.pxU : a.o.pxT;
     float* Bm = KIND == 1 ? a.o.pxB : nullptr;
     const long e0 = (long)blockIdx.y * PX_CHAIN_THREADS * PX_EPT + tid;
