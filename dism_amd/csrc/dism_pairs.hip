@@ -986,12 +986,10 @@ __device__ __forceinline__ void rows_item(const PathArgs& a, int base, int k0, i
     }
 }
 
-// 4 waves per SIMD (128 VGPRs) where the spill stays small (bf16 rows, R <= 8: at most a
-// few dozen bytes per lane; 82 -> 73 us at B4 H16 T16384 d8 DV64); no constraint otherwise
-constexpr int rows_occupancy(int tsize, int R) { return tsize == 2 && R <= 8 ? 4 : 1; }
+// No occupancy target: at 4 waves/SIMD (128 VGPRs) the 16-label walk steps and the run-list
+// lookups spill 356 bytes per lane, 220 MB of scratch writes per launch at configs[2]
 template <typename T, int R, int DV>
-__global__ __launch_bounds__(64 * WAVES)
-__attribute__((amdgpu_waves_per_eu(rows_occupancy(sizeof(T), R)))) void pairs_rows_kernel(PathArgs a) {
+__global__ __launch_bounds__(64 * WAVES) void pairs_rows_kernel(PathArgs a) {
     __shared__ RowsLds<R> s_all[WAVES];
     RowsLds<R>& S = s_all[wave_id_v()];
     constexpr int GS = lanes_small(DV, false), GM = lanes_medium(DV);

@@ -78,7 +78,8 @@ def prepare_workspace(sq, sk, v, idx_q, idx_k):
 
 def row_modes(workspace, sq, v):
     """Row modes [B,H] int32 of a workspace prepared for vectors shaped like sq/v: 0 sparse,
-    1 dense (direct tile kernels), 2 sparse with strip-bounded walks."""
+    1 dense (direct tile kernels), 2 sparse with strip-bounded walks, 3 dense level rows,
+    4 dense prefix rows (every label with one predecessor label)."""
     b, n, h, r = sq.shape
     dv = v.shape[3]
     out = torch.empty((b, h), dtype=torch.int32, device=workspace.device)

@@ -128,7 +128,10 @@ int32_t dism_hard_forward_noalloc(const void* sq, const void* sk, const void* v,
 /* Row modes of a prepared workspace, [B*H] int32 to `modes` (device memory): 0 = sparse row
  * (label scans + bigram walks), 1 = dense row (the bucketed label collisions exceed N^2/64:
  * direct tile kernels), 2 = sparse row whose walks stop at 64-row strip boundaries (the walk
- * probe estimated their cost above N^2).  An introspection aid for tests and tuning; no
+ * probe estimated their cost above N^2), 3 = dense level row (labels below 256, N <= 4096,
+ * R*DV <= 512, at most 32 distinct match lengths: sums per match length), 4 = dense prefix
+ * row (every label has one predecessor label, so every match runs to the key's row start:
+ * prefix sums with per-key weights).  An introspection aid for tests and tuning; no
  * reference counterpart. */
 int32_t dism_hard_row_modes(const void* workspace, int64_t workspace_bytes, int64_t B,
                             int64_t N, int64_t H, int32_t R, int32_t DV, int32_t* modes,
