@@ -56,7 +56,7 @@ struct Layout {
     int64_t stage[2][2], bhcount[2], own[2], ocount, mode, onebyte;
     int64_t pnb, prow, mcount, mdig, dflag, dlist, dcount, dbound, dcost, runs, runcnt;
     int64_t lvent, lvlc, lvlf, lvlk, lvmeta, lvq, lvqidx, lvkidx, lvF, lvFk, lvP, lvQ, lvY, lvZ, lvK;  // -1: none
-    int64_t pxT, pxB, pxU, pxS, pxR, pxK, pxKR;  // -1: none
+    int64_t pxT, pxB, pxU, pxS, pxR, pxK, pxKR, pxE, pxL;  // -1: none
     int64_t total;
     int prow_stride;
 };
@@ -189,6 +189,8 @@ Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     L.pxR = px ? take(BH * pseg * 16) : -1;
     L.pxK = px ? take(BH * pseg * 8) : -1;
     L.pxKR = px ? take(BH * pseg * 8) : -1;
+    L.pxE = px ? take(BH * 2 * N * 4) : -1;
+    L.pxL = px ? take(BH * 2 * N * 4) : -1;
     L.total = o;
     return L;
 }
@@ -251,6 +253,8 @@ dism::Orders orders(const Layout& L, void* ws) {
     o.pxR = reinterpret_cast<float4*>(opt(L.pxR));
     o.pxK = reinterpret_cast<float2*>(opt(L.pxK));
     o.pxKR = reinterpret_cast<float2*>(opt(L.pxKR));
+    o.pxE = reinterpret_cast<int32_t*>(opt(L.pxE));
+    o.pxL = reinterpret_cast<int32_t*>(opt(L.pxL));
     return o;
 }
 
@@ -312,7 +316,7 @@ int32_t prepare_impl(const void* sq, const void* sk, const void* v, int32_t dtyp
     sa.BH = B * H;
     sa.n = (int)N;
     sa.cls_n = (int)cls_n;
-    sa.prefix = wlo == nullptr && (cls_n <= 0 || cls_n >= N) ? 1 : 0;
+    sa.prefix = wlo == nullptr ? 1 : 0;
     for (int t = 0; t < 3; ++t) sa.tmp[t] = at<int32_t>(workspace, L.tmp[t]);
     sa.o = orders(L, workspace);
     sa.pnb = at<int32_t>(workspace, L.pnb);
@@ -1119,6 +1123,7 @@ int32_t dism_hard_prefill(const void* sq, const void* sk, const void* v, int32_t
         return st;
     dism::PathArgs a = path(L, workspace, B, N, H, iq, ik, ones, nullptr, 0, lut, lut_stride);
     a.wlo = reset ? wlo : nullptr;
+    a.cls_n = (int)n_valid;  // prefix rows take their real positions only
     a.sq = sq;
     a.sk = sk;
     a.v = v;

@@ -48,109 +48,103 @@ __device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long x,
 }
 
 // ---------------------------------------------------------------------------------------
-// Classification.  Bucket counts of positions [lo, hi) of one row's labels (both sides) into
-// LDS (runs of equal buckets in a thread's 16 consecutive labels are added with one atomic).
-__device__ __forceinline__ void count_buckets(const int32_t* __restrict__ iq,
-                                              const int32_t* __restrict__ ik, int lo, int hi,
-                                              uint32_t (&cnt)[2][DENSE_BUCKETS]) {
+// Classification, one 1024-thread workgroup per (b,h) row, counting the first cn positions (a
+// prefill's rows are padded after the real tokens): bucket counts of both sides in LDS (runs
+// of equal buckets in a thread's consecutive labels added with one atomic), M = sum over the
+// buckets of #queries x #keys, dense when 64 M > cn^2 (rows longer than DENSE_MAX_N never
+// are).  With `prefix`, a dense row becomes a prefix row (mode 4) when every bucket holds one
+// label and, over the positions 1 .. cn - 1 of both sides, one predecessor label: one LDS
+// slot per bucket holding (1 << 32) | label, 0 = empty (dism_prefix.h).
+constexpr int CLS_THREADS = 1024;
+__global__ __launch_bounds__(CLS_THREADS) void dense_classify_kernel(
+    const int32_t* __restrict__ iq, const int32_t* __restrict__ ik, int n, int cn, int prefix,
+    int32_t* __restrict__ dflag, unsigned long long* __restrict__ dcost,
+    int32_t* __restrict__ runcnt) {
+    __shared__ uint32_t s_cnt[2][DENSE_BUCKETS];
+    __shared__ unsigned long long s_lab[DENSE_BUCKETS], s_pred[DENSE_BUCKETS];
+    __shared__ unsigned long long s_red[CLS_THREADS / 64];
+    const long bh = blockIdx.x;
     const int tid = threadIdx.x;
-    for (int x = tid; x < 2 * DENSE_BUCKETS; x += 256) (&cnt[0][0])[x] = 0u;
+    const int32_t* q = iq + bh * n;
+    const int32_t* k = ik + bh * n;
+    if (n > DENSE_MAX_N) {
+        if (tid == 0) {
+            dflag[bh] = 0;
+            dcost[bh] = 0ull;
+            if (runcnt) runcnt[bh] = 0;
+        }
+        return;
+    }
+    for (int x = tid; x < 2 * DENSE_BUCKETS; x += CLS_THREADS) (&s_cnt[0][0])[x] = 0u;
     __syncthreads();
+    // a thread's consecutive chunk of positions (runs of one bucket cost one atomic)
+    const int per = (cn + CLS_THREADS - 1) / CLS_THREADS;
+    const int lo = tid * per, hi = lo + per < cn ? lo + per : cn;
 #pragma unroll
     for (int side = 0; side < 2; ++side) {
-        const int32_t* lab = side ? ik : iq;
-        for (int base = lo + tid * 16; base < hi; base += 256 * 16) {
-            const int end = base + 16 < hi ? base + 16 : hi;
-            uint32_t cur = label_bucket(lab[base]), c = 1;
-            for (int x = base + 1; x < end; ++x) {
+        const int32_t* lab = side ? k : q;
+        if (lo < hi) {
+            uint32_t cur = label_bucket(lab[lo]), c = 1;
+            for (int x = lo + 1; x < hi; ++x) {
                 const uint32_t bk = label_bucket(lab[x]);
                 if (bk != cur) {
-                    atomicAdd(&cnt[side][cur], c);
+                    atomicAdd(&s_cnt[side][cur], c);
                     cur = bk;
                     c = 0;
                 }
                 ++c;
             }
-            atomicAdd(&cnt[side][cur], c);
+            atomicAdd(&s_cnt[side][cur], c);
         }
     }
     __syncthreads();
-}
-
-// the row's flag from its collision count t (a 256-thread block's partial sums m)
-__device__ __forceinline__ void classify_finish(unsigned long long m, int n, int cn, long bh,
-                                                int32_t* __restrict__ dflag,
-                                                unsigned long long* __restrict__ dcost,
-                                                int32_t* __restrict__ runcnt) {
-    __shared__ unsigned long long s_red[4];
-    const int tid = threadIdx.x;
+    unsigned long long m = 0;
+    for (int x = tid; x < DENSE_BUCKETS; x += CLS_THREADS)
+        m += (unsigned long long)s_cnt[0][x] * s_cnt[1][x];
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) m += shfl_xor_u64(m, o);
     if ((tid & 63) == 0) s_red[tid >> 6] = m;
     __syncthreads();
+    unsigned long long t = 0;
+    for (int w = 0; w < CLS_THREADS / 64; ++w) t += s_red[w];
+    const bool dense = t * 64ull > (unsigned long long)cn * (unsigned long long)cn;
+    bool pre = false;
+    if (dense && prefix) {
+        for (int x = tid; x < DENSE_BUCKETS; x += CLS_THREADS) {
+            s_lab[x] = 0ull;
+            s_pred[x] = 0ull;
+        }
+        __syncthreads();
+        auto put = [](unsigned long long* tab, uint32_t b, unsigned long long tag) {
+            unsigned long long cur = tab[b];
+            if (cur == 0ull) {
+                cur = atomicCAS(&tab[b], 0ull, tag);
+                if (cur == 0ull) cur = tag;
+            }
+            return cur != tag;
+        };
+        bool bad = false;
+        for (int base = 0; base < cn && !bad; base += CLS_THREADS) {
+            const int p = base + tid;
+            if (p < cn) {
+#pragma unroll
+                for (int side = 0; side < 2; ++side) {
+                    const int32_t* L = side ? k : q;
+                    const int32_t lab = L[p];
+                    const uint32_t b = label_bucket(lab);
+                    bad |= put(s_lab, b, (1ull << 32) | (uint32_t)lab);
+                    if (p >= 1) bad |= put(s_pred, b, (1ull << 32) | (uint32_t)L[p - 1]);
+                }
+            }
+            bad = __syncthreads_or(bad);
+        }
+        pre = !bad;
+    }
     if (tid == 0) {
+        dflag[bh] = dense ? (pre ? 4 : 1) : 0;
         dcost[bh] = 0ull;  // the walk probe adds to it
         if (runcnt) runcnt[bh] = 0;  // and lists the long runs
-        const unsigned long long t = s_red[0] + s_red[1] + s_red[2] + s_red[3];
-        dflag[bh] =
-            (n <= DENSE_MAX_N && t * 64ull > (unsigned long long)cn * (unsigned long long)cn)
-                ? 1 : 0;
     }
-}
-
-// One workgroup per (b,h) row of n positions, counting the first cn of them (a prefill's
-// rows are padded after the real tokens).  Rows longer than DENSE_MAX_N are never dense.
-__global__ __launch_bounds__(256) void dense_classify_kernel(
-    const int32_t* __restrict__ iq, const int32_t* __restrict__ ik, int n, int cn,
-    int32_t* __restrict__ dflag, unsigned long long* __restrict__ dcost,
-    int32_t* __restrict__ runcnt) {
-    __shared__ uint32_t s_cnt[2][DENSE_BUCKETS];
-    const long bh = blockIdx.x;
-    unsigned long long m = 0;
-    if (n <= DENSE_MAX_N) {
-        count_buckets(iq + bh * n, ik + bh * n, 0, cn, s_cnt);
-        for (int x = threadIdx.x; x < DENSE_BUCKETS; x += 256)
-            m += (unsigned long long)s_cnt[0][x] * s_cnt[1][x];
-    }
-    classify_finish(m, n, cn, bh, dflag, dcost, runcnt);
-}
-
-// Long rows (cn > DENSE_CLS_SEG): workgroup per (row, segment of DENSE_CLS_SEG positions)
-// writes its segment's counts (all buckets) to part[bh][seg][2][DENSE_BUCKETS]; a second
-// kernel sums the segments per bucket.
-constexpr int DENSE_CLS_SEG = 8192;
-__global__ __launch_bounds__(256) void dense_count_kernel(const int32_t* __restrict__ iq,
-                                                          const int32_t* __restrict__ ik, int n,
-                                                          int cn, uint32_t* __restrict__ part,
-                                                          long part_stride) {
-    __shared__ uint32_t s_cnt[2][DENSE_BUCKETS];
-    const long bh = blockIdx.x;
-    const int seg = blockIdx.y;
-    const int lo = seg * DENSE_CLS_SEG, hi = lo + DENSE_CLS_SEG < cn ? lo + DENSE_CLS_SEG : cn;
-    count_buckets(iq + bh * n, ik + bh * n, lo, hi, s_cnt);
-    uint4* dst = reinterpret_cast<uint4*>(part + bh * part_stride +
-                                          (long)seg * 2 * DENSE_BUCKETS);
-    const uint4* src = reinterpret_cast<const uint4*>(&s_cnt[0][0]);
-    for (int x = threadIdx.x; x < 2 * DENSE_BUCKETS / 4; x += 256) dst[x] = src[x];
-}
-
-__global__ __launch_bounds__(256) void dense_collide_kernel(const uint32_t* __restrict__ part,
-                                                            long part_stride, int segs, int n,
-                                                            int cn, int32_t* __restrict__ dflag,
-                                                            unsigned long long* __restrict__ dcost,
-                                                            int32_t* __restrict__ runcnt) {
-    const long bh = blockIdx.x;
-    const uint32_t* p = part + bh * part_stride;
-    unsigned long long m = 0;
-    for (int x = threadIdx.x; x < DENSE_BUCKETS; x += 256) {
-        uint32_t cq = 0, ck = 0;
-        for (int sg = 0; sg < segs; ++sg) {
-            cq += p[(long)sg * 2 * DENSE_BUCKETS + x];
-            ck += p[(long)sg * 2 * DENSE_BUCKETS + DENSE_BUCKETS + x];
-        }
-        m += (unsigned long long)cq * ck;
-    }
-    classify_finish(m, n, cn, bh, dflag, dcost, runcnt);
 }
 
 // Row modes and lists (one workgroup, after the walk probe and the level lists): mode 2 for
@@ -716,26 +710,11 @@ __global__ __launch_bounds__(DENSE_THREADS) void dense_keys_kernel(PathArgs a) {
 
 // ---------------------------------------------------------------------------------------
 hipError_t launch_dense_classify(const int32_t* iq, const int32_t* ik, long BH, int n,
-                                 int cls_n, int32_t* dflag, unsigned long long* dcost,
-                                 uint16_t* dbound, int32_t* runcnt, hipStream_t s) {
+                                 int cls_n, int prefix, int32_t* dflag,
+                                 unsigned long long* dcost, int32_t* runcnt, hipStream_t s) {
     const int cn = cls_n > 0 && cls_n < n ? cls_n : n;
-    const int segs = (cn + DENSE_CLS_SEG - 1) / DENSE_CLS_SEG;
-    if (segs <= 1 || n > DENSE_MAX_N || !dbound) {
-        hipLaunchKernelGGL(dense_classify_kernel, dim3((unsigned)BH), dim3(256), 0, s, iq, ik,
-                           n, cn, dflag, dcost, runcnt);
-        return hipGetLastError();
-    }
-    // the segment counts go to the rows' boundary-row space, written later by the prepare
-    // (each row holds 2 * dense_row_entries(n) >= segs * 32 KiB bytes for n > DENSE_CLS_SEG)
-    uint32_t* part = reinterpret_cast<uint32_t*>(dbound);
-    const long stride = dense_row_entries(n) / 2;  // uint32 per row
-    if ((long)segs * 2 * DENSE_BUCKETS > stride) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(dense_count_kernel, dim3((unsigned)BH, (unsigned)segs), dim3(256), 0, s,
-                       iq, ik, n, cn, part, stride);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(dense_collide_kernel, dim3((unsigned)BH), dim3(256), 0, s, part, stride,
-                       segs, n, cn, dflag, dcost, runcnt);
+    hipLaunchKernelGGL(dense_classify_kernel, dim3((unsigned)BH), dim3(CLS_THREADS), 0, s, iq,
+                       ik, n, cn, prefix, dflag, dcost, runcnt);
     return hipGetLastError();
 }
 

@@ -132,6 +132,8 @@ struct Orders {
     float4* pxR;
     float2* pxK;
     float2* pxKR;
+    int32_t* pxE;     // [..][2N] a padded prefill row's list (entries of its real positions)
+    int32_t* pxL;     // [..][2N] their labels
 };
 constexpr int LEVEL_MAX_N = 4096;   // longest level row (16-bit list indices and counts)
 constexpr int LEVEL_MAX = 32;       // most levels (longest match) of a level row
@@ -178,8 +180,8 @@ struct SortArgs {
     int role_base;          // first role of a launch (blockIdx.y + role_base)
     int lds_rows;           // rows with one label byte go to prepare_lds_kernel (sort skips them)
     int cls_n;              // positions the dense-row classification counts (0: all n)
-    int prefix;             // 1: dense rows may become prefix rows (fixed-length rows of all
-                            // n positions, no resets or documents; o.pxT set)
+    int prefix;             // 1: dense rows may become prefix rows (fixed-length rows, no
+                            // resets or documents; o.pxT set)
 };
 
 // Per query row record (prow, valid when the row's bigram pair count pnb > 0):
@@ -346,9 +348,10 @@ hipError_t launch_scan_rows(const PathArgs& a, int R, int DV, int dtype, hipStre
 hipError_t launch_pairs_keys(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 // dense rows (dism_dense.hip): classification (before the label scans), the row list and the
 // boundary rows (before the dense kernels), then the tile kernels for the flagged hard rows
+// (prefix: dense rows may become prefix rows, mode 4; calls without resets or documents)
 hipError_t launch_dense_classify(const int32_t* iq, const int32_t* ik, long BH, int n,
-                                 int cls_n, int32_t* dflag, unsigned long long* dcost,
-                                 uint16_t* dbound, int32_t* runcnt, hipStream_t s);
+                                 int cls_n, int prefix, int32_t* dflag,
+                                 unsigned long long* dcost, int32_t* runcnt, hipStream_t s);
 hipError_t launch_walk_probe(const PathArgs& a, hipStream_t s);
 // level lists of the dense rows that qualify (mode 1 -> 3; dism_sort.hip), before the row
 // lists of launch_dense_prepare
@@ -358,11 +361,8 @@ hipError_t launch_level_prep(const PathArgs& a, hipStream_t s);
 hipError_t launch_level_forward(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_level_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_level_keys(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
-// prefix rows: the classification (mode 1 -> 4, right after the dense-row flags), forward
-// (segment totals, chain, readout), backward query rows, backward keys (dism_prefix.hip);
-// no-ops without prefix rows
-hipError_t launch_prefix_check(const int32_t* iq, const int32_t* ik, long BH, int n,
-                               int32_t* dflag, hipStream_t s);
+// prefix rows (classified by launch_dense_classify): forward (segment totals, chain, readout),
+// backward query rows, backward keys (dism_prefix.h); no-ops without prefix rows
 hipError_t launch_prefix_forward(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_prefix_rows(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_prefix_keys(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);

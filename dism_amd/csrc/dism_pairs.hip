@@ -330,12 +330,9 @@ static SortArgs sort_args(const SortArgs& sa, const PathArgs& pa) {
 }
 
 hipError_t launch_classify(const SortArgs& sa, hipStream_t s) {
-    const hipError_t e = launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n,
-                                               sa.o.dflag, sa.o.dcost, sa.o.dbound, sa.o.runcnt,
-                                               s);
-    if (e != hipSuccess || !sa.prefix || !sa.o.pxT || sa.n > DENSE_MAX_N) return e;
-    if (sa.cls_n > 0 && sa.cls_n < sa.n) return e;
-    return launch_prefix_check(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.o.dflag, s);
+    const int prefix = sa.prefix && sa.o.pxT ? 1 : 0;
+    return launch_dense_classify(sa.lab[0], sa.lab[1], sa.BH, sa.n, sa.cls_n, prefix,
+                                 sa.o.dflag, sa.o.dcost, sa.o.runcnt, s);
 }
 
 hipError_t launch_prepare_labels(const SortArgs& sa, const PathArgs& pa, hipStream_t s) {

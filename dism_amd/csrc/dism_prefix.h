@@ -27,7 +27,8 @@
 //
 // A row is a prefix row when it is dense (dense_classify_kernel), has no query resets or
 // documents, and every label bucket (the classification's 12-bit label hash) holds one label
-// and, over positions >= 1 on either side, one predecessor label (prefix_check_kernel).
+// and, over positions >= 1 on either side, one predecessor label (dense_classify_kernel,
+// dism_dense.hip).
 #pragma once
 #include "dism_path.h"
 
@@ -44,9 +45,6 @@ constexpr int PX_HAS = 1 << 20, PX_RESET = 1 << 21;
 __device__ __forceinline__ int pxrl(int x, int t) { return __builtin_amdgcn_readlane(x, t); }
 __device__ __forceinline__ float pxrlf(float x, int t) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), t));
-}
-__device__ __forceinline__ uint32_t px_bucket(int32_t x) {
-    return ((uint32_t)x * 0x9E3779B1u) >> 20;
 }
 __device__ __forceinline__ void px_wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -71,20 +69,28 @@ struct PxSeg {
     long sbase;      // the segment's slot in the per-segment buffers (bh * nseg + s)
 };
 
+// positions a prefix row holds: a prefill's rows are padded after their first cls_n real
+// tokens, and their list is the combined order without the padding (prefix_compact_kernel)
+__device__ __forceinline__ int px_cn(const PathArgs& a) {
+    return a.cls_n > 0 && a.cls_n < a.n ? a.cls_n : a.n;
+}
+
 __device__ __forceinline__ PxSeg px_seg(const PathArgs& a, int bh, int s) {
     PxSeg g;
     const int lane = lane_id();
+    const int cn = px_cn(a);
     g.bh = bh;
     g.n = a.n;
     g.b = bh / a.H;
     g.h = bh - g.b * a.H;
-    g.nseg = px_segs(a.n);
+    g.nseg = px_segs(a.n);  // the per-segment buffers' row stride
     g.s = s;
-    const int n2 = 2 * a.n;
+    const int n2 = 2 * cn;
     g.x0 = s * PREFIX_SEG;
     g.cnt = n2 - g.x0 < PREFIX_SEG ? n2 - g.x0 : PREFIX_SEG;
-    const int32_t* E = a.o.corder + (long)bh * n2;
-    const int32_t* LB = a.o.clab + (long)bh * n2;
+    const bool padded = cn < a.n;
+    const int32_t* E = (padded ? a.o.pxE : a.o.corder) + (long)bh * 2 * a.n;
+    const int32_t* LB = (padded ? a.o.pxL : a.o.clab) + (long)bh * 2 * a.n;
     const bool in = lane < g.cnt;
     g.e = in ? E[g.x0 + lane] : 0;
     g.lab = in ? LB[g.x0 + lane] : 0;
@@ -137,7 +143,7 @@ __global__ __launch_bounds__(PX_THREADS) void prefix_tot_kernel(PathArgs a) {
     __shared__ __align__(16) unsigned char s_r[PX_WAVES][64 * RB];
     __shared__ __align__(16) unsigned char s_v[PX_WAVES][64 * VB];
     const int w = wave_id(), lane = lane_id();
-    const int BH = a.B * a.H, nseg = px_segs(a.n);
+    const int BH = a.B * a.H, nseg = px_segs(px_cn(a));
     const int rows = a.o.dcount[3];
     const long items = (long)rows * nseg;
     const long RD = (long)R * DV;
@@ -316,8 +322,8 @@ __global__ __launch_bounds__(PX_CHAIN_THREADS) void prefix_chain_kernel(PathArgs
     __shared__ float2 s_m[PX_MAX_SEGS];
     const int bh = blockIdx.x, tid = threadIdx.x;
     if (a.o.dflag[bh] != 4 || !a.hard[bh]) return;
-    const int nseg = px_segs(a.n);
-    const long sb = (long)bh * nseg;
+    const int nseg = px_segs(px_cn(a));
+    const long sb = (long)bh * px_segs(a.n);
     for (int s = tid; s < nseg; s += PX_CHAIN_THREADS) {
         if constexpr (KIND < 2) {
             const float4 t = a.o.pxS[sb + s];
@@ -521,7 +527,7 @@ __global__ __launch_bounds__(PX_THREADS) void prefix_forward_kernel(PathArgs a) 
     __shared__ __align__(16) unsigned char s_q[PX_WAVES][64 * RB];
     __shared__ __align__(16) unsigned char s_v[PX_WAVES][64 * VB];
     const int w = wave_id(), lane = lane_id();
-    const int BH = a.B * a.H, nseg = px_segs(a.n);
+    const int BH = a.B * a.H, nseg = px_segs(px_cn(a));
     const int rows = a.o.dcount[3];
     const long items = (long)rows * nseg;
     const long RD = (long)R * DV;
@@ -654,7 +660,7 @@ __global__ __launch_bounds__(PX_THREADS) void prefix_rows_kernel(PathArgs a) {
     __shared__ __align__(16) unsigned char s_d[PX_WAVES][64 * VB];
     __shared__ __align__(16) unsigned char s_v[PX_WAVES][64 * VB];
     const int w = wave_id(), lane = lane_id();
-    const int BH = a.B * a.H, nseg = px_segs(a.n);
+    const int BH = a.B * a.H, nseg = px_segs(px_cn(a));
     const int rows = a.o.dcount[3];
     const long items = (long)rows * nseg;
     const long RD = (long)R * DV;
@@ -815,7 +821,7 @@ __global__ __launch_bounds__(PX_THREADS) void prefix_keys_kernel(PathArgs a) {
     __shared__ __align__(16) unsigned char s_d[PX_WAVES][64 * VB];
     __shared__ __align__(16) unsigned char s_v[PX_WAVES][64 * VB];
     const int w = wave_id(), lane = lane_id();
-    const int BH = a.B * a.H, nseg = px_segs(a.n);
+    const int BH = a.B * a.H, nseg = px_segs(px_cn(a));
     const int rows = a.o.dcount[3];
     const long items = (long)rows * nseg;
     const long RD = (long)R * DV;
@@ -956,6 +962,41 @@ __global__ __launch_bounds__(PX_THREADS) void prefix_keys_kernel(PathArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
+// A padded prefill row's list: the combined order's entries of the first cls_n positions, in
+// order (block-wide ballot scan per 1024-entry chunk).
+template <int UNUSED>
+__global__ __launch_bounds__(1024) void prefix_compact_kernel(PathArgs a) {
+    __shared__ int s_w[16];
+    const int bh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    if (a.o.dflag[bh] != 4) return;
+    const int n2 = 2 * a.n, cn = px_cn(a);
+    const int32_t* E = a.o.corder + (long)bh * n2;
+    const int32_t* LB = a.o.clab + (long)bh * n2;
+    int32_t* oE = a.o.pxE + (long)bh * n2;
+    int32_t* oL = a.o.pxL + (long)bh * n2;
+    int base = 0;
+    for (int c0 = 0; c0 < n2; c0 += 1024) {
+        const int x = c0 + tid;
+        const int e = x < n2 ? E[x] : 0;
+        const bool keep = x < n2 && (e >> 1) < cn;
+        const unsigned long long m = __ballot(keep);
+        if (lane == 0) s_w[w] = __popcll(m);
+        __syncthreads();
+        int off = base;
+        for (int v = 0; v < w; ++v) off += s_w[v];
+        if (keep) {
+            const int at = off + __popcll(m & ((1ull << lane) - 1ull));
+            oE[at] = e;
+            oL[at] = LB[x];
+        }
+        int t = 0;
+        for (int v = 0; v < 16; ++v) t += s_w[v];
+        base += t;
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 // launchers: WHICH 0 forward, 1 backward query side, 2 backward key side (one translation
 // unit each: dism_prefix.hip, dism_prefix_rows.hip, dism_prefix_keys.hip)
 template <int WHICH, typename T, int R, int DV>
@@ -963,6 +1004,10 @@ static hipError_t prefix_go(const PathArgs& a, hipStream_t s) {
     const unsigned BH = (unsigned)(a.B * a.H);
     const int RD = R * DV;
     const dim3 cg(BH, (unsigned)((RD + PX_CHAIN_THREADS * PX_EPT - 1) / (PX_CHAIN_THREADS * PX_EPT)));
+    if constexpr (WHICH == 0) {
+        if (a.cls_n > 0 && a.cls_n < a.n)
+            hipLaunchKernelGGL(prefix_compact_kernel<0>, dim3(BH), dim3(1024), 0, s, a);
+    }
     hipLaunchKernelGGL((prefix_tot_kernel<T, R, DV, WHICH>), dim3(PX_GRID), dim3(PX_THREADS), 0, s, a);
     hipLaunchKernelGGL((prefix_chain_kernel<WHICH>), cg, dim3(PX_CHAIN_THREADS), 0, s, a, RD);
     if constexpr (WHICH == 0)
