@@ -1,5 +1,7 @@
 """Writes tests/golden/golden.json: SHA-256 digests and sample values of the CPU model's
-outputs on the BASELINE configs' generators (configs[0] exactly, configs[1] at reduced size).
+outputs on the BASELINE configs' generators (configs[0] exactly, configs[1] at reduced size:
+level rows) and on identical-label rows at the reference's benchmark row shape (reduced to
+T=512: prefix rows).
 
 The reference ships no golden vectors (its tests build inputs from seeds), so these fixtures
 come from this build's CPU model (oracle/), which tests/test_oracle.py pins against closed
@@ -37,6 +39,14 @@ def config_inputs(name):
         k = rng.standard_normal((B, T, H, D), dtype=np.float32)
         v = oracle.bf16_round(rng.standard_normal((B, T, H, DV), dtype=np.float32))
         do = oracle.bf16_round(rng.standard_normal((B, T, H, DV), dtype=np.float32))
+    elif name == "prefix_s":  # the reference's identical-label benchmark rows, reduced: B=1,
+        # H=2, T=512, R=32, DV=64 with q, k >= 0 (every label 255: prefix rows, mode 4)
+        rng = np.random.default_rng(20261207)
+        B, T, H, D, DV = 1, 512, 2, 32, 64
+        q = oracle.bf16_round(np.abs(rng.standard_normal((B, T, H, D), dtype=np.float32)))
+        k = oracle.bf16_round(np.abs(rng.standard_normal((B, T, H, D), dtype=np.float32)))
+        v = oracle.bf16_round(rng.standard_normal((B, T, H, DV), dtype=np.float32))
+        do = oracle.bf16_round(rng.standard_normal((B, T, H, DV), dtype=np.float32))
     else:
         raise ValueError(name)
     tau = np.linspace(-0.5, 0.5, H).astype(np.float32)
@@ -66,7 +76,7 @@ def compute(name):
 def main():
     oracle.build()
     table = {}
-    for name in ("cfg1", "cfg2s"):
+    for name in ("cfg1", "cfg2s", "prefix_s"):
         res = compute(name)
         table[name] = {
             "digests": {k: digest(v) for k, v in res.items()},
