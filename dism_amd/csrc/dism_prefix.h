@@ -5,8 +5,9 @@
 // so its match runs back to the key's row start: L_ij = j + 1.  The weight of a pair,
 // exp2(LUT[j+1] - m_i), is then a function of the key alone (up to the query's maximum m_i),
 // and a query's sum over its valid keys is a prefix sum over its label group.  The reference
-// computes these rows with the same O(N^2) pairwise loop as every other row; here they cost
-// O(N R DV) (the prefix matrices) plus O(N x 32) pairwise work inside 64-entry segments.
+// computes these rows with the same O(N^2) pairwise loop as every other row
+// (dism_v3/src/hard_forward.cu:28-118, hard_backward.cu:26-154); here they cost O(N R DV)
+// (the prefix matrices) plus O(N x 32) pairwise work inside 64-entry segments.
 //
 // The list is the combined label order (corder: entries e = 2p + s sorted by (label, p, s)),
 // cut into segments of PREFIX_SEG = 64 entries; one wave holds a segment, lane = entry slot.

@@ -707,7 +707,12 @@ int orc_level_row(const int32_t* q, const int32_t* k, long N, int R, int DV) {
  *   p = exp2(l_j - l2_i); s, e, ps, pe as above; dk[r] = dk[r] + lane_tree(pe * sq_i[r]);
  *   ascending: dv[d] = fma(ps, dO_i[d], dv[d]).
  * wave_tree: xor butterfly t[l] = t[l] + t[l ^ o], o = 32, ..., 1, over 64 lanes (0 where no
- * term); lane_tree: lane_reduce's order over per-lane terms. */
+ * term); lane_tree: lane_reduce's order over per-lane terms.
+ * These are the sums of the reference's readout (dism_v3/include/forward/readout.cuh:16-61,
+ * online maximum from 0 and unit fallback) and of its backward with the four-moment tau terms
+ * (dism_v3/src/hard_backward.cu:26-154, 156-197), which the reference takes pair by pair
+ * over every causal pair of these rows; only the association differs (pinned against
+ * direct_forward_row / direct_backward_row and FP64 in tests/test_prefix_rows.py). */
 #define PREFIX_SEG 64L
 
 static float lane_reduce(const float* a, const float* b, int DV, int R);
