@@ -8,14 +8,15 @@ from .hard_backward import backward_hard, backward_hard_recompute
 from .hard_forward import forward_hard, hard_dlog_weights, hard_log_weights, hard_readout
 from .labels import sign_labels, vocab_argmax_labels, vocab_labels
 from .summary import hard_boundary, hard_chunk_scan, summarize_hard
-from .core import dism_core, dism_core_hard, hard_core, hard_core_backward, voc_dism
+from .core import (dism_core, dism_core_hard, dism_core_hybrid, hard_core, hard_core_backward,
+                   voc_dism)
 from .varlen import VarlenLayout
 from .inference import HardDismDecoder, HardDismPrefill, PreparedHardPrefill
 
 __all__ = ["forward_hard", "hard_readout", "hard_log_weights", "hard_dlog_weights",
            "backward_hard", "backward_hard_recompute", "summarize_hard", "hard_chunk_scan",
            "hard_boundary", "sign_labels", "vocab_labels", "vocab_argmax_labels", "dism_core",
-           "voc_dism",
+           "voc_dism", "dism_core_hybrid",
            "dism_core_hard", "hard_core",
            "hard_core_backward", "VarlenLayout", "HardDismPrefill", "PreparedHardPrefill",
            "HardDismDecoder"]

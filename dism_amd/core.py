@@ -172,6 +172,31 @@ def dism_core(q, k, sq, sk, v, q_lse, k_lse, idx_q, idx_k, direction, hard, rtau
     return _SoftOperands.apply(out, q, k, q_lse, k_lse)
 
 
+def dism_core_hybrid(q, k, sq, sk, v, lq, lk, iq, ik, direction, hard, tau, *, soft_core,
+                     layout=None, ctas=0, _lse_preabsorbed=False):
+    """The reference's mixed training core (_MixedCore / dism_core_hybrid,
+    flash_dism/hard_training.py:343-409) with the soft part supplied by the caller: O = the
+    soft core's output + the hard core's output, gradients the sum of both (the reference adds
+    backward_hard_recompute's FP32 gradients for sq, sk, v and tau to the soft ones).
+
+    ``soft_core(q, k, sq, sk, v, lq, lk, iq, ik, direction, hard, tau, layout=..., ctas=...,
+    _lse_preabsorbed=...)`` must return the soft DISM output [B,N,H,DV] with autograd, zero on
+    hard rows (the reference's soft core skips them, include/forward/producer.cuh:18); the soft
+    DISM kernels are not part of this build.  The hard part is ``dism_core_hard``, which gives
+    zero output and zero gradients on soft rows.  With an empty hard side (sq.shape[1] == 0)
+    the result is the soft output alone, as in the reference."""
+    if not callable(soft_core):
+        raise TypeError("soft_core must be a callable returning the soft DISM output")
+    if layout is not None and ctas:
+        raise ValueError("ctas is only supported for fixed-length execution")
+    soft = soft_core(q, k, sq, sk, v, lq, lk, iq, ik, direction, hard, tau, layout=layout,
+                     ctas=ctas, _lse_preabsorbed=_lse_preabsorbed)
+    if sq.shape[1] == 0:
+        return soft
+    hard_out = dism_core_hard(sq, sk, v, iq, ik, hard, tau, layout=layout)
+    return soft + hard_out.to(soft.dtype)
+
+
 def voc_dism(q, k, sq, sk, v, q_vocab, k_vocab, rtau, *, direction, hard, cu_seqlens=None,
              layout=None, ctas=0, beta=1.0, hard_planner=None, all_hard=None):
     """The reference's vocabulary entry (flash_dism/__init__.py:43-56, voc.py:7-40) for rows

@@ -121,3 +121,59 @@ def test_forward_backward_graph_replay():
             assert torch.equal(got, want), i
         run()  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_hybrid_core_checks_cpu():
+    """dism_core_hybrid (the reference's _MixedCore with a caller-supplied soft core):
+    argument checks before anything runs on a device; an empty hard side returns the soft
+    output alone."""
+    sq, sk, v, iq, ik, hard, tau = _fake_inputs(b=1, n=256, h=2)
+    q, k = torch.zeros_like(sq), torch.zeros_like(sk)
+    lse = torch.zeros(1, 2, 256)
+    direction = torch.zeros(1, 2, dtype=torch.uint8)
+    with pytest.raises(TypeError, match="soft_core"):
+        dism_amd.dism_core_hybrid(q, k, sq, sk, v, lse, lse, iq, ik, direction, hard, tau,
+                                  soft_core=None)
+    with pytest.raises(ValueError, match="ctas"):
+        dism_amd.dism_core_hybrid(q, k, sq, sk, v, lse, lse, iq, ik, direction, hard, tau,
+                                  soft_core=lambda *a, **kw: None, layout=object(), ctas=4)
+    soft = torch.ones(1, 256, 2, 64)
+    empty = sq[:, :0]
+    got = dism_amd.dism_core_hybrid(q, k, empty, empty, v[:, :0], lse, lse, iq, ik, direction,
+                                    hard, tau, soft_core=lambda *a, **kw: soft)
+    assert got is soft
+
+
+@pytest.mark.gpu
+def test_hybrid_core_sums_soft_and_hard():
+    """O = soft + hard, gradients the sum of both parts' (hard rows mixed with soft rows: the
+    hard core is zero on soft rows, the toy soft core zero on hard rows)."""
+    from tests._data import labels, taus, vectors
+    n, b, h = 512, 2, 3
+    sq, sk, v = vectors(n, b, h)
+    ql, kl = labels(n, "random", b, h)
+    d = torch.device("cuda")
+    iq, ik = torch.from_numpy(ql).to(d), torch.from_numpy(kl).to(d)
+    hard = torch.tensor([[True, False, True], [False, True, True]], device=d)
+    leaves = [torch.from_numpy(a).to(d, torch.bfloat16).requires_grad_() for a in (sq, sk, v)]
+    tau = torch.from_numpy(taus(h)).to(d).requires_grad_()
+    lse = torch.zeros((b, h, n), device=d)
+    direction = torch.zeros((b, h), dtype=torch.uint8, device=d)
+    soft_mask = (~hard).float().view(b, 1, h, 1)
+
+    def soft_core(q, k, sq_, sk_, v_, lq, lk, iq_, ik_, dirn, hard_, tau_, **kw):
+        return (v_.float() * 0.5 + sq_.float().sum(-1, keepdim=True)) * soft_mask
+
+    out = dism_amd.dism_core_hybrid(leaves[0], leaves[1], *leaves, lse, lse, iq, ik, direction,
+                                    hard, tau, soft_core=soft_core)
+    dout = torch.randn(out.shape, device=d, generator=torch.Generator(d).manual_seed(3))
+    out.backward(dout)
+    got = [t.grad.clone() for t in leaves] + [tau.grad.clone()]
+    for t in leaves + [tau]:
+        t.grad = None
+    hard_out = dism_amd.dism_core_hard(*leaves, iq, ik, hard, tau)
+    soft_out = soft_core(None, None, *leaves, lse, lse, iq, ik, direction, hard, tau)
+    torch.testing.assert_close(out, soft_out + hard_out.float(), rtol=0, atol=0)
+    (soft_out + hard_out.float()).backward(dout)
+    for a, c in zip(got, [t.grad for t in leaves] + [tau.grad]):
+        torch.testing.assert_close(a, c, rtol=0, atol=0)
