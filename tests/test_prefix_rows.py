@@ -114,3 +114,34 @@ def test_long_row_rescaling():
     segment totals, chains and queries all rescale; and tau < 0, where LUT saturates."""
     q, k = labels(1500, "equal", b=1, h=2)
     _pair_check(q, k, 8, 32, np.array([1.0, -0.7], np.float32), seed=5, fp64=False)
+
+
+def test_random_predecessor_functions_against_direct():
+    """Rows generated from random predecessor functions (each label's successor chosen at
+    random, some labels only on one side): whenever the rule holds the row is a prefix row,
+    and its prefix definition matches the direct one; rows that break the rule are not."""
+    rng = np.random.default_rng(77)
+    for trial in range(12):
+        n = int(rng.integers(70, 260))
+        alpha = int(rng.integers(1, 9))
+        succ = rng.integers(0, alpha, alpha)        # label -> next label
+        q = np.empty(n, np.int32)
+        q[0] = rng.integers(0, alpha)
+        for p in range(1, n):
+            q[p] = succ[q[p - 1]]
+        shift = int(rng.integers(0, 3))
+        k = np.concatenate([q[shift:], q[:shift]])  # the same chain, started later
+        for p in range(n - shift, n):
+            k[p] = succ[k[p - 1]] if p > 0 else k[p]
+        if trial % 4 == 3:                          # break the rule once
+            k[n // 2] = (k[n // 2] + 1) % max(alpha, 2)
+        qq, kk = q[None, None], k[None, None]
+        is_prefix = oracle.prefix_row(q, k)
+        assert is_prefix == int(_brute_prefix(q, k) and oracle.dense_rows(
+            qq, kk, np.ones((1, 1), bool))[0, 0])
+        if not is_prefix:
+            continue
+        L = _brute_L(q, k)
+        i, j = np.nonzero(L)
+        assert (L[i, j] == j + 1).all()
+        _pair_check(qq, kk, 4, 32, np.array([0.3], np.float32), seed=trial, fp64=False)
