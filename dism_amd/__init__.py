@@ -10,7 +10,8 @@ from .labels import sign_labels, vocab_argmax_labels, vocab_labels
 from .summary import hard_boundary, hard_chunk_scan, summarize_hard
 from .core import (dism_core, dism_core_hard, dism_core_hybrid, hard_core, hard_core_backward,
                    voc_dism)
-from .varlen import VarlenLayout
+from .varlen import (VarlenLayout, graph_layout_maximum, layout_from_table, make_graph_layout,
+                     update_graph_layout)
 from .inference import HardDismDecoder, HardDismPrefill, PreparedHardPrefill
 
 __all__ = ["forward_hard", "hard_readout", "hard_log_weights", "hard_dlog_weights",
@@ -18,5 +19,6 @@ __all__ = ["forward_hard", "hard_readout", "hard_log_weights", "hard_dlog_weight
            "hard_boundary", "sign_labels", "vocab_labels", "vocab_argmax_labels", "dism_core",
            "voc_dism", "dism_core_hybrid",
            "dism_core_hard", "hard_core",
-           "hard_core_backward", "VarlenLayout", "HardDismPrefill", "PreparedHardPrefill",
+           "hard_core_backward", "VarlenLayout", "make_graph_layout", "update_graph_layout",
+           "graph_layout_maximum", "layout_from_table", "HardDismPrefill", "PreparedHardPrefill",
            "HardDismDecoder"]

@@ -1,7 +1,8 @@
 // dism_packed.hip -- packed batch-1 (varlen) layouts on the fixed-length kernels.
 //
-// A packed call holds documents [cu[d], cu[d+1]) of one sequence (B = 1, no empty documents
-// in the offsets the library receives); matches never cross a document.  Instead of
+// A packed call holds documents [cu[d], cu[d+1]) of one sequence (B = 1; cu non-decreasing,
+// a repeated entry is an empty document that no token belongs to, since a token's document is
+// the LAST d with cu[d] <= t); matches never cross a document.  Instead of
 // per-document task records the hard core runs unchanged on document-tagged labels:
 //   tag = rank * docs + d   (uint32)
 // with rank the dense rank of the raw label among the distinct labels of its (head) row --

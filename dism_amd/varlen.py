@@ -14,6 +14,7 @@ allocates the outputs.  Packed strip-32 summaries/boundaries use the reference's
 document s, head h at offset ForwardOffset[s]*H + h*((L-1)//32)*L, a [(L-1)//32, L] block in
 document-local coordinates.
 """
+import weakref
 from dataclasses import dataclass
 
 import torch
@@ -83,8 +84,15 @@ class VarlenLayout:
 
     @classmethod
     def for_graph(cls, table, total_tokens):
-        raise NotImplementedError("CUDA Graph layout capacities are not implemented by the "
-                                  "MI355X hard core")
+        """Layout over a fixed-capacity graph table (make_graph_layout); reference
+        varlen.py:28-36.  Capacities (checkpoint elements, LUT length) follow max_seqlen, so
+        they stay valid after update_graph_layout rewrites the documents in place."""
+        maximum = graph_layout_maximum(table)
+        if not maximum:
+            raise ValueError("expected an owned CUDA Graph layout")
+        return cls(table, tuple(table[:, 1].tolist()), total_tokens, total_tokens,
+                   total_tokens * ((maximum - 1) // 32), total_tokens * ((maximum - 1) // 16),
+                   total_tokens * (maximum // 32), maximum)
 
     @property
     def documents(self):
@@ -101,6 +109,9 @@ class VarlenLayout:
 
     def offsets(self, device):
         """Device int32 offsets of the non-empty documents, [docs+1] (cached per device)."""
+        state = _graph_state(self.table)
+        if state is not None:
+            return state.device_offsets(torch.device(device))
         key = str(torch.device(device))
         cache = self._device_offsets
         if key not in cache:
@@ -119,6 +130,162 @@ class VarlenLayout:
                             3 * self.backward_elements)
 
 
+# ---- fixed-capacity layouts for graph replay (reference dism_v3/src/host/graph_layout.h) ----
+#
+# A graph captures kernel launches with their pointer arguments, so a layout that changes
+# between replays must keep every device buffer at a fixed address and size.  The table is a
+# CPU int64 [tokens/256, 7] tensor (the most documents `tokens` can hold): its non-empty
+# documents first, then padding rows (begin = tokens, length 0).  The kernels read a device
+# int32 offsets array [tokens/256 + 1] built from the begin column plus `tokens`; padding rows
+# repeat `tokens`, which the packed kernels read as empty documents.  update_graph_layout
+# validates new boundaries, rewrites the table in place and refreshes every device copy in
+# place with an async copy on the owning stream, ordered after the previous replay and before
+# the next one.  The state hangs off the table's storage: views share it, clones do not.
+
+_GRAPH_STATES = weakref.WeakKeyDictionary()
+
+
+class _GraphState:
+    def __init__(self, tokens, maximum, row_tokens):
+        self.tokens, self.maximum, self.row_tokens = tokens, maximum, row_tokens
+        self.documents = tokens // 256
+        self.storage = None  # weak: set by make_graph_layout
+        self.offsets = {}    # device -> int32 [documents + 1]
+        self.device_index = -1
+        self.stream_id = None
+
+    def rows(self):
+        storage = self.storage()
+        return torch.empty(0, dtype=torch.int64).set_(storage, 0, (self.documents, 7))
+
+    def host_offsets(self):
+        begins = self.rows()[:, BEGIN].to(torch.int32)
+        return torch.cat([begins, torch.tensor([self.tokens], dtype=torch.int32)])
+
+    def check_stream(self, device):
+        stream = torch.cuda.current_stream(device)
+        if self.device_index < 0:
+            self.device_index, self.stream_id = device.index, stream.stream_id
+        require(self.device_index == device.index and self.stream_id == stream.stream_id,
+                "graph metadata must be staged, captured and replayed on its owning stream")
+
+    def device_offsets(self, device):
+        if device.type != "cuda":
+            return self.host_offsets().to(device)
+        if device.index is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        self.check_stream(device)
+        found = self.offsets.get(device.index)
+        if found is not None:
+            return found
+        _outside_capture(device)
+        gpu = self.host_offsets().pin_memory().to(device, non_blocking=True)
+        self.offsets[device.index] = gpu
+        return gpu
+
+
+def _outside_capture(device):
+    with torch.cuda.device(device):
+        require(not torch.cuda.is_current_stream_capturing(),
+                "prepare/update graph metadata outside CUDA Graph capture")
+
+
+def _graph_state(table):
+    if not isinstance(table, torch.Tensor) or table.device.type != "cpu":
+        return None
+    return _GRAPH_STATES.get(table.untyped_storage())
+
+
+def _graph_rows(state, boundaries):
+    """Validated table rows for new boundaries (reference graph_layout.h update), or raise
+    before anything is changed."""
+    require(isinstance(boundaries, torch.Tensor) and boundaries.device.type == "cpu" and
+            boundaries.dtype == torch.int32 and boundaries.dim() == 1 and
+            boundaries.is_contiguous() and boundaries.numel() >= 2,
+            "graph boundaries must be contiguous CPU int32 [documents+1]")
+    cu = [int(x) for x in boundaries.tolist()]
+    require(cu[0] == 0 and cu[-1] == state.tokens, "invalid graph boundary endpoints")
+    rows = []
+    f = v = b = 0
+    for begin, end in zip(cu[:-1], cu[1:]):
+        n = end - begin
+        require(begin >= 0 and begin % 256 == 0 and n >= 0 and n % 256 == 0 and
+                n <= state.maximum,
+                "graph documents must be monotonic, 256-aligned and within max_seqlen")
+        if not n:
+            continue  # empty documents have no work and no table row
+        require(begin // state.row_tokens == (begin + n - 1) // state.row_tokens,
+                "document cannot cross a hard training-row boundary")
+        require(len(rows) < state.documents, "too many graph documents")
+        rows.append([begin, n, begin, n, f, v, b])
+        f += (n - 1) // 32 * n
+        v += (n - 1) // 16 * n
+        b += n // 32 * n
+    rows += [[state.tokens, 0, state.tokens, 0, f, v, b]] * (state.documents - len(rows))
+    return torch.tensor(rows, dtype=torch.int64)
+
+
+def make_graph_layout(boundaries, tokens, maximum, row_tokens):
+    """Fixed-capacity graph layout table (reference cu.make_graph_layout,
+    dism_v3/src/host/graph_layout.h create): tokens, max_seqlen and training-row length are
+    256-aligned capacities fixed for the table's life; ``boundaries`` is the first pack."""
+    tokens, maximum, row_tokens = int(tokens), int(maximum), int(row_tokens)
+    require(0 < tokens <= 2**31 - 1 - 256 and tokens % 256 == 0 and 0 < maximum <= tokens and
+            maximum % 256 == 0 and row_tokens > 0 and row_tokens % 256 == 0 and
+            tokens % row_tokens == 0 and maximum <= row_tokens,
+            "invalid graph token/max_seqlen/training-row capacities")
+    # documents are told apart by tagging label ranks with their index: 2 * N * docs <= 2^32
+    require(2 * tokens * (tokens // 256) <= 2**32,
+            "graph layout tokens exceed the packed core's document-tag range "
+            "(2 * tokens * tokens/256 <= 2^32)")
+    state = _GraphState(tokens, maximum, row_tokens)
+    table = _graph_rows(state, boundaries)
+    storage = table.untyped_storage()
+    state.storage = weakref.ref(storage)
+    _GRAPH_STATES[storage] = state
+    return table
+
+
+def update_graph_layout(table, boundaries):
+    """Rewrite a graph layout's documents in place (reference cu.update_graph_layout).  All
+    input is validated before anything changes; device copies are refreshed in place on the
+    owning stream, so call it between replays, outside capture."""
+    state = _graph_state(table)
+    require(state is not None, "expected an owned graph layout")
+    rows = _graph_rows(state, boundaries)
+    for index in state.offsets:
+        device = torch.device("cuda", index)
+        _outside_capture(device)
+        state.check_stream(device)
+    state.rows().copy_(rows)
+    host = state.host_offsets()
+    for index, gpu in state.offsets.items():
+        with torch.cuda.device(index):
+            gpu.copy_(host.pin_memory(), non_blocking=True)
+
+
+def graph_layout_maximum(table):
+    """max_seqlen of a graph layout table, 0 for any other tensor (reference
+    cu.graph_layout_maximum)."""
+    state = _graph_state(table)
+    return state.maximum if state is not None else 0
+
+
+def layout_from_table(table, tokens):
+    """VarlenLayout from a layout table without any device readback (reference
+    hard_training.py:328-340): graph tables keep their fixed capacities."""
+    if table is None:
+        return None
+    table = table.view(-1, 7)
+    if graph_layout_maximum(table):
+        return VarlenLayout.for_graph(table, tokens)
+    lengths = tuple(table[:, 1].tolist())
+    return VarlenLayout(table, lengths, tokens, tokens,
+                        sum((n - 1) // 32 * n for n in lengths if n),
+                        sum((n - 1) // 16 * n for n in lengths if n),
+                        sum((n + 31) // 32 * n for n in lengths))
+
+
 def check_packed_rows(layout, n, hard, h, device):
     """Packed batch-1 preconditions of the reference (hard_forward.cpp:57-75): returns the
     training-row length."""
@@ -132,6 +299,9 @@ def check_packed_rows(layout, n, hard, h, device):
     require(n % rows == 0 and (n // rows) % 256 == 0,
             "packed hard rows must evenly divide tokens into 256-aligned training rows")
     row_n = n // rows
+    state = _graph_state(layout.table)
+    require(state is None or state.row_tokens == row_n,
+            "packed hard rows must match the graph layout's training-row length")
     for begin, length in layout.spans():
         require(begin // row_n == (begin + length - 1) // row_n,
                 "document cannot cross a hard training-row boundary")

@@ -225,7 +225,8 @@ int32_t dism_hard_tau_reduce(const float* rowtau, int64_t B, int64_t H, int64_t 
 
 /* ---- Packed (varlen) batch-1 layouts.  One token sequence of N tokens (B = 1) holds the
  * documents [cu_seqlens[d], cu_seqlens[d+1]), d < docs (device int32 [docs+1], 0 = first,
- * N = last, strictly increasing: the caller drops empty documents); matches never cross a
+ * N = last, non-decreasing: a repeated entry is an empty document, which is how a
+ * fixed-capacity graph layout pads its table with entries equal to N); matches never cross a
  * document.  Hard flags are per training row: hard [rows, H] with N/rows tokens per row (a
  * multiple of 256), and no document crosses a training row (the caller checks the offsets on
  * the host, as the reference's layout does).  Soft training rows get zero outputs and

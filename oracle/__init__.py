@@ -208,15 +208,17 @@ def level_count(q, k, R, DV):
     return int(lib().orc_level_row(_p(q), _p(k), q.shape[-1], R, DV))
 
 
-def packed_dense_flags(iq, ik, offsets):
+def packed_dense_flags(iq, ik, offsets, slots=None):
     """Row classification of a packed call (B = 1): the HIP path classifies each head row of
-    its document-tagged labels tag = rank * docs + d (rank: dense rank of the raw label among
-    the row's distinct labels in unsigned order; d: index among the non-empty documents).
-    Returns uint8 [1, H]."""
+    its document-tagged labels tag = rank * slots + d (rank: dense rank of the raw label among
+    the row's distinct labels in unsigned order; d: index among the non-empty documents;
+    slots: the document count the library receives, by default the non-empty documents, for
+    a fixed-capacity graph layout tokens / 256).  Returns uint8 [1, H]."""
     iq, ik = _i32(iq), _i32(ik)
     _, H, N = iq.shape
     offs = [int(x) for x in offsets]
     docs = [(a, z) for a, z in zip(offs, offs[1:]) if z > a]
+    slots = len(docs) if slots is None else int(slots)
     dindex = np.empty(N, np.uint64)
     for d, (a, z) in enumerate(docs):
         dindex[a:z] = d
@@ -227,7 +229,7 @@ def packed_dense_flags(iq, ik, offsets):
         uniq = np.unique(np.concatenate([uq, uk]))
         for src, dst in ((uq, tq), (uk, tk)):
             rank = np.searchsorted(uniq, src).astype(np.uint64)
-            tag = (rank * np.uint64(len(docs)) + dindex) & np.uint64(0xFFFFFFFF)
+            tag = (rank * np.uint64(slots) + dindex) & np.uint64(0xFFFFFFFF)
             dst[0, h] = tag.astype(np.uint32).view(np.int32)
     return dense_rows(tq, tk, np.ones((1, H), bool))
 

@@ -38,7 +38,7 @@ def _inputs(n, pattern, h=2, r=8, dv=64, seed=0):
     return sq, sk, v, do, q, k, taus(h)
 
 
-def _expected(x, offsets, hard):
+def _expected(x, offsets, hard, slots=None):
     """Per-document CPU model results assembled into packed tensors (soft rows as the model
     gives them for a soft row: zeros, lmax 0, argmax -1)."""
     sq, sk, v, do, q, k, tau = x
@@ -53,7 +53,7 @@ def _expected(x, offsets, hard):
     rowtau = np.zeros((1, h, n), np.float32)
     # each head row of the packed call is computed with its own classification (dense rows:
     # the direct definition) for all of its documents
-    dense = oracle.packed_dense_flags(q, k, offsets)
+    dense = oracle.packed_dense_flags(q, k, offsets, slots)
     for a, z in _docs(offsets):
         flags = hard[a // row_n:a // row_n + 1]
         lut = oracle.log_weights(tau, z - a)
