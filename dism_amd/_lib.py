@@ -87,6 +87,11 @@ def load():
         lib.dism_last_error.argtypes = []
         lib.dism_abi_version.restype = ctypes.c_int32
         lib.dism_abi_version.argtypes = []
+        lib.dism_layout_check.restype = ctypes.c_int32
+        lib.dism_layout_check.argtypes = []
+        if lib.dism_layout_check() != 0:
+            raise DismNativeMissing(
+                f"{LIB_PATH}: {lib.dism_last_error().decode(errors='replace')}")
         for name, args in SIZE_SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = args

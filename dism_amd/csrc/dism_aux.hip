@@ -5,6 +5,8 @@
 #include "dism_device.h"
 #include "dism_launch.h"
 
+DISM_TU_LAYOUT(aux)
+
 namespace dism {
 
 // ---- labels: x [B,N,H,d] -> labels [B,H,N], bit k set iff x[...,k] > 0 (NaN, +-0 -> 0).

@@ -37,6 +37,34 @@ int32_t hip_status(hipError_t e, const char* what) {
     return fail(DISM_ERR_HIP, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
 }
 
+// Layout fingerprints of the translation units (DISM_TU_LAYOUT, dism_launch.h): every kernel
+// unit must have been compiled against this unit's argument-struct layout.
+#define DISM_TU_LIST(X)                                                                    \
+    X(aux) X(sort) X(msort) X(pairs) X(scan) X(packed) X(dense) X(levels) X(prefix)          \
+    X(prefix_rows) X(prefix_keys) X(decode) X(vocab)
+#define DISM_TU_DECL(tu) extern "C" const unsigned long long dism_layout_##tu;
+DISM_TU_LIST(DISM_TU_DECL)
+#undef DISM_TU_DECL
+
+std::string layout_mismatch() {
+    std::string bad;
+    constexpr unsigned long long want = dism::layout_fingerprint();
+#define DISM_TU_CMP(tu)                                                                     \
+    if (dism_layout_##tu != want) bad += (bad.empty() ? "" : ", ") + std::string("dism_" #tu);
+    DISM_TU_LIST(DISM_TU_CMP)
+#undef DISM_TU_CMP
+    return bad;
+}
+
+// DISM_OK once every unit matches (checked once per process), else an error naming the units
+int32_t layout_guard() {
+    static const std::string bad = layout_mismatch();
+    if (bad.empty()) return DISM_OK;
+    return fail(DISM_ERR_INVALID,
+                "library linked from objects with mismatched argument-struct layouts (stale: "
+                "%s); rebuild every translation unit", bad.c_str());
+}
+
 bool dims_ok(int64_t B, int64_t N, int64_t H) {
     return B > 0 && H > 0 && N > 0 && N <= INT_MAX / 64 && B * H <= 65535;
 }
@@ -283,6 +311,7 @@ dism::PathArgs path(const Layout& L, void* ws, int64_t B, int64_t N, int64_t H,
 int32_t check_common(const void* sq, const void* sk, const void* v, int32_t dtype,
                      const int32_t* iq, const int32_t* ik, int64_t B, int64_t N, int64_t H,
                      int32_t R, int32_t DV, const void* ws, int64_t ws_bytes, const char* what) {
+    if (int32_t st = layout_guard()) return st;
     if (!sq || !sk || !v || !iq || !ik || !ws)
         return fail(DISM_ERR_INVALID, "%s: null pointer", what);
     if (!dims_ok(B, N, H)) return fail(DISM_ERR_INVALID, "%s: positive dimensions required", what);
@@ -331,7 +360,11 @@ int32_t prepare_impl(const void* sq, const void* sk, const void* v, int32_t dtyp
 extern "C" {
 
 const char* dism_last_error(void) { return g_error.c_str(); }
-int32_t dism_abi_version(void) { return 6; }
+int32_t dism_layout_check(void) {
+    if (int32_t st = layout_guard()) return st;
+    return ok();
+}
+int32_t dism_abi_version(void) { return 7; }
 
 int32_t dism_sign_labels(const void* x, int32_t dtype, int64_t B, int64_t N, int64_t H, int32_t d,
                          int32_t* labels, void* stream) {
@@ -592,6 +625,7 @@ int32_t dism_hard_forward_noalloc(const void* sq, const void* sk, const void* v,
                                   int64_t H, int32_t R, int32_t DV, void* out, int32_t out_dtype,
                                   float* lse2, int32_t* lmax, int32_t* jarg, void* stream) {
     const char* what = "hard forward (no allocation)";
+    if (int32_t lg = layout_guard()) return lg;
     if (!dims_ok(B, N, H) || B * H * N > INT_MAX || !rdv_ok(R, DV) || !dtype_ok(dtype))
         return fail(DISM_ERR_INVALID, "%s: unsupported dimensions or dtype", what);
     const int64_t need = layout(B, N, H, R, DV).total;
@@ -888,6 +922,7 @@ int32_t dism_hard_packed_prepare(const void* sq, const void* sk, const void* v, 
                                  int32_t R, int32_t DV, void* workspace,
                                  int64_t workspace_bytes, void* stream) {
     const char* what = "packed hard prepare";
+    if (int32_t lg = layout_guard()) return lg;
     int32_t st = check_packed(sq, sk, v, dtype, N, H, R, DV, workspace, workspace_bytes, what);
     if (st) return st;
     if (!iq || !ik || !cu_seqlens) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
@@ -934,6 +969,7 @@ int32_t dism_hard_packed_readout(const void* sq, const void* sk, const void* v, 
                                  void* out, int32_t out_dtype, float* lse2, int32_t* lmax,
                                  int32_t* jarg, void* stream) {
     const char* what = "packed hard readout";
+    if (int32_t lg = layout_guard()) return lg;
     int32_t st = check_packed(sq, sk, v, dtype, N, H, R, DV, workspace, workspace_bytes, what);
     if (st) return st;
     if ((st = check_rows(hard, rows, N, lut, lut_stride, max_length, what))) return st;
@@ -971,6 +1007,7 @@ int32_t dism_hard_packed_backward(const void* sq, const void* sk, const void* v,
                                   int64_t workspace_bytes, float* dsq, float* dsk, float* dv,
                                   float* rowtau, float* dtau, void* stream) {
     const char* what = "packed hard backward";
+    if (int32_t lg = layout_guard()) return lg;
     int32_t st = check_packed(sq, sk, v, dtype, N, H, R, DV, workspace, workspace_bytes, what);
     if (st) return st;
     if ((st = check_rows(hard, rows, N, lut, lut_stride, max_length, what))) return st;
@@ -1098,6 +1135,7 @@ int32_t dism_hard_prefill(const void* sq, const void* sk, const void* v, int32_t
                           int64_t n_valid, int64_t H, int32_t R, int32_t DV, void* workspace,
                           int64_t workspace_bytes, float* out, float* lse2, void* stream) {
     const char* what = "hard prefill";
+    if (int32_t lg = layout_guard()) return lg;
     int32_t st = check_common(sq, sk, v, dtype, iq, ik, B, N, H, R, DV, workspace,
                               workspace_bytes, what);
     if (st) return st;
@@ -1147,6 +1185,7 @@ int64_t dism_decoder_state_bytes(int64_t rows, int32_t R, int32_t DV, int64_t ca
 int32_t dism_decoder_init(void* state, int64_t state_bytes, int64_t rows, int32_t R, int32_t DV,
                           int64_t capacity, int32_t slots, int32_t dtype, void* stream) {
     const char* what = "decoder init";
+    if (int32_t lg = layout_guard()) return lg;
     if (!state) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
     if (!decoder_dims_ok(rows, R, DV, capacity, slots, dtype))
         return fail(DISM_ERR_INVALID, "%s: invalid decoder dimensions", what);
@@ -1163,6 +1202,7 @@ int32_t dism_decoder_step(void* state, int64_t state_bytes, int64_t B, int64_t H
                           const void* sq, const void* sk, const void* v, const float* lut,
                           int64_t lut_stride, float* out, float* lse2, void* stream) {
     const char* what = "decoder step";
+    if (int32_t lg = layout_guard()) return lg;
     if (!state || !iq || !ik || !sk || !v) return fail(DISM_ERR_INVALID, "%s: null pointer", what);
     const int64_t rows = B * H;
     if (B <= 0 || H <= 0 || !decoder_dims_ok(rows, R, DV, capacity, slots, dtype))
@@ -1196,6 +1236,7 @@ int32_t dism_vocab_labels(const void* x, const void* vocab, int64_t vocab_head_s
                           int64_t N, int64_t H, int64_t V, int32_t D, int32_t* labels,
                           int32_t* scratch, void* stream) {
     const char* what = "vocabulary labels";
+    if (int32_t lg = layout_guard()) return lg;
     if (!x || !vocab || !labels || !scratch)
         return fail(DISM_ERR_INVALID, "%s: null pointer", what);
     if (B <= 0 || N <= 0 || H <= 0 || V <= 0 || V > INT_MAX || B * H * N >= INT_MAX)
@@ -1231,6 +1272,7 @@ int32_t dism_decoder_prime(void* state, int64_t state_bytes, int64_t B, int64_t 
                            const void* sk, const void* v, void* workspace,
                            int64_t workspace_bytes, void* stream) {
     const char* what = "decoder prime";
+    if (int32_t lg = layout_guard()) return lg;
     if (!state || !iq || !ik || !sk || !v || !workspace)
         return fail(DISM_ERR_INVALID, "%s: null pointer", what);
     const int64_t rows = B * H;

@@ -22,6 +22,8 @@
 // other lanes after an agent-scope fence per token.
 #include "dism_path.h"
 
+DISM_TU_LAYOUT(decode)
+
 namespace dism {
 
 constexpr int DEC_WAVES = 4;

@@ -33,6 +33,8 @@
 // non-finite value, for which such cells are skipped explicitly.
 #include "dism_path.h"
 
+DISM_TU_LAYOUT(dense)
+
 namespace dism {
 
 constexpr int DENSE_THREADS = 256;
@@ -148,25 +150,26 @@ __global__ __launch_bounds__(CLS_THREADS) void dense_classify_kernel(
 }
 
 // Row modes and lists (one workgroup, after the walk probe and the level lists): mode 2 for
-// the sparse rows whose walk-cost estimate exceeds N^2; the mode-1 rows ascending in
+// the sparse rows whose walk-cost estimate exceeds cn^2 (cn: the positions the classification
+// counted, a prefill's real tokens; the estimate covers only those); the mode-1 rows ascending in
 // dlist[0..), the rows of modes 1 and 2 in dlist[BH..), the mode-3 rows in dlist[2 BH..), the
 // mode-4 rows in dlist[3 BH..), their counts in dcount[0..3].
 __global__ __launch_bounds__(1024) void dense_mode_kernel(int32_t* __restrict__ dflag,
                                                           const unsigned long long* __restrict__ dcost,
-                                                          int BH, int n,
+                                                          int BH, int n, int cn,
                                                           int32_t* __restrict__ dlist,
                                                           int32_t* __restrict__ dcount) {
     constexpr int NL = 4;
     __shared__ int s_w[NL][16];
     __shared__ int s_base[NL];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const unsigned long long nn = (unsigned long long)n * (unsigned long long)n;
+    const unsigned long long nn = (unsigned long long)cn * (unsigned long long)cn;
     if (tid < NL) s_base[tid] = 0;
     __syncthreads();
     for (int c0 = 0; c0 < BH; c0 += 1024) {
         const int x = c0 + tid;
         int mode = x < BH ? dflag[x] : 0;
-        if (x < BH && mode == 0 && n <= DENSE_MAX_N && n > 64 && dcost[x] > nn) {
+        if (x < BH && mode == 0 && n <= DENSE_MAX_N && cn > 64 && dcost[x] > nn) {
             mode = 2;
             dflag[x] = 2;
         }
@@ -722,7 +725,8 @@ hipError_t launch_dense_prepare(const PathArgs& a, hipStream_t s) {
     const hipError_t le = launch_level_prep(a, s);
     if (le != hipSuccess) return le;
     hipLaunchKernelGGL(dense_mode_kernel, dim3(1), dim3(1024), 0, s, a.o.dflag, a.o.dcost,
-                       a.B * a.H, a.n, a.o.dlist, a.o.dcount);
+                       a.B * a.H, a.n, a.cls_n > 0 && a.cls_n < a.n ? a.cls_n : a.n, a.o.dlist,
+                       a.o.dcount);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.n > DENSE_MAX_N || a.n <= 64) return e;
     hipLaunchKernelGGL(dense_bound_kernel, dim3(DENSE_GRID), dim3(256), 0, s, a);

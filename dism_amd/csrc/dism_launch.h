@@ -2,6 +2,7 @@
 // layer (dism_capi.cpp).  Plain pointers and sizes only.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 namespace dism {
@@ -372,4 +373,59 @@ hipError_t launch_dense_rows(const PathArgs& a, int R, int DV, int dtype, hipStr
 hipError_t launch_dense_keys(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 hipError_t launch_scan_keys(const PathArgs& a, int R, int DV, int dtype, hipStream_t s);
 
+// ---------------------------------------------------------------------------------------
+// Layout fingerprint of the argument structs the kernels take by value.  Every translation
+// unit records the fingerprint it was compiled with (DISM_TU_LAYOUT); dism_layout_check()
+// in dism_capi.cpp compares them on load and on the first call, so a library linked from
+// objects compiled against different versions of these structs refuses to run instead of
+// launching kernels that read their arguments at the wrong offsets.
+static_assert(sizeof(void*) == 8 && sizeof(long) == 8, "LP64 host and device");
+static_assert(sizeof(Orders) == 448, "Orders changed: update the size and the fingerprint");
+static_assert(sizeof(SortArgs) == 528, "SortArgs changed: update the size and the fingerprint");
+static_assert(sizeof(PathArgs) == 680, "PathArgs changed: update the size and the fingerprint");
+static_assert(sizeof(PackedZero) == 112, "PackedZero changed: update the size");
+static_assert(sizeof(DecodeArgs) == 216, "DecodeArgs changed: update the size");
+
+constexpr unsigned long long fp_mix(unsigned long long h, unsigned long long v) {
+    return (h ^ v) * 1099511628211ull;  // FNV-1a step over whole values
+}
+#define DISM_FP(S, f) h = fp_mix(h, offsetof(S, f))
+constexpr unsigned long long layout_fingerprint() {
+    unsigned long long h = 1469598103934665603ull;
+    h = fp_mix(h, sizeof(Orders));
+    h = fp_mix(h, sizeof(SortArgs));
+    h = fp_mix(h, sizeof(PathArgs));
+    h = fp_mix(h, sizeof(PackedZero));
+    h = fp_mix(h, sizeof(DecodeArgs));
+    DISM_FP(Orders, bpos); DISM_FP(Orders, shift); DISM_FP(Orders, stage);
+    DISM_FP(Orders, ocount); DISM_FP(Orders, mcount); DISM_FP(Orders, dflag);
+    DISM_FP(Orders, dlist); DISM_FP(Orders, dbound); DISM_FP(Orders, runs);
+    DISM_FP(Orders, lvent); DISM_FP(Orders, lvK); DISM_FP(Orders, pxT);
+    DISM_FP(Orders, pxE); DISM_FP(Orders, pxL);
+    DISM_FP(SortArgs, BH); DISM_FP(SortArgs, n); DISM_FP(SortArgs, tmp);
+    DISM_FP(SortArgs, pnb); DISM_FP(SortArgs, o); DISM_FP(SortArgs, role_base);
+    DISM_FP(SortArgs, lds_rows); DISM_FP(SortArgs, cls_n); DISM_FP(SortArgs, prefix);
+    DISM_FP(PathArgs, iq); DISM_FP(PathArgs, hard); DISM_FP(PathArgs, lut);
+    DISM_FP(PathArgs, dlut); DISM_FP(PathArgs, lut_stride); DISM_FP(PathArgs, bound);
+    DISM_FP(PathArgs, strip); DISM_FP(PathArgs, o); DISM_FP(PathArgs, sq);
+    DISM_FP(PathArgs, sk); DISM_FP(PathArgs, v); DISM_FP(PathArgs, dout);
+    DISM_FP(PathArgs, out); DISM_FP(PathArgs, out_dtype); DISM_FP(PathArgs, lse2);
+    DISM_FP(PathArgs, lmax); DISM_FP(PathArgs, jarg); DISM_FP(PathArgs, pnb);
+    DISM_FP(PathArgs, prow); DISM_FP(PathArgs, prow_stride); DISM_FP(PathArgs, dsq);
+    DISM_FP(PathArgs, dsk); DISM_FP(PathArgs, dv); DISM_FP(PathArgs, rowtau);
+    DISM_FP(PathArgs, dstart); DISM_FP(PathArgs, wlo); DISM_FP(PathArgs, cls_n);
+    DISM_FP(PathArgs, fwd_phase);
+    DISM_FP(PackedZero, R); DISM_FP(PackedZero, out); DISM_FP(PackedZero, rowtau);
+    DISM_FP(DecodeArgs, meta); DISM_FP(DecodeArgs, pool_blocks); DISM_FP(DecodeArgs, n);
+    DISM_FP(DecodeArgs, sq); DISM_FP(DecodeArgs, lut_stride); DISM_FP(DecodeArgs, lse2);
+    return h;
+}
+#undef DISM_FP
+
 }  // namespace dism
+
+// One per translation unit: the fingerprint the unit was compiled with (read by
+// dism_layout_check; an object compiled before a struct changed carries the old value).
+#define DISM_TU_LAYOUT(tu) \
+    extern "C" __attribute__((visibility("hidden"))) const unsigned long long \
+        dism_layout_##tu = dism::layout_fingerprint();

@@ -44,6 +44,8 @@
 // hold +0, then x = x + shfl_xor(x, o) for o = 32, 16, ..., 1.
 #include "dism_path.h"
 
+DISM_TU_LAYOUT(levels)
+
 namespace dism {
 
 constexpr int LV_THREADS = 256;

@@ -17,6 +17,8 @@
 // launched, and passes beyond a row's digit count exit at once.
 #include "dism_path.h"
 
+DISM_TU_LAYOUT(msort)
+
 namespace dism {
 
 constexpr int MS_THREADS = 256;

@@ -18,6 +18,8 @@
 #include "dism_device.h"
 #include "dism_launch.h"
 
+DISM_TU_LAYOUT(packed)
+
 namespace dism {
 
 // thread per token t: its document index and start; the first H tokens also write the

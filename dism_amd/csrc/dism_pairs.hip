@@ -38,6 +38,8 @@
 //     dsk[r] += cdk[r]; dv[d] += cdv[d].
 #include "dism_path.h"
 
+DISM_TU_LAYOUT(pairs)
+
 namespace dism {
 
 constexpr int PAIR_SLOTS = 64;        // pairs per wave per round (one per lane)

@@ -29,6 +29,8 @@
 //   fma(N[r][l+64], v[l+64], N[r][l]*v[l]) (DV = 128) or N[r][l]*v[l] (0 beyond DV).
 #include "dism_path.h"
 
+DISM_TU_LAYOUT(scan)
+
 namespace dism {
 
 // ---------------------------------------------------------------------------------------

@@ -18,6 +18,8 @@
 #include "dism_device.h"
 #include "dism_launch.h"
 
+DISM_TU_LAYOUT(sort)
+
 namespace dism {
 
 constexpr int SORT_THREADS = 1024;

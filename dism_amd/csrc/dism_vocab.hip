@@ -19,6 +19,8 @@
 // sums in the same order), and takes the first maximal index.
 #include "dism_path.h"
 
+DISM_TU_LAYOUT(vocab)
+
 namespace dism {
 
 typedef short vshort4 __attribute__((ext_vector_type(4)));

@@ -35,6 +35,12 @@ enum { DISM_BF16 = 0, DISM_F32 = 1 };
 const char* dism_last_error(void);
 /* ABI version of this library. */
 int32_t dism_abi_version(void);
+/* DISM_OK when every translation unit of the library was compiled against the same layout of
+ * the argument structs its kernels take by value; otherwise DISM_ERR_INVALID, naming the stale
+ * units.  Every compute entry point performs the same check (once per process).  No
+ * counterpart in the reference: its extension is one build-system target, this library is
+ * linked from per-unit objects. */
+int32_t dism_layout_check(void);
 
 /* Sign binarizer, the label producer of this build: labels[b,h,n] = sum_k [x[b,n,h,k] > 0] 2^k
  * for k < d (d <= 30).  Replaces the vocabulary argmax label producer

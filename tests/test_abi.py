@@ -35,13 +35,14 @@ def test_header_symbols_exported(lib):
 def test_python_signatures_cover_header(lib):
     from dism_amd import _lib
     declared = set(_declared())
-    special = {"dism_last_error", "dism_abi_version"}
+    special = {"dism_last_error", "dism_abi_version", "dism_layout_check"}
     bound = set(_lib.SIGNATURES) | set(_lib.SIZE_SIGNATURES)
     assert declared - special == bound, declared ^ bound
 
 
 def test_version_and_workspace(lib):
-    assert lib.dism_abi_version() == 6
+    assert lib.dism_abi_version() == 7
+    assert lib.dism_layout_check() == 0, lib.dism_last_error()
     ws = lib.dism_hard_workspace_bytes(4, 16384, 16, 8, 64, 0)
     assert ws > 4 * 16384 * 16 * 64 * 4  # holds one fp32 readout row per query
     assert ws % 256 == 0
