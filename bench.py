@@ -109,6 +109,49 @@ def valid_pairs(iq, ik):
     return out
 
 
+def causal_counts(qc, kc):
+    """Per position of one row: #keys j <= i with kc[j] == qc[i] (query side) and #queries
+    i >= j with qc[i] == kc[j] (key side), int64 [N] each."""
+    N = qc.shape[0]
+    side = np.r_[np.zeros(N, np.int8), np.ones(N, np.int8)]
+    pos = np.r_[np.arange(N), np.arange(N)]
+    order = np.lexsort((side, pos, np.r_[kc, qc]))
+    lab = np.r_[kc, qc][order]
+    isq = side[order] == 1
+    starts = np.r_[True, lab[1:] != lab[:-1]]
+    gid = np.cumsum(starts) - 1
+    keys_before = np.cumsum(~isq)
+    qs_before = np.cumsum(isq)
+    first = np.flatnonzero(starts)
+    gk0 = np.where(first > 0, keys_before[first - 1], 0)[gid]
+    gq0 = np.where(first > 0, qs_before[first - 1], 0)[gid]
+    gq_tot = np.add.reduceat(isq.astype(np.int64), first)[gid]
+    qcount = np.zeros(N, np.int64)
+    kcount = np.zeros(N, np.int64)
+    qcount[pos[order][isq]] = (keys_before - gk0)[isq]
+    # queries at positions >= j: the group's queries not counted before the key
+    kcount[pos[order][~isq]] = (gq_tot - (qs_before - gq0))[~isq]
+    return qcount, kcount
+
+
+def bigram_pair_counts(iq, ik):
+    """Bigram pairs (L >= 2: iq[i] == ik[j] and iq[i-1] == ik[j-1], 1 <= j <= i) over all
+    rows: (pairs, query owners with a pair, key owners with a pair)."""
+    B, H, N = iq.shape
+    pairs = qown = kown = 0
+    for r in range(B * H):
+        q = iq.reshape(-1, N)[r].astype(np.int64)
+        k = ik.reshape(-1, N)[r].astype(np.int64)
+        # positions >= 1 carry the bigram (label[p-1], label[p]); a key at 0 has none
+        qc = (q[:-1] << 32) | (q[1:] & 0xFFFFFFFF)
+        kc = (k[:-1] << 32) | (k[1:] & 0xFFFFFFFF)
+        qn, kn = causal_counts(qc, kc)
+        pairs += int(qn.sum())
+        qown += int((qn > 0).sum())
+        kown += int((kn > 0).sum())
+    return pairs, qown, kown
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -289,9 +332,9 @@ def bench_train(args):
     if fwd_only:
         cand = ("forward",) if fused else ("readout",)
     elif dense_rows:
-        cand = ("forward", "queries", "keys")
+        cand = ("forward", "queries", "keys", "row_pairs", "key_pairs")
     else:
-        cand = ("queries", "keys")
+        cand = ("queries", "keys", "row_pairs", "key_pairs")
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     live = [stage_events(cand) for _ in range(args.steps)]
     t0 = time.perf_counter()
@@ -369,6 +412,29 @@ def bench_train(args):
                 "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s", "frac": achieved / FP32_PEAK,
                 "traffic": None, "alg_flops_per_launch": flops, "valid_pairs": vp,
                 "launch_ms": live_ms[dom]}
+    elif dom in ("row_pairs", "key_pairs"):
+        # bigram-pair corrections: gathers bound by latency, priced at the bytes they must
+        # move once -- per owner its record (16 B), its own rows and its result; per pair the
+        # partner's rows and two table entries (LUT, dLUT)
+        npairs, qown, kown = bigram_pair_counts(iq_t.cpu().numpy(), ik_t.cpu().numpy())
+        if dom == "row_pairs":   # owner: sq, dO, lse2, record (R + 4 floats); partner: sk, v
+            own_b = 16 + D * esz + DV * esz + 4 + 4 * (D + 4)
+            pair_b = D * esz + DV * esz + 8
+            owners = qown
+            kern = "pairs_rows_kernel"
+        else:                    # owner: sk, v, dSK/dV read+write; partner: sq, dO, lse2
+            own_b = 16 + D * esz + DV * esz + 8 * (D + DV)
+            pair_b = D * esz + DV * esz + 4 + 8
+            owners = kown
+            kern = "pairs_keys_kernel"
+        alg_bytes = owners * own_b + npairs * pair_b
+        achieved = alg_bytes / (live_ms[dom] / 1e3)
+        roof = {"kernel": kern, "bound": "hbm", "achieved": achieved / 1e9,
+                "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": achieved / HBM_PEAK,
+                "traffic": measured_traffic(kern) if args.config == 2 else None,
+                "alg_bytes_per_launch": alg_bytes, "owners": owners, "bigram_pairs": npairs,
+                "owner_bytes": own_b, "pair_bytes": pair_b, "launch_ms": live_ms[dom],
+                "stage": dom}
     else:
         # HBM bytes per B*H*T unit that the stage must read and write once
         per_unit = {
