@@ -130,10 +130,12 @@ def dism_core(q, k, sq, sk, v, q_lse, k_lse, idx_q, idx_k, direction, hard, rtau
 
     The soft-row check reads ``hard`` on the host.  Inside torch.compile that read is not
     possible, so a compiled caller must assert ``all_hard=True`` (otherwise tracing raises);
-    ``all_hard=True`` also skips the host read in eager mode."""
-    if hard_planner is not None:
-        raise NotImplementedError("the asynchronous hard planner is not part of the MI355X "
-                                  "hard core")
+    ``all_hard=True`` also skips the host read in eager mode.
+
+    ``hard_planner``: the reference routes an explicit AsyncHardPlanner to its hybrid core
+    (flash_dism/__init__.py:29-37), which plans the hard rows on the host.  This core plans
+    every row on the device, so a planner object is accepted and not used; the result is
+    the same hard output (soft rows still need the soft core, see dism_core_hybrid)."""
     packed = cu_seqlens is not None or layout is not None
     if packed:
         if ctas:
@@ -208,10 +210,8 @@ def voc_dism(q, k, sq, sk, v, q_vocab, k_vocab, rtau, *, direction, hard, cu_seq
     and their normalizers feed only the soft core, so for hard rows q, k, q_vocab and k_vocab
     receive zero gradients and ``beta`` (the soft gate's vocabulary temperature, a positive
     finite scalar or 0-dim tensor) does not change the result.  Soft rows raise
-    NotImplementedError; under torch.compile pass ``all_hard=True`` (see dism_core)."""
-    if hard_planner is not None:
-        raise NotImplementedError("the asynchronous hard planner is not part of the MI355X "
-                                  "hard core")
+    NotImplementedError; under torch.compile pass ``all_hard=True`` (see dism_core).
+    ``hard_planner`` is accepted and not used, as in dism_core."""
     if not torch.compiler.is_compiling():
         bv = float(beta.detach().item()) if isinstance(beta, torch.Tensor) else float(beta)
         require(bv > 0.0 and bv != float("inf"), "beta must be a positive finite temperature")

@@ -86,7 +86,10 @@ class VarlenLayout:
     def for_graph(cls, table, total_tokens):
         """Layout over a fixed-capacity graph table (make_graph_layout); reference
         varlen.py:28-36.  Capacities (checkpoint elements, LUT length) follow max_seqlen, so
-        they stay valid after update_graph_layout rewrites the documents in place."""
+        they stay valid after update_graph_layout rewrites the documents in place.
+        ``lengths`` (and ``documents``, which counts the padding rows) describe the table at
+        construction; after update_graph_layout, read the current documents from ``spans()``,
+        which reads the live table."""
         maximum = graph_layout_maximum(table)
         if not maximum:
             raise ValueError("expected an owned CUDA Graph layout")
@@ -120,10 +123,25 @@ class VarlenLayout:
         return cache[key]
 
     def pack(self, tensor, *, vectors):
-        """Diagnostic compatibility only: vectors [1,T,H,D] -> [T,H,D]."""
+        """Diagnostic compatibility only (reference varlen.py:42-47, varlen_pack_cuda in
+        src/probe/host/varlen_pack.cpp:42-58).  Vectors [1,T,H,C] are returned as the view
+        [T,H,C] (no copy).  Per-token metadata [1,H,T] (labels, normalizers) is copied into
+        the documents' head-major blocks: for a document at ``begin`` of length ``n``,
+        ``out[begin*H + h*n + t] = x[0, h, begin + t]``; the result is flat [T*H].  A
+        permutation of whole elements (no arithmetic): a torch gather on the input's device."""
+        require(isinstance(tensor, torch.Tensor) and tensor.is_contiguous() and
+                tensor.dim() == (4 if vectors else 3) and tensor.shape[0] == 1,
+                "expected contiguous CUDA vectors [1,T,H,C] or metadata [1,H,T]")
+        require(tensor.shape[1 if vectors else 2] == self.tokens, "packed token count mismatch")
         if vectors:
             return tensor.squeeze(0)
-        raise NotImplementedError("label packing diagnostics are not implemented")
+        heads = tensor.shape[1]
+        index = torch.empty(self.tokens * heads, dtype=torch.int64)
+        for begin, n in self.spans():
+            h = torch.arange(heads, dtype=torch.int64).view(-1, 1)
+            t = torch.arange(n, dtype=torch.int64).view(1, -1)
+            index[begin * heads:(begin + n) * heads] = (h * self.tokens + begin + t).reshape(-1)
+        return tensor.reshape(-1)[index.to(tensor.device)]
 
     def checkpoint_bytes(self, heads):
         return 4 * heads * (self.forward_elements + self.vertical_elements +

@@ -82,6 +82,9 @@ def test_compiled_matches_eager():
     ref = dism_amd.dism_core_hard(*(torch.from_numpy(a).to(d, torch.bfloat16) for a in (sq, sk, v)),
                                   iq, ik, hard, torch.from_numpy(taus(h)).to(d))
     assert torch.equal(ref, eager[0])
+    # an explicit planner object (the reference's hybrid route) gives the same result
+    planned = run(functools.partial(dism_amd.dism_core, hard_planner=object()))
+    assert torch.equal(planned[0], eager[0])
 
 
 @pytest.mark.gpu

@@ -133,3 +133,28 @@ def test_graph_layout_capacity_validation(tokens, maximum, row, match):
     from dism_amd import make_graph_layout
     with pytest.raises(RuntimeError, match=match):
         make_graph_layout(_cu([0, tokens]), tokens, maximum, row)
+
+
+def test_pack_vectors_is_a_view_and_metadata_is_document_head_major():
+    """VarlenLayout.pack (reference varlen.py:42-47; pack kernel
+    src/probe/varlen_pack.cu:10-24): vectors return the squeezed view; per-token metadata
+    [1,H,T] becomes, per document, a head-major block of its tokens -- checked against an
+    explicit loop over documents, heads and tokens."""
+    layout = VarlenLayout.from_cu_seqlens(_cu([0, 256, 256, 768, 1024]), 1024)
+    x = torch.zeros((1, 1024, 3, 8), dtype=torch.bfloat16)
+    assert layout.pack(x, vectors=True).data_ptr() == x.data_ptr()
+    assert tuple(layout.pack(x, vectors=True).shape) == (1024, 3, 8)
+    with pytest.raises(RuntimeError, match="token count"):
+        layout.pack(x[:, :512].contiguous(), vectors=True)
+    with pytest.raises(RuntimeError, match="metadata"):
+        layout.pack(x, vectors=False)
+    labels = torch.randint(0, 1 << 20, (1, 3, 1024), dtype=torch.int32)
+    got = layout.pack(labels, vectors=False)
+    want = torch.empty(1024 * 3, dtype=torch.int32)
+    for begin, n in ((0, 256), (256, 512), (768, 256)):
+        for h in range(3):
+            for t in range(n):
+                want[begin * 3 + h * n + t] = labels[0, h, begin + t]
+    assert got.dtype == torch.int32 and torch.equal(got, want)
+    # an exact permutation: every element once
+    assert torch.equal(torch.sort(got).values, torch.sort(labels.reshape(-1)).values)

@@ -30,9 +30,6 @@ def test_voc_checks_and_fake_shapes():
     with pytest.raises(RuntimeError, match="beta"):
         dism_amd.voc_dism(q, q, sq, sq, v, voc, voc, torch.zeros(2), direction=direction,
                           hard=hard, beta=0.0)
-    with pytest.raises(NotImplementedError, match="planner"):
-        dism_amd.voc_dism(q, q, sq, sq, v, voc, voc, torch.zeros(2), direction=direction,
-                          hard=hard, hard_planner=object())
 
 
 def _inputs(b, n, h, d, r, dv, vsize, seed):
