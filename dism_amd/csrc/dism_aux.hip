@@ -135,17 +135,23 @@ __global__ __launch_bounds__(256) void chunk_kernel(const int32_t* __restrict__ 
 }
 
 // ---- tau reduction: dtau[h] = sum over (b, i) of rowtau[b,h,i], in the fixed order
-// "blocks of TAU_BLOCK consecutive (b, i) rows summed sequentially in double, then block
-// sums added sequentially in double", one workgroup per head.
-constexpr int TAU_BLOCK = 256;
-constexpr int TAU_THREADS = 1024;
-// One workgroup per head; each lane sums one block in order (contiguous rows are read as
-// float4 when the block lies inside one aligned (b, h) row), lane 0 adds the block sums in
-// order.  Rounds of TAU_THREADS blocks.
+// "blocks of TAU_BLOCK consecutive (b, i) rows summed sequentially in double, groups of
+// TAU_GROUP consecutive block sums summed sequentially in double, then the group sums added
+// sequentially in double", one workgroup per head.
+constexpr int TAU_BLOCK = 64;
+constexpr int TAU_GROUP = 32;
+constexpr int TAU_THREADS = 1024;  // one block per lane: a round is TAU_THREADS / TAU_GROUP groups
+static_assert(TAU_THREADS % TAU_GROUP == 0, "rounds hold whole groups");
+// Each lane sums one block in order (16 float4 loads in flight when the block lies inside one
+// aligned (b, h) row), lanes 0..31 sum one group each from LDS, lane 0 adds the round's group
+// sums in order.  The chains are 64 + 32 + (groups) double adds long instead of one lane
+// adding every block sum.
 __global__ __launch_bounds__(TAU_THREADS) void tau_reduce_kernel(const float* __restrict__ rowtau,
                                                                  int B, int H, long n,
                                                                  float* __restrict__ dtau) {
+    constexpr int GPR = TAU_THREADS / TAU_GROUP;  // groups per round
     __shared__ double part[TAU_THREADS];
+    __shared__ double gsum[GPR];
     const int h = blockIdx.x, tid = threadIdx.x;
     const long total = (long)B * n;
     const long blocks = (total + TAU_BLOCK - 1) / TAU_BLOCK;
@@ -159,13 +165,15 @@ __global__ __launch_bounds__(TAU_THREADS) void tau_reduce_kernel(const float* __
             if (rows4) {
                 const long b = x0 / n, i = x0 - b * n;
                 const float4* p = reinterpret_cast<const float4*>(rowtau + (b * H + h) * n + i);
-#pragma unroll 16
+                float4 w[TAU_BLOCK / 4];
+#pragma unroll
+                for (int u = 0; u < TAU_BLOCK / 4; ++u) w[u] = p[u];
+#pragma unroll
                 for (int u = 0; u < TAU_BLOCK / 4; ++u) {
-                    const float4 w = p[u];
-                    inner += (double)w.x;
-                    inner += (double)w.y;
-                    inner += (double)w.z;
-                    inner += (double)w.w;
+                    inner += (double)w[u].x;
+                    inner += (double)w[u].y;
+                    inner += (double)w[u].z;
+                    inner += (double)w[u].w;
                 }
             } else {
                 const long cnt = total - x0 < TAU_BLOCK ? total - x0 : TAU_BLOCK;
@@ -177,17 +185,19 @@ __global__ __launch_bounds__(TAU_THREADS) void tau_reduce_kernel(const float* __
         }
         part[tid] = inner;
         __syncthreads();
+        const long left = blocks - base;  // blocks of this round: min(left, TAU_THREADS)
+        if (tid < GPR) {
+            const long g0 = (long)tid * TAU_GROUP;
+            const int cnt = left - g0 <= 0 ? 0 : (left - g0 < TAU_GROUP ? (int)(left - g0) : TAU_GROUP);
+            double mid = 0.0;
+            for (int u = 0; u < cnt; ++u) mid += part[g0 + u];
+            gsum[tid] = mid;
+        }
+        __syncthreads();
         if (tid == 0) {
-            const int cnt = blocks - base < TAU_THREADS ? (int)(blocks - base) : TAU_THREADS;
-            int u = 0;
-            for (; u + 8 <= cnt; u += 8) {  // batched LDS reads, adds in order
-                double x[8];
-#pragma unroll
-                for (int t = 0; t < 8; ++t) x[t] = part[u + t];
-#pragma unroll
-                for (int t = 0; t < 8; ++t) outer += x[t];
-            }
-            for (; u < cnt; ++u) outer += part[u];
+            const long gl = (left + TAU_GROUP - 1) / TAU_GROUP;
+            const int ng = gl < GPR ? (int)gl : GPR;
+            for (int u = 0; u < ng; ++u) outer += gsum[u];
         }
         __syncthreads();
     }

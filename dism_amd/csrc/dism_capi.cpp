@@ -99,6 +99,7 @@ int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 struct SideStream {
     hipStream_t stream = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
+    hipEvent_t mid = nullptr;  // a point inside the side chain the caller's stream waits for
 };
 
 constexpr int MAX_DEVICES = 64;
@@ -123,8 +124,10 @@ class SideLease {
             return;
         }
         if (hipEventCreateWithFlags(&c->fork, hipEventDisableTiming) != hipSuccess ||
-            hipEventCreateWithFlags(&c->join, hipEventDisableTiming) != hipSuccess) {
+            hipEventCreateWithFlags(&c->join, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&c->mid, hipEventDisableTiming) != hipSuccess) {
             if (c->fork) hipEventDestroy(c->fork);
+            if (c->join) hipEventDestroy(c->join);
             hipStreamDestroy(c->stream);
             delete c;
             return;
@@ -539,10 +542,10 @@ int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t
     // the scan takes the rows prepared in LDS, counting their bigram partners itself (phase
     // 1); after the join the scan takes the remaining rows from the plan's counts (phase 2),
     // then the pair kernels run.  Without a side stream the same launches run in order.
+    // The row flags (classification) are read by the bigram half and by the scan, not by
+    // the label order: with a side stream they are computed there, first, concurrently with
+    // the label order, and the caller's stream waits for them just before the scan.
     const hipStream_t s = S(stream);
-    // the row flags first, on the caller's stream: both halves read them
-    const hipError_t ce = dism::launch_classify(sa, s);
-    if (ce != hipSuccess) return hip_status(ce, "hard forward");
     SideLease lease;
     SideStream* side = lease.get();
     hipStream_t ps = s;
@@ -553,7 +556,13 @@ int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t
         else
             ps = side->stream;
     }
-    hipError_t e = dism::launch_prepare_labels(sa, a, s);
+    hipError_t e = dism::launch_classify(sa, ps);
+    bool classified = true;
+    if (e == hipSuccess && side) classified = hipEventRecord(side->mid, ps) == hipSuccess;
+    if (e == hipSuccess) e = dism::launch_prepare_labels(sa, a, s);
+    if (e == hipSuccess && side && classified)
+        classified = hipStreamWaitEvent(s, side->mid, 0) == hipSuccess;
+    if (e == hipSuccess && !classified) e = hipErrorUnknown;
     if (e == hipSuccess) e = dism::launch_prepare_pairs(sa, a, ps);
     if (e == hipSuccess) {
         a.fwd_phase = 1;

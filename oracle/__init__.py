@@ -72,7 +72,7 @@ def lib():
         L.orc_suffix_walk_from.restype = i64
         L.orc_suffix_walk_from.argtypes = [P, P, i64, i64, i64]
         L.orc_backward_direct.argtypes = L.orc_backward.argtypes
-        L.orc_tau_reduce.argtypes = [P, i32, i32, i64, i64, P]
+        L.orc_tau_reduce.argtypes = [P, i32, i32, i64, i64, i64, P]
         L.orc_forward_flags.argtypes = L.orc_forward.argtypes + [P, P]
         L.orc_backward_flags.argtypes = L.orc_backward.argtypes + [P]
         L.orc_bucket_collisions.restype = ctypes.c_uint64
@@ -281,8 +281,19 @@ def forward(sq, sk, v, iq, ik, hard, lut, threads=0, direct=False, reset=None, d
     return out, lse2, lmax, jarg
 
 
-def backward(sq, sk, v, dout, iq, ik, hard, lut, dlut, lse2, threads=0, block=256,
-             direct=False, dense=None):
+def tau_reduce(rowtau, block=64, group=32):
+    """dtau [H] from rowtau [B,H,N] in the fixed order of the HIP reduction (orc_tau_reduce:
+    blocks of `block` rows, groups of `group` blocks, each level summed sequentially in
+    double, rounded to float)."""
+    rowtau = _f32(rowtau)
+    B, H, N = rowtau.shape
+    dtau = np.empty(H, dtype=np.float32)
+    lib().orc_tau_reduce(_p(rowtau), B, H, N, block, group, _p(dtau))
+    return dtau
+
+
+def backward(sq, sk, v, dout, iq, ik, hard, lut, dlut, lse2, threads=0, direct=False,
+             dense=None):
     """CPU model backward.  Returns (dSQ, dSK, dV fp32, dtau [H], rowtau [B,H,N]).
     `direct` and `dense` as in forward()."""
     sq, sk, v, dout, lut, dlut, lse2 = map(_f32, (sq, sk, v, dout, lut, dlut, lse2))
@@ -302,9 +313,7 @@ def backward(sq, sk, v, dout, iq, ik, hard, lut, dlut, lse2, threads=0, block=25
         lib().orc_backward_flags(*args, _p(dflags))
     else:
         (lib().orc_backward_direct if direct else lib().orc_backward)(*args)
-    dtau = np.empty(H, dtype=np.float32)
-    lib().orc_tau_reduce(_p(rowtau), B, H, N, block, _p(dtau))
-    return dsq, dsk, dv, dtau, rowtau
+    return dsq, dsk, dv, tau_reduce(rowtau), rowtau
 
 
 def vocab_labels(x, vocab):

@@ -1417,20 +1417,27 @@ static void level_backward_row(const float* sq, const float* sk, const float* v,
     level_maps_free(&Mp);
 }
 
-/* dtau_h: for each head, the B*N row terms in (b, i) order are cut into blocks of
- * `block` rows; each block is summed sequentially in double; block sums are then summed
- * sequentially in double; the result is rounded to float. */
-void orc_tau_reduce(const float* rowtau, int B, int H, long N, long block, float* dtau) {
+/* dtau_h: for each head, the B*N row terms in (b, i) order are cut into blocks of `block`
+ * rows; each block is summed sequentially in double; the block sums are cut into groups of
+ * `group` consecutive blocks, each group summed sequentially in double; the group sums are
+ * summed sequentially in double; the result is rounded to float. */
+void orc_tau_reduce(const float* rowtau, int B, int H, long N, long block, long group,
+                    float* dtau) {
     for (int h = 0; h < H; ++h) {
         long total = (long)B * N;
-        double outer = 0.0;
-        for (long s = 0; s < total; s += block) {
+        double outer = 0.0, mid = 0.0;
+        long t = 0;  /* block index */
+        for (long s = 0; s < total; s += block, ++t) {
             double inner = 0.0;
             for (long x = s; x < s + block && x < total; ++x) {
                 long b = x / N, i = x % N;
                 inner += (double)rowtau[((long)b * H + h) * N + i];
             }
-            outer += inner;
+            mid += inner;
+            if ((t + 1) % group == 0 || s + block >= total) {
+                outer += mid;
+                mid = 0.0;
+            }
         }
         dtau[h] = (float)outer;
     }

@@ -67,8 +67,7 @@ def _expected(x, offsets, hard, slots=None):
                                               dense=dense)
         g[0][:, a:z], g[1][:, a:z], g[2][:, a:z] = dsq, dsk, dv
         rowtau[:, :, a:z] = rt
-    dtau = np.empty(h, dtype=np.float32)
-    oracle.lib().orc_tau_reduce(oracle._p(rowtau), 1, h, n, 256, oracle._p(dtau))
+    dtau = oracle.tau_reduce(rowtau)
     return o, l2, lm, ja, g, dtau
 
 

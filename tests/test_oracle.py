@@ -292,20 +292,26 @@ def test_backward_finite_differences():
 
 
 def test_tau_reduce_order():
+    """orc_tau_reduce against an explicit three-level loop (blocks of 64 rows, groups of 32
+    blocks) and the exact sum; lengths on and off the block and group grid."""
     rng = np.random.default_rng(1)
-    rowtau = rng.standard_normal((3, 4, 700)).astype(np.float32)
-    out = np.empty(4, np.float32)
-    lib = oracle.lib()
-    lib.orc_tau_reduce(oracle._p(rowtau), 3, 4, 700, 256, oracle._p(out))
-    for h in range(4):
-        flat = rowtau[:, h, :].reshape(-1).astype(np.float64)
-        outer = 0.0
-        for s in range(0, flat.size, 256):
-            inner = 0.0
-            for x in flat[s:s + 256]:
-                inner += x
-            outer += inner
-        assert out[h] == np.float32(outer)
+    for B, H, N in ((3, 4, 700), (2, 2, 4096), (1, 3, 64 * 32 * 3 + 5)):
+        rowtau = rng.standard_normal((B, H, N)).astype(np.float32)
+        out = oracle.tau_reduce(rowtau)
+        for h in range(H):
+            flat = rowtau[:, h, :].reshape(-1).astype(np.float64)
+            outer = 0.0
+            for g in range(0, flat.size, 64 * 32):
+                mid = 0.0
+                for s in range(g, min(g + 64 * 32, flat.size), 64):
+                    inner = 0.0
+                    for x in flat[s:s + 64]:
+                        inner += x
+                    mid += inner
+                outer += mid
+            assert out[h] == np.float32(outer)
+            assert abs(float(out[h]) - float(np.sum(flat, dtype=np.longdouble))) <= \
+                2e-7 * max(1.0, float(np.abs(flat).sum()))
 
 
 def test_forward_with_query_resets_pinned_by_fp64():
