@@ -530,7 +530,8 @@ def layer_arrays():
 
 
 def layer_step_ms(args):
-    """configs[4] layer step on the GPU: bf16 projections q = x wq, k = x wk, v = x wv, the
+    """configs[4] layer step on the GPU: bf16 projections q = x wq, k = x wk, v = x wv (one GEMM
+    over the concatenated weights), the
     hard core through autograd (labels by the sign binarizer of q and k, sq = q, sk = k), the
     output projection, and the backward of all of it from dy (weights' and tau's gradients).
     Returns the mean ms per step over args.steps steps after args.warmup."""
@@ -542,17 +543,22 @@ def layer_step_ms(args):
     x, wq, wk, wv, wo, _, dy = layer_arrays()
     put = lambda a: torch.from_numpy(a).to(dev, torch.bfloat16)  # noqa: E731
     x, dy = put(x), put(dy)
-    ws = [put(w).requires_grad_() for w in (wq, wk, wv, wo)]
+    # the three input projections as one [1280, H*(2*8 + 128)] weight: one GEMM forward and
+    # two backward instead of three each (the same products; q, k, v are column blocks)
+    wqkv = put(np.concatenate([wq, wk, wv], axis=1)).requires_grad_()
+    wout = put(wo).requires_grad_()
     tau = torch.full((H,), args.tau, dtype=torch.float32, device=dev, requires_grad=True)
     hard = torch.ones((B, H), dtype=torch.bool, device=dev)
+    nq = H * D
 
     def step():
-        q = (x @ ws[0]).view(B, T, H, D)
-        k = (x @ ws[1]).view(B, T, H, D)
-        v = (x @ ws[2]).view(B, T, H, DV)
+        qkv = x @ wqkv
+        q = qkv[..., :nq].reshape(B, T, H, D).contiguous()
+        k = qkv[..., nq:2 * nq].reshape(B, T, H, D).contiguous()
+        v = qkv[..., 2 * nq:].reshape(B, T, H, DV).contiguous()
         iq, ik = dism_amd.sign_labels(q.detach()), dism_amd.sign_labels(k.detach())
         o = dism_amd.dism_core_hard(q, k, v, iq, ik, hard, tau)
-        (o.reshape(B, T, H * DV) @ ws[3]).backward(dy)
+        (o.reshape(B, T, H * DV) @ wout).backward(dy)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
