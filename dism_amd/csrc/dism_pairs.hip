@@ -420,8 +420,10 @@ __device__ __forceinline__ bool load_slot(const PathArgs& a, int base, int k0, i
     s.h = r.x - b * a.H;
     s.p = r.y;
     s.lo = r.z;
-    s.hard = a.hard[r.x] != 0;  // soft rows compute but write nothing (and walk unbounded:
-    s.cnt = in ? r.w : 0;       // their carry boundary is unset), off the dependent chain
+    // soft rows compute but write nothing (and walk unbounded: their carry boundary is
+    // unset), off the dependent chain; the prepare's walk probe runs without row flags
+    s.hard = a.hard ? a.hard[r.x] != 0 : true;
+    s.cnt = in ? r.w : 0;
     s.so = (long)r.x * a.n;
     s.row0 = (long)b * a.n * a.H + s.h;
     int mx = s.cnt;

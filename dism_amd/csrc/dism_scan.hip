@@ -256,7 +256,8 @@ __global__ __launch_bounds__(64 * WAVES) void scan_forward_kernel(PathArgs a) {
                 while (kv) {
                     const int l = __ffsll((long long)kv) - 1;
                     kv &= kv - 1;
-                    if (isq && l < lane && pl == readlane_i(pl, l)) ++c;
+                    const int pll = readlane_i(pl, l);  // uniform: read by every lane
+                    if (isq && l < lane && pl == pll) ++c;
                 }
                 nb = isq ? c : 0;
                 asm volatile("" ::: "memory");
