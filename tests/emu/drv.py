@@ -108,3 +108,72 @@ def staged(sq, sk, v, iq, ik, hard, lut, dtype=0, out_dtype=1):
     call("dism_hard_readout", p(a), p(b), p(c), dtype, p(iq), p(ik), p(hd), None, 0, p(lut),
          lut.shape[1], B, N, H, R, DV, p(ws), nb, p(out), out_dtype, p(lse2), p(lmax), p(jarg), None)
     return out, lse2, lmax, jarg, (ws, nb, a, b, c, iq, ik, hd, lut)
+
+
+def packed(sq, sk, v, do, iq, ik, hard_rows, lut, dlut, offsets, longest, dtype=0):
+    """packed prepare + readout + backward; offsets are the non-empty documents' starts + N"""
+    _, N, H, R = sq.shape
+    DV = v.shape[-1]
+    a, b, c, d = vec(sq, dtype), vec(sk, dtype), vec(v, dtype), vec(do, dtype)
+    iq = np.ascontiguousarray(iq, np.int32); ik = np.ascontiguousarray(ik, np.int32)
+    cu = np.ascontiguousarray(offsets, np.int32)
+    hd = np.ascontiguousarray(hard_rows, np.uint8)
+    lut = np.ascontiguousarray(lut, np.float32); dlut = np.ascontiguousarray(dlut, np.float32)
+    nb = lib.dism_hard_packed_workspace_bytes(N, H, R, DV, dtype)
+    ws = aligned(nb); ws[:] = 0xCD
+    call("dism_hard_packed_prepare", p(a), p(b), p(c), dtype, p(iq), p(ik), p(cu), cu.size - 1,
+         N, H, R, DV, p(ws), nb, None)
+    out = np.empty((1, N, H, DV), np.float32); lse2 = np.empty((1, H, N), np.float32)
+    lmax = np.empty((1, H, N), np.int32); jarg = np.empty((1, H, N), np.int32)
+    call("dism_hard_packed_readout", p(a), p(b), p(c), dtype, p(hd), hd.shape[0], p(lut),
+         lut.shape[1], longest, N, H, R, DV, p(ws), nb, p(out), 1, p(lse2), p(lmax), p(jarg), None)
+    dsq = np.empty((1, N, H, R), np.float32); dsk = np.empty_like(dsq)
+    dv = np.empty((1, N, H, DV), np.float32); rowtau = np.empty((1, H, N), np.float32)
+    dtau = np.empty(H, np.float32)
+    call("dism_hard_packed_backward", p(a), p(b), p(c), p(d), dtype, p(hd), hd.shape[0], p(lut),
+         p(dlut), lut.shape[1], longest, p(lse2), N, H, R, DV, p(ws), nb, p(dsq), p(dsk), p(dv),
+         p(rowtau), p(dtau), None)
+    return out, lse2, lmax, jarg, dsq, dsk, dv, dtau, rowtau
+
+
+class Decoder:
+    def __init__(self, B, H, R, DV, capacity, lut, slots=64, dtype=0):
+        self.B, self.H, self.R, self.DV, self.cap, self.slots, self.dtype = B, H, R, DV, capacity, slots, dtype
+        self.lut = np.ascontiguousarray(lut, np.float32)
+        self.nb = lib.dism_decoder_state_bytes(B * H, R, DV, capacity, slots, dtype)
+        self.state = aligned(self.nb); self.state[:] = 0xCD
+        call("dism_decoder_init", p(self.state), self.nb, B * H, R, DV, capacity, slots, dtype, None)
+
+    def append(self, iq, ik, sq, sk, v, reset=None):
+        n = iq.shape[-1]
+        iq = np.ascontiguousarray(iq, np.int32); ik = np.ascontiguousarray(ik, np.int32)
+        a, b, c = vec(sq, self.dtype), vec(sk, self.dtype), vec(v, self.dtype)
+        out = np.empty((self.B, n, self.H, self.DV), np.float32)
+        rs = None if reset is None else np.ascontiguousarray(reset, np.uint8)
+        call("dism_decoder_step", p(self.state), self.nb, self.B, self.H, self.R, self.DV,
+             self.cap, self.slots, self.dtype, n, p(iq), p(ik), p(rs), p(a), p(b), p(c),
+             p(self.lut), self.lut.shape[1], p(out), None, None)
+        return out
+
+    def prime(self, iq, ik, sk, v):
+        n = iq.shape[-1]
+        iq = np.ascontiguousarray(iq, np.int32); ik = np.ascontiguousarray(ik, np.int32)
+        b, c = vec(sk, self.dtype), vec(v, self.dtype)
+        wb = lib.dism_decoder_prime_workspace_bytes(self.B, n, self.H, self.R, self.DV, self.dtype)
+        ws = aligned(wb); ws[:] = 0xCD
+        call("dism_decoder_prime", p(self.state), self.nb, self.B, self.H, self.R, self.DV,
+             self.cap, self.slots, self.dtype, n, p(iq), p(ik), None, p(b), p(c), p(ws), wb, None)
+
+
+def noalloc(sq, sk, v, iq, ik, hard, lut, dtype=0):
+    B, N, H, R = sq.shape
+    DV = v.shape[-1]
+    a, b, c = vec(sq, dtype), vec(sk, dtype), vec(v, dtype)
+    iq = np.ascontiguousarray(iq, np.int32); ik = np.ascontiguousarray(ik, np.int32)
+    hd = np.ascontiguousarray(np.broadcast_to(hard, (B, H)), np.uint8)
+    lut = np.ascontiguousarray(lut, np.float32)
+    out = np.empty((B, N, H, DV), np.float32); lse2 = np.empty((B, H, N), np.float32)
+    lmax = np.empty((B, H, N), np.int32); jarg = np.empty((B, H, N), np.int32)
+    call("dism_hard_forward_noalloc", p(a), p(b), p(c), dtype, p(iq), p(ik), p(hd), p(lut),
+         lut.shape[1], B, N, H, R, DV, p(out), 1, p(lse2), p(lmax), p(jarg), None)
+    return out, lse2, lmax, jarg

@@ -138,6 +138,77 @@ def prefill_other():
         assert same_bits(l2[:, :, :n], wl2), pattern
 
 
+
+def packed_docs():
+    """a packed batch-1 call with documents [0, 256) and [256, 512) in two training rows
+    (hard flags [[T], [F]] per head pair): every hard document equals the CPU model on that
+    document alone, soft documents give zeros; dtau over the hard documents"""
+    N, H, R, DV = 512, 2, 8, 64
+    q, k, v, do, iq, ik = _inputs(1, N, H, R, DV, 31)
+    hard_rows = np.array([[True, False], [False, True]])
+    tau = np.array([0.4, -0.3], np.float32)
+    offsets = [0, 256, 512]
+    lut = oracle.log_weights(tau, 256)
+    dlut = oracle.dlog_weights(tau, 256)
+    out, l2, lm, ja, dsq, dsk, dv, dtau, rowtau = drv.packed(q, k, v, do, iq, ik, hard_rows,
+                                                            lut, dlut, offsets, 256)
+    want_rt = np.zeros((1, H, N), np.float32)
+    dense = oracle.packed_dense_flags(iq, ik, offsets)
+    for d, (a, z) in enumerate(((0, 256), (256, 512))):
+        flags = hard_rows[d:d + 1]
+        args = (q[:, a:z], k[:, a:z], v[:, a:z])
+        labs = (iq[:, :, a:z], ik[:, :, a:z])
+        o, l2o, lmo, jao = oracle.forward(*args, *labs, flags, lut, dense=dense)
+        assert same_bits(out[:, a:z], o), ("packed output", d)
+        assert same_bits(l2[:, :, a:z], l2o), ("packed normalizer", d)
+        assert np.array_equal(lm[:, :, a:z], lmo), ("packed lmax", d)
+        assert np.array_equal(ja[:, :, a:z], np.where(jao >= 0, jao + a, -1)), ("jarg", d)
+        g = oracle.backward(*args, do[:, a:z], *labs, flags, lut, dlut, l2o, dense=dense)
+        for x, y, name in zip((dsq[:, a:z], dsk[:, a:z], dv[:, a:z]), g[:3], ("dsq", "dsk", "dv")):
+            assert same_bits(x, y), (name, d)
+        want_rt[:, :, a:z] = g[4]
+    assert same_bits(rowtau, want_rt), "rowtau"
+    assert same_bits(dtau, oracle.tau_reduce(want_rt)), "dtau"
+
+
+def decode_chunks():
+    """incremental decoding (prime 31 tokens, then chunks of 1, 5, 1, 11 and the rest) of the
+    inference tests' random and identical-label rows: equal to the CPU model's decomposed
+    forward bit for bit"""
+    tau = np.array([0.0, 0.35], np.float32)
+    for pattern in ("random", "repeat"):
+        rng = np.random.default_rng(83)
+        n = 79
+        iq = rng.integers(0, 4, (2, 2, n)).astype(np.int32)
+        ik = rng.integers(0, 4, (2, 2, n)).astype(np.int32)
+        if pattern == "repeat":
+            iq[:] = 0
+            ik[:] = 0
+        sq, sk, v = (oracle.bf16_round(rng.standard_normal((2, n, 2, c)) * 0.2)
+                     for c in (16, 16, 32))
+        want, _, _, _ = oracle.forward(sq, sk, v, iq, ik, np.ones((2, 2), bool),
+                                       oracle.log_weights(tau, n), dense=0)
+        dec = drv.Decoder(2, 2, 16, 32, 79, oracle.log_weights(tau, 256), slots=64)
+        dec.prime(iq[..., :31], ik[..., :31], sk[:, :31], v[:, :31])
+        outs, t = [], 31
+        for step in (1, 5, 1, 11, n - 49):
+            outs.append(dec.append(iq[..., t:t + step], ik[..., t:t + step], sq[:, t:t + step],
+                                   sk[:, t:t + step], v[:, t:t + step]))
+            t += step
+        assert same_bits(np.concatenate(outs, axis=1), want[:, 31:]), pattern
+
+
+def noalloc_forward():
+    """the allocation-free forward (library scratch) equals the CPU model"""
+    q, k, v, do, iq, ik = _inputs(1, 256, 2, 8, 64, 5)
+    tau = np.array([0.5, -0.1], np.float32)
+    hard = np.ones((1, 2), bool)
+    lut = oracle.log_weights(tau, 256)
+    out, l2, lm, ja = drv.noalloc(q, k, v, iq, ik, hard, lut)
+    o, l2o, lmo, jao = oracle.forward(q, k, v, iq, ik, hard, lut)
+    assert same_bits(out, o) and same_bits(l2, l2o)
+    assert np.array_equal(lm, lmo) and np.array_equal(ja, jao)
+
 if __name__ == "__main__":
     for name in sys.argv[1:]:
         globals()[name]()
