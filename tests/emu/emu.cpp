@@ -272,6 +272,21 @@ void run_grid(void (*body)(void*), void* ctx, dim3 grid, dim3 block) {
 }
 }  // namespace emu
 
+#define EMU_ATOMIC_DEFS(T)                                                        \
+    T atomicAdd(T* p, T v) { T o = *p; *p = o + v; return o; }                      \
+    T atomicOr(T* p, T v) { T o = *p; *p = o | v; return o; }                       \
+    T atomicMax(T* p, T v) { T o = *p; if (v > o) *p = v; return o; }               \
+    T atomicMin(T* p, T v) { T o = *p; if (v < o) *p = v; return o; }               \
+    T atomicExch(T* p, T v) { T o = *p; *p = v; return o; }                         \
+    T atomicCAS(T* p, T c, T v) { T o = *p; if (o == c) *p = v; return o; }
+EMU_ATOMIC_DEFS(int)
+EMU_ATOMIC_DEFS(unsigned)
+EMU_ATOMIC_DEFS(unsigned long long)
+EMU_ATOMIC_DEFS(long long)
+float atomicAdd(float* p, float v) { float o = *p; *p = o + v; return o; }
+float atomicMax(float* p, float v) { float o = *p; if (v > o) *p = v; return o; }
+float atomicExch(float* p, float v) { float o = *p; *p = v; return o; }
+
 // basic-block hook (-fsanitize-coverage=trace-pc on the kernel units): every lane stops at
 // every basic block; the scheduler runs a wave's lanes at the lowest code position one block
 // at a time -- lockstep with reconvergence for structured control flow

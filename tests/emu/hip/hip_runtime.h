@@ -161,12 +161,22 @@ inline int __clzll(long long x) { return x ? __builtin_clzll((unsigned long long
 inline int __ffsll(long long x) { return __builtin_ffsll(x); }
 inline int __ffsll(unsigned long long x) { return __builtin_ffsll((long long)x); }
 
-template <typename T> inline T atomicAdd(T* p, T v) { T o = *p; *p = o + v; return o; }
-template <typename T> inline T atomicOr(T* p, T v) { T o = *p; *p = o | v; return o; }
-template <typename T> inline T atomicMax(T* p, T v) { T o = *p; if (v > o) *p = v; return o; }
-template <typename T> inline T atomicMin(T* p, T v) { T o = *p; if (v < o) *p = v; return o; }
-template <typename T> inline T atomicExch(T* p, T v) { T o = *p; *p = v; return o; }
-template <typename T> inline T atomicCAS(T* p, T c, T v) { T o = *p; if (o == c) *p = v; return o; }
+// Atomics live in emu.cpp, which has no basic-block hooks: a lane cannot be switched out
+// between an atomic's read and its write.
+#define EMU_ATOMICS(T)                  \
+    T atomicAdd(T* p, T v);             \
+    T atomicOr(T* p, T v);              \
+    T atomicMax(T* p, T v);             \
+    T atomicMin(T* p, T v);             \
+    T atomicExch(T* p, T v);            \
+    T atomicCAS(T* p, T c, T v);
+EMU_ATOMICS(int)
+EMU_ATOMICS(unsigned)
+EMU_ATOMICS(unsigned long long)
+EMU_ATOMICS(long long)
+float atomicAdd(float* p, float v);
+float atomicMax(float* p, float v);
+float atomicExch(float* p, float v);
 
 // host runtime stubs: synchronous, one device
 inline hipError_t hipGetLastError() { hipError_t e = emu::g_last_error; emu::g_last_error = 0; return e; }

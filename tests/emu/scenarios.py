@@ -209,7 +209,39 @@ def noalloc_forward():
     assert same_bits(out, o) and same_bits(l2, l2o)
     assert np.array_equal(lm, lmo) and np.array_equal(ja, jao)
 
+
+def grid(spec):
+    """one fwd+bwd case "pattern:R:DV:dtype:N[:staged]" over the five label patterns of the
+    reference (tests/_data.labels) with soft rows (tests/_data.flags), B=2, H=2"""
+    from tests._data import flags, labels, taus, vectors
+    parts = spec.split(":")
+    pattern, R, DV, dtype, N = parts[0], int(parts[1]), int(parts[2]), parts[3], int(parts[4])
+    fused = not (len(parts) > 5 and parts[5] == "staged")
+    B, H = 2, 2
+    iq, ik = labels(N, pattern, b=B, h=H)
+    sq, sk, v = vectors(N, b=B, h=H, r=R, dv=DV)
+    rng = np.random.default_rng(R * 1000 + DV)
+    do = oracle.bf16_round(rng.standard_normal(v.shape))
+    if dtype == "f32":
+        sq = sq + np.float32(1e-3) * rng.standard_normal(sq.shape).astype(np.float32)
+    code = 0 if dtype == "bf16" else 1
+    hard = flags(B, H)
+    tau = taus(H)
+    lut = oracle.log_weights(tau, N)
+    fwd = drv.forward if fused else drv.staged
+    out, l2, lm, ja, st = fwd(sq, sk, v, iq, ik, hard, lut, dtype=code)
+    o, l2o, lmo, jao = oracle.forward(sq, sk, v, iq, ik, hard, lut)
+    assert same_bits(out, o), "forward output"
+    assert same_bits(l2, l2o), "normalizer"
+    assert np.array_equal(lm, lmo) and np.array_equal(ja, jao), "lmax/argmax"
+    dl = oracle.dlog_weights(tau, N)
+    got = drv.backward(st, do, dl, l2, dtype=code)
+    ref = oracle.backward(sq, sk, v, do, iq, ik, hard, lut, dl, l2o)
+    for g, r, name in zip(got, ref, ("dsq", "dsk", "dv", "dtau", "rowtau")):
+        assert same_bits(g, r), name
+
 if __name__ == "__main__":
     for name in sys.argv[1:]:
-        globals()[name]()
+        fn, _, arg = name.partition("=")
+        globals()[fn](*([arg] if arg else []))
         print("OK", name, flush=True)
