@@ -250,10 +250,13 @@ hipError_t launch_pair_plan(const PathArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Owner lists: grid (B*H, 2 sides); workgroup (bh, side) finds its row's offset in each class
-// list (rows before it) and the class totals, then copies its staged records (and, for
-// query rows, their pair counts into pnb, whose other entries are zero).
+// Owner lists: grid (B*H, 2 sides, slices); workgroup (bh, side, z) finds its row's offset in
+// each class list (rows before it) and the class totals, then copies slice z of its staged
+// records of each class (and, for query rows, their pair counts into pnb, whose other
+// entries are zero).  Slices of a row split each class's records evenly, so long rows are
+// copied by many workgroups instead of one.
 constexpr int LIST_THREADS = 256;
+constexpr int LIST_SLICE = 512;   // positions per slice of a row (the grid's z extent)
 __global__ __launch_bounds__(LIST_THREADS) void owner_lists_kernel(PathArgs a) {
     __shared__ int s_red[LIST_THREADS / 64][8];
     const int bh = blockIdx.x, side = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
@@ -298,22 +301,26 @@ __global__ __launch_bounds__(LIST_THREADS) void owner_lists_kernel(PathArgs a) {
     const int base[3] = {0, total[0], total[0] + total[1]};
     const long so = (long)bh * n;
     int4* own = a.o.own[side];
+    const int z = blockIdx.z, slices = gridDim.z;
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
         const int m = pairless_mode(dense[bh]) ? 0 : cnt[(long)bh * 4 + c];
+        const int per = (m + slices - 1) / slices;
+        const int k0 = z * per, k1 = k0 + per < m ? k0 + per : m;
         const int4* src = a.o.stage[side][c == 1 ? 1 : 0] + so;
-        for (int k = tid; k < m; k += LIST_THREADS) {
+        for (int k = k0 + tid; k < k1; k += LIST_THREADS) {
             const int4 rec = src[c == 2 ? n - 1 - k : k];
             own[base[c] + before[c] + k] = rec;
             if (side == 0) a.pnb[so + rec.y] = rec.w;  // pair count of the query row
         }
     }
-    if (bh == 0 && tid < 3) a.o.ocount[4 * side + tid] = total[tid];
+    if (bh == 0 && z == 0 && tid < 3) a.o.ocount[4 * side + tid] = total[tid];
 }
 
 hipError_t launch_owner_lists(const PathArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(owner_lists_kernel, dim3((unsigned)(a.B * a.H), 2), dim3(LIST_THREADS), 0,
-                       s, a);
+    const unsigned slices = (unsigned)((a.n + LIST_SLICE - 1) / LIST_SLICE);
+    hipLaunchKernelGGL(owner_lists_kernel, dim3((unsigned)(a.B * a.H), 2, slices),
+                       dim3(LIST_THREADS), 0, s, a);
     return hipGetLastError();
 }
 
