@@ -201,6 +201,42 @@ __device__ __forceinline__ int owner_class(int cnt) {
     return cnt <= OWNER_SMALL ? 0 : cnt <= OWNER_MEDIUM ? 1 : 2;
 }
 
+// ---- walk-cost probe of one bigram pair (walk_probe_kernel below; pair_plan_kernel probes
+// the small-class query owners of the rows it plans itself)
+constexpr int WALK_EXACT = 64;
+constexpr int WALK_COUNTED = 16;
+
+// the run's exact length (its walk, once per run end)
+__device__ __forceinline__ int probe_run(const int32_t* __restrict__ q,
+                                         const int32_t* __restrict__ k, int i, int j, int dlo) {
+    int c = i - 1 >= dlo ? 2 : 1;
+    if (c == 2 && walk_step<4>(q, k, i, j, dlo, c)) {
+        while (walk_step<16>(q, k, i, j, dlo, c)) {
+        }
+    }
+    return c;
+}
+
+// query i's pair with key j of row bh: when the pair ends its diagonal run, the run's walk
+// cost (runs of at least WALK_COUNTED labels) and, for runs of at least RUN_MIN labels in
+// rows that list them, a run-list entry
+__device__ __forceinline__ unsigned long long probe_pair(const PathArgs& a, int bh,
+                                                         const int32_t* __restrict__ q,
+                                                         const int32_t* __restrict__ k, int i,
+                                                         int j, int dlo, bool next_reset,
+                                                         bool listed) {
+    const int n = a.n;
+    const bool ends = i + 1 >= n || j + 1 >= n || next_reset || q[i + 1] != k[j + 1];
+    if (!ends) return 0ull;
+    const int lr = probe_run(q, k, i, j, dlo);
+    if (lr >= RUN_MIN && listed) {
+        const int slot = atomicAdd(&a.o.runcnt[bh], 1);
+        if (slot < RUN_CAP) a.o.runs[(long)bh * RUN_CAP + slot] = make_int4(i - j, i, lr, 0);
+    }
+    const unsigned long long l = (unsigned long long)lr;
+    return l >= WALK_COUNTED ? l * l / 2 : 0ull;
+}
+
 // Plan of the rows prepared in global memory (mode 0): one lane per owner (both sides,
 // grid = 2 * B*H * ceil(N/64) items, one 64-owner chunk each): partner range by binary
 // searches in the bigram orders, pair count per query row (pnb, by position), and the owner
@@ -225,6 +261,20 @@ __global__ __launch_bounds__(64 * WAVES) void pair_plan_kernel(PathArgs a) {
         if (side == 0) a.pnb[so + p] = cnt;
     }
     const int cls = owner_class(cnt);
+    // the walk-cost probe of this row's small-class query owners (walk_probe_kernel skips
+    // them): their partners are at hand here, one lane per owner, at most OWNER_SMALL pairs
+    if (side == 0 && own && cnt > 0 && cls == 0 && !pairless_mode(a.o.dflag[bh])) {
+        const int32_t* kb = a.o.bpos[1] + so;
+        const int32_t* q = a.iq + so;
+        const int32_t* k = a.ik + so;
+        const int dlo = walk_lo(a, so, p);
+        const bool next_reset = p + 1 < n && walk_lo(a, so, p + 1) == p + 1;
+        const bool listed = a.o.runs && !a.wlo && !a.dstart;
+        unsigned long long cost = 0;
+        for (int x = 0; x < cnt; ++x)
+            cost += probe_pair(a, bh, q, k, p, kb[lo + x], dlo, next_reset, listed);
+        if (cost) atomicAdd(&a.o.dcost[bh], cost);
+    }
     const bool has = own && cnt > 0;
     const int4 rec = make_int4(bh, p, lo, cnt);
     int32_t* counts = a.o.bhcount[side] + (long)bh * 4;
@@ -523,24 +573,14 @@ __device__ __forceinline__ unsigned long long shfl_xor64(unsigned long long x, i
 // comparisons each, and a row that is not dense has at most about N^2/64 label-equal pairs,
 // so together they cost under N^2/4; leaving them out keeps the per-row sum's atomics (one
 // cache line for all rows) to the rare long runs.
-constexpr int WALK_EXACT = 64;
-constexpr int WALK_COUNTED = 16;
-
-// the run's exact length (its walk, once per run end)
-__device__ __forceinline__ int probe_run(const int32_t* __restrict__ q,
-                                         const int32_t* __restrict__ k, int i, int j, int dlo) {
-    int c = i - 1 >= dlo ? 2 : 1;
-    if (c == 2 && walk_step<4>(q, k, i, j, dlo, c)) {
-        while (walk_step<16>(q, k, i, j, dlo, c)) {
-        }
-    }
-    return c;
-}
+// (WALK_EXACT, WALK_COUNTED, probe_run and probe_pair: before pair_plan_kernel)
 
 template <int G>
 __device__ __forceinline__ void probe_item(const PathArgs& a, int base, int k0, int ncls) {
     Slot s;
     if (!load_slot<0, G>(a, base, k0, ncls, s)) return;
+    // small-class owners of rows planned in global memory were probed by pair_plan_kernel
+    if (G == OWNER_SMALL && !a.o.mode[s.bh]) s.cnt = 0;
     const int n = a.n, sub = lane_id() % G;
     const int i = s.p;
     const int32_t* kb = a.o.bpos[1] + s.so;
@@ -552,20 +592,7 @@ __device__ __forceinline__ void probe_item(const PathArgs& a, int base, int k0, 
     unsigned long long cost = 0;
     for (int c0 = 0; c0 < s.maxcnt; c0 += G) {
         const int kq = c0 + sub;
-        if (kq < s.cnt) {
-            const int j = kb[s.lo + kq];
-            const bool ends = i + 1 >= n || j + 1 >= n || next_reset || q[i + 1] != k[j + 1];
-            if (ends) {
-                const int lr = probe_run(q, k, i, j, dlo);
-                const unsigned long long l = (unsigned long long)lr;
-                if (l >= WALK_COUNTED) cost += l * l / 2;
-                if (lr >= RUN_MIN && listed) {
-                    const int slot = atomicAdd(&a.o.runcnt[s.bh], 1);
-                    if (slot < RUN_CAP)
-                        a.o.runs[(long)s.bh * RUN_CAP + slot] = make_int4(i - j, i, lr, 0);
-                }
-            }
-        }
+        if (kq < s.cnt) cost += probe_pair(a, s.bh, q, k, i, kb[s.lo + kq], dlo, next_reset, listed);
     }
 #pragma unroll
     for (int o = G / 2; o >= 1; o >>= 1) cost += shfl_xor64(cost, o);

@@ -240,6 +240,74 @@ def grid(spec):
     for g, r, name in zip(got, ref, ("dsq", "dsk", "dv", "dtau", "rowtau")):
         assert same_bits(g, r), name
 
+
+def long_runs(alphabet="1024"):
+    """copied spans longer than RUN_MIN (the run list) in rows planned in global memory
+    (labels of two bytes) or in LDS (one byte), N = 1024; fwd+bwd bit-exact"""
+    A = int(alphabet)
+    N = 1024
+
+    def labels(rng):
+        iq = rng.integers(0, A, (1, 2, N)).astype(np.int32)
+        ik = rng.integers(0, A, (1, 2, N)).astype(np.int32)
+        iq[0, :, 600:720] = ik[0, :, 100:220]
+        iq[0, 1, 900:1000] = ik[0, 1, 300:400]
+        return iq, ik
+    x = _inputs(1, N, 2, 8, 32, 13, labels)
+    check_fwd_bwd(*x, np.array([0.5, -0.2], np.float32))
+
+
+def prefill_resets():
+    """prefill of identical-label rows with query resets every 19 tokens (the inference
+    tests' case): the CPU model with resets"""
+    tau = np.array([0.0, 0.35], np.float32)
+    rng = np.random.default_rng(83)
+    n, pad = 79, 256
+    iq = np.zeros((2, 2, n), np.int32)
+    ik = np.zeros((2, 2, n), np.int32)
+    sq, sk, v = (oracle.bf16_round(rng.standard_normal((2, n, 2, c)) * 0.2)
+                 for c in (16, 16, 32))
+    reset = np.zeros((2, 2, n), bool)
+    reset[..., 17::19] = True
+    padl = lambda x: np.concatenate([x, np.zeros((2, 2, pad - n), x.dtype)], 2)  # noqa
+    padv = lambda x: np.concatenate([x, np.zeros((2, pad - n) + x.shape[2:], np.float32)], 1)  # noqa
+    out, l2 = drv.prefill(padv(sq), padv(sk), padv(v), padl(iq), padl(ik),
+                          oracle.log_weights(tau, pad), n, reset=padl(reset.astype(np.uint8)))
+    want, wl2, _, _ = oracle.forward(sq, sk, v, iq, ik, np.ones((2, 2), bool),
+                                     oracle.log_weights(tau, n), reset=reset)
+    assert same_bits(out[:, :n], want) and same_bits(l2[:, :, :n], wl2)
+
+
+def probe_modes():
+    """the walk-cost probe: rows with a period of 80 distinct labels (sparse: M = N^2/80, but
+    every diagonal d = 80 m is one long run, cost ~ N^3/480 > N^2) become strip-bounded rows
+    (mode 2), planned in global memory (two-byte labels) or in LDS (one byte); random rows
+    stay mode 0; fwd+bwd bit-exact"""
+    N = 1024
+
+    def labels(rng):
+        iq = rng.integers(0, 256, (1, 4, N)).astype(np.int32)
+        ik = rng.integers(0, 256, (1, 4, N)).astype(np.int32)
+        per2 = rng.permutation(5000)[:80].astype(np.int32) + 300   # two-byte labels
+        per1 = rng.permutation(256)[:80].astype(np.int32)          # one-byte labels
+        iq[0, 0] = ik[0, 0] = per2[np.arange(N) % 80]
+        iq[0, 1] = ik[0, 1] = per1[np.arange(N) % 80]
+        iq[0, 3] = rng.integers(0, 3000, N)                         # random, two-byte
+        ik[0, 3] = rng.integers(0, 3000, N)
+        return iq, ik
+    q, k, v, do, iq, ik = _inputs(1, N, 4, 8, 32, 17, labels)
+    assert (oracle.row_modes(iq, ik, 8, 32) == 0).all()
+    a, b, c = drv.vec(q, 0), drv.vec(k, 0), drv.vec(v, 0)
+    nb = drv.lib.dism_hard_workspace_bytes(1, N, 4, 8, 32, 0)
+    ws = drv.aligned(nb)
+    ws[:] = 0xCD
+    drv.call("dism_hard_prepare", drv.p(a), drv.p(b), drv.p(c), 0, drv.p(iq), drv.p(ik), 1, N,
+             4, 8, 32, drv.p(ws), nb, None)
+    modes = np.empty((1, 4), np.int32)
+    drv.call("dism_hard_row_modes", drv.p(ws), nb, 1, N, 4, 8, 32, drv.p(modes), None)
+    assert modes.tolist() == [[2, 2, 0, 0]], modes
+    check_fwd_bwd(q, k, v, do, iq, ik, np.linspace(-0.3, 0.3, 4).astype(np.float32))
+
 if __name__ == "__main__":
     for name in sys.argv[1:]:
         fn, _, arg = name.partition("=")
