@@ -16,6 +16,8 @@ UNITS = ["dism_aux", "dism_sort", "dism_msort", "dism_pairs", "dism_scan", "dism
 
 def build(out_dir, csrc=os.path.join(ROOT, "dism_amd", "csrc")):
     os.makedirs(out_dir, exist_ok=True)
+    # -O0: basic blocks stay in source order, which the lowest-code-position scheduling
+    # relies on (with -O1 block layout and if-conversion the lockstep order breaks)
     flags = ["-std=c++17", "-O0", "-g", "-fno-omit-frame-pointer", "-fPIC", "-ffp-contract=off",
              "-fno-fast-math", "-Wno-attributes", "-fsanitize=address", "-I" + HERE,
              "-I" + csrc]
