@@ -1,14 +1,16 @@
 """The allocation-free forward (dism_hard_forward_noalloc: workspace in the library's device
 array, every launch on the caller's stream) against the existing one-call forward with a caller
 workspace (dism_hard_forward), bit for bit: two calls in a row, the second smaller (the array
-keeps the first call's contents), with sparse, dense and strip-bounded rows and soft rows.
-Also the size limit's error."""
+keeps the first call's contents), with sparse, dense and strip-bounded rows and soft rows;
+the fp32 call also against the CPU model (oracle.forward), bit for bit.  Also the size
+limit's error."""
 import ctypes
 
 import numpy as np
 import pytest
 import torch
 
+import oracle
 from tests._data import labels, taus, vectors
 
 pytestmark = pytest.mark.gpu
@@ -76,6 +78,16 @@ def test_noalloc_forward_matches_workspace_forward():
                                       (torch.int32 if g.dtype.is_floating_point else g.dtype)),
                                w.view(torch.int16 if w.dtype == torch.bfloat16 else
                                       (torch.int32 if w.dtype.is_floating_point else w.dtype))), name
+        if od == torch.float32:
+            sq, sk, v, q, k, hard, tau = x
+            ref = oracle.forward(sq, sk, v, q, k, hard, oracle.log_weights(tau, sq.shape[1]))
+            for g, w, name in zip(got, ref, ("out", "lse2", "lmax", "jarg")):
+                g = g.numpy()
+                if g.dtype == np.float32:
+                    assert np.array_equal(g.view(np.uint32),
+                                          np.asarray(w, np.float32).view(np.uint32)), name
+                else:
+                    assert np.array_equal(g, w), name
 
 
 def test_noalloc_forward_rejects_large_shapes():
