@@ -177,3 +177,15 @@ def noalloc(sq, sk, v, iq, ik, hard, lut, dtype=0):
     call("dism_hard_forward_noalloc", p(a), p(b), p(c), dtype, p(iq), p(ik), p(hd), p(lut),
          lut.shape[1], B, N, H, R, DV, p(out), 1, p(lse2), p(lmax), p(jarg), None)
     return out, lse2, lmax, jarg
+
+
+def vocab_labels(x, vocab):
+    """codebook argmax labels of x [B,N,H,D] (bf16 values) against vocab [H,V,D] or [V,D]"""
+    B, N, H, D = x.shape
+    V = vocab.shape[-2]
+    a, b = bf16_bits(x), bf16_bits(vocab)
+    out = np.empty((B, H, N), np.int32)
+    scratch = np.empty(1 + 2 * H + B * H * N, np.int32)
+    call("dism_vocab_labels", p(a), p(b), 0 if vocab.ndim == 2 else V * D, B, N, H, V, D,
+         p(out), p(scratch), None)
+    return out, int(scratch[0])

@@ -57,6 +57,9 @@ static size_t g_stack_size = size_t(1) << 20;
 static std::vector<unsigned char*> g_stacks;
 
 Lane* cur() { return g_cur; }
+static MfmaStage g_mfma[64];
+MfmaStage& mfma_stage(int wave) { return g_mfma[wave & 63]; }
+int wave_of_cur() { return g_cur->wave; }
 const dim3& tid_of(Lane* l) { return l->tid; }
 int lane_of_cur() { return g_cur->lane; }
 

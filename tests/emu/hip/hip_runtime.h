@@ -147,7 +147,43 @@ inline void emu_global_load_lds(const void* src, void* dst, int size, int, int) 
     std::memcpy(static_cast<unsigned char*>(dst) + emu::lane_of_cur() * size, src, size);
 }
 #define __builtin_amdgcn_global_load_lds(s, d, sz, o, a) emu_global_load_lds(s, (void*)(d), sz, o, a)
-#define __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(...) (abort(), decltype(__VA_ARGS__)())
+// v_mfma_f32_32x32x8_bf16 (1k): A 32x8 (lane l: row l % 32, k = 4 (l / 32) + 0..3), B 8x32
+// (lane l: column l % 32, same k), C/D 32x32 (lane l: column l % 32; register r: row
+// 8 (r / 4) + 4 (l / 32) + r % 4).  The wave's operands meet in a staging table at a wave
+// barrier; each lane then forms its own column (products exact in fp32, summed in k order,
+// added to C).  Only the vocabulary kernels use it (clang units: ext_vector_type operands).
+inline float __uint_as_float(uint32_t u);
+namespace emu {
+struct MfmaStage { uint16_t a[64][4], b[64][4]; };
+MfmaStage& mfma_stage(int wave);
+int wave_of_cur();
+}
+template <typename AB, typename C>
+inline C emu_mfma_32x32x8bf16(AB a, AB b, C c, int, int, int) {
+    const int l = emu::lane_of_cur();
+    emu::MfmaStage& st = emu::mfma_stage(emu::wave_of_cur());
+    for (int t = 0; t < 4; ++t) {
+        st.a[l][t] = (uint16_t)a[t];
+        st.b[l][t] = (uint16_t)b[t];
+    }
+    emu::wave_op(emu::OP_BARRIER, 0, 0);
+    const int j = l % 32, half = l / 32;
+    C d = c;
+    for (int r = 0; r < 16; ++r) {
+        const int i = 8 * (r / 4) + 4 * half + r % 4;
+        float acc = 0.0f;
+        for (int k = 0; k < 8; ++k) {
+            const int la = i + 32 * (k / 4), lb = j + 32 * (k / 4);
+            const float x = __uint_as_float((uint32_t)st.a[la][k % 4] << 16);
+            const float y = __uint_as_float((uint32_t)st.b[lb][k % 4] << 16);
+            acc = __builtin_fmaf(x, y, acc);
+        }
+        d[r] = c[r] + acc;
+    }
+    emu::wave_op(emu::OP_BARRIER, 0, 0);
+    return d;
+}
+#define __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(a, b, c, x, y, z) emu_mfma_32x32x8bf16(a, b, c, x, y, z)
 
 inline float __uint_as_float(uint32_t u) { float f; std::memcpy(&f, &u, 4); return f; }
 inline uint32_t __float_as_uint(float f) { uint32_t u; std::memcpy(&u, &f, 4); return u; }

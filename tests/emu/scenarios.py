@@ -308,6 +308,25 @@ def probe_modes():
     assert modes.tolist() == [[2, 2, 0, 0]], modes
     check_fwd_bwd(q, k, v, do, iq, ik, np.linspace(-0.3, 0.3, 4).astype(np.float32))
 
+
+def vocab():
+    """codebook argmax labels on the emulated matrix-core tiles: random, duplicated (exact
+    ties: first index) and near-tie rows, per-head and shared vocabularies, a vocabulary that
+    is not a multiple of 32 rows; equal to the exact CPU model"""
+    rng = np.random.default_rng(21)
+    B, N, H = 1, 64, 2
+    for D, V, shared in ((32, 96, False), (64, 70, True), (128, 40, False)):
+        x = oracle.bf16_round(rng.standard_normal((B, N, H, D)))
+        voc = oracle.bf16_round(rng.standard_normal((V, D) if shared else (H, V, D)))
+        if not shared:
+            # duplicated rows: exact ties (first index wins), and tokens equal to them
+            voc[:, V - 3] = voc[:, 7]
+            x[0, :8, :, :] = voc[:, 7][None, :, :].transpose(0, 1, 2)
+        got, rescored = drv.vocab_labels(x, voc)
+        want = oracle.vocab_labels(x, voc)
+        assert np.array_equal(got, want), (D, V, shared, int((got != want).sum()))
+        assert shared or rescored > 0, "ties must be rescored in fp64"
+
 if __name__ == "__main__":
     for name in sys.argv[1:]:
         fn, _, arg = name.partition("=")

@@ -42,3 +42,9 @@ def test_padded_prefill_prefix_rows(emu_lib):
     """dism_hard_prefill on rows padded from 79 to 256 tokens whose real positions form
     prefix rows (the compacted segment list): bit-exact, no invalid access"""
     _run(emu_lib, "prefill_padded")
+
+
+def test_codebook_labels(emu_lib):
+    """dism_vocab_labels on emulated v_mfma_f32_32x32x8_bf16 tiles (operand layouts of the
+    instruction), with exact ties rescored in fp64: equal to the exact CPU model"""
+    _run(emu_lib, "vocab")
