@@ -1198,13 +1198,18 @@ __global__ __launch_bounds__(SORT_THREADS) void level_lvl_kernel(PathArgs a, int
 }
 
 // Mode 3 for the rows level_lvl_kernel built whose levels end within LEVEL_MAX and the
-// budget; the level offsets, segment bases and per-position summaries.
+// budget; the level offsets, segment bases and per-position summaries.  Grid (B*H, slices of
+// 256 positions): every workgroup of a row decides the same way from the row's level
+// counts; slice 0 writes the row's offsets and mode, slice y the summaries of its positions.
+// A slice may start after slice 0 has set mode 3, so mode 3 counts as "dense" here (no other
+// kernel sets it before this one).
 __global__ __launch_bounds__(256) void level_finalize_kernel(PathArgs a) {
     __shared__ uint32_t s_or;
     __shared__ int s_nlev;
-    const int bh = blockIdx.x, tid = threadIdx.x, n = a.n;
+    const int bh = blockIdx.x, tid = threadIdx.x, n = a.n, y = blockIdx.y;
     const int nv = a.cls_n > 0 && a.cls_n < n ? a.cls_n : n;
-    if (a.o.dflag[bh] != 1) return;
+    const int f = a.o.dflag[bh];
+    if (f != 1 && f != 3) return;
     const long so = (long)bh * n;
     if (tid == 0) s_or = 0;
     __syncthreads();
@@ -1221,13 +1226,15 @@ __global__ __launch_bounds__(256) void level_finalize_kernel(PathArgs a) {
         int nlev = z ? __builtin_ctzll(z) : -1, total = 0;
         if (nlev > 0) {
             int segs = 0;
-            meta[1] = 0;
-            meta[LEVEL_MAX + 2] = 0;
+            if (y == 0 && tid == 0) {
+                meta[1] = 0;
+                meta[LEVEL_MAX + 2] = 0;
+            }
             for (int l = 1; l <= nlev; ++l) {
                 const int cl = __shfl(c, l - 1);
                 total += cl;
                 segs += (cl + LEVEL_SEG - 1) / LEVEL_SEG;
-                if (tid == 0) {
+                if (y == 0 && tid == 0) {
                     meta[1 + l] = total;
                     meta[LEVEL_MAX + 2 + l] = segs;
                 }
@@ -1241,7 +1248,7 @@ __global__ __launch_bounds__(256) void level_finalize_kernel(PathArgs a) {
     if (nlev <= 0) return;
     const uint8_t* lf = a.o.lvlf + (long)bh * (LEVEL_MAX + 1) * n;
     const uint16_t* lk = a.o.lvlk + (long)bh * LEVEL_MAX * n;
-    for (int p = tid; p < n; p += 256) {
+    for (int p = y * 256 + tid; p < n && p < (y + 1) * 256; p += 256) {
         int kq = 0, lq = 0, kk = 0;
         for (int l0 = 1; l0 <= nlev; l0 += 8) {  // eight levels' loads in flight
             int f[8];
@@ -1256,8 +1263,7 @@ __global__ __launch_bounds__(256) void level_finalize_kernel(PathArgs a) {
         }
         a.o.lvq[so + p] = make_int4(lq, lq > 0 ? (int)lk[(long)(lq - 1) * n + p] : -1, kq, kk);
     }
-    __syncthreads();
-    if (tid == 0) {
+    if (y == 0 && tid == 0) {
         meta[0] = nlev;
         a.o.dflag[bh] = 3;
     }
@@ -1270,7 +1276,8 @@ hipError_t launch_level_prep(const PathArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(level_lvl_kernel, dim3(BH, 16), dim3(SORT_THREADS), 0, s, a, 1);
     hipLaunchKernelGGL(level_lvl_kernel, dim3(BH, LEVEL_MAX + 1 - 16), dim3(SORT_THREADS), 0, s,
                        a, 17);
-    hipLaunchKernelGGL(level_finalize_kernel, dim3(BH), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(level_finalize_kernel, dim3(BH, (unsigned)((a.n + 255) / 256)),
+                       dim3(256), 0, s, a);
     hipLaunchKernelGGL(level_prep_kernel, dim3(BH), dim3(SORT_THREADS), 0, s, a);
     return hipGetLastError();
 }
