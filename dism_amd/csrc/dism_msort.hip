@@ -10,7 +10,8 @@
 //   scatter: workgroup (row, s) derives the start of each digit run of its segment from the
 //            count table (runs of earlier digits anywhere, then the same digit in earlier
 //            segments), ranks its elements in order (per-wave digit counts, lane masks built
-//            with LDS atomic ORs) and writes them.
+//            with LDS atomic ORs), chunk by chunk into digit order in LDS, and writes each
+//            chunk out with the elements of one digit at consecutive positions.
 // Both are stable, so the result equals sort_kernel's (same digits, same pass order, same
 // outputs).  The digits used by a row are only known on the device: msort_mask_kernel
 // records the label bits each row uses, every pass up to the most a row can need is
@@ -209,13 +210,22 @@ __global__ __launch_bounds__(MS_THREADS) void msort_hist_kernel(SortArgs a, int 
     counts[((long)row * MS_RADIX + tid) * S + s] = s_cnt[tid];
 }
 
-// grid (rows, S): stable scatter of segment s
+// grid (rows, S): stable scatter of segment s, in chunks of MS_CHUNK elements staged in LDS:
+// a chunk is ranked in order (per-wave digit counts, lane masks built with LDS atomic ORs)
+// into its digit-sorted order in LDS, then written out by consecutive threads, so that the
+// elements of one digit go to consecutive output positions (runs of about MS_CHUNK / 256
+// elements instead of single 4-byte stores).
+constexpr int MS_CHUNK = MS_THREADS * MS_U;  // 2048: 512 elements per wave
 __global__ __launch_bounds__(MS_THREADS) void msort_scatter_kernel(SortArgs a, int kind,
                                                                    int pass, int S,
                                                                    const int32_t* counts) {
     __shared__ int s_scan[MS_RADIX];
     __shared__ int s_wcnt[MS_WAVES][MS_RADIX];
     __shared__ unsigned long long s_mask[MS_WAVES][MS_RADIX];
+    __shared__ int s_start[MS_RADIX];   // chunk-local start of each digit's run
+    __shared__ int s_base[MS_RADIX];    // output position of each digit's next element
+    __shared__ int s_v[MS_CHUNK], s_l1[MS_CHUNK], s_l2[MS_CHUNK];
+    __shared__ uint8_t s_d[MS_CHUNK];
     const int row = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     MsRow r;
@@ -231,94 +241,110 @@ __global__ __launch_bounds__(MS_THREADS) void msort_scatter_kernel(SortArgs a, i
             if (t < s) pre += v;
         }
     }
-    // exclusive scan of the totals over digits (one wave, 4 digits per lane)
-    s_scan[tid] = tot;
-    __syncthreads();
-    if (tid < 64) {
-        const int v0 = s_scan[4 * tid], v1 = s_scan[4 * tid + 1], v2 = s_scan[4 * tid + 2],
-                  v3 = s_scan[4 * tid + 3];
-        const int sum = v0 + v1 + v2 + v3;
-        int inc = sum;
+    // exclusive scan over digits (one wave, 4 digits per lane): s_scan[d] = the scan of v[d]
+    auto digit_scan = [&](int v) {
+        s_scan[tid] = v;
+        __syncthreads();
+        if (tid < 64) {
+            const int v0 = s_scan[4 * tid], v1 = s_scan[4 * tid + 1], v2 = s_scan[4 * tid + 2],
+                      v3 = s_scan[4 * tid + 3];
+            const int sum = v0 + v1 + v2 + v3;
+            int inc = sum;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int t = __shfl_up(inc, o);
-            if (lane >= o) inc += t;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int t = __shfl_up(inc, o);
+                if (lane >= o) inc += t;
+            }
+            int ex = inc - sum;
+            s_scan[4 * tid] = ex;
+            ex += v0;
+            s_scan[4 * tid + 1] = ex;
+            ex += v1;
+            s_scan[4 * tid + 2] = ex;
+            ex += v2;
+            s_scan[4 * tid + 3] = ex;
         }
-        int ex = inc - sum;
-        s_scan[4 * tid] = ex;
-        ex += v0;
-        s_scan[4 * tid + 1] = ex;
-        ex += v1;
-        s_scan[4 * tid + 2] = ex;
-        ex += v2;
-        s_scan[4 * tid + 3] = ex;
-    }
-    __syncthreads();
-    const int run0 = s_scan[tid];  // start of digit tid's run in the whole row
+        __syncthreads();
+        const int res = s_scan[tid];
+        __syncthreads();
+        return res;
+    };
+    const int run0 = digit_scan(tot);  // start of digit tid's run in the whole row
     if (r.table && s == 0) {
         r.table[tid] = run0;
         if (tid == 0) r.table[MS_RADIX] = r.m;
     }
-    // per-wave sub-segments of the segment, in order; per-wave digit counts
-    const int wseg = ((g.end - g.beg + MS_WAVES - 1) / MS_WAVES + 63) / 64 * 64;
-    const int wb = g.beg + wave * wseg < g.end ? g.beg + wave * wseg : g.end;
-    const int we = wb + wseg < g.end ? wb + wseg : g.end;
-    for (int w = 0; w < MS_WAVES; ++w) {
-        s_wcnt[w][tid] = 0;
-        s_mask[w][tid] = 0ull;
-    }
-    __syncthreads();
-    for (int x0 = wb; x0 < we; x0 += 64 * MS_U) {
-        int dig[MS_U];
+    s_base[tid] = run0 + pre;
+    const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    for (int c0 = g.beg; c0 < g.end; c0 += MS_CHUNK) {
+        const int cn = g.end - c0 < MS_CHUNK ? g.end - c0 : MS_CHUNK;
+        // wave w takes elements [wb, we) of the chunk, in order
+        const int wb = c0 + wave * (MS_CHUNK / MS_WAVES);
+        const int we = wb + MS_CHUNK / MS_WAVES < c0 + cn ? wb + MS_CHUNK / MS_WAVES : c0 + cn;
+        for (int w = 0; w < MS_WAVES; ++w) {
+            s_wcnt[w][tid] = 0;
+            s_mask[w][tid] = 0ull;
+        }
+        __syncthreads();
+        int vv[MS_U], dd[MS_U], c1[MS_U], c2[MS_U];
 #pragma unroll
-        for (int u = 0; u < MS_U; ++u) {
-            const int x = x0 + 64 * u + lane;
-            int v, l1, l2;
-            ms_elem(r, kind, x < we ? x : we - 1, v, dig[u], l1, l2);
+        for (int u = 0; u < MS_U; ++u) {  // all loads of the wave's part in flight together
+            const int x = wb + 64 * u + lane;
+            ms_elem(r, kind, x < we ? x : (we > wb ? we - 1 : c0), vv[u], dd[u], c1[u], c2[u]);
         }
 #pragma unroll
         for (int u = 0; u < MS_U; ++u)
-            if (x0 + 64 * u + lane < we) atomicAdd(&s_wcnt[wave][dig[u]], 1);
-    }
-    __syncthreads();
-    {
-        int run = run0 + pre;
-        for (int w = 0; w < MS_WAVES; ++w) {
-            const int c = s_wcnt[w][tid];
-            s_wcnt[w][tid] = run;
-            run += c;
-        }
-    }
-    __syncthreads();
-    const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
-    for (int b0 = wb; b0 < we; b0 += 64 * MS_U) {
-      int vv[MS_U], dd[MS_U], c1[MS_U], c2[MS_U];
-#pragma unroll
-      for (int u = 0; u < MS_U; ++u) {
-          const int x = b0 + 64 * u + lane;
-          ms_elem(r, kind, x < we ? x : we - 1, vv[u], dd[u], c1[u], c2[u]);
-      }
-#pragma unroll
-      for (int u = 0; u < MS_U; ++u) {
-        const int x = b0 + 64 * u + lane;
-        if (x < we) {
-            const int v = vv[u], dig = dd[u], l1 = c1[u], l2 = c2[u];
-            atomicOr(&s_mask[wave][dig], 1ull << lane);
-            __builtin_amdgcn_wave_barrier();
-            const unsigned long long eq = s_mask[wave][dig];
-            const int rank = __popcll(eq & below);
-            const int dst = s_wcnt[wave][dig] + rank;
-            __builtin_amdgcn_wave_barrier();
-            if (rank == 0) {
-                s_wcnt[wave][dig] += __popcll(eq);
-                s_mask[wave][dig] = 0ull;
+            if (wb + 64 * u + lane < we) atomicAdd(&s_wcnt[wave][dd[u]], 1);
+        __syncthreads();
+        // digit tid: the chunk's count, its run start in the chunk, each wave's start
+        int ctot = 0;
+        for (int w = 0; w < MS_WAVES; ++w) ctot += s_wcnt[w][tid];
+        const int cstart = digit_scan(ctot);
+        s_start[tid] = cstart;
+        {
+            int run = cstart;
+            for (int w = 0; w < MS_WAVES; ++w) {
+                const int c = s_wcnt[w][tid];
+                s_wcnt[w][tid] = run;
+                run += c;
             }
-            __builtin_amdgcn_wave_barrier();
-            r.out[dst] = v;
-            if (r.lab_out) r.lab_out[dst] = l1;
-            if (r.plab_out) r.plab_out[dst] = l2;
         }
-      }
+        __syncthreads();
+        // rank in order within the wave: chunk-local positions in digit order
+#pragma unroll
+        for (int u = 0; u < MS_U; ++u) {
+            const int x = wb + 64 * u + lane;
+            if (x < we) {
+                const int dig = dd[u];
+                atomicOr(&s_mask[wave][dig], 1ull << lane);
+                __builtin_amdgcn_wave_barrier();
+                const unsigned long long eq = s_mask[wave][dig];
+                const int rank = __popcll(eq & below);
+                const int lp = s_wcnt[wave][dig] + rank;
+                __builtin_amdgcn_wave_barrier();
+                if (rank == 0) {
+                    s_wcnt[wave][dig] += __popcll(eq);
+                    s_mask[wave][dig] = 0ull;
+                }
+                __builtin_amdgcn_wave_barrier();
+                s_v[lp] = vv[u];
+                s_l1[lp] = c1[u];
+                s_l2[lp] = c2[u];
+                s_d[lp] = (uint8_t)dig;
+            }
+        }
+        __syncthreads();
+        // write out: consecutive chunk positions of one digit go to consecutive outputs
+        for (int t = tid; t < cn; t += MS_THREADS) {
+            const int d = s_d[t];
+            const int dst = s_base[d] + (t - s_start[d]);
+            r.out[dst] = s_v[t];
+            if (r.lab_out) r.lab_out[dst] = s_l1[t];
+            if (r.plab_out) r.plab_out[dst] = s_l2[t];
+        }
+        __syncthreads();
+        s_base[tid] += ctot;
+        __syncthreads();
     }
 }
 

@@ -139,22 +139,30 @@ def prefill_other():
 
 
 
-def packed_docs():
-    """a packed batch-1 call with documents [0, 256) and [256, 512) in two training rows
-    (hard flags [[T], [F]] per head pair): every hard document equals the CPU model on that
-    document alone, soft documents give zeros; dtau over the hard documents"""
-    N, H, R, DV = 512, 2, 8, 64
-    q, k, v, do, iq, ik = _inputs(1, N, H, R, DV, 31)
+def packed_docs(size="512"):
+    """a packed batch-1 call of two documents of N/2 tokens in two training rows (hard flags
+    [[T, F], [F, T]]): every hard document equals the CPU model on that document alone, soft
+    documents give zeros; dtau over the hard documents.  N = 4096 with two-byte labels takes
+    the multi-block sort through two chunks per segment and two digits per key"""
+    N, H, R, DV = int(size), 2, 8, 64
+    half = N // 2
+    if N > 512:
+        def labels(rng):
+            return (rng.integers(0, 3000, (1, H, N)).astype(np.int32),
+                    rng.integers(0, 3000, (1, H, N)).astype(np.int32))
+        q, k, v, do, iq, ik = _inputs(1, N, H, R, DV, 31, labels)
+    else:
+        q, k, v, do, iq, ik = _inputs(1, N, H, R, DV, 31)
     hard_rows = np.array([[True, False], [False, True]])
     tau = np.array([0.4, -0.3], np.float32)
-    offsets = [0, 256, 512]
-    lut = oracle.log_weights(tau, 256)
-    dlut = oracle.dlog_weights(tau, 256)
+    offsets = [0, half, N]
+    lut = oracle.log_weights(tau, half)
+    dlut = oracle.dlog_weights(tau, half)
     out, l2, lm, ja, dsq, dsk, dv, dtau, rowtau = drv.packed(q, k, v, do, iq, ik, hard_rows,
-                                                            lut, dlut, offsets, 256)
+                                                            lut, dlut, offsets, half)
     want_rt = np.zeros((1, H, N), np.float32)
     dense = oracle.packed_dense_flags(iq, ik, offsets)
-    for d, (a, z) in enumerate(((0, 256), (256, 512))):
+    for d, (a, z) in enumerate(((0, half), (half, N))):
         flags = hard_rows[d:d + 1]
         args = (q[:, a:z], k[:, a:z], v[:, a:z])
         labs = (iq[:, :, a:z], ik[:, :, a:z])
