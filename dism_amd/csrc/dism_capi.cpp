@@ -564,6 +564,12 @@ int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t
         classified = hipStreamWaitEvent(s, side->mid, 0) == hipSuccess;
     if (e == hipSuccess && !classified) e = hipErrorUnknown;
     if (e == hipSuccess) e = dism::launch_prepare_pairs(sa, a, ps);
+    // rows of the pairless modes (dense tiles, level rows, prefix rows) read neither the
+    // scan's records nor the pair plan: their readouts follow the prepare on the side stream,
+    // off the scan -> pair-correction chain (their launches exit at once without such rows)
+    if (e == hipSuccess) e = dism::launch_dense_forward(a, R, DV, dtype, ps);
+    if (e == hipSuccess) e = dism::launch_level_forward(a, R, DV, dtype, ps);
+    if (e == hipSuccess) e = dism::launch_prefix_forward(a, R, DV, dtype, ps);
     if (e == hipSuccess) {
         a.fwd_phase = 1;
         e = dism::launch_scan_forward(a, R, DV, dtype, s);
@@ -577,14 +583,7 @@ int32_t dism_hard_forward(const void* sq, const void* sk, const void* v, int32_t
     a.fwd_phase = 2;
     if ((st = hip_status(dism::launch_scan_forward(a, R, DV, dtype, s), "hard forward")))
         return st;
-    if ((st = hip_status(dism::launch_pairs_finish(a, R, DV, dtype, s), "hard forward pairs")))
-        return st;
-    if ((st = hip_status(dism::launch_dense_forward(a, R, DV, dtype, s), "hard forward dense rows")))
-        return st;
-    if ((st = hip_status(dism::launch_level_forward(a, R, DV, dtype, s),
-                         "hard forward level rows")))
-        return st;
-    return hip_status(dism::launch_prefix_forward(a, R, DV, dtype, s), "hard forward prefix rows");
+    return hip_status(dism::launch_pairs_finish(a, R, DV, dtype, s), "hard forward pairs");
 }
 
 }  // extern "C"

@@ -159,8 +159,9 @@ int32_t dism_hard_readout(const void* sq, const void* sk, const void* v, int32_t
 
 /* dism_hard_prepare followed by dism_hard_readout, in one call with the same arguments as
  * dism_hard_readout (the workspace need not be prepared; it is on return, for the backward).
- * The bigram half of the preparation runs on the calling thread's side stream (see
- * dism_hard_backward), overlapped with the length-1 label scan, and is joined back into
+ * The row classification, the bigram half of the preparation and the readouts of dense,
+ * level and prefix rows run on the calling thread's side stream (see dism_hard_backward),
+ * overlapped with the label order and the length-1 label scan, and are joined back into
  * `stream` before the pair kernels.  Outputs are bit-identical to the two-call sequence.
  * Replaces the forward_hard chain summary -> chunk -> readout
  * (dism_v3/python/flash_dism/hard_forward.py:36-47). */
