@@ -335,6 +335,37 @@ def vocab():
         assert np.array_equal(got, want), (D, V, shared, int((got != want).sum()))
         assert shared or rescored > 0, "ties must be rescored in fp64"
 
+
+def packed_graph_offsets():
+    """a packed call with the fixed-capacity offsets of a graph layout: one slot per 256
+    tokens, the padding slots repeating the token count (empty documents at the end), and
+    the documents' labels tagged with that slot count (oracle.packed_dense_flags slots=)"""
+    N, H, R, DV = 1024, 2, 8, 32
+    q, k, v, do, iq, ik = _inputs(1, N, H, R, DV, 41)
+    hard_rows = np.ones((1, H), bool)
+    tau = np.array([0.2, -0.4], np.float32)
+    docs = ((0, 256), (256, 1024))
+    offsets = [0, 256, 1024, 1024, 1024]
+    lut = oracle.log_weights(tau, N)
+    dlut = oracle.dlog_weights(tau, N)
+    out, l2, lm, ja, dsq, dsk, dv, dtau, rowtau = drv.packed(q, k, v, do, iq, ik, hard_rows,
+                                                            lut, dlut, offsets, 768)
+    dense = oracle.packed_dense_flags(iq, ik, offsets, slots=len(offsets) - 1)
+    want_rt = np.zeros((1, H, N), np.float32)
+    for a, z in docs:
+        lt = oracle.log_weights(tau, z - a)
+        dt = oracle.dlog_weights(tau, z - a)
+        args = (q[:, a:z], k[:, a:z], v[:, a:z])
+        labs = (iq[:, :, a:z], ik[:, :, a:z])
+        o, l2o, lmo, jao = oracle.forward(*args, *labs, hard_rows, lt, dense=dense)
+        assert same_bits(out[:, a:z], o), ("out", a)
+        assert same_bits(l2[:, :, a:z], l2o), ("lse2", a)
+        g = oracle.backward(*args, do[:, a:z], *labs, hard_rows, lt, dt, l2o, dense=dense)
+        for x, y, name in zip((dsq[:, a:z], dsk[:, a:z], dv[:, a:z]), g[:3], ("dsq", "dsk", "dv")):
+            assert same_bits(x, y), (name, a)
+        want_rt[:, :, a:z] = g[4]
+    assert same_bits(dtau, oracle.tau_reduce(want_rt)), "dtau"
+
 if __name__ == "__main__":
     for name in sys.argv[1:]:
         fn, _, arg = name.partition("=")
