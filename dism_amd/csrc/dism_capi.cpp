@@ -148,6 +148,38 @@ class SideLease {
     SideStream* s_ = nullptr;
 };
 
+// A leased side stream forked from `s` for the backward's pairless-mode kernels (dense
+// tiles, level rows, prefix rows): their rows are disjoint from the label scans' rows, so
+// they run beside the scan instead of ahead of it on the same chain (at the headline shape
+// they find no rows, but each launch still waits for free compute units).  join() records
+// the side stream's work and makes `s` wait for it; without a side stream everything stays
+// on `s`.
+class PairlessFork {
+  public:
+    explicit PairlessFork(hipStream_t s) : s_(s) {
+        side_ = lease_.get();
+        if (side_ && (hipEventRecord(side_->fork, s_) != hipSuccess ||
+                      hipStreamWaitEvent(side_->stream, side_->fork, 0) != hipSuccess))
+            side_ = nullptr;
+    }
+    hipStream_t side() const { return side_ ? side_->stream : s_; }
+    bool join() {
+        if (!side_) return true;
+        const bool ok = hipEventRecord(side_->join, side_->stream) == hipSuccess &&
+                        hipStreamWaitEvent(s_, side_->join, 0) == hipSuccess;
+        side_ = nullptr;
+        return ok;
+    }
+    ~PairlessFork() { join(); }
+    PairlessFork(const PairlessFork&) = delete;
+    PairlessFork& operator=(const PairlessFork&) = delete;
+
+  private:
+    hipStream_t s_;
+    SideLease lease_;
+    SideStream* side_ = nullptr;
+};
+
 Layout layout(int64_t B, int64_t N, int64_t H, int32_t R, int32_t DV) {
     Layout L;
     const int64_t BH = B * H;
@@ -716,18 +748,20 @@ int32_t dism_hard_backward_queries(const void* sq, const void* sk, const void* v
     a.dlut = dlut;
     a.dsq = dsq;
     a.rowtau = rowtau;
-    // the dense, level and prefix rows first: their kernels mostly find no rows, and such
-    // launches drain fastest before the label scan fills the device
-    if ((st = hip_status(dism::launch_dense_rows(a, R, DV, dtype, S(stream)),
-                         "hard backward dense rows")))
-        return st;
-    if ((st = hip_status(dism::launch_level_rows(a, R, DV, dtype, S(stream)),
-                         "hard backward level rows")))
-        return st;
-    if ((st = hip_status(dism::launch_prefix_rows(a, R, DV, dtype, S(stream)),
-                         "hard backward prefix rows")))
-        return st;
-    return hip_status(dism::launch_scan_rows(a, R, DV, dtype, S(stream)), "hard backward rows");
+    // the dense, level and prefix rows (disjoint from the scan's rows) beside the label scan
+    PairlessFork fork(S(stream));
+    if ((st = hip_status(dism::launch_dense_rows(a, R, DV, dtype, fork.side()),
+                         "hard backward dense rows")) ||
+        (st = hip_status(dism::launch_level_rows(a, R, DV, dtype, fork.side()),
+                         "hard backward level rows")) ||
+        (st = hip_status(dism::launch_prefix_rows(a, R, DV, dtype, fork.side()),
+                         "hard backward prefix rows")) ||
+        (st = hip_status(dism::launch_scan_rows(a, R, DV, dtype, S(stream)),
+                         "hard backward rows")))
+        fork.join();
+    else
+        st = fork.join() ? DISM_OK : fail(DISM_ERR_HIP, "hard backward rows: stream join failed");
+    return st;
 }
 
 int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, const void* dout,
@@ -745,16 +779,20 @@ int32_t dism_hard_backward_keys(const void* sq, const void* sk, const void* v, c
     if (!dsk || !dv) return fail(DISM_ERR_INVALID, "hard backward: null pointer");
     a.dsk = dsk;
     a.dv = dv;
-    if ((st = hip_status(dism::launch_dense_keys(a, R, DV, dtype, S(stream)),
-                         "hard backward dense keys")))
-        return st;
-    if ((st = hip_status(dism::launch_level_keys(a, R, DV, dtype, S(stream)),
-                         "hard backward level keys")))
-        return st;
-    if ((st = hip_status(dism::launch_prefix_keys(a, R, DV, dtype, S(stream)),
-                         "hard backward prefix keys")))
-        return st;
-    return hip_status(dism::launch_scan_keys(a, R, DV, dtype, S(stream)), "hard backward keys");
+    // the dense, level and prefix rows' keys (disjoint from the scan's rows) beside the scan
+    PairlessFork fork(S(stream));
+    if ((st = hip_status(dism::launch_dense_keys(a, R, DV, dtype, fork.side()),
+                         "hard backward dense keys")) ||
+        (st = hip_status(dism::launch_level_keys(a, R, DV, dtype, fork.side()),
+                         "hard backward level keys")) ||
+        (st = hip_status(dism::launch_prefix_keys(a, R, DV, dtype, fork.side()),
+                         "hard backward prefix keys")) ||
+        (st = hip_status(dism::launch_scan_keys(a, R, DV, dtype, S(stream)),
+                         "hard backward keys")))
+        fork.join();
+    else
+        st = fork.join() ? DISM_OK : fail(DISM_ERR_HIP, "hard backward keys: stream join failed");
+    return st;
 }
 
 int32_t dism_hard_backward_key_pairs(const void* sq, const void* sk, const void* v,

@@ -4,9 +4,10 @@
  * Library: dism_amd/libdism_hip.so (gfx950).  Every entry point takes raw device pointers,
  * sizes and a HIP stream (passed as void*, a hipStream_t; NULL = default stream), enqueues
  * its kernels on that stream and returns without synchronising.  The caller allocates all
- * outputs; the library owns no device memory and keeps no mutable global state beyond one
- * side stream and two events per calling thread and device (dism_hard_backward), so calls on
- * different streams or threads are independent.  Return value: 0 on success, otherwise
+ * outputs; the library owns no device memory and keeps no mutable global state beyond a pool
+ * of side streams (three events each, default priority) per device, one leased for the
+ * duration of each entry point that forks (dism_hard_forward, dism_hard_backward and its
+ * queries / keys stages), so calls on different streams or threads are independent.  Return value: 0 on success, otherwise
  * a DISM_ERR_* code with a thread-local message from dism_last_error().
  *
  * Layouts follow the reference: vectors BNHD ([B,N,H,R] / [B,N,H,DV], contiguous), labels
@@ -189,8 +190,9 @@ int32_t dism_hard_backward(const void* sq, const void* sk, const void* v, const 
                            int32_t DV, void* workspace, int64_t workspace_bytes, float* dsq,
                            float* dsk, float* dv, float* rowtau, float* dtau, void* stream);
 
-/* Stages of dism_hard_backward, one kernel each, callable separately in this order (same
- * arguments as above).  Together they replace the hard_dlog_weights / hard_backward /
+/* Stages of dism_hard_backward, callable separately in this order (same arguments as
+ * above).  queries and keys run the kernels of dense, level and prefix rows on a leased side
+ * stream beside their label scan and join it back before returning.  Together they replace the hard_dlog_weights / hard_backward /
  * hard_tau_reduce launch sequence of dism_v3/src/host/hard_backward.cpp:242-252:
  *   row_pairs:  corrections of the query rows' bigram pairs into the workspace;
  *   queries:    label scan of the query rows -> dsq, rowtau (uses row_pairs);
